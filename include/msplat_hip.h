@@ -1,0 +1,166 @@
+/*
+ * msplat_hip.h — C ABI of the MI355X (gfx950) splatting hot path.
+ *
+ * This is the drop-in for msplat's backend boundary
+ * /root/reference/core/metal/bindings.h: every entry point below replaces one
+ * declaration there (cited per function).  Plain pointers and sizes only;
+ * per-gaussian arrays are device pointers in the reference's row-major AoS
+ * layouts:
+ *   means[N,3]  scales[N,3] (log)  quats[N,4] (w,x,y,z)
+ *   features_dc[N,3]  features_rest[N,K-1,3]  opacities[N] (logits)
+ *   images [H,W,3] fp32.
+ * Camera matrices and the background colour are passed by value (host).
+ *
+ * Errors: every function returns MSPLAT_OK (0) or a negative code;
+ * msplat_hip_last_error() returns a message for the last failure.
+ * Threading: one context per process, not reentrant (as bindings.h).  All GPU
+ * work is issued in order on one HIP stream (the context's own stream, or the
+ * caller's via msplat_hip_set_stream).
+ */
+#ifndef MSPLAT_HIP_H
+#define MSPLAT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSPLAT_OK 0
+#define MSPLAT_ERR_ARG (-1)
+#define MSPLAT_ERR_HIP (-2)
+#define MSPLAT_ERR_NOINIT (-3)
+#define MSPLAT_ERR_NOMEM (-4)
+
+/* Everything msplat_render takes (bindings.h:37-46). */
+typedef struct MsplatRenderArgs {
+    int32_t num_points;
+    const float* means3d;
+    const float* scales;
+    float glob_scale;
+    const float* quats;
+    float viewmat[16];
+    float projmat[16];
+    float fx, fy, cx, cy;
+    uint32_t img_height, img_width;
+    int32_t tile_bounds[3];
+    float clip_thresh;
+    uint32_t degree;
+    uint32_t degrees_to_use;
+    float cam_pos[3];
+    const float* features_dc;
+    const float* features_rest;
+    const float* opacities;
+    float background[3];
+} MsplatRenderArgs;
+
+/* Everything msplat_train_step takes (bindings.h:50-67).  The six Adam
+ * groups are means, scales, quats, features_dc, features_rest, opacities;
+ * adam_params[g] must alias the matching render pointer.  The three
+ * v_*_out pointers are optional device outputs of the projection backward
+ * (NULL: not written). */
+typedef struct MsplatTrainArgs {
+    MsplatRenderArgs r;
+    const float* gt;
+    float ssim_weight;
+    float loss_inv_n;
+    int32_t features_rest_bases;
+    int32_t num_adam_groups;
+    float* adam_params[6];
+    float* adam_exp_avg[6];
+    float* adam_exp_avg_sq[6];
+    float adam_step_sizes[6];
+    float adam_bc2_sqrts[6];
+    float adam_beta1, adam_beta2, adam_eps;
+    float* vis_counts;
+    float* xys_grad_norm;
+    float* max_2d_size;
+    float inv_max_dim;
+    float* v_mean3d_out;
+    float* v_scale_out;
+    float* v_quat_out;
+} MsplatTrainArgs;
+
+/* Everything msplat_densify takes (bindings.h:69-84) except the nine scratch
+ * tensors, which the library owns.  random_samples: device [2N,3] standard
+ * normals, or NULL to draw them on the GPU from seed. */
+typedef struct MsplatDensifyArgs {
+    int32_t N;
+    int32_t buf_capacity;
+    float grad_thresh, size_thresh, screen_thresh;
+    int32_t check_screen;
+    float cull_alpha_thresh, cull_scale_thresh, cull_screen_size;
+    int32_t check_huge;
+    const float* xys_grad_norm;
+    const float* vis_counts;
+    const float* max_2d_size;
+    float half_max_dim;
+    float* bufs[6];            /* means, scales, quats, f_dc, f_rest, opacities */
+    int32_t fr_stride;
+    float* adam_exp_avg_buf[6];
+    float* adam_exp_avg_sq_buf[6];
+    const float* random_samples;
+    uint64_t seed;
+} MsplatDensifyArgs;
+
+/* Context (replaces the lazily created MetalContext, msplat_metal.mm:173-288,
+ * and cleanup_msplat_metal, bindings.h:8). */
+int msplat_hip_init(int device);
+int msplat_hip_shutdown(void);
+const char* msplat_hip_last_error(void);
+int msplat_hip_set_stream(void* hip_stream);   /* NULL: back to the context's own stream */
+void* msplat_hip_get_stream(void);
+
+/* Memory (gpu_empty / gpu_zeros, bindings.h:18-19).  Copies are ordered on
+ * the context stream; d2h returns after the data has arrived. */
+int msplat_hip_alloc(void** ptr, size_t bytes);
+int msplat_hip_free(void* ptr);
+int msplat_hip_memset(void* ptr, int value, size_t bytes);
+int msplat_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int msplat_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int msplat_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);
+
+/* msplat_commit (bindings.h:22): flush; a no-op on HIP (work is issued eagerly).
+ * msplat_gpu_sync (bindings.h:25): wait for all work on the stream. */
+int msplat_hip_commit(void);
+int msplat_hip_sync(void);
+
+/* msplat_render (bindings.h:37-46).  Writes the image [H,W,3] to out_img
+ * (device); NULL leaves it in the context's own buffer, readable with
+ * msplat_hip_copy_intermediate("out_img"). */
+int msplat_hip_render(const MsplatRenderArgs* a, float* out_img);
+
+/* msplat_train_step (bindings.h:50-67).  radii_out: optional device [N];
+ * loss_out: optional host float — when given the call waits for the step
+ * and returns sum(pixel loss)/(H*W) (the reference reads it unsynchronised,
+ * msplat_metal.mm:1328). */
+int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* loss_out);
+
+/* msplat_densify (bindings.h:69-84).  Waits for the result and returns the
+ * new gaussian count in *new_count. */
+int msplat_hip_densify(const MsplatDensifyArgs* a, int32_t* new_count);
+
+/* Fill dst[n] with standard normals from a counter-based generator
+ * (the reference fills random_samples with mt19937 on the host,
+ * model.cpp:248-253). */
+int msplat_hip_randn(float* dst, int64_t n, uint64_t seed);
+
+/* Per-stage GPU timing (msplat_enable_gpu_timing / msplat_drain_stage_times,
+ * bindings.h:28-33; stage names as msplat_metal.mm:30-34).  When enabled each
+ * stage is bracketed by HIP events; drain returns the per-stage milliseconds
+ * of the last completed call. */
+int msplat_hip_enable_stage_timing(int enable);
+int msplat_hip_drain_stage_times(double* ms, const char** names, int max_stages, int* n_stages);
+
+/* Copy a named intermediate of the last render / train step to host memory.
+ * Names: xys, depths, radii, conics, colors, aabb, num_tiles_hit,
+ * tile_bins, gaussian_ids, final_Ts, final_index, out_img, v_rendered,
+ * v_xy, v_conic, v_rgb, v_opacity, meta.  *nbytes is set to the size; pass
+ * dst == NULL to query it. */
+int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

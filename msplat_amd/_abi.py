@@ -1,0 +1,142 @@
+"""ctypes binding of the C ABI in include/msplat_hip.h (libmsplat_hip.so).
+
+The library is built in-tree by ``make -C msplat_amd`` (see __graft_entry__.build).
+There is no fallback: if the shared object is missing or fails to load, every
+entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmsplat_hip.so")
+
+
+class RenderArgs(ctypes.Structure):
+    """MsplatRenderArgs — everything msplat_render takes (bindings.h:37-46)."""
+
+    _fields_ = [
+        ("num_points", c_int32),
+        ("means3d", c_void_p),
+        ("scales", c_void_p),
+        ("glob_scale", c_float),
+        ("quats", c_void_p),
+        ("viewmat", c_float * 16),
+        ("projmat", c_float * 16),
+        ("fx", c_float), ("fy", c_float), ("cx", c_float), ("cy", c_float),
+        ("img_height", c_uint32), ("img_width", c_uint32),
+        ("tile_bounds", c_int32 * 3),
+        ("clip_thresh", c_float),
+        ("degree", c_uint32),
+        ("degrees_to_use", c_uint32),
+        ("cam_pos", c_float * 3),
+        ("features_dc", c_void_p),
+        ("features_rest", c_void_p),
+        ("opacities", c_void_p),
+        ("background", c_float * 3),
+    ]
+
+
+class TrainArgs(ctypes.Structure):
+    """MsplatTrainArgs — everything msplat_train_step takes (bindings.h:50-67)."""
+
+    _fields_ = [
+        ("r", RenderArgs),
+        ("gt", c_void_p),
+        ("ssim_weight", c_float),
+        ("loss_inv_n", c_float),
+        ("features_rest_bases", c_int32),
+        ("num_adam_groups", c_int32),
+        ("adam_params", c_void_p * 6),
+        ("adam_exp_avg", c_void_p * 6),
+        ("adam_exp_avg_sq", c_void_p * 6),
+        ("adam_step_sizes", c_float * 6),
+        ("adam_bc2_sqrts", c_float * 6),
+        ("adam_beta1", c_float), ("adam_beta2", c_float), ("adam_eps", c_float),
+        ("vis_counts", c_void_p),
+        ("xys_grad_norm", c_void_p),
+        ("max_2d_size", c_void_p),
+        ("inv_max_dim", c_float),
+        ("v_mean3d_out", c_void_p),
+        ("v_scale_out", c_void_p),
+        ("v_quat_out", c_void_p),
+    ]
+
+
+class DensifyArgs(ctypes.Structure):
+    """MsplatDensifyArgs — msplat_densify's arguments (bindings.h:69-84)."""
+
+    _fields_ = [
+        ("N", c_int32),
+        ("buf_capacity", c_int32),
+        ("grad_thresh", c_float), ("size_thresh", c_float), ("screen_thresh", c_float),
+        ("check_screen", c_int32),
+        ("cull_alpha_thresh", c_float), ("cull_scale_thresh", c_float), ("cull_screen_size", c_float),
+        ("check_huge", c_int32),
+        ("xys_grad_norm", c_void_p),
+        ("vis_counts", c_void_p),
+        ("max_2d_size", c_void_p),
+        ("half_max_dim", c_float),
+        ("bufs", c_void_p * 6),
+        ("fr_stride", c_int32),
+        ("adam_exp_avg_buf", c_void_p * 6),
+        ("adam_exp_avg_sq_buf", c_void_p * 6),
+        ("random_samples", c_void_p),
+        ("seed", c_uint64),
+    ]
+
+
+# (name, restype, argtypes) for every symbol declared in include/msplat_hip.h
+SIGNATURES = [
+    ("msplat_hip_init", c_int, [c_int]),
+    ("msplat_hip_shutdown", c_int, []),
+    ("msplat_hip_last_error", c_char_p, []),
+    ("msplat_hip_set_stream", c_int, [c_void_p]),
+    ("msplat_hip_get_stream", c_void_p, []),
+    ("msplat_hip_alloc", c_int, [POINTER(c_void_p), c_size_t]),
+    ("msplat_hip_free", c_int, [c_void_p]),
+    ("msplat_hip_memset", c_int, [c_void_p, c_int, c_size_t]),
+    ("msplat_hip_memcpy_h2d", c_int, [c_void_p, c_void_p, c_size_t]),
+    ("msplat_hip_memcpy_d2h", c_int, [c_void_p, c_void_p, c_size_t]),
+    ("msplat_hip_memcpy_d2d", c_int, [c_void_p, c_void_p, c_size_t]),
+    ("msplat_hip_commit", c_int, []),
+    ("msplat_hip_sync", c_int, []),
+    ("msplat_hip_render", c_int, [POINTER(RenderArgs), c_void_p]),
+    ("msplat_hip_train_step", c_int, [POINTER(TrainArgs), c_void_p, POINTER(c_float)]),
+    ("msplat_hip_densify", c_int, [POINTER(DensifyArgs), POINTER(c_int32)]),
+    ("msplat_hip_randn", c_int, [c_void_p, c_int64, c_uint64]),
+    ("msplat_hip_enable_stage_timing", c_int, [c_int]),
+    ("msplat_hip_drain_stage_times", c_int, [POINTER(c_double), POINTER(c_char_p), c_int, POINTER(c_int)]),
+    ("msplat_hip_copy_intermediate", c_int, [c_char_p, c_void_p, POINTER(c_size_t)]),
+]
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libmsplat_hip.so (once) and declare its signatures.  Raises if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is missing: build the HIP extension first (python -c 'import __graft_entry__ as g; g.build()')")
+    lib = ctypes.CDLL(path)
+    for name, res, args in SIGNATURES:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+class MsplatError(RuntimeError):
+    pass
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = load().msplat_hip_last_error()
+        raise MsplatError(f"msplat_hip error {rc}: {msg.decode() if msg else ''}")

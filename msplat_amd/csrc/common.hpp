@@ -1,0 +1,115 @@
+// common.hpp — device-side math shared by the gfx950 kernels.
+//
+// Numerics: every kernel is compiled with -ffp-contract=off and correctly
+// rounded fp32 division / sqrt, so a*b+c rounds twice unless written as
+// fmaf(), which is used exactly where msplat_metal.metal writes fma().
+// exp() is the Cody–Waite / Taylor exp below, built only from +, *, fma and
+// integer ops so that it gives the same bits on every IEEE target.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace msp {
+
+constexpr int BLOCK = 16;              // tile edge (msplat.hpp:4-5)
+constexpr int TILE_PIX = BLOCK * BLOCK;
+constexpr int CHUNK = 512;             // depth chunk (.metal:2616)
+constexpr int MONO_MAX = 2048;         // largest tile rasterised in one piece (.metal:2021)
+constexpr int CHUNK_MODE_TILES = 400;  // below this many tiles every tile is chunked (.mm:876)
+
+// SH constants (.metal:14-39).
+constexpr float SH_C0 = 0.28209479177387814f;
+constexpr float SH_C1 = 0.4886025119029199f;
+constexpr float SH_C2_0 = 1.0925484305920792f, SH_C2_1 = -1.0925484305920792f,
+                SH_C2_2 = 0.31539156525252005f, SH_C2_3 = -1.0925484305920792f,
+                SH_C2_4 = 0.5462742152960396f;
+constexpr float SH_C3_0 = -0.5900435899266435f, SH_C3_1 = 2.890611442640554f,
+                SH_C3_2 = -0.4570457994644658f, SH_C3_3 = 0.3731763325901154f,
+                SH_C3_4 = -0.4570457994644658f, SH_C3_5 = 1.445305721320277f,
+                SH_C3_6 = -0.5900435899266435f;
+
+// 11-tap Gaussian (sigma 1.5) of the separable SSIM (.metal:3041-3045).
+static constexpr float GAUSS_1D[11] = {
+    0.0010283801f, 0.0075987581f, 0.0360007721f, 0.1093606895f, 0.2130055377f, 0.2660117249f,
+    0.2130055377f, 0.1093606895f, 0.0360007721f, 0.0075987581f, 0.0010283801f};
+constexpr float SSIM_C1 = 0.0001f;
+constexpr float SSIM_C2 = 0.0009f;
+
+// exp(x): Cody–Waite reduction x = k ln2 + r with ln2 split into a 16-bit head
+// and a tail, degree-7 Taylor polynomial in Horner form, scaling by 2^k via the
+// exponent field.  x < -87 -> 0 (no subnormal results), x > 88 -> +inf.
+__device__ __forceinline__ float exp_cw(float x) {
+    if (x != x) return x;
+    if (x < -87.0f) return 0.0f;
+    if (x > 88.0f) return __int_as_float(0x7f800000);
+    const float k = rintf(x * 1.44269504f);
+    float r = fmaf(k, -0.693145751953125f, x);
+    r = fmaf(k, -1.42860682e-6f, r);
+    float p = 1.98412698e-4f;
+    p = fmaf(p, r, 1.38888889e-3f);
+    p = fmaf(p, r, 8.33333333e-3f);
+    p = fmaf(p, r, 4.16666667e-2f);
+    p = fmaf(p, r, 1.66666667e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const int ki = (int)k;
+    return p * __int_as_float((ki + 127) << 23);
+}
+
+__device__ __forceinline__ float sigmoid(float o) { return 1.f / (1.f + exp_cw(-o)); }
+
+// float -> int with the operand clamped to [-2^30, 2^30] first: one defined
+// result for every input (the plain conversion is undefined out of range).
+__device__ __forceinline__ int f2i(float v) {
+    return (int)fminf(fmaxf(v, -1073741824.f), 1073741824.f);
+}
+
+__device__ __forceinline__ float clamp01(float v) { return fminf(fmaxf(v, 0.f), 1.f); }
+
+// Tile rectangle of a gaussian: get_tile_bbox (.metal:57-87).
+__device__ __forceinline__ void tile_rect(float x, float y, float ex, float ey, int tbx, int tby,
+                                          int& x0, int& y0, int& x1, int& y1) {
+    const float tcx = x / (float)BLOCK, tcy = y / (float)BLOCK;
+    const float trx = ex / (float)BLOCK, try_ = ey / (float)BLOCK;
+    x0 = min(max(0, f2i(tcx - trx)), tbx);
+    x1 = min(max(0, f2i(tcx + trx + 1)), tbx);
+    y0 = min(max(0, f2i(tcy - try_)), tby);
+    y1 = min(max(0, f2i(tcy + try_ + 1)), tby);
+}
+
+// Number of depth chunks a tile with n entries is rasterised in.
+__device__ __host__ __forceinline__ int tile_chunks(int n, int num_tiles) {
+    if (n <= 0) return 1;
+    if (num_tiles < CHUNK_MODE_TILES || n > MONO_MAX) return (n + CHUNK - 1) / CHUNK;
+    return 1;
+}
+
+// ---------------------------------------------------------------- wave64 ops
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the 64 lanes; every lane gets the total.  All lanes must be active.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp<0x124>(v);   // row_ror:4
+    v += dpp<0x128>(v);   // row_ror:8   -> every lane holds its 16-lane row sum
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ int wave_max_i(int v) {
+    for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ unsigned lane_id() { return __lane_id(); }
+
+}  // namespace msp

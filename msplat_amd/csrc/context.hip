@@ -1,0 +1,634 @@
+// context.hip — the C ABI (include/msplat_hip.h): context, buffer cache and
+// the stage order of one render / train step on a single HIP stream.
+//
+// Replaces MetalContext + FusedTensorCache + forward_pipeline /
+// msplat_render / msplat_train_step / msplat_densify
+// (msplat_metal.mm:173-288, 348-454, 462-769, 771-1330, 1337-1592).
+// Stage order (.mm:1295-1326): zero -> project -> scan/scatter/sort ->
+// raster forward (+merge) -> SSIM fwd/bwd -> raster backward ->
+// projection backward + Adam + grad stats.  Intermediate buffers live in a
+// grow-only cache owned by the context.  One host synchronisation per step:
+// after the tile scan the host reads the intersection count and tile-size
+// summary (a few bytes) to size the key/packed buffers and the launch grids
+// exactly, instead of the reference's fixed 16N capacity and 2048-per-tile
+// bins.
+#include "../../include/msplat_hip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+namespace {
+
+using namespace msp;
+
+struct Buf {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+
+struct Ctx {
+    int device = -1;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+    bool timing = false;
+    hipEvent_t ev[9] = {};
+    int n_ev_used = 0;
+    double stage_ms[8] = {};
+    int n_stages = 0;
+
+    // per gaussian
+    Buf xy, conic, rgb, depth, radii, aabb, tiles_hit, gacc;
+    // per tile
+    Buf tile_cnt, tile_bins, tile_K, tile_item0, l_chunked, l_large, l_huge;
+    // per intersection
+    Buf keys, scratch, pk_geo, pk_col, pk_bl, pk_ids;
+    // per item
+    Buf it_tile, it_k, c_T, c_C, c_idx, c_pT, c_aC;
+    // per pixel
+    Buf final_T, final_idx, out_img, hbuf, dbuf, v_rendered, loss_part;
+    // scalars
+    Buf meta_d, loss_d, count_d;
+    Meta* meta_h = nullptr;
+    float* loss_h = nullptr;
+    int* count_h = nullptr;
+    // densify scratch
+    Buf d_split, d_dup, d_sp, d_dp, d_keep, d_kp, d_tot, d_scratch, d_rnd;
+
+    Meta meta{};
+    int last_N = 0, last_T = 0, last_W = 0, last_H = 0;
+    bool have_bwd = false;
+};
+
+Ctx* g_ctx = nullptr;
+std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                        \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return fail(MSPLAT_ERR_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                        __FILE__, __LINE__);                                                 \
+    } while (0)
+
+// Grow-only device buffer; new memory is zero-filled.
+int ensure(Buf& b, size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    if (bytes <= b.bytes) return MSPLAT_OK;
+    size_t want = std::max(bytes, b.bytes + b.bytes / 4);
+    want = (want + 255) & ~(size_t)255;
+    if (b.p) {
+        HIP_TRY(hipStreamSynchronize(g_ctx->stream));
+        HIP_TRY(hipFree(b.p));
+        b.p = nullptr;
+        b.bytes = 0;
+    }
+    if (hipMalloc(&b.p, want) != hipSuccess) {
+        b.p = nullptr;
+        return fail(MSPLAT_ERR_NOMEM, "hipMalloc of %zu bytes failed", want);
+    }
+    b.bytes = want;
+    HIP_TRY(hipMemsetAsync(b.p, 0, want, g_ctx->stream));
+    return MSPLAT_OK;
+}
+
+#define ENSURE(b, n)                      \
+    do {                                  \
+        int r_ = ensure((b), (n));        \
+        if (r_ != MSPLAT_OK) return r_;   \
+    } while (0)
+
+template <typename T>
+T* P(Buf& b) { return reinterpret_cast<T*>(b.p); }
+
+void free_all(Ctx* c) {
+    Buf* bufs[] = {&c->xy, &c->conic, &c->rgb, &c->depth, &c->radii, &c->aabb, &c->tiles_hit,
+                   &c->gacc, &c->tile_cnt, &c->tile_bins, &c->tile_K, &c->tile_item0,
+                   &c->l_chunked, &c->l_large, &c->l_huge, &c->keys, &c->scratch, &c->pk_geo,
+                   &c->pk_col, &c->pk_bl, &c->pk_ids, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
+                   &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
+                   &c->hbuf, &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
+                   &c->count_d, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
+                   &c->d_tot, &c->d_scratch, &c->d_rnd};
+    for (Buf* b : bufs)
+        if (b->p) { (void)hipFree(b->p); b->p = nullptr; b->bytes = 0; }
+    if (c->meta_h) (void)hipHostFree(c->meta_h);
+    if (c->loss_h) (void)hipHostFree(c->loss_h);
+    if (c->count_h) (void)hipHostFree(c->count_h);
+    for (auto& e : c->ev)
+        if (e) (void)hipEventDestroy(e);
+    if (c->own) (void)hipStreamDestroy(c->own);
+}
+
+GaussOut gauss_out(Ctx* c) {
+    GaussOut go;
+    go.xy = P<float2>(c->xy);
+    go.conic = P<float4>(c->conic);
+    go.rgb = P<float4>(c->rgb);
+    go.depth = P<float>(c->depth);
+    go.radii = P<int>(c->radii);
+    go.aabb = P<float2>(c->aabb);
+    go.tiles_hit = P<int>(c->tiles_hit);
+    return go;
+}
+
+Items items(Ctx* c) {
+    Items it;
+    it.tile = P<int>(c->it_tile);
+    it.k = P<int>(c->it_k);
+    it.tile_K = P<int>(c->tile_K);
+    it.tile_item0 = P<int>(c->tile_item0);
+    return it;
+}
+
+Packed packed(Ctx* c) {
+    Packed pk;
+    pk.geo = P<float4>(c->pk_geo);
+    pk.col = P<float4>(c->pk_col);
+    pk.bl = P<float>(c->pk_bl);
+    pk.ids = P<int>(c->pk_ids);
+    return pk;
+}
+
+ChunkBufs chunks(Ctx* c) {
+    ChunkBufs cb;
+    cb.cT = P<float>(c->c_T);
+    cb.cC = P<float>(c->c_C);
+    cb.cidx = P<int>(c->c_idx);
+    cb.pT = P<float>(c->c_pT);
+    cb.aC = P<float>(c->c_aC);
+    return cb;
+}
+
+int sh_bases(int degree) { return degree == 0 ? 1 : degree == 1 ? 4 : degree == 2 ? 9 : degree == 3 ? 16 : 25; }
+
+void stage_mark(Ctx* c) {
+    if (!c->timing) return;
+    if (c->n_ev_used < 9) (void)hipEventRecord(c->ev[c->n_ev_used++], c->stream);
+}
+
+int check_render_args(const MsplatRenderArgs* a) {
+    if (!a) return fail(MSPLAT_ERR_ARG, "null args");
+    if (a->num_points < 0) return fail(MSPLAT_ERR_ARG, "num_points < 0");
+    if (a->img_width == 0 || a->img_height == 0) return fail(MSPLAT_ERR_ARG, "empty image");
+    if ((uint64_t)a->img_width * a->img_height > (1ull << 31) / 16)
+        return fail(MSPLAT_ERR_ARG, "image too large");
+    if (a->degree > 4) return fail(MSPLAT_ERR_ARG, "SH degree %u > 4", a->degree);
+    const int tbx = (int)((a->img_width + BLOCK - 1) / BLOCK);
+    const int tby = (int)((a->img_height + BLOCK - 1) / BLOCK);
+    if (a->tile_bounds[0] != tbx || a->tile_bounds[1] != tby)
+        return fail(MSPLAT_ERR_ARG, "tile_bounds (%d,%d) != (%d,%d) for a %ux%u image",
+                    a->tile_bounds[0], a->tile_bounds[1], tbx, tby, a->img_width, a->img_height);
+    if (a->num_points > 0 && (!a->means3d || !a->scales || !a->quats || !a->features_dc ||
+                              !a->opacities || (a->degree > 0 && !a->features_rest)))
+        return fail(MSPLAT_ERR_ARG, "null gaussian array");
+    if (reinterpret_cast<uintptr_t>(a->quats) % 16 != 0)
+        return fail(MSPLAT_ERR_ARG, "quats must be 16-byte aligned");
+    return MSPLAT_OK;
+}
+
+CamParams cam_params(const MsplatRenderArgs* a) {
+    CamParams p;
+    p.N = a->num_points;
+    p.glob_scale = a->glob_scale;
+    std::memcpy(p.vm, a->viewmat, sizeof(p.vm));
+    std::memcpy(p.pm, a->projmat, sizeof(p.pm));
+    p.fx = a->fx; p.fy = a->fy; p.cx = a->cx; p.cy = a->cy;
+    p.W = (int)a->img_width;
+    p.H = (int)a->img_height;
+    p.tbx = a->tile_bounds[0];
+    p.tby = a->tile_bounds[1];
+    p.clip = a->clip_thresh;
+    p.degree = (int)a->degree;
+    p.dtu = (int)std::min(a->degrees_to_use, a->degree);
+    p.rest_per = (sh_bases(p.degree) - 1) * 3;
+    for (int i = 0; i < 3; ++i) { p.cam[i] = a->cam_pos[i]; p.bg[i] = a->background[i]; }
+    return p;
+}
+
+// forward_pipeline (.mm:462-750): project -> bin/sort/pack -> raster (+merge).
+int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
+    const CamParams p = cam_params(a);
+    const int N = p.N, T = p.tbx * p.tby;
+    const size_t Px = (size_t)p.W * p.H;
+    ENSURE(c->xy, (size_t)N * 8);
+    ENSURE(c->conic, (size_t)N * 16);
+    ENSURE(c->rgb, (size_t)N * 16);
+    ENSURE(c->depth, (size_t)N * 4);
+    ENSURE(c->radii, (size_t)N * 4);
+    ENSURE(c->aabb, (size_t)N * 8);
+    ENSURE(c->tiles_hit, (size_t)N * 4);
+    ENSURE(c->gacc, (size_t)N * 36);
+    ENSURE(c->tile_cnt, (size_t)T * 4);
+    ENSURE(c->tile_bins, (size_t)T * 8);
+    ENSURE(c->tile_K, (size_t)T * 4);
+    ENSURE(c->tile_item0, (size_t)T * 4);
+    ENSURE(c->l_chunked, (size_t)T * 4);
+    ENSURE(c->l_large, (size_t)T * 4);
+    ENSURE(c->l_huge, (size_t)T * 4);
+    ENSURE(c->final_T, Px * 4);
+    ENSURE(c->final_idx, Px * 4);
+    ENSURE(c->out_img, Px * 12);
+    ENSURE(c->meta_d, sizeof(Meta));
+    c->last_N = N; c->last_T = T; c->last_W = p.W; c->last_H = p.H;
+    c->have_bwd = false;
+
+    stage_mark(c);   // start of proj_sh_fwd
+    HIP_TRY(hipMemsetAsync(c->tile_cnt.p, 0, (size_t)T * 4, c->stream));
+    GaussOut go = gauss_out(c);
+    launch_project_fwd(c->stream, p, a->means3d, a->scales, a->quats, a->features_dc,
+                       a->features_rest, a->opacities, go, P<int>(c->tile_cnt), P<float>(c->gacc));
+    stage_mark(c);   // start of prefix_sort_pack
+    TileLists tl{P<int>(c->l_chunked), P<int>(c->l_large), P<int>(c->l_huge)};
+    Items it = items(c);
+    launch_tile_scan(c->stream, T, P<int>(c->tile_cnt), P<int>(c->tile_bins), it, tl,
+                     P<Meta>(c->meta_d));
+    HIP_TRY(hipMemcpyAsync(c->meta_h, c->meta_d.p, sizeof(Meta), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->meta = *c->meta_h;
+    const Meta& m = c->meta;
+    if (m.total_isect > (int64_t)0x7FFFFFFF - 4096)
+        return fail(MSPLAT_ERR_ARG, "%lld tile intersections exceed the 32-bit index range",
+                    (long long)m.total_isect);
+    const size_t I = (size_t)std::max<int64_t>(m.total_isect, 1);
+    ENSURE(c->keys, I * 8);
+    ENSURE(c->pk_geo, I * 16);
+    ENSURE(c->pk_col, I * 16);
+    ENSURE(c->pk_bl, I * 4);
+    ENSURE(c->pk_ids, I * 4);
+    if (m.n_huge > 0) ENSURE(c->scratch, I * 16);
+    ENSURE(c->it_tile, (size_t)m.n_items * 4);
+    ENSURE(c->it_k, (size_t)m.n_items * 4);
+    if (m.n_chunked_tiles > 0) {
+        const size_t S = (size_t)m.n_items * TILE_PIX;
+        ENSURE(c->c_T, S * 4);
+        ENSURE(c->c_C, S * 12);
+        ENSURE(c->c_idx, S * 4);
+        if (training) {
+            ENSURE(c->c_pT, S * 4);
+            ENSURE(c->c_aC, S * 12);
+        }
+    }
+    it = items(c);
+    launch_build_items(c->stream, T, it);
+    launch_scatter(c->stream, p, go, P<int>(c->tile_bins), P<int>(c->tile_cnt), P<uint64_t>(c->keys));
+    Packed pk = packed(c);
+    launch_sort_pack(c->stream, T, m, P<int>(c->tile_bins), tl, P<uint64_t>(c->keys),
+                     P<uint64_t>(c->scratch), go, pk);
+    stage_mark(c);   // start of rast_fwd
+    ChunkBufs cb = chunks(c);
+    launch_raster_fwd(c->stream, p, m.n_items, it, P<int>(c->tile_bins), pk, P<float>(c->final_T),
+                      P<int>(c->final_idx), P<float>(c->out_img), cb);
+    launch_raster_merge(c->stream, p, m.n_chunked_tiles, P<int>(c->l_chunked), it,
+                        P<float>(c->final_T), P<int>(c->final_idx), P<float>(c->out_img), cb,
+                        training);
+    HIP_TRY(hipGetLastError());
+    return MSPLAT_OK;
+}
+
+const char* kStageNames[7] = {"proj_sh_fwd", "prefix_sort_pack", "rast_fwd", "loss_fwd_bwd",
+                              "rast_bwd", "proj_sh_bwd_adam", "grad_stats"};
+
+}  // namespace
+
+extern "C" {
+
+int msplat_hip_init(int device) {
+    if (g_ctx) {
+        if (g_ctx->device == device) return MSPLAT_OK;
+        return fail(MSPLAT_ERR_ARG, "already initialised on device %d", g_ctx->device);
+    }
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(MSPLAT_ERR_ARG, "device %d of %d", device, n);
+    HIP_TRY(hipSetDevice(device));
+    Ctx* c = new Ctx();
+    c->device = device;
+    g_ctx = c;
+    if (hipStreamCreate(&c->own) != hipSuccess) {   // blocking stream, default priority
+        g_ctx = nullptr;
+        delete c;
+        return fail(MSPLAT_ERR_HIP, "hipStreamCreate failed");
+    }
+    c->stream = c->own;
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->meta_h), sizeof(Meta)));
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->loss_h), 16));
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->count_h), 16));
+    for (auto& e : c->ev) HIP_TRY(hipEventCreate(&e));
+    return MSPLAT_OK;
+}
+
+int msplat_hip_shutdown(void) {
+    if (!g_ctx) return MSPLAT_OK;
+    (void)hipStreamSynchronize(g_ctx->stream);
+    free_all(g_ctx);
+    delete g_ctx;
+    g_ctx = nullptr;
+    return MSPLAT_OK;
+}
+
+const char* msplat_hip_last_error(void) { return g_err.c_str(); }
+
+int msplat_hip_set_stream(void* s) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    g_ctx->stream = s ? reinterpret_cast<hipStream_t>(s) : g_ctx->own;
+    return MSPLAT_OK;
+}
+
+void* msplat_hip_get_stream(void) { return g_ctx ? (void*)g_ctx->stream : nullptr; }
+
+int msplat_hip_alloc(void** ptr, size_t bytes) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!ptr) return fail(MSPLAT_ERR_ARG, "null ptr");
+    if (hipMalloc(ptr, bytes ? bytes : 4) != hipSuccess) return fail(MSPLAT_ERR_NOMEM, "hipMalloc(%zu)", bytes);
+    return MSPLAT_OK;
+}
+
+int msplat_hip_free(void* ptr) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (ptr) {
+        HIP_TRY(hipStreamSynchronize(g_ctx->stream));
+        HIP_TRY(hipFree(ptr));
+    }
+    return MSPLAT_OK;
+}
+
+int msplat_hip_memset(void* ptr, int value, size_t bytes) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    HIP_TRY(hipMemsetAsync(ptr, value, bytes, g_ctx->stream));
+    return MSPLAT_OK;
+}
+
+int msplat_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_ctx->stream));
+    HIP_TRY(hipStreamSynchronize(g_ctx->stream));
+    return MSPLAT_OK;
+}
+
+int msplat_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_ctx->stream));
+    HIP_TRY(hipStreamSynchronize(g_ctx->stream));
+    return MSPLAT_OK;
+}
+
+int msplat_hip_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_ctx->stream));
+    return MSPLAT_OK;
+}
+
+int msplat_hip_commit(void) { return g_ctx ? MSPLAT_OK : fail(MSPLAT_ERR_NOINIT, "not initialised"); }
+
+int msplat_hip_sync(void) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    HIP_TRY(hipStreamSynchronize(g_ctx->stream));
+    return MSPLAT_OK;
+}
+
+int msplat_hip_render(const MsplatRenderArgs* a, float* out_img) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    int r = check_render_args(a);
+    if (r != MSPLAT_OK) return r;
+    c->n_ev_used = 0;
+    r = forward(c, a, false);
+    if (r != MSPLAT_OK) return r;
+    stage_mark(c);
+    if (out_img)
+        HIP_TRY(hipMemcpyAsync(out_img, c->out_img.p, (size_t)a->img_width * a->img_height * 12,
+                               hipMemcpyDeviceToDevice, c->stream));
+    return MSPLAT_OK;
+}
+
+int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* loss_out) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!a) return fail(MSPLAT_ERR_ARG, "null args");
+    int r = check_render_args(&a->r);
+    if (r != MSPLAT_OK) return r;
+    if (a->num_adam_groups != 6) return fail(MSPLAT_ERR_ARG, "num_adam_groups must be 6");
+    if (!a->gt) return fail(MSPLAT_ERR_ARG, "null gt");
+    const float* rp[6] = {a->r.means3d, a->r.scales, a->r.quats, a->r.features_dc,
+                          a->r.features_rest, a->r.opacities};
+    for (int g = 0; g < 6; ++g) {
+        if (g == 4 && a->r.degree == 0) continue;
+        if (a->adam_params[g] != rp[g])
+            return fail(MSPLAT_ERR_ARG, "adam_params[%d] must alias the render array", g);
+        if (!a->adam_exp_avg[g] || !a->adam_exp_avg_sq[g])
+            return fail(MSPLAT_ERR_ARG, "null Adam state for group %d", g);
+    }
+    if (!a->vis_counts || !a->xys_grad_norm || !a->max_2d_size)
+        return fail(MSPLAT_ERR_ARG, "null grad-stat array");
+    c->n_ev_used = 0;
+    r = forward(c, &a->r, true);
+    if (r != MSPLAT_OK) return r;
+    const CamParams p = cam_params(&a->r);
+    const size_t Px = (size_t)p.W * p.H;
+    const dim3 sgrid((p.W + 15) / 16, (p.H + 15) / 16);
+    ENSURE(c->hbuf, Px * 60);
+    ENSURE(c->dbuf, Px * 36);
+    ENSURE(c->v_rendered, Px * 12);
+    ENSURE(c->loss_part, (size_t)sgrid.x * sgrid.y * 12);
+    ENSURE(c->loss_d, 16);
+    stage_mark(c);   // start of loss_fwd_bwd
+    launch_ssim(c->stream, p.H, p.W, P<float>(c->out_img), a->gt, a->ssim_weight, a->loss_inv_n,
+                P<float>(c->hbuf), P<float>(c->dbuf), P<float>(c->v_rendered),
+                P<float>(c->loss_part), P<float>(c->loss_d));
+    stage_mark(c);   // start of rast_bwd
+    launch_raster_bwd(c->stream, p, c->meta.n_items, items(c), P<int>(c->tile_bins), packed(c),
+                      P<float>(c->final_T), P<int>(c->final_idx), chunks(c),
+                      P<float>(c->v_rendered), P<float>(c->gacc));
+    stage_mark(c);   // start of proj_sh_bwd_adam
+    AdamHP hp;
+    for (int g = 0; g < 6; ++g) { hp.step[g] = a->adam_step_sizes[g]; hp.bc2[g] = a->adam_bc2_sqrts[g]; }
+    hp.b1 = a->adam_beta1;
+    hp.b2 = a->adam_beta2;
+    hp.eps = a->adam_eps;
+    GaussOut go = gauss_out(c);
+    launch_sh_rest_adam(c->stream, p, a->r.means3d, go.radii, P<float>(c->gacc),
+                        a->adam_params[4], a->adam_exp_avg[4], a->adam_exp_avg_sq[4], hp);
+    launch_proj_bwd_adam(c->stream, p, a->adam_params, a->adam_exp_avg, a->adam_exp_avg_sq, hp, go,
+                         P<float>(c->gacc), a->vis_counts, a->xys_grad_norm, a->max_2d_size,
+                         a->inv_max_dim, a->v_mean3d_out, a->v_scale_out, a->v_quat_out);
+    stage_mark(c);   // end
+    c->have_bwd = true;
+    if (radii_out && p.N > 0)
+        HIP_TRY(hipMemcpyAsync(radii_out, c->radii.p, (size_t)p.N * 4, hipMemcpyDeviceToDevice,
+                               c->stream));
+    HIP_TRY(hipGetLastError());
+    if (loss_out) {
+        HIP_TRY(hipMemcpyAsync(c->loss_h, c->loss_d.p, 4, hipMemcpyDeviceToHost, c->stream));
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        *loss_out = c->loss_h[0] / (float)(p.H * p.W);
+    }
+    return MSPLAT_OK;
+}
+
+int msplat_hip_randn(float* dst, int64_t n, uint64_t seed) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    launch_randn(g_ctx->stream, dst, n, seed);
+    HIP_TRY(hipGetLastError());
+    return MSPLAT_OK;
+}
+
+int msplat_hip_densify(const MsplatDensifyArgs* a, int32_t* new_count) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!a || !new_count) return fail(MSPLAT_ERR_ARG, "null args");
+    const int N = a->N;
+    if (N <= 0) { *new_count = N; return MSPLAT_OK; }
+    const int64_t worst = 3 * (int64_t)N;
+    if (worst > a->buf_capacity)
+        return fail(MSPLAT_ERR_ARG, "3*N = %lld exceeds buf_capacity %d", (long long)worst,
+                    a->buf_capacity);
+    for (int g = 0; g < 6; ++g)
+        if (!a->bufs[g] || !a->adam_exp_avg_buf[g] || !a->adam_exp_avg_sq_buf[g])
+            if (!(g == 4 && a->fr_stride == 0)) return fail(MSPLAT_ERR_ARG, "null buffer %d", g);
+    ENSURE(c->d_split, (size_t)N * 4);
+    ENSURE(c->d_dup, (size_t)N * 4);
+    ENSURE(c->d_sp, (size_t)N * 4);
+    ENSURE(c->d_dp, (size_t)N * 4);
+    ENSURE(c->d_keep, (size_t)worst * 4);
+    ENSURE(c->d_kp, (size_t)worst * 4);
+    ENSURE(c->d_tot, (size_t)scan_block_count(worst) * 4 + 64);
+    ENSURE(c->d_scratch, (size_t)worst * std::max(4, a->fr_stride) * 4);
+    ENSURE(c->count_d, 16);
+    const float* rnd = a->random_samples;
+    if (!rnd) {
+        ENSURE(c->d_rnd, (size_t)2 * N * 3 * 4);
+        launch_randn(c->stream, P<float>(c->d_rnd), (int64_t)2 * N * 3, a->seed);
+        rnd = P<float>(c->d_rnd);
+    }
+    DensifyHP hp;
+    hp.N = N;
+    hp.grad_thresh = a->grad_thresh;
+    hp.size_thresh = a->size_thresh;
+    hp.screen_thresh = a->screen_thresh;
+    hp.check_screen = a->check_screen;
+    hp.cull_alpha = a->cull_alpha_thresh;
+    hp.cull_scale = a->cull_scale_thresh;
+    hp.cull_screen = a->cull_screen_size;
+    hp.check_huge = a->check_huge;
+    hp.half_max_dim = a->half_max_dim;
+    hp.fr = a->fr_stride;
+    launch_densify(c->stream, hp, a->xys_grad_norm, a->vis_counts, a->max_2d_size, a->bufs,
+                   a->adam_exp_avg_buf, a->adam_exp_avg_sq_buf, rnd, P<int>(c->d_split),
+                   P<int>(c->d_dup), P<int>(c->d_sp), P<int>(c->d_dp), P<int>(c->d_keep),
+                   P<int>(c->d_kp), P<int>(c->d_tot), P<float>(c->d_scratch), P<int>(c->count_d));
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipMemcpyAsync(c->count_h, c->count_d.p, 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    *new_count = c->count_h[0];
+    return MSPLAT_OK;
+}
+
+int msplat_hip_enable_stage_timing(int enable) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    g_ctx->timing = enable != 0;
+    return MSPLAT_OK;
+}
+
+int msplat_hip_drain_stage_times(double* ms, const char** names, int max_stages, int* n_stages) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    const int n = std::max(0, c->n_ev_used - 1);
+    int out = 0;
+    for (int i = 0; i < n && out < max_stages; ++i, ++out) {
+        float t = 0.f;
+        HIP_TRY(hipEventElapsedTime(&t, c->ev[i], c->ev[i + 1]));
+        if (ms) ms[out] = t;
+        if (names) names[out] = kStageNames[i];
+    }
+    if (n_stages) *n_stages = out;
+    return MSPLAT_OK;
+}
+
+int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!name || !nbytes) return fail(MSPLAT_ERR_ARG, "null args");
+    const size_t N = (size_t)c->last_N, T = (size_t)c->last_T, Px = (size_t)c->last_W * c->last_H;
+    const size_t I = (size_t)std::max<int64_t>(c->meta.total_isect, 0);
+    const std::string n(name);
+    // Direct copies.
+    struct D { const char* name; Buf* b; size_t bytes; };
+    const D direct[] = {
+        {"xys", &c->xy, N * 8},           {"depths", &c->depth, N * 4},
+        {"radii", &c->radii, N * 4},      {"aabb", &c->aabb, N * 8},
+        {"num_tiles_hit", &c->tiles_hit, N * 4}, {"tile_bins", &c->tile_bins, T * 8},
+        {"gaussian_ids", &c->pk_ids, I * 4}, {"final_Ts", &c->final_T, Px * 4},
+        {"final_index", &c->final_idx, Px * 4}, {"out_img", &c->out_img, Px * 12},
+        {"v_rendered", &c->v_rendered, Px * 12}, {"gacc", &c->gacc, N * 36},
+    };
+    for (const D& d : direct) {
+        if (n != d.name) continue;
+        *nbytes = d.bytes;
+        if (!dst || d.bytes == 0) return MSPLAT_OK;
+        HIP_TRY(hipMemcpyAsync(dst, d.b->p, d.bytes, hipMemcpyDeviceToHost, c->stream));
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        return MSPLAT_OK;
+    }
+    if (n == "meta") {
+        *nbytes = sizeof(Meta);
+        if (dst) std::memcpy(dst, &c->meta, sizeof(Meta));
+        return MSPLAT_OK;
+    }
+    // Repacked views of the internal layouts.
+    auto fetch4 = [&](Buf& b, std::vector<float>& h) -> int {
+        h.resize(N * 4);
+        if (N == 0) return MSPLAT_OK;
+        HIP_TRY(hipMemcpyAsync(h.data(), b.p, N * 16, hipMemcpyDeviceToHost, c->stream));
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        return MSPLAT_OK;
+    };
+    std::vector<float> h;
+    if (n == "conics" || n == "colors" || n == "opacity_sigmoid") {
+        const bool op = n == "opacity_sigmoid";
+        const size_t per = op ? 1 : 3;
+        *nbytes = N * per * 4;
+        if (!dst) return MSPLAT_OK;
+        int r = fetch4(n == "colors" ? c->rgb : c->conic, h);
+        if (r != MSPLAT_OK) return r;
+        float* o = static_cast<float*>(dst);
+        for (size_t g = 0; g < N; ++g) {
+            if (op) o[g] = h[4 * g + 3];
+            else for (int k = 0; k < 3; ++k) o[3 * g + k] = h[4 * g + k];
+        }
+        return MSPLAT_OK;
+    }
+    const int q0 = n == "v_xy" ? 0 : n == "v_conic" ? 2 : n == "v_rgb" ? 5 : n == "v_opacity" ? 8 : -1;
+    if (q0 >= 0) {
+        const int per = n == "v_xy" ? 2 : n == "v_opacity" ? 1 : 3;
+        *nbytes = N * per * 4;
+        if (!dst) return MSPLAT_OK;
+        h.resize(N * 9);
+        if (N) {
+            HIP_TRY(hipMemcpyAsync(h.data(), c->gacc.p, N * 36, hipMemcpyDeviceToHost, c->stream));
+            HIP_TRY(hipStreamSynchronize(c->stream));
+        }
+        float* o = static_cast<float*>(dst);
+        for (size_t g = 0; g < N; ++g)
+            for (int k = 0; k < per; ++k) o[g * per + k] = h[g * 9 + q0 + k];
+        return MSPLAT_OK;
+    }
+    return fail(MSPLAT_ERR_ARG, "unknown intermediate '%s'", name);
+}
+
+}  // extern "C"

@@ -1,0 +1,309 @@
+// densify.hip — GPU-resident densification: classify, split / duplicate
+// append, cull classify and stable compaction of all 18 per-gaussian buffers.
+//
+// Reference: msplat_densify (msplat_metal.mm:1337-1592) with
+// densify_classify_kernel (.metal:3475-3509), densify_append_split_kernel
+// (.metal:3514-3600), densify_append_dup_kernel (.metal:3604-3651),
+// densify_cull_classify_kernel (.metal:3656-3694), compact_scatter /
+// compact_copy_back (.metal:3698-3729) and the two-level block scan
+// (.metal:2368-2439).  The scans here are three-pass (block totals, scan of
+// the totals, block scans with offsets) over 1024-element blocks.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace msp {
+
+namespace {
+
+constexpr int SB = 1024;   // elements per scan block (256 threads x 4)
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// Box–Muller from two counter-hashed uniforms per output element.
+__global__ __launch_bounds__(256) void k_randn(float* __restrict__ dst, int64_t n, uint64_t seed) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t a = splitmix64(seed ^ (2ull * (uint64_t)i) * 0xD1B54A32D192ED03ull);
+    const uint64_t b = splitmix64(a ^ 0x8BB84B93962EACC9ull);
+    const float u1 = (float)((a >> 40) + 1) * (1.0f / 16777216.0f);   // (0, 1]
+    const float u2 = (float)(b >> 40) * (1.0f / 16777216.0f);         // [0, 1)
+    dst[i] = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+}
+
+__device__ __forceinline__ int block_sum_256(int v, int* sh) {
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const int t = sh[0] + sh[1] + sh[2] + sh[3];
+    __syncthreads();
+    return t;
+}
+
+__global__ __launch_bounds__(256) void k_block_reduce(const int* __restrict__ in, int64_t n,
+                                                      int* __restrict__ tot) {
+    __shared__ int sh[4];
+    const int64_t base = (int64_t)blockIdx.x * SB;
+    int v = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int64_t i = base + k * 256 + threadIdx.x;
+        if (i < n) v += in[i];
+    }
+    const int t = block_sum_256(v, sh);
+    if (threadIdx.x == 0) tot[blockIdx.x] = t;
+}
+
+// Exclusive scan of nb block totals in place (one workgroup).
+__global__ __launch_bounds__(1024) void k_scan_totals(int* __restrict__ tot, int nb) {
+    __shared__ int s[1024];
+    const int per = (nb + 1023) / 1024;
+    const int b = min((int)threadIdx.x * per, nb), e = min(b + per, nb);
+    int sum = 0;
+    for (int i = b; i < e; ++i) sum += tot[i];
+    s[threadIdx.x] = sum;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int v = threadIdx.x >= (unsigned)off ? s[threadIdx.x - off] : 0;
+        __syncthreads();
+        s[threadIdx.x] += v;
+        __syncthreads();
+    }
+    int run = s[threadIdx.x] - sum;
+    for (int i = b; i < e; ++i) {
+        const int v = tot[i];
+        tot[i] = run;
+        run += v;
+    }
+}
+
+// Inclusive scan of each 1024-element block plus its offset.
+__global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
+                                                    int* __restrict__ out, int64_t n,
+                                                    const int* __restrict__ tot) {
+    __shared__ int s[SB];
+    const int64_t base = (int64_t)blockIdx.x * SB;
+    for (int k = threadIdx.x; k < SB; k += 256) {
+        const int64_t i = base + k;
+        s[k] = i < n ? in[i] : 0;
+    }
+    __syncthreads();
+    // each thread scans 4 consecutive values, then a 256-wide scan of thread sums
+    const int t = threadIdx.x;
+    int v0 = s[4 * t], v1 = v0 + s[4 * t + 1], v2 = v1 + s[4 * t + 2], v3 = v2 + s[4 * t + 3];
+    __shared__ int ts[256];
+    ts[t] = v3;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        const int v = t >= off ? ts[t - off] : 0;
+        __syncthreads();
+        ts[t] += v;
+        __syncthreads();
+    }
+    const int pre = ts[t] - v3 + tot[blockIdx.x];
+    const int vals[4] = {v0, v1, v2, v3};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int64_t i = base + 4 * t + k;
+        if (i < n) out[i] = pre + vals[k];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_classify(DensifyHP hp, const float* __restrict__ gnorm,
+                                                  const float* __restrict__ vis,
+                                                  const float* __restrict__ scales,
+                                                  const float* __restrict__ max2d,
+                                                  int* __restrict__ split, int* __restrict__ dup) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= hp.N) return;
+    const float vc = vis[i];
+    if (vc <= 0.0f) {
+        split[i] = 0;
+        dup[i] = 0;
+        return;
+    }
+    const float avg = (gnorm[i] / vc) * hp.half_max_dim;
+    const bool high = avg > hp.grad_thresh;
+    const float mx = fmaxf(fmaxf(exp_cw(scales[3 * i]), exp_cw(scales[3 * i + 1])),
+                           exp_cw(scales[3 * i + 2]));
+    const bool large = mx > hp.size_thresh;
+    bool do_split = large;
+    if (hp.check_screen && max2d[i] > hp.screen_thresh) do_split = true;
+    do_split = do_split && high;
+    split[i] = do_split ? 1 : 0;
+    dup[i] = (!large && high) ? 1 : 0;
+}
+
+struct Bufs18 {
+    float* b[6];
+    float* m[6];
+    float* v[6];
+};
+
+__global__ __launch_bounds__(256) void k_append_split(int N, int fr, const int* __restrict__ split,
+                                                      const int* __restrict__ sp,
+                                                      const float* __restrict__ rnd, float lsf,
+                                                      Bufs18 B) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N || split[i] == 0) return;
+    const int strides[6] = {3, 3, 4, 3, fr, 1};
+    const int ord = sp[i] - 1;
+    const float* q = B.b[2] + 4 * (size_t)i;
+    float qw = q[0], qx = q[1], qy = q[2], qz = q[3];
+    const float ql = sqrtf(qw * qw + qx * qx + qy * qy + qz * qz);
+    qw /= ql; qx /= ql; qy /= ql; qz /= ql;
+    float* sc = B.b[1];
+    float* mb = B.b[0];
+    const float sx = exp_cw(sc[3 * i]), sy = exp_cw(sc[3 * i + 1]), sz = exp_cw(sc[3 * i + 2]);
+    for (int k = 0; k < 2; ++k) {
+        const int ch = N + 2 * ord + k, ri = ord * 2 + k;
+        const float r0 = rnd[3 * ri] * sx, r1 = rnd[3 * ri + 1] * sy, r2 = rnd[3 * ri + 2] * sz;
+        const float v0 = (1 - 2 * (qy * qy + qz * qz)) * r0 + 2 * (qx * qy - qw * qz) * r1 +
+                         2 * (qx * qz + qw * qy) * r2;
+        const float v1 = 2 * (qx * qy + qw * qz) * r0 + (1 - 2 * (qx * qx + qz * qz)) * r1 +
+                         2 * (qy * qz - qw * qx) * r2;
+        const float v2 = 2 * (qx * qz - qw * qy) * r0 + 2 * (qy * qz + qw * qx) * r1 +
+                         (1 - 2 * (qx * qx + qy * qy)) * r2;
+        mb[3 * (size_t)ch] = mb[3 * (size_t)i] + v0;
+        mb[3 * (size_t)ch + 1] = mb[3 * (size_t)i + 1] + v1;
+        mb[3 * (size_t)ch + 2] = mb[3 * (size_t)i + 2] + v2;
+        for (int j = 0; j < 3; ++j) sc[3 * (size_t)ch + j] = sc[3 * (size_t)i + j] - lsf;
+        for (int j = 0; j < 4; ++j) B.b[2][4 * (size_t)ch + j] = B.b[2][4 * (size_t)i + j];
+        for (int j = 0; j < 3; ++j) B.b[3][3 * (size_t)ch + j] = B.b[3][3 * (size_t)i + j];
+        for (int j = 0; j < fr; ++j) B.b[4][(size_t)fr * ch + j] = B.b[4][(size_t)fr * i + j];
+        B.b[5][ch] = B.b[5][i];
+        for (int gi = 0; gi < 6; ++gi)
+            for (int j = 0; j < strides[gi]; ++j) {
+                B.m[gi][(size_t)strides[gi] * ch + j] = 0.f;
+                B.v[gi][(size_t)strides[gi] * ch + j] = 0.f;
+            }
+    }
+    for (int j = 0; j < 3; ++j) sc[3 * (size_t)i + j] -= lsf;
+}
+
+__global__ __launch_bounds__(256) void k_append_dup(int N, int fr, const int* __restrict__ dup,
+                                                    const int* __restrict__ dp,
+                                                    const int* __restrict__ sp, Bufs18 B) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N || dup[i] == 0) return;
+    const int strides[6] = {3, 3, 4, 3, fr, 1};
+    const int nS = sp[N - 1];
+    const int dst = N + 2 * nS + dp[i] - 1;
+    for (int gi = 0; gi < 6; ++gi)
+        for (int j = 0; j < strides[gi]; ++j) {
+            B.b[gi][(size_t)strides[gi] * dst + j] = B.b[gi][(size_t)strides[gi] * i + j];
+            B.m[gi][(size_t)strides[gi] * dst + j] = 0.f;
+            B.v[gi][(size_t)strides[gi] * dst + j] = 0.f;
+        }
+}
+
+__global__ __launch_bounds__(256) void k_cull(DensifyHP hp, int worst, const int* __restrict__ sp,
+                                              const int* __restrict__ dp,
+                                              const int* __restrict__ split,
+                                              const float* __restrict__ opac,
+                                              const float* __restrict__ scales,
+                                              const float* __restrict__ max2d,
+                                              int* __restrict__ keep) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= worst) return;
+    const int N = hp.N;
+    const int Nn = N + 2 * sp[N - 1] + dp[N - 1];
+    if (i >= Nn) {
+        keep[i] = 0;
+        return;
+    }
+    const float os = 1.0f / (1.0f + exp_cw(-opac[i]));
+    bool cull = os < hp.cull_alpha;
+    if (i < N && split[i] != 0) cull = true;
+    if (hp.check_huge) {
+        const float mx = fmaxf(fmaxf(exp_cw(scales[3 * (size_t)i]), exp_cw(scales[3 * (size_t)i + 1])),
+                               exp_cw(scales[3 * (size_t)i + 2]));
+        if (mx > hp.cull_scale) cull = true;
+        if (hp.check_screen && i < N && max2d[i] > hp.cull_screen) cull = true;
+    }
+    keep[i] = cull ? 0 : 1;
+}
+
+__global__ __launch_bounds__(256) void k_compact_scatter(const float* __restrict__ src,
+                                                         float* __restrict__ dst,
+                                                         const int* __restrict__ kp,
+                                                         const int* __restrict__ keep, int64_t n,
+                                                         int stride) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t elem = t / stride, sub = t - elem * stride;
+    if (elem >= n || keep[elem] == 0) return;
+    dst[(int64_t)(kp[elem] - 1) * stride + sub] = src[t];
+}
+
+__global__ __launch_bounds__(256) void k_copy_back(const float* __restrict__ src,
+                                                   float* __restrict__ dst,
+                                                   const int* __restrict__ kp, int64_t last,
+                                                   int64_t n, int stride) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * stride) return;
+    const int64_t cnt = kp[last];
+    if (t / stride >= cnt) return;
+    dst[t] = src[t];
+}
+
+__global__ void k_read_count(const int* kp, int64_t last, int* out) { out[0] = kp[last]; }
+
+inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+int64_t scan_block_count(int64_t n) { return (n + SB - 1) / SB; }
+
+void launch_randn(hipStream_t s, float* dst, int64_t n, uint64_t seed) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_randn, dim3(blocks_for(n)), dim3(256), 0, s, dst, n, seed);
+}
+
+void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* tot) {
+    if (n <= 0) return;
+    const int nb = (int)scan_block_count(n);
+    hipLaunchKernelGGL(k_block_reduce, dim3(nb), dim3(256), 0, s, in, n, tot);
+    hipLaunchKernelGGL(k_scan_totals, dim3(1), dim3(1024), 0, s, tot, nb);
+    hipLaunchKernelGGL(k_block_scan, dim3(nb), dim3(256), 0, s, in, out, n, (const int*)tot);
+}
+
+void launch_densify(hipStream_t s, const DensifyHP& hp, const float* gnorm, const float* vis,
+                    const float* max2d, float* const bufs[6], float* const m[6],
+                    float* const v[6], const float* rnd, int* split, int* dup, int* sp, int* dp,
+                    int* keep, int* kp, int* tot, float* scratch, int* count_out) {
+    const int N = hp.N;
+    const int64_t worst = 3 * (int64_t)N;
+    Bufs18 B;
+    for (int i = 0; i < 6; ++i) { B.b[i] = bufs[i]; B.m[i] = m[i]; B.v[i] = v[i]; }
+    hipLaunchKernelGGL(k_classify, dim3(blocks_for(N)), dim3(256), 0, s, hp, gnorm, vis, bufs[1],
+                       max2d, split, dup);
+    launch_scan_i32(s, split, sp, N, tot);
+    launch_scan_i32(s, dup, dp, N, tot);
+    hipLaunchKernelGGL(k_append_split, dim3(blocks_for(N)), dim3(256), 0, s, N, hp.fr,
+                       (const int*)split, (const int*)sp, rnd, logf(1.6f), B);
+    hipLaunchKernelGGL(k_append_dup, dim3(blocks_for(N)), dim3(256), 0, s, N, hp.fr,
+                       (const int*)dup, (const int*)dp, (const int*)sp, B);
+    hipLaunchKernelGGL(k_cull, dim3(blocks_for(worst)), dim3(256), 0, s, hp, (int)worst,
+                       (const int*)sp, (const int*)dp, (const int*)split, (const float*)bufs[5],
+                       (const float*)bufs[1], max2d, keep);
+    launch_scan_i32(s, keep, kp, worst, tot);
+    const int strides[6] = {3, 3, 4, 3, hp.fr, 1};
+    for (int set = 0; set < 3; ++set)
+        for (int gi = 0; gi < 6; ++gi) {
+            float* buf = set == 0 ? bufs[gi] : set == 1 ? m[gi] : v[gi];
+            const int st = strides[gi];
+            if (st == 0) continue;
+            hipLaunchKernelGGL(k_compact_scatter, dim3(blocks_for(worst * st)), dim3(256), 0, s,
+                               (const float*)buf, scratch, (const int*)kp, (const int*)keep, worst,
+                               st);
+            hipLaunchKernelGGL(k_copy_back, dim3(blocks_for(worst * st)), dim3(256), 0, s,
+                               (const float*)scratch, buf, (const int*)kp, worst - 1, worst, st);
+        }
+    hipLaunchKernelGGL(k_read_count, dim3(1), dim3(1), 0, s, (const int*)kp, worst - 1, count_out);
+}
+
+}  // namespace msp

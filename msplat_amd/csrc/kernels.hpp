@@ -1,0 +1,148 @@
+// kernels.hpp — launch interface between the C-ABI orchestration (context.hip)
+// and the kernel translation units.  Host-callable launchers only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace msp {
+
+// Camera / render constants shared by projection, binning and raster.
+struct CamParams {
+    int N;
+    float glob_scale;
+    float vm[16];
+    float pm[16];
+    float fx, fy, cx, cy;
+    int W, H;
+    int tbx, tby;
+    float clip;
+    int degree;          // SH degree of the stored coefficients
+    int dtu;             // degrees_to_use (clamped to degree)
+    int rest_per;        // floats per gaussian in features_rest
+    float cam[3];
+    float bg[3];
+};
+
+// Per-gaussian outputs of the projection (internal layout).
+struct GaussOut {
+    float2* xy;          // pixel centre
+    float4* conic;       // (a, b, c, sigmoid(opacity))
+    float4* rgb;         // (r, g, b, 0) raw SH colour (no +0.5)
+    float* depth;
+    int* radii;
+    float2* aabb;        // per-axis pixel extents
+    int* tiles_hit;
+};
+
+// Per-entry (tile-sorted) packed records.
+struct Packed {
+    float4* geo;         // (x, y, conic_a, conic_b)
+    float4* col;         // (conic_c, opacity, r_raw, g_raw)
+    float* bl;           // b_raw
+    int* ids;            // gaussian id
+};
+
+// Work items of the rasteriser: item i covers chunk item_k[i] of tile item_tile[i].
+struct Items {
+    int* tile;
+    int* k;
+    int* tile_K;         // chunks per tile
+    int* tile_item0;     // first item of each tile
+};
+
+// Host-visible summary written by the tile scan.
+struct Meta {
+    int64_t total_isect;
+    int32_t max_count;
+    int32_t n_items;
+    int32_t n_chunked_tiles;   // tiles with more than one chunk
+    int32_t n_large;           // tiles sorted by the 16384-key LDS kernel
+    int32_t n_huge;            // tiles sorted in global memory
+    int32_t pad;
+};
+
+// Tile lists written by the tile scan (order within a list is arbitrary).
+struct TileLists {
+    int* chunked;
+    int* large;
+    int* huge;
+};
+
+constexpr int SORT_SMALL = 2048;     // keys per tile sorted by the 16 KB LDS kernel
+constexpr int SORT_LARGE = 16384;    // keys per tile sorted by the 128 KB LDS kernel
+
+// Per-pixel chunk state, indexed by item * 256 + local pixel.
+struct ChunkBufs {
+    float* cT;
+    float* cC;           // x3
+    int* cidx;
+    float* pT;
+    float* aC;           // x3
+};
+
+void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
+                        const float* scales, const float* quats, const float* f_dc,
+                        const float* f_rest, const float* opac_logits, GaussOut go,
+                        int* tile_cnt, float* gacc);
+
+void launch_tile_scan(hipStream_t s, int T, const int* tile_cnt, int* tile_bins, Items it,
+                      TileLists tl, Meta* meta);
+void launch_build_items(hipStream_t s, int T, Items it);
+void launch_scatter(hipStream_t s, const CamParams& p, GaussOut go, const int* tile_bins,
+                    int* tile_cnt, uint64_t* keys);
+void launch_sort_pack(hipStream_t s, int T, const Meta& meta, const int* tile_bins,
+                      TileLists tl, uint64_t* keys, uint64_t* scratch, GaussOut go, Packed pk);
+
+void launch_raster_fwd(hipStream_t s, const CamParams& p, int n_items, Items it,
+                       const int* tile_bins, Packed pk, float* final_T, int* final_idx,
+                       float* out_img, ChunkBufs cb);
+void launch_raster_merge(hipStream_t s, const CamParams& p, int n_chunked, const int* chunked,
+                         Items it, float* final_T, int* final_idx, float* out_img, ChunkBufs cb,
+                         bool with_suffix);
+void launch_raster_bwd(hipStream_t s, const CamParams& p, int n_items, Items it,
+                       const int* tile_bins, Packed pk, const float* final_T,
+                       const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc);
+
+void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
+                 float inv_n, float* hbuf, float* dbuf, float* v_rendered, float* loss_part,
+                 float* loss_out);
+
+struct AdamHP {
+    float step[6];
+    float bc2[6];
+    float b1, b2, eps;
+};
+
+void launch_sh_rest_adam(hipStream_t s, const CamParams& p, const float* means,
+                         const int* radii, const float* gacc, float* f_rest, float* m,
+                         float* v, const AdamHP& hp);
+void launch_proj_bwd_adam(hipStream_t s, const CamParams& p, float* const params[6],
+                          float* const m[6], float* const v[6], const AdamHP& hp,
+                          GaussOut go, const float* gacc, float* vis, float* gnorm,
+                          float* max2d, float inv_max_dim, float* v_mean_out,
+                          float* v_scale_out, float* v_quat_out);
+
+void launch_split_gacc(hipStream_t s, int N, const float* gacc, float* v_xy, float* v_conic,
+                       float* v_rgb, float* v_opac);
+
+// Densification.
+struct DensifyHP {
+    int N;
+    float grad_thresh, size_thresh, screen_thresh;
+    int check_screen;
+    float cull_alpha, cull_scale, cull_screen;
+    int check_huge;
+    float half_max_dim;
+    int fr;
+};
+void launch_randn(hipStream_t s, float* dst, int64_t n, uint64_t seed);
+void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot);
+int64_t scan_block_count(int64_t n);
+void launch_densify(hipStream_t s, const DensifyHP& hp, const float* gnorm, const float* vis,
+                    const float* max2d, float* const bufs[6], float* const m[6],
+                    float* const v[6], const float* rnd, int* split, int* dup, int* sp,
+                    int* dp, int* keep, int* kp, int* block_tot, float* scratch,
+                    int* count_out);
+
+}  // namespace msp

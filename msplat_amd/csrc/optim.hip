@@ -1,0 +1,379 @@
+// optim.hip — projection backward, SH backward and Adam, fused per gaussian.
+//
+// Reference: project_and_sh_backward_kernel (.metal:1813-1986) with
+// project_pix_vjp (.metal:1216-1234), cov2d_to_conic_vjp (.metal:1253-1264),
+// project_cov3d_ewa_vjp (.metal:1339-1407), quat_to_rotmat_vjp
+// (.metal:1409-1452), scale_rot_to_cov3d_vjp (.metal:1498-1531) and
+// adam_update_element (.metal:1791-1800); then fused_adam_kernel
+// (.metal:1666-1689) on groups 0, 1, 2, 5 and accumulate_grad_stats
+// (.metal:1643-1664).
+//
+// MI355X layout: the reference writes v_mean3d / v_scale / v_quat to memory
+// and runs four more Adam passes over them; here one thread per gaussian
+// computes the gradients in registers and applies Adam to means, scales,
+// quats, opacity and f_dc directly (dense for the first four, visible-only for
+// f_dc, as in the reference), plus the densify statistics.  The 45 floats of
+// f_rest per gaussian are updated by a separate element-parallel kernel whose
+// loads and stores are contiguous across the wave; it runs first because it
+// reads the pre-update means for the view direction.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace msp {
+
+namespace {
+
+struct F3 { float x, y, z; };
+struct M3 { float m[3][3]; };   // column-major like Metal's float3x3: m[col][row]
+
+__device__ __forceinline__ F3 mat_vec(const M3& A, F3 v) {
+    return F3{A.m[0][0] * v.x + A.m[1][0] * v.y + A.m[2][0] * v.z,
+              A.m[0][1] * v.x + A.m[1][1] * v.y + A.m[2][1] * v.z,
+              A.m[0][2] * v.x + A.m[1][2] * v.y + A.m[2][2] * v.z};
+}
+__device__ __forceinline__ M3 mat_mul(const M3& A, const M3& B) {
+    M3 C;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const F3 col = mat_vec(A, F3{B.m[j][0], B.m[j][1], B.m[j][2]});
+        C.m[j][0] = col.x;
+        C.m[j][1] = col.y;
+        C.m[j][2] = col.z;
+    }
+    return C;
+}
+__device__ __forceinline__ M3 transpose(const M3& A) {
+    M3 T;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) T.m[i][j] = A.m[j][i];
+    return T;
+}
+__device__ __forceinline__ float dot3(F3 a, F3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+
+__device__ __forceinline__ M3 quat_to_rotmat(float4 q) {
+    const float s = 1.f / sqrtf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+    const float w = q.x * s, x = q.y * s, y = q.z * s, z = q.w * s;
+    M3 R;
+    R.m[0][0] = 1.f - 2.f * (y * y + z * z);
+    R.m[0][1] = 2.f * (x * y + w * z);
+    R.m[0][2] = 2.f * (x * z - w * y);
+    R.m[1][0] = 2.f * (x * y - w * z);
+    R.m[1][1] = 1.f - 2.f * (x * x + z * z);
+    R.m[1][2] = 2.f * (y * z + w * x);
+    R.m[2][0] = 2.f * (x * z + w * y);
+    R.m[2][1] = 2.f * (y * z - w * x);
+    R.m[2][2] = 1.f - 2.f * (x * x + y * y);
+    return R;
+}
+
+__device__ __forceinline__ void adam_elem(float& p, float& m, float& v, float g, float step,
+                                          float b1, float b2, float bc2, float eps) {
+    const float mn = fmaf(b1, m, (1.0f - b1) * g);
+    const float vn = fmaf(b2, v, (1.0f - b2) * g * g);
+    p -= step * mn / (sqrtf(vn) / bc2 + eps);
+    m = mn;
+    v = vn;
+}
+
+// SH basis value b (0-based over the rest coefficients) along d (.metal:1936-1977).
+__device__ __forceinline__ float sh_basis(int b, float x, float y, float z) {
+    const float xx = x * x, xy = x * y, xz = x * z, yy = y * y, yz = y * z, zz = z * z;
+    switch (b) {
+        case 0: return -SH_C1 * y;
+        case 1: return SH_C1 * z;
+        case 2: return -SH_C1 * x;
+        case 3: return SH_C2_0 * xy;
+        case 4: return SH_C2_1 * yz;
+        case 5: return SH_C2_2 * (2.f * zz - xx - yy);
+        case 6: return SH_C2_3 * xz;
+        case 7: return SH_C2_4 * (xx - yy);
+        case 8: return SH_C3_0 * y * (3.f * xx - yy);
+        case 9: return SH_C3_1 * xy * z;
+        case 10: return SH_C3_2 * y * (4.f * zz - xx - yy);
+        case 11: return SH_C3_3 * z * (2.f * zz - 3.f * xx - 3.f * yy);
+        case 12: return SH_C3_4 * x * (4.f * zz - xx - yy);
+        case 13: return SH_C3_5 * z * (xx - yy);
+        default: return SH_C3_6 * x * (xx - 3.f * yy);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_sh_rest_adam(int64_t n, int rest_per, int n_used,
+                                                      const float* __restrict__ means,
+                                                      float cx, float cy, float cz,
+                                                      const int* __restrict__ radii,
+                                                      const float* __restrict__ gacc,
+                                                      float* __restrict__ f_rest,
+                                                      float* __restrict__ m, float* __restrict__ v,
+                                                      AdamHP hp) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const int g = (int)(e / rest_per);
+    const int rem = (int)(e - (int64_t)g * rest_per);
+    const int b = rem / 3, c = rem - 3 * (rem / 3);
+    if (b >= n_used || radii[g] <= 0) return;
+    const float dx = means[3 * g] - cx, dy = means[3 * g + 1] - cy, dz = means[3 * g + 2] - cz;
+    const float inv = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
+    const float grad = sh_basis(b, dx * inv, dy * inv, dz * inv) * gacc[(size_t)g * 9 + 5 + c];
+    float p = f_rest[e], mm = m[e], vv = v[e];
+    adam_elem(p, mm, vv, grad, hp.step[4], hp.b1, hp.b2, hp.bc2[4], hp.eps);
+    f_rest[e] = p;
+    m[e] = mm;
+    v[e] = vv;
+}
+
+struct BwdPtrs {
+    float* params[6];
+    float* m[6];
+    float* v[6];
+};
+
+__global__ __launch_bounds__(256) void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
+                                                       GaussOut go, const float* __restrict__ gacc,
+                                                       float* __restrict__ vis,
+                                                       float* __restrict__ gnorm,
+                                                       float* __restrict__ max2d, float inv_max_dim,
+                                                       float* __restrict__ v_mean_out,
+                                                       float* __restrict__ v_scale_out,
+                                                       float* __restrict__ v_quat_out) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= p.N) return;
+    float* means = P.params[0];
+    float* scales = P.params[1];
+    float* quats = P.params[2];
+    const int rad = go.radii[g];
+    const float* ga = gacc + (size_t)g * 9;
+    F3 vm{0.f, 0.f, 0.f};
+    float vs[3] = {0.f, 0.f, 0.f}, vq[4] = {0.f, 0.f, 0.f, 0.f};
+    const F3 pw{means[3 * g], means[3 * g + 1], means[3 * g + 2]};
+    const float4 q = reinterpret_cast<const float4*>(quats)[g];
+    if (rad > 0) {
+        const float vxy0 = ga[0], vxy1 = ga[1];
+        // project_pix_vjp: x/y rows through a fixed 1/w (the w row is dropped).
+        {
+            const float* m = p.pm;
+            const float hw = m[12] * pw.x + m[13] * pw.y + m[14] * pw.z + m[15];
+            const float rw = 1.f / (hw + 1e-6f);
+            const float vpx = 0.5f * (float)p.W * vxy0 * rw, vpy = 0.5f * (float)p.H * vxy1 * rw;
+            const float vpz = 0.f;
+            vm.x = m[0] * vpx + m[4] * vpy + m[8] * vpz;
+            vm.y = m[1] * vpx + m[5] * vpy + m[9] * vpz;
+            vm.z = m[2] * vpx + m[6] * vpy + m[10] * vpz;
+            const float v_z = 0.f;   // v_depth is zero-filled and never written (.mm:1168)
+            vm.x = vm.x + p.vm[8] * v_z;
+            vm.y = vm.y + p.vm[9] * v_z;
+            vm.z = vm.z + p.vm[10] * v_z;
+        }
+        // cov2d_to_conic_vjp: v_Sigma = -X G X.
+        float vc2[3];
+        {
+            const float4 cn = go.conic[g];
+            const float X[2][2] = {{cn.x, cn.y}, {cn.y, cn.z}};
+            const float G[2][2] = {{ga[2], ga[3]}, {ga[3], ga[4]}};
+            float nX[2][2], T1[2][2], S[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) nX[i][j] = -1.f * X[i][j];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) T1[j][i] = nX[0][i] * G[j][0] + nX[1][i] * G[j][1];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) S[j][i] = T1[0][i] * X[j][0] + T1[1][i] * X[j][1];
+            vc2[0] = S[0][0];
+            vc2[1] = S[1][0] + S[0][1];
+            vc2[2] = S[1][1];
+        }
+        // Recompute cov3d from scale and rotation.
+        const float es[3] = {exp_cw(scales[3 * g]), exp_cw(scales[3 * g + 1]),
+                             exp_cw(scales[3 * g + 2])};
+        const M3 R = quat_to_rotmat(q);
+        float cov[6];
+        {
+            M3 M;
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+#pragma unroll
+                for (int i = 0; i < 3; ++i) M.m[j][i] = R.m[j][i] * (p.glob_scale * es[j]);
+            auto t = [&](int i, int j) {
+                return M.m[0][i] * M.m[0][j] + M.m[1][i] * M.m[1][j] + M.m[2][i] * M.m[2][j];
+            };
+            cov[0] = t(0, 0); cov[1] = t(1, 0); cov[2] = t(2, 0);
+            cov[3] = t(1, 1); cov[4] = t(2, 1); cov[5] = t(2, 2);
+        }
+        // project_cov3d_ewa_vjp.
+        float vcov3[6];
+        {
+            const float* w = p.vm;
+            F3 pv{w[0] * pw.x + w[1] * pw.y + w[2] * pw.z + w[3],
+                  w[4] * pw.x + w[5] * pw.y + w[6] * pw.z + w[7],
+                  w[8] * pw.x + w[9] * pw.y + w[10] * pw.z + w[11]};
+            const float tan_fovx = 0.5f * (float)p.W / p.fx, tan_fovy = 0.5f * (float)p.H / p.fy;
+            const float lim_x = 1.3f * tan_fovx, lim_y = 1.3f * tan_fovy;
+            pv.x = pv.z * fminf(lim_x, fmaxf(-lim_x, pv.x / pv.z));
+            pv.y = pv.z * fminf(lim_y, fmaxf(-lim_y, pv.y / pv.z));
+            const float rz = 1.f / pv.z, rz2 = rz * rz;
+            M3 Wm;
+            Wm.m[0][0] = w[0]; Wm.m[0][1] = w[4]; Wm.m[0][2] = w[8];
+            Wm.m[1][0] = w[1]; Wm.m[1][1] = w[5]; Wm.m[1][2] = w[9];
+            Wm.m[2][0] = w[2]; Wm.m[2][1] = w[6]; Wm.m[2][2] = w[10];
+            M3 J;
+            J.m[0][0] = p.fx * rz; J.m[0][1] = 0.f; J.m[0][2] = 0.f;
+            J.m[1][0] = 0.f; J.m[1][1] = p.fy * rz; J.m[1][2] = 0.f;
+            J.m[2][0] = -p.fx * pv.x * rz2; J.m[2][1] = -p.fy * pv.y * rz2; J.m[2][2] = 0.f;
+            M3 V;
+            V.m[0][0] = cov[0]; V.m[0][1] = cov[1]; V.m[0][2] = cov[2];
+            V.m[1][0] = cov[1]; V.m[1][1] = cov[3]; V.m[1][2] = cov[4];
+            V.m[2][0] = cov[2]; V.m[2][1] = cov[4]; V.m[2][2] = cov[5];
+            M3 vc;
+            vc.m[0][0] = vc2[0]; vc.m[0][1] = 0.5f * vc2[1]; vc.m[0][2] = 0.f;
+            vc.m[1][0] = 0.5f * vc2[1]; vc.m[1][1] = vc2[2]; vc.m[1][2] = 0.f;
+            vc.m[2][0] = 0.f; vc.m[2][1] = 0.f; vc.m[2][2] = 0.f;
+            const M3 T = mat_mul(J, Wm);
+            const M3 vV = mat_mul(mat_mul(transpose(T), vc), T);
+            const M3 A1 = mat_mul(mat_mul(vc, T), transpose(V));
+            const M3 A2 = mat_mul(mat_mul(transpose(vc), T), V);
+            M3 vT;
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+#pragma unroll
+                for (int j = 0; j < 3; ++j) vT.m[i][j] = A1.m[i][j] + A2.m[i][j];
+            vcov3[0] = vV.m[0][0];
+            vcov3[1] = vV.m[0][1] + vV.m[1][0];
+            vcov3[2] = vV.m[0][2] + vV.m[2][0];
+            vcov3[3] = vV.m[1][1];
+            vcov3[4] = vV.m[1][2] + vV.m[2][1];
+            vcov3[5] = vV.m[2][2];
+            const M3 vJ = mat_mul(vT, transpose(Wm));
+            const float fx_rz2 = p.fx * rz2, fy_rz2 = p.fy * rz2, rz3 = rz2 * rz;
+            const F3 vt{-fx_rz2 * vJ.m[2][0], -fy_rz2 * vJ.m[2][1],
+                        -fx_rz2 * vJ.m[0][0] + 2.f * p.fx * pv.x * rz3 * vJ.m[2][0] -
+                            fy_rz2 * vJ.m[1][1] + 2.f * p.fy * pv.y * rz3 * vJ.m[2][1]};
+            vm.x += dot3(vt, F3{Wm.m[0][0], Wm.m[0][1], Wm.m[0][2]});
+            vm.y += dot3(vt, F3{Wm.m[1][0], Wm.m[1][1], Wm.m[1][2]});
+            vm.z += dot3(vt, F3{Wm.m[2][0], Wm.m[2][1], Wm.m[2][2]});
+        }
+        // scale_rot_to_cov3d_vjp + chain rule through exp.
+        {
+            M3 vV;
+            vV.m[0][0] = vcov3[0]; vV.m[0][1] = 0.5f * vcov3[1]; vV.m[0][2] = 0.5f * vcov3[2];
+            vV.m[1][0] = 0.5f * vcov3[1]; vV.m[1][1] = vcov3[3]; vV.m[1][2] = 0.5f * vcov3[4];
+            vV.m[2][0] = 0.5f * vcov3[2]; vV.m[2][1] = 0.5f * vcov3[4]; vV.m[2][2] = vcov3[5];
+            M3 S{};
+            S.m[0][0] = p.glob_scale * es[0];
+            S.m[1][1] = p.glob_scale * es[1];
+            S.m[2][2] = p.glob_scale * es[2];
+            const M3 M = mat_mul(R, S);
+            M3 vM = mat_mul(vV, M);
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+#pragma unroll
+                for (int j = 0; j < 3; ++j) vM.m[i][j] = 2.f * vM.m[i][j];
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+                vs[i] = dot3(F3{R.m[i][0], R.m[i][1], R.m[i][2]},
+                             F3{vM.m[i][0], vM.m[i][1], vM.m[i][2]}) * es[i];
+            const M3 vR = mat_mul(vM, S);
+            const float s = 1.f / sqrtf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+            const float w = q.x * s, x = q.y * s, y = q.z * s, z = q.w * s;
+            const auto& Rv = vR.m;
+            vq[0] = 2.f * (x * (Rv[1][2] - Rv[2][1]) + y * (Rv[2][0] - Rv[0][2]) +
+                           z * (Rv[0][1] - Rv[1][0]));
+            vq[1] = 2.f * (-2.f * x * (Rv[1][1] + Rv[2][2]) + y * (Rv[0][1] + Rv[1][0]) +
+                           z * (Rv[0][2] + Rv[2][0]) + w * (Rv[1][2] - Rv[2][1]));
+            vq[2] = 2.f * (x * (Rv[0][1] + Rv[1][0]) - 2.f * y * (Rv[0][0] + Rv[2][2]) +
+                           z * (Rv[1][2] + Rv[2][1]) + w * (Rv[2][0] - Rv[0][2]));
+            vq[3] = 2.f * (x * (Rv[0][2] + Rv[2][0]) + y * (Rv[1][2] + Rv[2][1]) -
+                           2.f * z * (Rv[0][0] + Rv[1][1]) + w * (Rv[0][1] - Rv[1][0]));
+        }
+        // f_dc Adam (visible only) and densify statistics.
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const size_t i = 3 * (size_t)g + c;
+            adam_elem(P.params[3][i], P.m[3][i], P.v[3][i], SH_C0 * ga[5 + c], hp.step[3], hp.b1,
+                      hp.b2, hp.bc2[3], hp.eps);
+        }
+        vis[g] += 1.0f;
+        gnorm[g] += sqrtf(vxy0 * vxy0 + vxy1 * vxy1);
+        max2d[g] = fmaxf(max2d[g], (float)rad * inv_max_dim);
+    }
+    if (v_mean_out) {
+        v_mean_out[3 * g] = vm.x; v_mean_out[3 * g + 1] = vm.y; v_mean_out[3 * g + 2] = vm.z;
+    }
+    if (v_scale_out) {
+        v_scale_out[3 * g] = vs[0]; v_scale_out[3 * g + 1] = vs[1]; v_scale_out[3 * g + 2] = vs[2];
+    }
+    if (v_quat_out) {
+        v_quat_out[4 * g] = vq[0]; v_quat_out[4 * g + 1] = vq[1];
+        v_quat_out[4 * g + 2] = vq[2]; v_quat_out[4 * g + 3] = vq[3];
+    }
+    // Dense Adam on means, scales, quats, opacities.
+    const float gm[3] = {vm.x, vm.y, vm.z};
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const size_t i = 3 * (size_t)g + k;
+        adam_elem(P.params[0][i], P.m[0][i], P.v[0][i], gm[k], hp.step[0], hp.b1, hp.b2,
+                  hp.bc2[0], hp.eps);
+        adam_elem(P.params[1][i], P.m[1][i], P.v[1][i], vs[k], hp.step[1], hp.b1, hp.b2,
+                  hp.bc2[1], hp.eps);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const size_t i = 4 * (size_t)g + k;
+        adam_elem(P.params[2][i], P.m[2][i], P.v[2][i], vq[k], hp.step[2], hp.b1, hp.b2,
+                  hp.bc2[2], hp.eps);
+    }
+    adam_elem(P.params[5][g], P.m[5][g], P.v[5][g], ga[8], hp.step[5], hp.b1, hp.b2, hp.bc2[5],
+              hp.eps);
+}
+
+__global__ __launch_bounds__(256) void k_split_gacc(int N, const float* __restrict__ gacc,
+                                                    float* v_xy, float* v_conic, float* v_rgb,
+                                                    float* v_opac) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= N) return;
+    const float* a = gacc + (size_t)g * 9;
+    if (v_xy) { v_xy[2 * g] = a[0]; v_xy[2 * g + 1] = a[1]; }
+    if (v_conic) { v_conic[3 * g] = a[2]; v_conic[3 * g + 1] = a[3]; v_conic[3 * g + 2] = a[4]; }
+    if (v_rgb) { v_rgb[3 * g] = a[5]; v_rgb[3 * g + 1] = a[6]; v_rgb[3 * g + 2] = a[7]; }
+    if (v_opac) v_opac[g] = a[8];
+}
+
+}  // namespace
+
+void launch_sh_rest_adam(hipStream_t s, const CamParams& p, const float* means,
+                         const int* radii, const float* gacc, float* f_rest, float* m, float* v,
+                         const AdamHP& hp) {
+    const int dtu = p.dtu < 3 ? p.dtu : 3;
+    const int n_used = dtu >= 3 ? 15 : dtu == 2 ? 8 : dtu == 1 ? 3 : 0;
+    if (n_used == 0 || p.rest_per == 0 || p.N <= 0) return;
+    const int64_t n = (int64_t)p.N * p.rest_per;
+    hipLaunchKernelGGL(k_sh_rest_adam, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, n,
+                       p.rest_per, n_used, means, p.cam[0], p.cam[1], p.cam[2], radii, gacc,
+                       f_rest, m, v, hp);
+}
+
+void launch_proj_bwd_adam(hipStream_t s, const CamParams& p, float* const params[6],
+                          float* const m[6], float* const v[6], const AdamHP& hp, GaussOut go,
+                          const float* gacc, float* vis, float* gnorm, float* max2d,
+                          float inv_max_dim, float* v_mean_out, float* v_scale_out,
+                          float* v_quat_out) {
+    if (p.N <= 0) return;
+    BwdPtrs P;
+    for (int i = 0; i < 6; ++i) { P.params[i] = params[i]; P.m[i] = m[i]; P.v[i] = v[i]; }
+    hipLaunchKernelGGL(k_proj_bwd_adam, dim3((p.N + 255) / 256), dim3(256), 0, s, p, P, hp, go,
+                       gacc, vis, gnorm, max2d, inv_max_dim, v_mean_out, v_scale_out, v_quat_out);
+}
+
+void launch_split_gacc(hipStream_t s, int N, const float* gacc, float* v_xy, float* v_conic,
+                       float* v_rgb, float* v_opac) {
+    if (N <= 0) return;
+    hipLaunchKernelGGL(k_split_gacc, dim3((N + 255) / 256), dim3(256), 0, s, N, gacc, v_xy,
+                       v_conic, v_rgb, v_opac);
+}
+
+}  // namespace msp

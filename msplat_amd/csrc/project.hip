@@ -1,0 +1,182 @@
+// project.hip — projection + SH colour of every gaussian (one thread each),
+// fused with the per-tile intersection count and the zeroing of the raster
+// gradient accumulators.
+//
+// Follows project_and_sh_forward_kernel (.metal:1695-1787) and its helpers
+// quat_to_rotmat (.metal:111-131), scale_rot_to_cov3d (.metal:175-188),
+// project_cov3d_ewa (.metal:241-281), compute_cov2d_bounds (.metal:283-305),
+// project_pix (.metal:308-317), get_tile_bbox (.metal:57-87) and
+// sh_coeffs_to_color (.metal:587-654).  The counting half of
+// scatter_to_prealloc_bins (.metal:2046-2058) happens here; the sigmoid of
+// the opacity logit that the reference evaluates per intersection at pack
+// time (.metal:2133) is evaluated once per gaussian here, same formula.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace msp {
+
+namespace {
+
+struct V3 { float x, y, z; };
+
+__device__ __forceinline__ V3 xf4x3(const float* m, V3 p) {
+    return V3{m[0] * p.x + m[1] * p.y + m[2] * p.z + m[3],
+              m[4] * p.x + m[5] * p.y + m[6] * p.z + m[7],
+              m[8] * p.x + m[9] * p.y + m[10] * p.z + m[11]};
+}
+
+// cov3d upper triangle from exp'd scale and quaternion (w,x,y,z).
+__device__ __forceinline__ void cov3d_of(const float s0, const float s1, const float s2,
+                                         float glob, float4 q, float* cov) {
+    const float s = 1.f / sqrtf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+    const float w = q.x * s, x = q.y * s, y = q.z * s, z = q.w * s;
+    // R[col][row]
+    const float R00 = 1.f - 2.f * (y * y + z * z), R01 = 2.f * (x * y + w * z), R02 = 2.f * (x * z - w * y);
+    const float R10 = 2.f * (x * y - w * z), R11 = 1.f - 2.f * (x * x + z * z), R12 = 2.f * (y * z + w * x);
+    const float R20 = 2.f * (x * z + w * y), R21 = 2.f * (y * z - w * x), R22 = 1.f - 2.f * (x * x + y * y);
+    const float g0 = glob * s0, g1 = glob * s1, g2 = glob * s2;
+    const float M00 = R00 * g0, M01 = R01 * g0, M02 = R02 * g0;
+    const float M10 = R10 * g1, M11 = R11 * g1, M12 = R12 * g1;
+    const float M20 = R20 * g2, M21 = R21 * g2, M22 = R22 * g2;
+    // tmp[j][i] = sum_k M[k][i] * M[k][j]
+    cov[0] = M00 * M00 + M10 * M10 + M20 * M20;
+    cov[1] = M01 * M00 + M11 * M10 + M21 * M20;
+    cov[2] = M02 * M00 + M12 * M10 + M22 * M20;
+    cov[3] = M01 * M01 + M11 * M11 + M21 * M21;
+    cov[4] = M02 * M01 + M12 * M11 + M22 * M21;
+    cov[5] = M02 * M02 + M12 * M12 + M22 * M22;
+}
+
+__device__ __forceinline__ void sh_color(int degree, V3 d, const float* dc, const float* rest,
+                                         float* col) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) col[c] = SH_C0 * dc[c];
+    if (degree < 1) return;
+    const float x = d.x, y = d.y, z = d.z;
+    const float xx = x * x, xy = x * y, xz = x * z, yy = y * y, yz = y * z, zz = z * z;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const float* r = rest + c;
+        col[c] += SH_C1 * (-y * r[0] + z * r[3] - x * r[6]);
+        if (degree < 2) continue;
+        col[c] += (SH_C2_0 * xy * r[9] + SH_C2_1 * yz * r[12] + SH_C2_2 * (2.f * zz - xx - yy) * r[15] +
+                   SH_C2_3 * xz * r[18] + SH_C2_4 * (xx - yy) * r[21]);
+        if (degree < 3) continue;
+        col[c] += (SH_C3_0 * y * (3.f * xx - yy) * r[24] + SH_C3_1 * xy * z * r[27] +
+                   SH_C3_2 * y * (4.f * zz - xx - yy) * r[30] +
+                   SH_C3_3 * z * (2.f * zz - 3.f * xx - 3.f * yy) * r[33] +
+                   SH_C3_4 * x * (4.f * zz - xx - yy) * r[36] + SH_C3_5 * z * (xx - yy) * r[39] +
+                   SH_C3_6 * x * (xx - 3.f * yy) * r[42]);
+        if (degree < 4) continue;
+        col[c] += (2.5033429417967046f * xy * (xx - yy) * r[45] +
+                   -1.7701307697799304f * yz * (3.f * xx - yy) * r[48] +
+                   0.9461746957575601f * xy * (7.f * zz - 1.f) * r[51] +
+                   -0.6690465435572892f * yz * (7.f * zz - 3.f) * r[54] +
+                   0.10578554691520431f * (zz * (35.f * zz - 30.f) + 3.f) * r[57] +
+                   -0.6690465435572892f * xz * (7.f * zz - 3.f) * r[60] +
+                   0.47308734787878004f * (xx - yy) * (7.f * zz - 1.f) * r[63] +
+                   -1.7701307697799304f * xz * (xx - 3.f * yy) * r[66] +
+                   0.6258357354491761f * (xx * (xx - 3.f * yy) - yy * (3.f * xx - yy)) * r[69]);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_project_fwd(
+    CamParams p, const float* __restrict__ means, const float* __restrict__ scales,
+    const float* __restrict__ quats, const float* __restrict__ f_dc,
+    const float* __restrict__ f_rest, const float* __restrict__ opac_logits, GaussOut go,
+    int* __restrict__ tile_cnt, float* __restrict__ gacc) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= p.N) return;
+#pragma unroll
+    for (int q = 0; q < 9; ++q) gacc[(size_t)g * 9 + q] = 0.f;
+    go.radii[g] = 0;
+    go.tiles_hit[g] = 0;
+
+    const V3 pw{means[3 * g], means[3 * g + 1], means[3 * g + 2]};
+    const V3 pv = xf4x3(p.vm, pw);
+    if (pv.z <= p.clip) return;
+
+    const float s0 = exp_cw(scales[3 * g]), s1 = exp_cw(scales[3 * g + 1]),
+                s2 = exp_cw(scales[3 * g + 2]);
+    const float4 q = reinterpret_cast<const float4*>(quats)[g];
+    float cov[6];
+    cov3d_of(s0, s1, s2, p.glob_scale, q, cov);
+
+    // EWA projection with the view-space clamp to 1.3 tan(fov).
+    const float tan_fovx = 0.5f * (float)p.W / p.fx, tan_fovy = 0.5f * (float)p.H / p.fy;
+    const float lim_x = 1.3f * tan_fovx, lim_y = 1.3f * tan_fovy;
+    const float cxv = pv.z * fminf(lim_x, fmaxf(-lim_x, pv.x / pv.z));
+    const float cyv = pv.z * fminf(lim_y, fmaxf(-lim_y, pv.y / pv.z));
+    const float rz = 1.f / pv.z, rz2 = rz * rz;
+    const float j00 = p.fx * rz, j11 = p.fy * rz;
+    const float j20 = -p.fx * cxv * rz2, j21 = -p.fy * cyv * rz2;
+    const float t0x = j00 * p.vm[0] + j20 * p.vm[8], t0y = j00 * p.vm[1] + j20 * p.vm[9],
+                t0z = j00 * p.vm[2] + j20 * p.vm[10];
+    const float t1x = j11 * p.vm[4] + j21 * p.vm[8], t1y = j11 * p.vm[5] + j21 * p.vm[9],
+                t1z = j11 * p.vm[6] + j21 * p.vm[10];
+    const float tv0x = t0x * cov[0] + t0y * cov[1] + t0z * cov[2];
+    const float tv0y = t0x * cov[1] + t0y * cov[3] + t0z * cov[4];
+    const float tv0z = t0x * cov[2] + t0y * cov[4] + t0z * cov[5];
+    const float tv1x = t1x * cov[0] + t1y * cov[1] + t1z * cov[2];
+    const float tv1y = t1x * cov[1] + t1y * cov[3] + t1z * cov[4];
+    const float tv1z = t1x * cov[2] + t1y * cov[4] + t1z * cov[5];
+    const float c2x = (tv0x * t0x + tv0y * t0y + tv0z * t0z) + 0.3f;
+    const float c2y = tv0x * t1x + tv0y * t1y + tv0z * t1z;
+    const float c2z = (tv1x * t1x + tv1y * t1y + tv1z * t1z) + 0.3f;
+
+    // Conic and 3-sigma radius.
+    const float det = c2x * c2z - c2y * c2y;
+    if (det == 0.f) return;
+    const float inv_det = 1.f / det;
+    const float ca = c2z * inv_det, cb = -c2y * inv_det, cc = c2x * inv_det;
+    const float b = 0.5f * (c2x + c2z);
+    const float disc = sqrtf(fmaxf(0.1f, b * b - det));
+    const float radius = ceilf(3.f * sqrtf(b + disc));
+
+    // Pixel centre.
+    const float* m = p.pm;
+    const float hx = m[0] * pw.x + m[1] * pw.y + m[2] * pw.z + m[3];
+    const float hy = m[4] * pw.x + m[5] * pw.y + m[6] * pw.z + m[7];
+    const float hw = m[12] * pw.x + m[13] * pw.y + m[14] * pw.z + m[15];
+    const float rw = 1.f / (hw + 1e-6f);
+    const float px = 0.5f * (float)p.W * (hx * rw) + p.cx - 0.5f;
+    const float py = 0.5f * (float)p.H * (hy * rw) + p.cy - 0.5f;
+
+    const float ex = ceilf(3.0f * sqrtf(c2x)), ey = ceilf(3.0f * sqrtf(c2z));
+    int x0, y0, x1, y1;
+    tile_rect(px, py, ex, ey, p.tbx, p.tby, x0, y0, x1, y1);
+    const int area = (x1 - x0) * (y1 - y0);
+    if (area <= 0) return;
+
+    go.tiles_hit[g] = area;
+    go.depth[g] = pv.z;
+    go.radii[g] = f2i(radius);
+    go.xy[g] = make_float2(px, py);
+    go.aabb[g] = make_float2(ex, ey);
+
+    // SH colour along normalize(p - cam_pos).
+    const float dx = pw.x - p.cam[0], dy = pw.y - p.cam[1], dz = pw.z - p.cam[2];
+    const float inv = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
+    const V3 dir{dx * inv, dy * inv, dz * inv};
+    float col[3];
+    sh_color(p.dtu, dir, f_dc + 3 * (size_t)g, f_rest + (size_t)p.rest_per * g, col);
+    go.conic[g] = make_float4(ca, cb, cc, sigmoid(opac_logits[g]));
+    go.rgb[g] = make_float4(col[0], col[1], col[2], 0.f);
+
+    for (int ty = y0; ty < y1; ++ty)
+        for (int tx = x0; tx < x1; ++tx) atomicAdd(&tile_cnt[ty * p.tbx + tx], 1);
+}
+
+}  // namespace
+
+void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
+                        const float* scales, const float* quats, const float* f_dc,
+                        const float* f_rest, const float* opac_logits, GaussOut go,
+                        int* tile_cnt, float* gacc) {
+    if (p.N <= 0) return;
+    const int blocks = (p.N + 255) / 256;
+    hipLaunchKernelGGL(k_project_fwd, dim3(blocks), dim3(256), 0, s, p, means, scales, quats,
+                       f_dc, f_rest, opac_logits, go, tile_cnt, gacc);
+}
+
+}  // namespace msp

@@ -1,0 +1,343 @@
+// raster.hip — alpha compositing forward, chunk merge and backward.
+//
+// Work decomposition: one 256-thread workgroup (four wave64) per (tile,
+// chunk) item; each wave owns one 8x8 quadrant of the 16x16 tile, one lane per
+// pixel.  Sorted entries are staged through LDS 256 at a time and read by all
+// lanes as broadcasts.  A tile that is rasterised in one piece writes the
+// final image directly; a chunked tile writes per-pixel chunk state that the
+// merge kernel folds front to back.
+//
+// Semantics follow the reference exactly:
+//   forward      nd_rasterize_forward_kernel (.metal:472-585)
+//   chunked fwd  rasterize_forward_chunked_kernel (.metal:2633-2741)
+//   merge        rasterize_forward_merge_kernel (.metal:2746-2799)
+//   prefix/sfx   compute_chunk_prefix_suffix_kernel (.metal:2804-2840)
+//   backward     rasterize_backward_kernel (.metal:898-1099) and
+//                rasterize_backward_chunked_kernel (.metal:2844-3031)
+// with these MI355X differences: a workgroup-wide vote stops the forward
+// once every pixel of the item has terminated; the backward reduces each
+// gaussian's per-pixel terms across the 64 lanes of a wave (DPP + readlane)
+// and nine lanes issue one float atomic each.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace msp {
+
+namespace {
+
+struct Px {
+    int i, j;      // pixel row / column
+    int lp;        // local pixel index within the tile (ly * 16 + lx)
+    bool inside;
+};
+
+__device__ __forceinline__ Px pixel_of(int t, int tbx, int W, int H) {
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int lx = (w & 1) * 8 + (l & 7), ly = (w >> 1) * 8 + (l >> 3);
+    Px p;
+    p.j = (t % tbx) * BLOCK + lx;
+    p.i = (t / tbx) * BLOCK + ly;
+    p.lp = ly * BLOCK + lx;
+    p.inside = p.i < H && p.j < W;
+    return p;
+}
+
+__device__ __forceinline__ void item_range(const Items& it, const int* tile_bins, int item,
+                                           int& t, int& K, int& cs, int& ce) {
+    t = it.tile[item];
+    const int k = it.k[item];
+    K = it.tile_K[t];
+    const int s = tile_bins[2 * t], e = tile_bins[2 * t + 1];
+    if (K == 1) {
+        cs = s;
+        ce = e;
+    } else {
+        cs = s + k * CHUNK;
+        ce = min(cs + CHUNK, e);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float bg0, float bg1,
+                                                    float bg2, Items it,
+                                                    const int* __restrict__ tile_bins, Packed pk,
+                                                    float* __restrict__ final_T,
+                                                    int* __restrict__ final_idx,
+                                                    float* __restrict__ out_img, ChunkBufs cb) {
+    __shared__ float4 s_geo[256];
+    __shared__ float4 s_col[256];
+    __shared__ float s_bl[256];
+    const int item = blockIdx.x;
+    int t, K, cs, ce;
+    item_range(it, tile_bins, item, t, K, cs, ce);
+    const Px px = pixel_of(t, tbx, W, H);
+    const float fx = (float)px.j, fy = (float)px.i;
+
+    float T = 1.f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
+    int last = cs - 1;
+    bool done = !px.inside;
+    const int tid = threadIdx.x;
+    for (int b = cs; b < ce; b += 256) {
+        if (__syncthreads_and(done)) break;
+        const int idx = b + tid;
+        if (idx < ce) {
+            float4 c = pk.col[idx];
+            c.z = fmaxf(c.z + 0.5f, 0.f);
+            c.w = fmaxf(c.w + 0.5f, 0.f);
+            s_geo[tid] = pk.geo[idx];
+            s_col[tid] = c;
+            s_bl[tid] = fmaxf(pk.bl[idx] + 0.5f, 0.f);
+        }
+        __syncthreads();
+        if (!done) {
+            const int nb = min(256, ce - b);
+            for (int q = 0; q < nb; ++q) {
+                const float4 g = s_geo[q];
+                const float4 c = s_col[q];
+                const float dx = g.x - fx, dy = g.y - fy;
+                const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
+                if (sigma < 0.f || sigma >= 5.55f) continue;
+                const float alpha = fminf(0.999f, c.y * exp_cw(-sigma));
+                if (alpha < 1.f / 255.f) continue;
+                const float nT = T * (1.f - alpha);
+                if (nT <= 1e-4f) {
+                    last = b + q - 1;
+                    done = true;
+                    break;
+                }
+                const float vis = alpha * T;
+                C0 = fmaf(c.z, vis, C0);
+                C1 = fmaf(c.w, vis, C1);
+                C2 = fmaf(s_bl[q], vis, C2);
+                T = nT;
+                last = b + q;
+            }
+        }
+    }
+    if (!px.inside) return;
+    if (K == 1) {
+        const size_t pix = (size_t)px.i * W + px.j;
+        final_T[pix] = T;
+        final_idx[pix] = last;
+        out_img[3 * pix + 0] = clamp01(fmaf(bg0, T, C0));
+        out_img[3 * pix + 1] = clamp01(fmaf(bg1, T, C1));
+        out_img[3 * pix + 2] = clamp01(fmaf(bg2, T, C2));
+    } else {
+        const size_t o = (size_t)item * TILE_PIX + px.lp;
+        cb.cT[o] = T;
+        cb.cC[3 * o + 0] = C0;
+        cb.cC[3 * o + 1] = C1;
+        cb.cC[3 * o + 2] = C2;
+        cb.cidx[o] = last;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, float bg0,
+                                                      float bg1, float bg2,
+                                                      const int* __restrict__ chunked, Items it,
+                                                      float* __restrict__ final_T,
+                                                      int* __restrict__ final_idx,
+                                                      float* __restrict__ out_img, ChunkBufs cb,
+                                                      int with_suffix) {
+    const int t = chunked[blockIdx.x];
+    const int K = it.tile_K[t], i0 = it.tile_item0[t];
+    const int lp = threadIdx.x, lx = lp & 15, ly = lp >> 4;
+    const int j = (t % tbx) * BLOCK + lx, i = (t / tbx) * BLOCK + ly;
+    if (i >= H || j >= W) return;
+    float Tr = 1.f, R0 = 0.f, R1 = 0.f, R2 = 0.f;
+    int li = -1, cutoff = K;
+    for (int k = 0; k < K; ++k) {
+        const size_t o = (size_t)(i0 + k) * TILE_PIX + lp;
+        const int cf = cb.cidx[o];
+        if (cf < 0 && k > 0) break;
+        const float cT = cb.cT[o];
+        R0 = fmaf(cb.cC[3 * o + 0], Tr, R0);
+        R1 = fmaf(cb.cC[3 * o + 1], Tr, R1);
+        R2 = fmaf(cb.cC[3 * o + 2], Tr, R2);
+        Tr *= cT;
+        if (cf >= 0) li = cf;
+        if (Tr <= 1e-4f) {
+            cutoff = k + 1;
+            break;
+        }
+    }
+    for (int k = cutoff; k < K; ++k) cb.cidx[(size_t)(i0 + k) * TILE_PIX + lp] = -1;
+    const size_t pix = (size_t)i * W + j;
+    final_T[pix] = Tr;
+    final_idx[pix] = li;
+    out_img[3 * pix + 0] = clamp01(fmaf(bg0, Tr, R0));
+    out_img[3 * pix + 1] = clamp01(fmaf(bg1, Tr, R1));
+    out_img[3 * pix + 2] = clamp01(fmaf(bg2, Tr, R2));
+    if (!with_suffix) return;
+    float pT = 1.f;
+    for (int k = 0; k < K; ++k) {
+        const size_t o = (size_t)(i0 + k) * TILE_PIX + lp;
+        cb.pT[o] = pT;
+        pT *= cb.cT[o];
+    }
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+    for (int k = K - 1; k >= 0; --k) {
+        const size_t o = (size_t)(i0 + k) * TILE_PIX + lp;
+        cb.aC[3 * o + 0] = a0;
+        cb.aC[3 * o + 1] = a1;
+        cb.aC[3 * o + 2] = a2;
+        const float p = cb.pT[o];
+        a0 += p * cb.cC[3 * o + 0];
+        a1 += p * cb.cC[3 * o + 1];
+        a2 += p * cb.cC[3 * o + 2];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float bg0, float bg1,
+                                                    float bg2, Items it,
+                                                    const int* __restrict__ tile_bins, Packed pk,
+                                                    const float* __restrict__ final_T,
+                                                    const int* __restrict__ final_idx,
+                                                    ChunkBufs cb, const float* __restrict__ v_out,
+                                                    float* __restrict__ gacc) {
+    __shared__ float4 s_geo[256];
+    __shared__ float4 s_col[256];
+    __shared__ float s_bl[256];
+    __shared__ int s_id[256];
+    __shared__ int s_max;
+    const int item = blockIdx.x;
+    int t, K, cs, ce;
+    item_range(it, tile_bins, item, t, K, cs, ce);
+    const Px px = pixel_of(t, tbx, W, H);
+    const float fx = (float)px.j, fy = (float)px.i;
+    const int tid = threadIdx.x, lane = tid & 63;
+
+    float T = 1.f, Tfin = 1.f, B0 = 0.f, B1 = 0.f, B2 = 0.f, vo0 = 0.f, vo1 = 0.f, vo2 = 0.f;
+    int bf = cs - 1;
+    if (px.inside) {
+        const size_t pix = (size_t)px.i * W + px.j;
+        Tfin = final_T[pix];
+        vo0 = v_out[3 * pix + 0];
+        vo1 = v_out[3 * pix + 1];
+        vo2 = v_out[3 * pix + 2];
+        if (K == 1) {
+            T = Tfin;
+            bf = final_idx[pix];
+        } else {
+            const size_t o = (size_t)item * TILE_PIX + px.lp;
+            T = cb.pT[o] * cb.cT[o];
+            B0 = cb.aC[3 * o + 0];
+            B1 = cb.aC[3 * o + 1];
+            B2 = cb.aC[3 * o + 2];
+            bf = cb.cidx[o];
+        }
+    }
+    const float tb0 = Tfin * bg0, tb1 = Tfin * bg1, tb2 = Tfin * bg2;
+    const int wave_bf = wave_max_i(bf);
+    if (tid == 0) s_max = cs - 1;
+    __syncthreads();
+    if (lane == 0) atomicMax(&s_max, wave_bf);
+    __syncthreads();
+    const int hi = min(ce - 1, s_max);
+
+    for (int top = hi; top >= cs; top -= 256) {
+        __syncthreads();
+        const int idx = top - tid;
+        if (idx >= cs) {
+            s_geo[tid] = pk.geo[idx];
+            s_col[tid] = pk.col[idx];
+            s_bl[tid] = pk.bl[idx];
+            s_id[tid] = pk.ids[idx];
+        }
+        __syncthreads();
+        const int nb = min(256, top - cs + 1);
+        for (int q = max(0, top - wave_bf); q < nb; ++q) {
+            const int e_idx = top - q;
+            const float4 g = s_geo[q];
+            const float4 c = s_col[q];
+            const float braw = s_bl[q];
+            const float dx = g.x - fx, dy = g.y - fy;
+            bool valid = px.inside && e_idx <= bf;
+            float alpha = 0.f;
+            if (valid) {
+                const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
+                if (sigma < 0.f || sigma >= 5.55f) {
+                    valid = false;
+                } else {
+                    alpha = fminf(0.999f, c.y * exp_cw(-sigma));
+                    if (alpha < 1.f / 255.f) valid = false;
+                }
+            }
+            if (__ballot(valid) == 0) continue;
+            float vx = 0.f, vy = 0.f, va = 0.f, vb = 0.f, vc = 0.f, vr = 0.f, vg = 0.f, vbl = 0.f,
+                  vop = 0.f;
+            if (valid && alpha < 0.999f) {
+                const float ra = 1.f / (1.f - alpha);
+                T *= ra;
+                const float fac = alpha * T;
+                vr = fac * vo0;
+                vg = fac * vo1;
+                vbl = fac * vo2;
+                const float r0 = fmaxf(c.z + 0.5f, 0.f), r1 = fmaxf(c.w + 0.5f, 0.f),
+                            r2 = fmaxf(braw + 0.5f, 0.f);
+                const float t0 = fmaf(r0, T, fmaf(-B0, ra, -ra * tb0));
+                const float t1 = fmaf(r1, T, fmaf(-B1, ra, -ra * tb1));
+                const float t2 = fmaf(r2, T, fmaf(-B2, ra, -ra * tb2));
+                const float v_alpha = 0.f + (t0 * vo0 + t1 * vo1 + t2 * vo2);
+                B0 = fmaf(r0, fac, B0);
+                B1 = fmaf(r1, fac, B1);
+                B2 = fmaf(r2, fac, B2);
+                const float v_sigma = -alpha * v_alpha;
+                const float hv = 0.5f * v_sigma;
+                va = hv * (dx * dx);
+                vb = hv * (dx * dy);
+                vc = hv * (dy * dy);
+                vx = v_sigma * fmaf(g.z, dx, g.w * dy);
+                vy = v_sigma * fmaf(g.w, dx, c.x * dy);
+                vop = -v_sigma * (1.f - c.y);
+            }
+            const float s0 = wave_sum(vx), s1 = wave_sum(vy), s2 = wave_sum(va), s3 = wave_sum(vb),
+                        s4 = wave_sum(vc), s5 = wave_sum(vr), s6 = wave_sum(vg),
+                        s7 = wave_sum(vbl), s8 = wave_sum(vop);
+            if (lane < 9) {
+                float val = s8;
+                bool ok = true;
+                switch (lane) {
+                    case 0: val = s0; break;
+                    case 1: val = s1; break;
+                    case 2: val = s2; break;
+                    case 3: val = s3; break;
+                    case 4: val = s4; break;
+                    case 5: val = s5; ok = c.z + 0.5f >= 0.f; break;
+                    case 6: val = s6; ok = c.w + 0.5f >= 0.f; break;
+                    case 7: val = s7; ok = braw + 0.5f >= 0.f; break;
+                    default: break;
+                }
+                if (ok) atomicAdd(&gacc[(size_t)s_id[q] * 9 + lane], val);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+void launch_raster_fwd(hipStream_t s, const CamParams& p, int n_items, Items it,
+                       const int* tile_bins, Packed pk, float* final_T, int* final_idx,
+                       float* out_img, ChunkBufs cb) {
+    if (n_items <= 0) return;
+    hipLaunchKernelGGL(k_raster_fwd, dim3(n_items), dim3(256), 0, s, p.W, p.H, p.tbx, p.bg[0],
+                       p.bg[1], p.bg[2], it, tile_bins, pk, final_T, final_idx, out_img, cb);
+}
+
+void launch_raster_merge(hipStream_t s, const CamParams& p, int n_chunked, const int* chunked,
+                         Items it, float* final_T, int* final_idx, float* out_img, ChunkBufs cb,
+                         bool with_suffix) {
+    if (n_chunked <= 0) return;
+    hipLaunchKernelGGL(k_raster_merge, dim3(n_chunked), dim3(256), 0, s, p.W, p.H, p.tbx, p.bg[0],
+                       p.bg[1], p.bg[2], chunked, it, final_T, final_idx, out_img, cb,
+                       with_suffix ? 1 : 0);
+}
+
+void launch_raster_bwd(hipStream_t s, const CamParams& p, int n_items, Items it,
+                       const int* tile_bins, Packed pk, const float* final_T,
+                       const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc) {
+    if (n_items <= 0) return;
+    hipLaunchKernelGGL(k_raster_bwd, dim3(n_items), dim3(256), 0, s, p.W, p.H, p.tbx, p.bg[0],
+                       p.bg[1], p.bg[2], it, tile_bins, pk, final_T, final_idx, cb, v_out, gacc);
+}
+
+}  // namespace msp

@@ -1,0 +1,241 @@
+// ssim.hip — separable 11-tap SSIM + L1 loss, forward and backward, on
+// 16x16 workgroups with LDS-staged halos.
+//
+// Three passes with the reference's training semantics:
+//   h-fwd        ssim_h_fwd_kernel (.metal:3053-3115): horizontal zero-padded
+//                sums of x=gt, y=render: mu_x, mu_y, E[x^2], E[y^2], E[xy]
+//   v-fwd+h-bwd  ssim_fused_v_fwd_h_bwd_kernel (.metal:3226-3313): vertical
+//                sums -> SSIM and its derivative fields f1, f2, f3 at every
+//                centre of the tile rows, including the 5-column halo outside
+//                the image (whose zero statistics give f = (0, -2/C2, 2/C2)),
+//                then the mirrored horizontal pass
+//   v-bwd        ssim_v_bwd_kernel (.metal:3396-3464): mirrored vertical pass
+//                (rows outside the image contribute nothing) and the
+//                combination with the L1 sign term.
+// The loss is reduced per workgroup into (sum SSIM, sum L1, pixel count) and
+// folded by one final workgroup in a fixed order; it equals the sum over
+// pixels of w*(1 - mean_c SSIM) + (1-w)*mean_c |gt - r|.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace msp {
+
+namespace {
+
+constexpr int TG = 16;
+constexpr int HALF = 5;
+constexpr int WIN = 11;
+constexpr int TW = TG + 2 * HALF;   // 26
+
+__global__ __launch_bounds__(256) void k_ssim_h_fwd(int W, int H, const float* __restrict__ img,
+                                                    const float* __restrict__ gt,
+                                                    float* __restrict__ hbuf) {
+    __shared__ float s_gt[3][TG][TW];
+    __shared__ float s_rd[3][TG][TW];
+    const int tr = threadIdx.x, lx = tr & 15, ly = tr >> 4;
+    const int bx = blockIdx.x * TG - HALF, by = blockIdx.y * TG;
+    for (int c = 0; c < 3; ++c)
+        for (int i = tr; i < TG * TW; i += 256) {
+            const int sy = i / TW, sx = i % TW, gy = by + sy, gx = bx + sx;
+            float gv = 0.f, rv = 0.f;
+            if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
+                const size_t q = ((size_t)gy * W + gx) * 3 + c;
+                gv = gt[q];
+                rv = img[q];
+            }
+            s_gt[c][sy][sx] = gv;
+            s_rd[c][sy][sx] = rv;
+        }
+    __syncthreads();
+    const int px = blockIdx.x * TG + lx, py = blockIdx.y * TG + ly;
+    if (px >= W || py >= H) return;
+    for (int c = 0; c < 3; ++c) {
+        float mx = 0.f, my = 0.f, sx = 0.f, sy = 0.f, cxy = 0.f;
+#pragma unroll
+        for (int d = 0; d < WIN; ++d) {
+            const float w = GAUSS_1D[d];
+            const float gv = s_gt[c][ly][lx + d], rv = s_rd[c][ly][lx + d];
+            mx += w * gv;
+            my += w * rv;
+            sx += w * gv * gv;
+            sy += w * rv * rv;
+            cxy += w * gv * rv;
+        }
+        float* o = hbuf + ((size_t)py * W + px) * 15 + c * 5;
+        o[0] = mx;
+        o[1] = my;
+        o[2] = sx;
+        o[3] = sy;
+        o[4] = cxy;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_ssim_fused(int W, int H, const float* __restrict__ img,
+                                                    const float* __restrict__ gt,
+                                                    const float* __restrict__ hbuf,
+                                                    float* __restrict__ dbuf,
+                                                    float* __restrict__ loss_part) {
+    __shared__ float s_hp[TW][TW][5];
+    __shared__ float s_f1[TG][TW], s_f2[TG][TW], s_f3[TG][TW];
+    __shared__ float s_red[3][4];
+    const int tr = threadIdx.x, lx = tr & 15, ly = tr >> 4;
+    const int bx = blockIdx.x * TG - HALF, by = blockIdx.y * TG - HALF;
+    float ssim_sum = 0.f, l1_sum = 0.f, cnt = 0.f;
+    for (int c = 0; c < 3; ++c) {
+        for (int i = tr; i < TW * TW; i += 256) {
+            const int sy = i / TW, sx = i % TW, gy = by + sy, gx = bx + sx;
+            if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
+                const float* h = hbuf + ((size_t)gy * W + gx) * 15 + c * 5;
+#pragma unroll
+                for (int f = 0; f < 5; ++f) s_hp[sy][sx][f] = h[f];
+            } else {
+#pragma unroll
+                for (int f = 0; f < 5; ++f) s_hp[sy][sx][f] = 0.f;
+            }
+        }
+        __syncthreads();
+        for (int i = tr; i < TG * TW; i += 256) {
+            const int dy = i / TW, dx = i % TW;
+            float mx = 0.f, my = 0.f, sx = 0.f, sy = 0.f, cxy = 0.f;
+#pragma unroll
+            for (int k = 0; k < WIN; ++k) {
+                const float w = GAUSS_1D[k];
+                const float* h = s_hp[dy + k][dx];
+                mx += w * h[0];
+                my += w * h[1];
+                sx += w * h[2];
+                sy += w * h[3];
+                cxy += w * h[4];
+            }
+            const float sxs = sx - mx * mx, sys = sy - my * my, sxy = cxy - mx * my;
+            const float A = 2.0f * mx * my + SSIM_C1, B = 2.0f * sxy + SSIM_C2;
+            const float Cd = mx * mx + my * my + SSIM_C1, D = sxs + sys + SSIM_C2;
+            const float iCD = 1.0f / (Cd * D);
+            const float dmu = 2.0f * B * (mx * Cd - A * my) / (Cd * Cd * D);
+            const float dsyq = -A * B * iCD / D, dsxy = 2.0f * A * iCD;
+            s_f1[dy][dx] = dmu - 2.0f * my * dsyq - mx * dsxy;
+            s_f2[dy][dx] = 2.0f * dsyq;
+            s_f3[dy][dx] = dsxy;
+            if (dx >= HALF && dx < HALF + TG) {
+                const int gpx = bx + dx, gpy = by + dy + HALF;
+                if (gpx >= 0 && gpx < W && gpy >= 0 && gpy < H) {
+                    const size_t q = ((size_t)gpy * W + gpx) * 3 + c;
+                    ssim_sum += (A * B) / (Cd * D);
+                    l1_sum += fabsf(gt[q] - img[q]);
+                    if (c == 0) cnt += 1.f;
+                }
+            }
+        }
+        __syncthreads();
+        const int px = blockIdx.x * TG + lx, py = blockIdx.y * TG + ly;
+        if (px < W && py < H) {
+            float h1 = 0.f, h2 = 0.f, h3 = 0.f;
+#pragma unroll
+            for (int d = 0; d < WIN; ++d) {
+                const float w = GAUSS_1D[WIN - 1 - d];
+                h1 += w * s_f1[ly][lx + d];
+                h2 += w * s_f2[ly][lx + d];
+                h3 += w * s_f3[ly][lx + d];
+            }
+            float* o = dbuf + ((size_t)py * W + px) * 9 + c * 3;
+            o[0] = h1;
+            o[1] = h2;
+            o[2] = h3;
+        }
+        __syncthreads();
+    }
+    // Workgroup partials of (sum SSIM, sum L1, pixels).
+    const float a = wave_sum(ssim_sum), b = wave_sum(l1_sum), n = wave_sum(cnt);
+    if ((tr & 63) == 0) {
+        s_red[0][tr >> 6] = a;
+        s_red[1][tr >> 6] = b;
+        s_red[2][tr >> 6] = n;
+    }
+    __syncthreads();
+    if (tr < 3) {
+        const float v = (s_red[tr][0] + s_red[tr][1]) + (s_red[tr][2] + s_red[tr][3]);
+        loss_part[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 3 + tr] = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_ssim_v_bwd(int W, int H, const float* __restrict__ img,
+                                                    const float* __restrict__ gt,
+                                                    const float* __restrict__ dbuf, float w_ssim,
+                                                    float inv_n, float* __restrict__ v_rendered) {
+    __shared__ float s_h[3][3][TW][TG];
+    const int tr = threadIdx.x, lx = tr & 15, ly = tr >> 4;
+    const int bx = blockIdx.x * TG, by = blockIdx.y * TG - HALF;
+    for (int c = 0; c < 3; ++c)
+        for (int i = tr; i < TW * TG; i += 256) {
+            const int sy = i / TG, sx = i % TG, gy = by + sy, gx = bx + sx;
+            float v1 = 0.f, v2 = 0.f, v3 = 0.f;
+            if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
+                const float* d = dbuf + ((size_t)gy * W + gx) * 9 + c * 3;
+                v1 = d[0];
+                v2 = d[1];
+                v3 = d[2];
+            }
+            s_h[c][0][sy][sx] = v1;
+            s_h[c][1][sy][sx] = v2;
+            s_h[c][2][sy][sx] = v3;
+        }
+    __syncthreads();
+    const int px = bx + lx, py = blockIdx.y * TG + ly;
+    if (px >= W || py >= H) return;
+    for (int c = 0; c < 3; ++c) {
+        float f1 = 0.f, f2 = 0.f, f3 = 0.f;
+#pragma unroll
+        for (int d = 0; d < WIN; ++d) {
+            const float w = GAUSS_1D[WIN - 1 - d];
+            f1 += w * s_h[c][0][ly + d][lx];
+            f2 += w * s_h[c][1][ly + d][lx];
+            f3 += w * s_h[c][2][ly + d][lx];
+        }
+        const size_t q = ((size_t)py * W + px) * 3 + c;
+        const float r = img[q], g = gt[q];
+        const float v_ssim = f1 + r * f2 + g * f3;
+        const float v_l1 = (g > r) ? -1.0f : ((g < r) ? 1.0f : 0.0f);
+        v_rendered[q] = inv_n * (-w_ssim * v_ssim + (1.0f - w_ssim) * v_l1);
+    }
+}
+
+// loss = sum_pixels [w (1 - mean SSIM) + (1-w) mean L1], folded in a fixed order.
+__global__ __launch_bounds__(256) void k_loss_final(int nparts, const float* __restrict__ part,
+                                                    float w_ssim, float* __restrict__ out) {
+    __shared__ double s[3][256];
+    double a = 0.0, b = 0.0, n = 0.0;
+    for (int i = threadIdx.x; i < nparts; i += 256) {
+        a += part[3 * i];
+        b += part[3 * i + 1];
+        n += part[3 * i + 2];
+    }
+    s[0][threadIdx.x] = a;
+    s[1][threadIdx.x] = b;
+    s[2][threadIdx.x] = n;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off)
+            for (int k = 0; k < 3; ++k) s[k][threadIdx.x] += s[k][threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const double w = w_ssim;
+        out[0] = (float)(w * s[2][0] - (w / 3.0) * s[0][0] + ((1.0 - w) / 3.0) * s[1][0]);
+    }
+}
+
+}  // namespace
+
+void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
+                 float inv_n, float* hbuf, float* dbuf, float* v_rendered, float* loss_part,
+                 float* loss_out) {
+    const dim3 grid((W + TG - 1) / TG, (H + TG - 1) / TG);
+    hipLaunchKernelGGL(k_ssim_h_fwd, grid, dim3(256), 0, s, W, H, img, gt, hbuf);
+    hipLaunchKernelGGL(k_ssim_fused, grid, dim3(256), 0, s, W, H, img, gt, hbuf, dbuf, loss_part);
+    hipLaunchKernelGGL(k_ssim_v_bwd, grid, dim3(256), 0, s, W, H, img, gt, dbuf, w, inv_n,
+                       v_rendered);
+    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(256), 0, s, (int)(grid.x * grid.y), loss_part,
+                       w, loss_out);
+}
+
+}  // namespace msp

@@ -1,0 +1,227 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle.
+
+Forward stages (projection, tile counts / offsets / sorted id lists, raster
+forward, SSIM and its input gradient) must be bit-exact; gradients and
+Adam-updated parameters match to rel 1e-3 with an absolute floor (float
+atomics sum in a different order than the oracle's fixed-order fp64 sums).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import orc
+from helpers import BG, LRS, assert_bits_equal, grad_close, small_scene, target_for
+from msplat_amd import camera, synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from msplat_amd import device
+    device.init(0)
+    return device
+
+
+def _render_and_compare(dev, scene, dtu=None, cam_idx=0):
+    deg = scene.sh_degree
+    dtu = deg if dtu is None else dtu
+    su = camera.prepare_cam(scene.cameras[cam_idx])
+    g = dev.DeviceGaussians.from_arrays(scene.params(), deg)
+    img = dev.render(g, su, dtu, BG).cpu().numpy()
+    cam = orc.camera(su, deg, dtu, BG)
+    p = orc.project(cam, scene.means, scene.scales, scene.quats, scene.f_dc, scene.f_rest)
+    n = scene.n
+    radii = dev.intermediate("radii", np.int32)
+    assert_bits_equal(radii, p["radii"], "radii")
+    assert_bits_equal(dev.intermediate("num_tiles_hit", np.int32), p["num_tiles_hit"], "num_tiles_hit")
+    vis = p["radii"] > 0
+    assert vis.sum() > 0
+    assert_bits_equal(dev.intermediate("xys").reshape(n, 2)[vis], p["xys"][vis], "xys")
+    assert_bits_equal(dev.intermediate("depths")[vis], p["depths"][vis], "depths")
+    assert_bits_equal(dev.intermediate("aabb").reshape(n, 2)[vis], p["aabb"][vis], "aabb")
+    assert_bits_equal(dev.intermediate("conics").reshape(n, 3)[vis], p["conics"][vis], "conics")
+    assert_bits_equal(dev.intermediate("colors").reshape(n, 3)[vis], p["colors"][vis], "colors")
+    counts, tile_bins, ids = orc.bin_sort(cam, p)
+    assert_bits_equal(dev.intermediate("tile_bins", np.int32).reshape(-1, 2), tile_bins, "tile_bins")
+    assert_bits_equal(dev.intermediate("gaussian_ids", np.int32), ids, "gaussian_ids")
+    r = orc.rasterize(cam, p, scene.opacities, tile_bins, ids)
+    H, W = su.height, su.width
+    assert_bits_equal(dev.intermediate("final_Ts").reshape(H, W), r["final_Ts"], "final_Ts")
+    assert_bits_equal(dev.intermediate("final_index", np.int32).reshape(H, W), r["final_index"], "final_index")
+    assert_bits_equal(img, r["out_img"], "out_img")
+    return dev.meta(), counts
+
+
+def test_render_config1(dev):
+    """Config 1 (10k SH0, 256x256, 256 tiles -> reference chunk mode)."""
+    meta, counts = _render_and_compare(dev, synthetic.config1())
+    assert meta["total_isect"] == int(counts.sum())
+
+
+def test_render_sh3_small(dev):
+    """Config-2 distributions at 4k gaussians, 160x112 (70 tiles, chunk mode)."""
+    _render_and_compare(dev, small_scene())
+
+
+def test_render_sh_degrees(dev):
+    for deg, dtu in ((1, 1), (2, 1), (3, 2), (4, 4)):
+        _render_and_compare(dev, small_scene(n=1500, degree=deg, seed_off=60 + deg), dtu=dtu)
+
+
+def test_render_monolithic_tiles(dev):
+    """>= 400 tiles: the monolithic kernel (reference selector, .mm:876)."""
+    meta, counts = _render_and_compare(dev, small_scene(n=20000, width=400, height=272, seed_off=70))
+    assert meta["n_chunked_tiles"] == int((counts > 2048).sum())
+
+
+def test_render_heavy_chunked_tiles(dev):
+    """Dense scene in chunk mode: tiles of several 512-entry chunks + merge."""
+    meta, counts = _render_and_compare(dev, small_scene(n=60000, width=128, height=96, seed_off=71, spread=0.6))
+    assert counts.max() > 1024 and meta["n_chunked_tiles"] > 0
+
+
+def test_render_large_and_huge_tiles(dev):
+    """Tiles beyond 2048 and 16384 entries: 128 KB LDS sort and the global-memory sort."""
+    sc = small_scene(n=40000, width=48, height=32, seed_off=72, spread=0.3, dist=6.0)
+    meta, counts = _render_and_compare(dev, sc)
+    assert counts.max() > 16384, counts.max()
+    assert meta["n_huge"] > 0
+
+
+def test_render_empty_and_culled(dev):
+    """No gaussian in front of the camera: every pixel is background."""
+    sc = small_scene(n=500, seed_off=73)
+    su = camera.prepare_cam(sc.cameras[0])
+    fwd = -np.asarray(sc.cameras[0].cam_to_world)[:3, 2]
+    sc.means = (np.asarray(sc.cameras[0].cam_to_world)[:3, 3] - 3.0 * fwd + 0.01 * sc.means).astype(np.float32)
+    g = dev.DeviceGaussians.from_arrays(sc.params(), 3)
+    img = dev.render(g, su, 3, BG).cpu().numpy()
+    assert dev.meta()["total_isect"] == 0
+    assert np.all(img == np.clip(BG, 0, 1)[None, None, :])
+
+
+def _train_compare(dev, scene, steps=1, dtu=None, check_grads=True):
+    deg = scene.sh_degree
+    dtu = deg if dtu is None else dtu
+    su = camera.prepare_cam(scene.cameras[0])
+    H, W = su.height, su.width
+    gt = target_for(scene, (H, W))
+    torch = pytest.importorskip("torch")
+    g = dev.DeviceGaussians.from_arrays(scene.params(), deg, capacity=scene.n)
+    gt_d = dev.to_dev(gt)
+    n = scene.n
+    grads = {k: torch.zeros((n, d), dtype=torch.float32, device="cuda") for k, d in
+             (("v_mean3d", 3), ("v_scale", 3), ("v_quat", 4))}
+    # oracle state
+    params = [np.ascontiguousarray(a, np.float32).copy() for a in scene.params()]
+    m = [np.zeros_like(a) for a in params]
+    v = [np.zeros_like(a) for a in params]
+    vis, gnorm, max2d = (np.zeros(n, np.float32) for _ in range(3))
+    cam = orc.camera(su, deg, dtu, BG)
+    for step in range(1, steps + 1):
+        loss_g = dev.train_step(g, su, dtu, BG, gt_d, 0.2, LRS, step, grads_out=grads)
+        want = ("out_img", "radii", "v_xy", "v_conic", "v_rgb", "v_opacity", "v_mean3d", "v_scale", "v_quat",
+                "v_rendered")
+        loss_o, o = orc.train_step(cam, params, m, v, orc.adam_hparams(LRS, step), gt, 0.2, vis, gnorm, max2d,
+                                   want=want)
+        assert abs(loss_g - loss_o) <= 1e-5 * abs(loss_o), (loss_g, loss_o)
+        if step == 1:
+            assert_bits_equal(dev.intermediate("out_img").reshape(H, W, 3), o["out_img"], "out_img")
+            assert_bits_equal(dev.intermediate("v_rendered").reshape(H, W, 3), o["v_rendered"], "v_rendered")
+            assert_bits_equal(dev.intermediate("radii", np.int32), o["radii"], "radii")
+        if check_grads and step == 1:
+            for k, d in (("v_xy", 2), ("v_conic", 3), ("v_rgb", 3), ("v_opacity", 1)):
+                grad_close(dev.intermediate(k).reshape(n, d) if d > 1 else dev.intermediate(k),
+                           o[k], what=k)
+            for k in ("v_mean3d", "v_scale", "v_quat"):
+                grad_close(grads[k].cpu().numpy(), o[k], what=k)
+    gp = g.numpy()
+    names = ("means", "scales", "quats", "f_dc", "f_rest", "opacities")
+    for i in range(6):
+        grad_close(gp[i], params[i], rtol=1e-3, floor=1e-6, what=f"param {names[i]}")
+        grad_close(g.m[i][:n].cpu().numpy(), m[i], what=f"exp_avg {names[i]}")
+        grad_close(g.v[i][:n].cpu().numpy(), v[i], rtol=2e-3, what=f"exp_avg_sq {names[i]}")
+    grad_close(g.vis[:n].cpu().numpy(), vis, rtol=0, floor=0, what="vis_counts")
+    grad_close(g.gnorm[:n].cpu().numpy(), gnorm, what="xys_grad_norm")
+    grad_close(g.max2d[:n].cpu().numpy(), max2d, rtol=0, floor=0, what="max_2d_size")
+
+
+def test_train_step_small(dev):
+    _train_compare(dev, small_scene(n=3000, seed_off=80))
+
+
+def test_train_step_chunked(dev):
+    """Chunk mode with multi-chunk tiles: prefix/suffix backward."""
+    _train_compare(dev, small_scene(n=30000, width=96, height=64, seed_off=81, spread=0.6))
+
+
+def test_train_step_monolithic(dev):
+    _train_compare(dev, small_scene(n=12000, width=336, height=208, seed_off=82))
+
+
+def test_train_three_steps(dev):
+    """Adam state carried over three steps (bias corrections t = 1, 2, 3)."""
+    _train_compare(dev, small_scene(n=2000, seed_off=83), steps=3, check_grads=False)
+
+
+def test_densify_parity(dev):
+    """Identical statistics and random samples -> identical densify result (counts, order, values)."""
+    torch = pytest.importorskip("torch")
+    sc = small_scene(n=5000, seed_off=84)
+    n = sc.n
+    cap = 3 * n
+    g = dev.DeviceGaussians.from_arrays(sc.params(), 3, capacity=cap)
+    st = synthetic.Stream(synthetic.BASE_SEED + 85)
+    vis = np.floor(st.uniform(n) * 4).astype(np.float32)
+    gnorm = (st.uniform(n) * 4e-3 * vis).astype(np.float32)
+    max2d = (st.uniform(n) * 0.2).astype(np.float32)
+    sc_logs = sc.scales.copy()
+    sc_logs[: n // 3] += 1.5   # some large gaussians
+    sc.scales = sc_logs
+    g.bufs[1][:n].copy_(torch.from_numpy(sc_logs))
+    m0 = [(st.uniform(b.numel()).reshape(tuple(b.shape)) * 0.1).astype(np.float32) for b in g.bufs]
+    for i in range(6):
+        g.m[i].copy_(torch.from_numpy(m0[i]))
+        g.v[i].copy_(torch.from_numpy(m0[i] * 0.5))
+    g.vis[:n].copy_(torch.from_numpy(vis))
+    g.gnorm[:n].copy_(torch.from_numpy(gnorm))
+    g.max2d[:n].copy_(torch.from_numpy(max2d))
+    rnd = torch.empty(2 * n * 3, dtype=torch.float32, device="cuda")
+    dev.init()
+    from msplat_amd import _abi
+    _abi.check(dev.init().msplat_hip_randn(dev.ptr(rnd), rnd.numel(), 1234))
+    rnd_h = rnd.cpu().numpy()
+    kw = dict(grad_thresh=2e-4, size_thresh=0.01, screen_thresh=0.05, check_screen=1, cull_alpha=0.005,
+              cull_scale=0.5, cull_screen=0.15, check_huge=1, half_max_dim=0.5 * 160)
+    # oracle
+    bufs = [b.cpu().numpy().copy() for b in g.bufs]
+    ms = [a.copy() for a in m0]
+    vs = [(a * 0.5).astype(np.float32) for a in m0]
+    oa = orc.OrcDensifyArgs()
+    oa.N = n
+    oa.grad_thresh, oa.size_thresh, oa.screen_thresh, oa.check_screen = 2e-4, 0.01, 0.05, 1
+    oa.cull_alpha_thresh, oa.cull_scale_thresh, oa.cull_screen_size, oa.check_huge = 0.005, 0.5, 0.15, 1
+    oa.half_max_dim, oa.fr_stride = 0.5 * 160, 45
+    nn_o, split, dup, keep = orc.densify(oa, gnorm, vis, max2d, bufs, ms, vs, rnd_h)
+    nn_g = dev.densify(g, random_samples=rnd, **kw)
+    assert split.sum() > 0 and dup.sum() > 0 and (keep == 0).sum() > split.sum()
+    assert nn_g == nn_o, (nn_g, nn_o)
+    for i in range(6):
+        assert_bits_equal(g.bufs[i][:nn_o].cpu().numpy(), bufs[i][:nn_o], f"densified param {i}")
+        assert_bits_equal(g.m[i][:nn_o].cpu().numpy(), ms[i][:nn_o], f"densified exp_avg {i}")
+        assert_bits_equal(g.v[i][:nn_o].cpu().numpy(), vs[i][:nn_o], f"densified exp_avg_sq {i}")
+
+
+def test_randn_statistics(dev):
+    torch = pytest.importorskip("torch")
+    from msplat_amd import _abi
+    x = torch.empty(1 << 20, dtype=torch.float32, device="cuda")
+    _abi.check(dev.init().msplat_hip_randn(dev.ptr(x), x.numel(), 99))
+    h = x.cpu().numpy().astype(np.float64)
+    assert abs(h.mean()) < 5e-3 and abs(h.std() - 1.0) < 5e-3
+    assert abs(((h > 1.0).mean()) - 0.158655) < 3e-3
