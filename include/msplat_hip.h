@@ -147,11 +147,14 @@ int msplat_hip_densify(const MsplatDensifyArgs* a, int32_t* new_count);
 int msplat_hip_randn(float* dst, int64_t n, uint64_t seed);
 
 /* Per-stage GPU timing (msplat_enable_gpu_timing / msplat_drain_stage_times,
- * bindings.h:28-33; stage names as msplat_metal.mm:30-34).  When enabled each
- * stage is bracketed by HIP events; drain returns the per-stage milliseconds
- * of the last completed call. */
+ * bindings.h:28-33).  When enabled every stage of every render / train call is
+ * bracketed by HIP events on the context stream (no extra synchronisation).
+ * drain waits for the stream, then returns for each stage i the summed
+ * milliseconds ms[i] and the number of timed instances counts[i] since the
+ * last drain (or enable), its name, and the number of calls timed. */
 int msplat_hip_enable_stage_timing(int enable);
-int msplat_hip_drain_stage_times(double* ms, const char** names, int max_stages, int* n_stages);
+int msplat_hip_drain_stage_times(double* ms, int64_t* counts, const char** names, int max_stages,
+                                 int* n_stages, int64_t* n_calls);
 
 /* Copy a named intermediate of the last render / train step to host memory.
  * Names: xys, depths, radii, conics, colors, aabb, num_tiles_hit,

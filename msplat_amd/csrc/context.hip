@@ -8,10 +8,10 @@
 // raster forward (+merge) -> SSIM fwd/bwd -> raster backward ->
 // projection backward + Adam + grad stats.  Intermediate buffers live in a
 // grow-only cache owned by the context.  One host synchronisation per step:
-// after the tile scan the host reads the intersection count and tile-size
-// summary (a few bytes) to size the key/packed buffers and the launch grids
-// exactly, instead of the reference's fixed 16N capacity and 2048-per-tile
-// bins.
+// after the depth sort the host reads the intersection total (8 bytes) to size
+// the intersection buffers exactly, instead of the reference's fixed 16N
+// capacity and 2048-per-tile bins; every later grid is an upper bound whose
+// surplus workgroups exit on the exact counts the GPU wrote.
 #include "../../include/msplat_hip.h"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -26,6 +26,14 @@ namespace {
 
 using namespace msp;
 
+// Stage names (as msplat_metal.mm:30-34 where they coincide).
+constexpr int kNumStages = 8;
+constexpr int kMaxMarks = 12;
+const char* kStageNames[kNumStages] = {"proj_sh_fwd", "depth_sort", "tile_lists", "rast_fwd",
+                                       "loss_fwd_bwd", "rast_bwd", "sh_rest_adam",
+                                       "proj_sh_bwd_adam"};
+enum Stage { S_PROJ, S_DEPTH, S_TILES, S_RFWD, S_LOSS, S_RBWD, S_SHADAM, S_PBWD, S_END };
+
 struct Buf {
     void* p = nullptr;
     size_t bytes = 0;
@@ -35,18 +43,25 @@ struct Ctx {
     int device = -1;
     hipStream_t own = nullptr;
     hipStream_t stream = nullptr;
+    // Stage timing: one event per stage boundary of the current call; the
+    // previous call's intervals are folded into the running sums at the next
+    // call's host synchronisation point, so timing adds no synchronisation.
     bool timing = false;
-    hipEvent_t ev[9] = {};
-    int n_ev_used = 0;
-    double stage_ms[8] = {};
-    int n_stages = 0;
+    hipEvent_t ev[2][kMaxMarks] = {};
+    int mark_stage[2][kMaxMarks] = {};
+    int n_marks[2] = {0, 0};
+    int cur = 0;
+    double stage_sum[kNumStages] = {};
+    int64_t stage_cnt[kNumStages] = {};
+    int64_t calls = 0;
 
     // per gaussian
     Buf xy, conic, rgb, depth, radii, aabb, tiles_hit, gacc;
+    Buf dkey, dval, dkey2, dval2, hits, eoff, dtemp, stemp;
     // per tile
-    Buf tile_cnt, tile_bins, tile_K, tile_item0, l_chunked, l_large, l_huge;
+    Buf tstart, tend, tile_bins, tile_K, tile_item0, l_chunked;
     // per intersection
-    Buf keys, scratch, pk_geo, pk_col, pk_bl, pk_ids;
+    Buf tkey, tval, tkey2, tval2, ttemp, pk_geo, pk_col, pk_bl, pk_ids;
     // per item
     Buf it_tile, it_k, c_T, c_C, c_idx, c_pT, c_aC;
     // per pixel
@@ -60,6 +75,8 @@ struct Ctx {
     Buf d_split, d_dup, d_sp, d_dp, d_keep, d_kp, d_tot, d_scratch, d_rnd;
 
     Meta meta{};
+    bool meta_valid = false;
+    int64_t max_items = 0;
     int last_N = 0, last_T = 0, last_W = 0, last_H = 0;
     bool have_bwd = false;
 };
@@ -117,8 +134,10 @@ T* P(Buf& b) { return reinterpret_cast<T*>(b.p); }
 
 void free_all(Ctx* c) {
     Buf* bufs[] = {&c->xy, &c->conic, &c->rgb, &c->depth, &c->radii, &c->aabb, &c->tiles_hit,
-                   &c->gacc, &c->tile_cnt, &c->tile_bins, &c->tile_K, &c->tile_item0,
-                   &c->l_chunked, &c->l_large, &c->l_huge, &c->keys, &c->scratch, &c->pk_geo,
+                   &c->gacc, &c->dkey, &c->dval, &c->dkey2, &c->dval2, &c->hits, &c->eoff,
+                   &c->dtemp, &c->stemp, &c->tstart, &c->tend, &c->tile_bins, &c->tile_K,
+                   &c->tile_item0, &c->l_chunked, &c->tkey, &c->tval, &c->tkey2, &c->tval2,
+                   &c->ttemp, &c->pk_geo,
                    &c->pk_col, &c->pk_bl, &c->pk_ids, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
                    &c->hbuf, &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
@@ -129,8 +148,9 @@ void free_all(Ctx* c) {
     if (c->meta_h) (void)hipHostFree(c->meta_h);
     if (c->loss_h) (void)hipHostFree(c->loss_h);
     if (c->count_h) (void)hipHostFree(c->count_h);
-    for (auto& e : c->ev)
-        if (e) (void)hipEventDestroy(e);
+    for (auto& row : c->ev)
+        for (auto& e : row)
+            if (e) (void)hipEventDestroy(e);
     if (c->own) (void)hipStreamDestroy(c->own);
 }
 
@@ -176,9 +196,38 @@ ChunkBufs chunks(Ctx* c) {
 
 int sh_bases(int degree) { return degree == 0 ? 1 : degree == 1 ? 4 : degree == 2 ? 9 : degree == 3 ? 16 : 25; }
 
-void stage_mark(Ctx* c) {
+// Record the start of stage `st` (S_END closes the call).
+void stage_mark(Ctx* c, int st) {
     if (!c->timing) return;
-    if (c->n_ev_used < 9) (void)hipEventRecord(c->ev[c->n_ev_used++], c->stream);
+    int& n = c->n_marks[c->cur];
+    if (n >= kMaxMarks) return;
+    (void)hipEventRecord(c->ev[c->cur][n], c->stream);
+    c->mark_stage[c->cur][n] = st;
+    ++n;
+}
+
+// Fold the finished intervals of the other event set into the sums.
+void stage_fold(Ctx* c, int set) {
+    const int n = c->n_marks[set];
+    for (int i = 0; i + 1 < n; ++i) {
+        float t = 0.f;
+        if (hipEventElapsedTime(&t, c->ev[set][i], c->ev[set][i + 1]) == hipSuccess) {
+            const int st = c->mark_stage[set][i];
+            if (st >= 0 && st < kNumStages) {
+                c->stage_sum[st] += t;
+                c->stage_cnt[st] += 1;
+            }
+        }
+    }
+    if (n > 1) c->calls += 1;
+    c->n_marks[set] = 0;
+}
+
+// Start a new call: its marks go to the other event set.
+void stage_begin(Ctx* c) {
+    if (!c->timing) return;
+    c->cur ^= 1;
+    c->n_marks[c->cur] = 0;
 }
 
 int check_render_args(const MsplatRenderArgs* a) {
@@ -220,26 +269,34 @@ CamParams cam_params(const MsplatRenderArgs* a) {
     return p;
 }
 
-// forward_pipeline (.mm:462-750): project -> bin/sort/pack -> raster (+merge).
+// forward_pipeline (.mm:462-750): project -> depth order -> tile lists -> raster (+merge).
 int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
     const CamParams p = cam_params(a);
     const int N = p.N, T = p.tbx * p.tby;
     const size_t Px = (size_t)p.W * p.H;
-    ENSURE(c->xy, (size_t)N * 8);
-    ENSURE(c->conic, (size_t)N * 16);
-    ENSURE(c->rgb, (size_t)N * 16);
-    ENSURE(c->depth, (size_t)N * 4);
-    ENSURE(c->radii, (size_t)N * 4);
-    ENSURE(c->aabb, (size_t)N * 8);
-    ENSURE(c->tiles_hit, (size_t)N * 4);
-    ENSURE(c->gacc, (size_t)N * 36);
-    ENSURE(c->tile_cnt, (size_t)T * 4);
+    const size_t Nn = (size_t)std::max(N, 1);
+    ENSURE(c->xy, Nn * 8);
+    ENSURE(c->conic, Nn * 16);
+    ENSURE(c->rgb, Nn * 16);
+    ENSURE(c->depth, Nn * 4);
+    ENSURE(c->radii, Nn * 4);
+    ENSURE(c->aabb, Nn * 8);
+    ENSURE(c->tiles_hit, Nn * 4);
+    ENSURE(c->gacc, Nn * 36);
+    ENSURE(c->dkey, Nn * 4);
+    ENSURE(c->dval, Nn * 4);
+    ENSURE(c->dkey2, Nn * 4);
+    ENSURE(c->dval2, Nn * 4);
+    ENSURE(c->hits, Nn * 4);
+    ENSURE(c->eoff, Nn * 4);
+    ENSURE(c->dtemp, (size_t)radix_temp_ints(N) * 4);
+    ENSURE(c->stemp, ((size_t)scan_block_count(N) + 8) * 4);
+    ENSURE(c->tstart, (size_t)T * 4);
+    ENSURE(c->tend, (size_t)T * 4);
     ENSURE(c->tile_bins, (size_t)T * 8);
     ENSURE(c->tile_K, (size_t)T * 4);
     ENSURE(c->tile_item0, (size_t)T * 4);
     ENSURE(c->l_chunked, (size_t)T * 4);
-    ENSURE(c->l_large, (size_t)T * 4);
-    ENSURE(c->l_huge, (size_t)T * 4);
     ENSURE(c->final_T, Px * 4);
     ENSURE(c->final_idx, Px * 4);
     ENSURE(c->out_img, Px * 12);
@@ -247,61 +304,66 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
     c->last_N = N; c->last_T = T; c->last_W = p.W; c->last_H = p.H;
     c->have_bwd = false;
 
-    stage_mark(c);   // start of proj_sh_fwd
-    HIP_TRY(hipMemsetAsync(c->tile_cnt.p, 0, (size_t)T * 4, c->stream));
+    stage_mark(c, S_PROJ);
     GaussOut go = gauss_out(c);
     launch_project_fwd(c->stream, p, a->means3d, a->scales, a->quats, a->features_dc,
-                       a->features_rest, a->opacities, go, P<int>(c->tile_cnt), P<float>(c->gacc));
-    stage_mark(c);   // start of prefix_sort_pack
-    TileLists tl{P<int>(c->l_chunked), P<int>(c->l_large), P<int>(c->l_huge)};
-    Items it = items(c);
-    launch_tile_scan(c->stream, T, P<int>(c->tile_cnt), P<int>(c->tile_bins), it, tl,
-                     P<Meta>(c->meta_d));
+                       a->features_rest, a->opacities, go, P<uint32_t>(c->dkey),
+                       P<uint32_t>(c->dval), P<float>(c->gacc));
+    stage_mark(c, S_DEPTH);
+    uint32_t* order = nullptr;
+    launch_depth_order(c->stream, N, P<uint32_t>(c->dkey), P<uint32_t>(c->dval),
+                       P<uint32_t>(c->dkey2), P<uint32_t>(c->dval2), P<int>(c->dtemp),
+                       P<int>(c->tiles_hit), P<int>(c->hits), P<int>(c->eoff), P<int>(c->stemp),
+                       P<Meta>(c->meta_d), &order);
     HIP_TRY(hipMemcpyAsync(c->meta_h, c->meta_d.p, sizeof(Meta), hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
-    c->meta = *c->meta_h;
-    const Meta& m = c->meta;
-    if (m.total_isect > (int64_t)0x7FFFFFFF - 4096)
+    if (c->timing) stage_fold(c, c->cur ^ 1);   // the previous call has completed
+    const int64_t I64 = c->meta_h->total_isect;
+    if (I64 > (int64_t)0x7FFFFFFF - 4096)
         return fail(MSPLAT_ERR_ARG, "%lld tile intersections exceed the 32-bit index range",
-                    (long long)m.total_isect);
-    const size_t I = (size_t)std::max<int64_t>(m.total_isect, 1);
-    ENSURE(c->keys, I * 8);
+                    (long long)I64);
+    const size_t I = (size_t)std::max<int64_t>(I64, 1);
+    ENSURE(c->tkey, I * 4);
+    ENSURE(c->tval, I * 4);
+    ENSURE(c->tkey2, I * 4);
+    ENSURE(c->tval2, I * 4);
+    ENSURE(c->ttemp, (size_t)radix_temp_ints((int64_t)I) * 4);
     ENSURE(c->pk_geo, I * 16);
     ENSURE(c->pk_col, I * 16);
     ENSURE(c->pk_bl, I * 4);
     ENSURE(c->pk_ids, I * 4);
-    if (m.n_huge > 0) ENSURE(c->scratch, I * 16);
-    ENSURE(c->it_tile, (size_t)m.n_items * 4);
-    ENSURE(c->it_k, (size_t)m.n_items * 4);
-    if (m.n_chunked_tiles > 0) {
-        const size_t S = (size_t)m.n_items * TILE_PIX;
-        ENSURE(c->c_T, S * 4);
-        ENSURE(c->c_C, S * 12);
-        ENSURE(c->c_idx, S * 4);
-        if (training) {
-            ENSURE(c->c_pT, S * 4);
-            ENSURE(c->c_aC, S * 12);
-        }
+    const int64_t max_items = items_bound(T, I64);
+    ENSURE(c->it_tile, (size_t)max_items * 4);
+    ENSURE(c->it_k, (size_t)max_items * 4);
+    const size_t S = (size_t)max_items * TILE_PIX;
+    ENSURE(c->c_T, S * 4);
+    ENSURE(c->c_C, S * 12);
+    ENSURE(c->c_idx, S * 4);
+    if (training) {
+        ENSURE(c->c_pT, S * 4);
+        ENSURE(c->c_aC, S * 12);
     }
-    it = items(c);
-    launch_build_items(c->stream, T, it);
-    launch_scatter(c->stream, p, go, P<int>(c->tile_bins), P<int>(c->tile_cnt), P<uint64_t>(c->keys));
+    c->max_items = max_items;
+    go = gauss_out(c);
+    stage_mark(c, S_TILES);
+    TileLists tl{P<int>(c->l_chunked), nullptr, nullptr};
+    Items it = items(c);
     Packed pk = packed(c);
-    launch_sort_pack(c->stream, T, m, P<int>(c->tile_bins), tl, P<uint64_t>(c->keys),
-                     P<uint64_t>(c->scratch), go, pk);
-    stage_mark(c);   // start of rast_fwd
+    launch_tile_lists(c->stream, p, I64, go, order, P<int>(c->eoff), P<int>(c->hits),
+                      P<uint32_t>(c->tkey), P<uint32_t>(c->tval), P<uint32_t>(c->tkey2),
+                      P<uint32_t>(c->tval2), P<int>(c->ttemp), P<int>(c->tstart), P<int>(c->tend),
+                      P<int>(c->tile_bins), it, tl, P<Meta>(c->meta_d), pk);
+    stage_mark(c, S_RFWD);
     ChunkBufs cb = chunks(c);
-    launch_raster_fwd(c->stream, p, m.n_items, it, P<int>(c->tile_bins), pk, P<float>(c->final_T),
-                      P<int>(c->final_idx), P<float>(c->out_img), cb);
-    launch_raster_merge(c->stream, p, m.n_chunked_tiles, P<int>(c->l_chunked), it,
+    launch_raster_fwd(c->stream, p, max_items, P<Meta>(c->meta_d), it, P<int>(c->tile_bins), pk,
+                      P<float>(c->final_T), P<int>(c->final_idx), P<float>(c->out_img), cb);
+    launch_raster_merge(c->stream, p, P<Meta>(c->meta_d), P<int>(c->l_chunked), it,
                         P<float>(c->final_T), P<int>(c->final_idx), P<float>(c->out_img), cb,
                         training);
     HIP_TRY(hipGetLastError());
+    c->meta_valid = false;
     return MSPLAT_OK;
 }
-
-const char* kStageNames[7] = {"proj_sh_fwd", "prefix_sort_pack", "rast_fwd", "loss_fwd_bwd",
-                              "rast_bwd", "proj_sh_bwd_adam", "grad_stats"};
 
 }  // namespace
 
@@ -328,7 +390,8 @@ int msplat_hip_init(int device) {
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->meta_h), sizeof(Meta)));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->loss_h), 16));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->count_h), 16));
-    for (auto& e : c->ev) HIP_TRY(hipEventCreate(&e));
+    for (auto& row : c->ev)
+        for (auto& e : row) HIP_TRY(hipEventCreate(&e));
     return MSPLAT_OK;
 }
 
@@ -406,10 +469,10 @@ int msplat_hip_render(const MsplatRenderArgs* a, float* out_img) {
     if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
     int r = check_render_args(a);
     if (r != MSPLAT_OK) return r;
-    c->n_ev_used = 0;
+    stage_begin(c);
     r = forward(c, a, false);
     if (r != MSPLAT_OK) return r;
-    stage_mark(c);
+    stage_mark(c, S_END);
     if (out_img)
         HIP_TRY(hipMemcpyAsync(out_img, c->out_img.p, (size_t)a->img_width * a->img_height * 12,
                                hipMemcpyDeviceToDevice, c->stream));
@@ -435,7 +498,7 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
     }
     if (!a->vis_counts || !a->xys_grad_norm || !a->max_2d_size)
         return fail(MSPLAT_ERR_ARG, "null grad-stat array");
-    c->n_ev_used = 0;
+    stage_begin(c);
     r = forward(c, &a->r, true);
     if (r != MSPLAT_OK) return r;
     const CamParams p = cam_params(&a->r);
@@ -446,27 +509,29 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
     ENSURE(c->v_rendered, Px * 12);
     ENSURE(c->loss_part, (size_t)sgrid.x * sgrid.y * 12);
     ENSURE(c->loss_d, 16);
-    stage_mark(c);   // start of loss_fwd_bwd
+    stage_mark(c, S_LOSS);
     launch_ssim(c->stream, p.H, p.W, P<float>(c->out_img), a->gt, a->ssim_weight, a->loss_inv_n,
                 P<float>(c->hbuf), P<float>(c->dbuf), P<float>(c->v_rendered),
                 P<float>(c->loss_part), P<float>(c->loss_d));
-    stage_mark(c);   // start of rast_bwd
-    launch_raster_bwd(c->stream, p, c->meta.n_items, items(c), P<int>(c->tile_bins), packed(c),
+    stage_mark(c, S_RBWD);
+    launch_raster_bwd(c->stream, p, c->max_items, P<Meta>(c->meta_d), items(c),
+                      P<int>(c->tile_bins), packed(c),
                       P<float>(c->final_T), P<int>(c->final_idx), chunks(c),
                       P<float>(c->v_rendered), P<float>(c->gacc));
-    stage_mark(c);   // start of proj_sh_bwd_adam
     AdamHP hp;
     for (int g = 0; g < 6; ++g) { hp.step[g] = a->adam_step_sizes[g]; hp.bc2[g] = a->adam_bc2_sqrts[g]; }
     hp.b1 = a->adam_beta1;
     hp.b2 = a->adam_beta2;
     hp.eps = a->adam_eps;
     GaussOut go = gauss_out(c);
+    stage_mark(c, S_SHADAM);
     launch_sh_rest_adam(c->stream, p, a->r.means3d, go.radii, P<float>(c->gacc),
                         a->adam_params[4], a->adam_exp_avg[4], a->adam_exp_avg_sq[4], hp);
+    stage_mark(c, S_PBWD);
     launch_proj_bwd_adam(c->stream, p, a->adam_params, a->adam_exp_avg, a->adam_exp_avg_sq, hp, go,
                          P<float>(c->gacc), a->vis_counts, a->xys_grad_norm, a->max_2d_size,
                          a->inv_max_dim, a->v_mean3d_out, a->v_scale_out, a->v_quat_out);
-    stage_mark(c);   // end
+    stage_mark(c, S_END);
     c->have_bwd = true;
     if (radii_out && p.N > 0)
         HIP_TRY(hipMemcpyAsync(radii_out, c->radii.p, (size_t)p.N * 4, hipMemcpyDeviceToDevice,
@@ -539,24 +604,33 @@ int msplat_hip_densify(const MsplatDensifyArgs* a, int32_t* new_count) {
 }
 
 int msplat_hip_enable_stage_timing(int enable) {
-    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
-    g_ctx->timing = enable != 0;
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    c->timing = enable != 0;
+    c->n_marks[0] = c->n_marks[1] = 0;
+    for (int i = 0; i < kNumStages; ++i) { c->stage_sum[i] = 0.0; c->stage_cnt[i] = 0; }
+    c->calls = 0;
     return MSPLAT_OK;
 }
 
-int msplat_hip_drain_stage_times(double* ms, const char** names, int max_stages, int* n_stages) {
+int msplat_hip_drain_stage_times(double* ms, int64_t* counts, const char** names, int max_stages,
+                                 int* n_stages, int64_t* n_calls) {
     Ctx* c = g_ctx;
     if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
     HIP_TRY(hipStreamSynchronize(c->stream));
-    const int n = std::max(0, c->n_ev_used - 1);
-    int out = 0;
-    for (int i = 0; i < n && out < max_stages; ++i, ++out) {
-        float t = 0.f;
-        HIP_TRY(hipEventElapsedTime(&t, c->ev[i], c->ev[i + 1]));
-        if (ms) ms[out] = t;
-        if (names) names[out] = kStageNames[i];
+    stage_fold(c, c->cur);
+    stage_fold(c, c->cur ^ 1);
+    const int n = std::min(max_stages, kNumStages);
+    for (int i = 0; i < n; ++i) {
+        if (ms) ms[i] = c->stage_sum[i];
+        if (counts) counts[i] = c->stage_cnt[i];
+        if (names) names[i] = kStageNames[i];
+        c->stage_sum[i] = 0.0;
+        c->stage_cnt[i] = 0;
     }
-    if (n_stages) *n_stages = out;
+    if (n_stages) *n_stages = n;
+    if (n_calls) *n_calls = c->calls;
+    c->calls = 0;
     return MSPLAT_OK;
 }
 
@@ -564,6 +638,12 @@ int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes) {
     Ctx* c = g_ctx;
     if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
     if (!name || !nbytes) return fail(MSPLAT_ERR_ARG, "null args");
+    if (!c->meta_valid) {
+        HIP_TRY(hipMemcpyAsync(c->meta_h, c->meta_d.p, sizeof(Meta), hipMemcpyDeviceToHost, c->stream));
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        c->meta = *c->meta_h;
+        c->meta_valid = true;
+    }
     const size_t N = (size_t)c->last_N, T = (size_t)c->last_T, Px = (size_t)c->last_W * c->last_H;
     const size_t I = (size_t)std::max<int64_t>(c->meta.total_isect, 0);
     const std::string n(name);

@@ -15,8 +15,6 @@ namespace msp {
 
 namespace {
 
-constexpr int SB = 1024;   // elements per scan block (256 threads x 4)
-
 __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
     z += 0x9E3779B97F4A7C15ull;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -33,84 +31,6 @@ __global__ __launch_bounds__(256) void k_randn(float* __restrict__ dst, int64_t 
     const float u1 = (float)((a >> 40) + 1) * (1.0f / 16777216.0f);   // (0, 1]
     const float u2 = (float)(b >> 40) * (1.0f / 16777216.0f);         // [0, 1)
     dst[i] = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
-}
-
-__device__ __forceinline__ int block_sum_256(int v, int* sh) {
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const int t = sh[0] + sh[1] + sh[2] + sh[3];
-    __syncthreads();
-    return t;
-}
-
-__global__ __launch_bounds__(256) void k_block_reduce(const int* __restrict__ in, int64_t n,
-                                                      int* __restrict__ tot) {
-    __shared__ int sh[4];
-    const int64_t base = (int64_t)blockIdx.x * SB;
-    int v = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int64_t i = base + k * 256 + threadIdx.x;
-        if (i < n) v += in[i];
-    }
-    const int t = block_sum_256(v, sh);
-    if (threadIdx.x == 0) tot[blockIdx.x] = t;
-}
-
-// Exclusive scan of nb block totals in place (one workgroup).
-__global__ __launch_bounds__(1024) void k_scan_totals(int* __restrict__ tot, int nb) {
-    __shared__ int s[1024];
-    const int per = (nb + 1023) / 1024;
-    const int b = min((int)threadIdx.x * per, nb), e = min(b + per, nb);
-    int sum = 0;
-    for (int i = b; i < e; ++i) sum += tot[i];
-    s[threadIdx.x] = sum;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const int v = threadIdx.x >= (unsigned)off ? s[threadIdx.x - off] : 0;
-        __syncthreads();
-        s[threadIdx.x] += v;
-        __syncthreads();
-    }
-    int run = s[threadIdx.x] - sum;
-    for (int i = b; i < e; ++i) {
-        const int v = tot[i];
-        tot[i] = run;
-        run += v;
-    }
-}
-
-// Inclusive scan of each 1024-element block plus its offset.
-__global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
-                                                    int* __restrict__ out, int64_t n,
-                                                    const int* __restrict__ tot) {
-    __shared__ int s[SB];
-    const int64_t base = (int64_t)blockIdx.x * SB;
-    for (int k = threadIdx.x; k < SB; k += 256) {
-        const int64_t i = base + k;
-        s[k] = i < n ? in[i] : 0;
-    }
-    __syncthreads();
-    // each thread scans 4 consecutive values, then a 256-wide scan of thread sums
-    const int t = threadIdx.x;
-    int v0 = s[4 * t], v1 = v0 + s[4 * t + 1], v2 = v1 + s[4 * t + 2], v3 = v2 + s[4 * t + 3];
-    __shared__ int ts[256];
-    ts[t] = v3;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-        const int v = t >= off ? ts[t - off] : 0;
-        __syncthreads();
-        ts[t] += v;
-        __syncthreads();
-    }
-    const int pre = ts[t] - v3 + tot[blockIdx.x];
-    const int vals[4] = {v0, v1, v2, v3};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int64_t i = base + 4 * t + k;
-        if (i < n) out[i] = pre + vals[k];
-    }
 }
 
 __global__ __launch_bounds__(256) void k_classify(DensifyHP hp, const float* __restrict__ gnorm,
@@ -256,19 +176,9 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
 
-int64_t scan_block_count(int64_t n) { return (n + SB - 1) / SB; }
-
 void launch_randn(hipStream_t s, float* dst, int64_t n, uint64_t seed) {
     if (n <= 0) return;
     hipLaunchKernelGGL(k_randn, dim3(blocks_for(n)), dim3(256), 0, s, dst, n, seed);
-}
-
-void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* tot) {
-    if (n <= 0) return;
-    const int nb = (int)scan_block_count(n);
-    hipLaunchKernelGGL(k_block_reduce, dim3(nb), dim3(256), 0, s, in, n, tot);
-    hipLaunchKernelGGL(k_scan_totals, dim3(1), dim3(1024), 0, s, tot, nb);
-    hipLaunchKernelGGL(k_block_scan, dim3(nb), dim3(256), 0, s, in, out, n, (const int*)tot);
 }
 
 void launch_densify(hipStream_t s, const DensifyHP& hp, const float* gnorm, const float* vis,

@@ -57,8 +57,8 @@ struct Meta {
     int32_t max_count;
     int32_t n_items;
     int32_t n_chunked_tiles;   // tiles with more than one chunk
-    int32_t n_large;           // tiles sorted by the 16384-key LDS kernel
-    int32_t n_huge;            // tiles sorted in global memory
+    int32_t n_large;           // unused (0)
+    int32_t n_huge;            // unused (0)
     int32_t pad;
 };
 
@@ -69,8 +69,6 @@ struct TileLists {
     int* huge;
 };
 
-constexpr int SORT_SMALL = 2048;     // keys per tile sorted by the 16 KB LDS kernel
-constexpr int SORT_LARGE = 16384;    // keys per tile sorted by the 128 KB LDS kernel
 
 // Per-pixel chunk state, indexed by item * 256 + local pixel.
 struct ChunkBufs {
@@ -84,24 +82,40 @@ struct ChunkBufs {
 void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
                         const float* scales, const float* quats, const float* f_dc,
                         const float* f_rest, const float* opac_logits, GaussOut go,
-                        int* tile_cnt, float* gacc);
+                        uint32_t* dkey, uint32_t* dval, float* gacc);
 
-void launch_tile_scan(hipStream_t s, int T, const int* tile_cnt, int* tile_bins, Items it,
-                      TileLists tl, Meta* meta);
-void launch_build_items(hipStream_t s, int T, Items it);
-void launch_scatter(hipStream_t s, const CamParams& p, GaussOut go, const int* tile_bins,
-                    int* tile_cnt, uint64_t* keys);
-void launch_sort_pack(hipStream_t s, int T, const Meta& meta, const int* tile_bins,
-                      TileLists tl, uint64_t* keys, uint64_t* scratch, GaussOut go, Packed pk);
+// Scans and radix sort (radix.hip).
+int64_t scan_block_count(int64_t n);
+void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot);
+void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot);
+int64_t radix_temp_ints(int64_t n);
+bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
+                       int64_t n, int bits, int* temp);
 
-void launch_raster_fwd(hipStream_t s, const CamParams& p, int n_items, Items it,
-                       const int* tile_bins, Packed pk, float* final_T, int* final_idx,
+// Binning (binning.hip).  launch_depth_order leaves the intersection total in
+// meta->total_isect; launch_tile_lists needs it on the host.
+void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
+                        uint32_t* dval2, int* radix_temp, const int* tiles_hit, int* hits_sorted,
+                        int* eoff, int* scan_temp, Meta* meta, uint32_t** order_out);
+void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go,
+                       const uint32_t* order, const int* eoff, const int* hits, uint32_t* tkey,
+                       uint32_t* tval, uint32_t* tkey2, uint32_t* tval2, int* radix_temp,
+                       int* tstart, int* tend, int* tile_bins, Items it, TileLists tl, Meta* meta,
+                       Packed pk);
+
+// Upper bound of the number of (tile, chunk) work items for I intersections.
+inline int64_t items_bound(int64_t T, int64_t I) { return T + I / 512 + I / 2048 + 1; }
+
+// Rasterisation (raster.hip); grids are sized by items_bound / T and the
+// kernels read the exact counts from meta.
+void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
+                       Items it, const int* tile_bins, Packed pk, float* final_T, int* final_idx,
                        float* out_img, ChunkBufs cb);
-void launch_raster_merge(hipStream_t s, const CamParams& p, int n_chunked, const int* chunked,
+void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
                          Items it, float* final_T, int* final_idx, float* out_img, ChunkBufs cb,
                          bool with_suffix);
-void launch_raster_bwd(hipStream_t s, const CamParams& p, int n_items, Items it,
-                       const int* tile_bins, Packed pk, const float* final_T,
+void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
+                       Items it, const int* tile_bins, Packed pk, const float* final_T,
                        const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc);
 
 void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
@@ -137,8 +151,6 @@ struct DensifyHP {
     int fr;
 };
 void launch_randn(hipStream_t s, float* dst, int64_t n, uint64_t seed);
-void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot);
-int64_t scan_block_count(int64_t n);
 void launch_densify(hipStream_t s, const DensifyHP& hp, const float* gnorm, const float* vis,
                     const float* max2d, float* const bufs[6], float* const m[6],
                     float* const v[6], const float* rnd, int* split, int* dup, int* sp,

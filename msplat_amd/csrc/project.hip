@@ -1,15 +1,16 @@
 // project.hip — projection + SH colour of every gaussian (one thread each),
-// fused with the per-tile intersection count and the zeroing of the raster
-// gradient accumulators.
+// fused with the depth-key output for the binning and the zeroing of the
+// raster gradient accumulators.
 //
 // Follows project_and_sh_forward_kernel (.metal:1695-1787) and its helpers
 // quat_to_rotmat (.metal:111-131), scale_rot_to_cov3d (.metal:175-188),
 // project_cov3d_ewa (.metal:241-281), compute_cov2d_bounds (.metal:283-305),
 // project_pix (.metal:308-317), get_tile_bbox (.metal:57-87) and
-// sh_coeffs_to_color (.metal:587-654).  The counting half of
-// scatter_to_prealloc_bins (.metal:2046-2058) happens here; the sigmoid of
-// the opacity logit that the reference evaluates per intersection at pack
-// time (.metal:2133) is evaluated once per gaussian here, same formula.
+// sh_coeffs_to_color (.metal:587-654).  It also writes the depth sort key
+// (depth bits, or 0xFFFFFFFF when culled) and value (the id) for the binning;
+// the sigmoid of the opacity logit that the reference evaluates per
+// intersection at pack time (.metal:2133) is evaluated once per gaussian
+// here, same formula.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -84,13 +85,15 @@ __global__ __launch_bounds__(256) void k_project_fwd(
     CamParams p, const float* __restrict__ means, const float* __restrict__ scales,
     const float* __restrict__ quats, const float* __restrict__ f_dc,
     const float* __restrict__ f_rest, const float* __restrict__ opac_logits, GaussOut go,
-    int* __restrict__ tile_cnt, float* __restrict__ gacc) {
+    uint32_t* __restrict__ dkey, uint32_t* __restrict__ dval, float* __restrict__ gacc) {
     const int g = blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= p.N) return;
 #pragma unroll
     for (int q = 0; q < 9; ++q) gacc[(size_t)g * 9 + q] = 0.f;
     go.radii[g] = 0;
     go.tiles_hit[g] = 0;
+    dkey[g] = 0xFFFFFFFFu;
+    dval[g] = (uint32_t)g;
 
     const V3 pw{means[3 * g], means[3 * g + 1], means[3 * g + 2]};
     const V3 pv = xf4x3(p.vm, pw);
@@ -162,9 +165,7 @@ __global__ __launch_bounds__(256) void k_project_fwd(
     sh_color(p.dtu, dir, f_dc + 3 * (size_t)g, f_rest + (size_t)p.rest_per * g, col);
     go.conic[g] = make_float4(ca, cb, cc, sigmoid(opac_logits[g]));
     go.rgb[g] = make_float4(col[0], col[1], col[2], 0.f);
-
-    for (int ty = y0; ty < y1; ++ty)
-        for (int tx = x0; tx < x1; ++tx) atomicAdd(&tile_cnt[ty * p.tbx + tx], 1);
+    dkey[g] = __float_as_uint(pv.z);
 }
 
 }  // namespace
@@ -172,11 +173,11 @@ __global__ __launch_bounds__(256) void k_project_fwd(
 void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
                         const float* scales, const float* quats, const float* f_dc,
                         const float* f_rest, const float* opac_logits, GaussOut go,
-                        int* tile_cnt, float* gacc) {
+                        uint32_t* dkey, uint32_t* dval, float* gacc) {
     if (p.N <= 0) return;
     const int blocks = (p.N + 255) / 256;
     hipLaunchKernelGGL(k_project_fwd, dim3(blocks), dim3(256), 0, s, p, means, scales, quats,
-                       f_dc, f_rest, opac_logits, go, tile_cnt, gacc);
+                       f_dc, f_rest, opac_logits, go, dkey, dval, gacc);
 }
 
 }  // namespace msp

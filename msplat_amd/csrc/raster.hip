@@ -58,7 +58,8 @@ __device__ __forceinline__ void item_range(const Items& it, const int* tile_bins
 }
 
 __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float bg0, float bg1,
-                                                    float bg2, Items it,
+                                                    float bg2, const Meta* __restrict__ meta,
+                                                    Items it,
                                                     const int* __restrict__ tile_bins, Packed pk,
                                                     float* __restrict__ final_T,
                                                     int* __restrict__ final_idx,
@@ -67,6 +68,7 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
     __shared__ float4 s_col[256];
     __shared__ float s_bl[256];
     const int item = blockIdx.x;
+    if (item >= meta->n_items) return;
     int t, K, cs, ce;
     item_range(it, tile_bins, item, t, K, cs, ce);
     const Px px = pixel_of(t, tbx, W, H);
@@ -133,11 +135,13 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
 
 __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, float bg0,
                                                       float bg1, float bg2,
+                                                      const Meta* __restrict__ meta,
                                                       const int* __restrict__ chunked, Items it,
                                                       float* __restrict__ final_T,
                                                       int* __restrict__ final_idx,
                                                       float* __restrict__ out_img, ChunkBufs cb,
                                                       int with_suffix) {
+    if ((int)blockIdx.x >= meta->n_chunked_tiles) return;
     const int t = chunked[blockIdx.x];
     const int K = it.tile_K[t], i0 = it.tile_item0[t];
     const int lp = threadIdx.x, lx = lp & 15, ly = lp >> 4;
@@ -188,7 +192,8 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
 }
 
 __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float bg0, float bg1,
-                                                    float bg2, Items it,
+                                                    float bg2, const Meta* __restrict__ meta,
+                                                    Items it,
                                                     const int* __restrict__ tile_bins, Packed pk,
                                                     const float* __restrict__ final_T,
                                                     const int* __restrict__ final_idx,
@@ -200,6 +205,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     __shared__ int s_id[256];
     __shared__ int s_max;
     const int item = blockIdx.x;
+    if (item >= meta->n_items) return;
     int t, K, cs, ce;
     item_range(it, tile_bins, item, t, K, cs, ce);
     const Px px = pixel_of(t, tbx, W, H);
@@ -315,29 +321,31 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
 
 }  // namespace
 
-void launch_raster_fwd(hipStream_t s, const CamParams& p, int n_items, Items it,
-                       const int* tile_bins, Packed pk, float* final_T, int* final_idx,
+void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
+                       Items it, const int* tile_bins, Packed pk, float* final_T, int* final_idx,
                        float* out_img, ChunkBufs cb) {
-    if (n_items <= 0) return;
-    hipLaunchKernelGGL(k_raster_fwd, dim3(n_items), dim3(256), 0, s, p.W, p.H, p.tbx, p.bg[0],
-                       p.bg[1], p.bg[2], it, tile_bins, pk, final_T, final_idx, out_img, cb);
+    if (max_items <= 0) return;
+    hipLaunchKernelGGL(k_raster_fwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
+                       p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx,
+                       out_img, cb);
 }
 
-void launch_raster_merge(hipStream_t s, const CamParams& p, int n_chunked, const int* chunked,
+void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
                          Items it, float* final_T, int* final_idx, float* out_img, ChunkBufs cb,
                          bool with_suffix) {
-    if (n_chunked <= 0) return;
-    hipLaunchKernelGGL(k_raster_merge, dim3(n_chunked), dim3(256), 0, s, p.W, p.H, p.tbx, p.bg[0],
-                       p.bg[1], p.bg[2], chunked, it, final_T, final_idx, out_img, cb,
+    const int T = p.tbx * p.tby;
+    hipLaunchKernelGGL(k_raster_merge, dim3(T), dim3(256), 0, s, p.W, p.H, p.tbx, p.bg[0], p.bg[1],
+                       p.bg[2], meta, chunked, it, final_T, final_idx, out_img, cb,
                        with_suffix ? 1 : 0);
 }
 
-void launch_raster_bwd(hipStream_t s, const CamParams& p, int n_items, Items it,
-                       const int* tile_bins, Packed pk, const float* final_T,
+void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
+                       Items it, const int* tile_bins, Packed pk, const float* final_T,
                        const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc) {
-    if (n_items <= 0) return;
-    hipLaunchKernelGGL(k_raster_bwd, dim3(n_items), dim3(256), 0, s, p.W, p.H, p.tbx, p.bg[0],
-                       p.bg[1], p.bg[2], it, tile_bins, pk, final_T, final_idx, cb, v_out, gacc);
+    if (max_items <= 0) return;
+    hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
+                       p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx, cb,
+                       v_out, gacc);
 }
 
 }  // namespace msp

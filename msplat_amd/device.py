@@ -83,6 +83,25 @@ class DeviceGaussians:
         z = lambda: T.zeros(cap, dtype=T.float32, device="cuda")
         return DeviceGaussians(bufs, ms, vs, z(), z(), z(), n, cap, sh_degree)
 
+    @staticmethod
+    def from_tensors(params, sh_degree: int, capacity: Optional[int] = None) -> "DeviceGaussians":
+        """Same as from_arrays for tensors already on the device."""
+        T = torch()
+        init()
+        n = int(params[0].shape[0])
+        cap = max(capacity or n, n, 1)
+        bufs, ms, vs = [], [], []
+        for a in params:
+            shape = (cap,) + tuple(a.shape[1:])
+            b = T.zeros(shape, dtype=T.float32, device="cuda")
+            if n:
+                b[:n].copy_(a)
+            bufs.append(b)
+            ms.append(T.zeros(shape, dtype=T.float32, device="cuda"))
+            vs.append(T.zeros(shape, dtype=T.float32, device="cuda"))
+        z = lambda: T.zeros(cap, dtype=T.float32, device="cuda")
+        return DeviceGaussians(bufs, ms, vs, z(), z(), z(), n, cap, sh_degree)
+
     def view(self, i: int):
         return self.bufs[i][: self.n]
 

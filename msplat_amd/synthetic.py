@@ -184,3 +184,29 @@ def make_targets(scene: Scene, render: Callable[[Scene, Camera], np.ndarray], se
         img = render(jit, cam)
         out.append((img + st.normal(img.size, 0.0, noise).reshape(img.shape)).astype(np.float32))
     return out
+
+
+def device_randn(n: int, seed: int, mean: float = 0.0, std: float = 1.0):
+    """n normals on cuda:0 from the library's counter-based generator."""
+    from . import _abi, device
+    T = device.torch()
+    x = T.empty(n, dtype=T.float32, device="cuda")
+    if n:
+        _abi.check(device.init().msplat_hip_randn(device.ptr(x), n, seed & 0xFFFFFFFFFFFFFFFF))
+    return x.mul_(std).add_(mean)
+
+
+def device_cloud(n: int, degree: int, seed: int):
+    """Config-2/3/5 gaussians generated on the GPU: means N(0,1.5^2) clipped to
+    +-4, log-scales N(-4.5,0.5), quats normalize(N(0,1)^4), opacity logits
+    N(0,1), DC N(0,0.3), higher bands N(0,0.05).  Returns 6 device tensors."""
+    nb = (degree + 1) ** 2 - 1
+    k = lambda i: (seed << 8) + i
+    means = device_randn(3 * n, k(0), 0.0, 1.5).clamp_(-4.0, 4.0).view(n, 3)
+    scales = device_randn(3 * n, k(1), -4.5, 0.5).view(n, 3)
+    quats = device_randn(4 * n, k(2)).view(n, 4)
+    quats /= quats.norm(dim=1, keepdim=True)
+    opac = device_randn(n, k(3)).view(n, 1)
+    f_dc = device_randn(3 * n, k(4), 0.0, 0.3).view(n, 3)
+    f_rest = device_randn(nb * 3 * n, k(5), 0.0, 0.05).view(n, nb, 3)
+    return [means, scales, quats.contiguous(), f_dc, f_rest, opac]
