@@ -58,6 +58,24 @@ __device__ __forceinline__ float exp_cw(float x) {
     return p * __int_as_float((ki + 127) << 23);
 }
 
+// exp_cw without the range branches, for arguments known to lie in
+// [-87, 88] or be NaN (the raster's -sigma in (-5.55, 0]): same bits as exp_cw.
+__device__ __forceinline__ float exp_cw_core(float x) {
+    const float k = rintf(x * 1.44269504f);
+    float r = fmaf(k, -0.693145751953125f, x);
+    r = fmaf(k, -1.42860682e-6f, r);
+    float p = 1.98412698e-4f;
+    p = fmaf(p, r, 1.38888889e-3f);
+    p = fmaf(p, r, 8.33333333e-3f);
+    p = fmaf(p, r, 4.16666667e-2f);
+    p = fmaf(p, r, 1.66666667e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const int ki = (int)k;
+    return p * __int_as_float((ki + 127) << 23);
+}
+
 __device__ __forceinline__ float sigmoid(float o) { return 1.f / (1.f + exp_cw(-o)); }
 
 // float -> int with the operand clamped to [-2^30, 2^30] first: one defined
@@ -103,6 +121,40 @@ __device__ __forceinline__ float wave_sum(float v) {
     const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
     const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
     return (r0 + r1) + (r2 + r3);
+}
+
+// Transposed sum over the 64 lanes of eight values v[0..7]: afterwards lane l
+// holds the total of value  4 * ((l >> 3) & 1) + {0, 2, 1, 3}[l >> 4].
+// Halves and rows are exchanged with gfx950's permlane32/16 swaps, the rest
+// with row DPP; about 21 VALU operations for the eight sums.  All lanes must
+// be active.
+__device__ __forceinline__ float swap_add32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap_add16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float wave_sum8_transposed(const float* v, int lane) {
+    const float r0 = swap_add32(v[0], v[1]);
+    const float r1 = swap_add32(v[2], v[3]);
+    const float r2 = swap_add32(v[4], v[5]);
+    const float r3 = swap_add32(v[6], v[7]);
+    const float s0 = swap_add16(r0, r1);
+    const float s1 = swap_add16(r2, r3);
+    const float t0 = s0 + dpp<0x128>(s0);   // row_ror:8 == lane ^ 8
+    const float t1 = s1 + dpp<0x128>(s1);
+    float u = (lane & 8) ? t1 : t0;
+    u += dpp<0xB1>(u);                      // quad_perm [1,0,3,2]
+    u += dpp<0x4E>(u);                      // quad_perm [2,3,0,1]
+    const float from_lo = dpp<0x124>(u);    // row_ror:4  -> value of lane (l - 4) mod 16
+    const float from_hi = dpp<0x12C>(u);    // row_ror:12 -> value of lane (l + 4) mod 16
+    return u + ((lane & 4) ? from_lo : from_hi);
+}
+__device__ __forceinline__ int sum8_value_of_lane(int lane) {
+    const int row = lane >> 4;
+    return 4 * ((lane >> 3) & 1) + (row == 1 ? 2 : row == 2 ? 1 : row);
 }
 
 __device__ __forceinline__ int wave_max_i(int v) {

@@ -14,10 +14,12 @@
 //   prefix/sfx   compute_chunk_prefix_suffix_kernel (.metal:2804-2840)
 //   backward     rasterize_backward_kernel (.metal:898-1099) and
 //                rasterize_backward_chunked_kernel (.metal:2844-3031)
-// with these MI355X differences: a workgroup-wide vote stops the forward
-// once every pixel of the item has terminated; the backward reduces each
-// gaussian's per-pixel terms across the 64 lanes of a wave (DPP + readlane)
-// and nine lanes issue one float atomic each.
+// with these MI355X differences: each loaded entry carries a conservative
+// mask of the 8x8 wave quadrants it can reach and a wave walks only the
+// entries of its own quadrant; a workgroup-wide vote stops the forward once
+// every pixel of the item has terminated; the backward reduces each
+// gaussian's per-pixel terms across the 64 lanes of a wave with a transposed
+// permlane/DPP reduction and nine lanes issue one float atomic each.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -57,6 +59,29 @@ __device__ __forceinline__ void item_range(const Items& it, const int* tile_bins
     }
 }
 
+// Conservative quadrant mask of one entry: bit w is set when the entry can
+// reach alpha >= 1/255 at a pixel of wave w's 8x8 quadrant of the tile at
+// (tx0, ty0).  The reach is the ellipse sigma < min(5.55, ln(255 o)) with
+// margins; entries outside a quadrant are exactly the ones the per-pixel
+// tests would skip there, so culling them changes no result.
+__device__ __forceinline__ int quad_mask(float x, float y, float a, float b, float c, float o,
+                                         int tx0, int ty0) {
+    if (!(o >= 0.0039f)) return o == o ? 0 : 0xF;      // alpha <= o < 1/255 everywhere
+    const float det = a * c - b * b;
+    if (!(det > 0.f) || !(fabsf(x) < 1e30f) || !(fabsf(y) < 1e30f)) return 0xF;
+    const float thr = fminf(5.55f, __logf(255.f * o) + 0.05f);
+    const float hx = sqrtf(2.f * thr * c / det) * 1.002f + 0.1f;
+    const float hy = sqrtf(2.f * thr * a / det) * 1.002f + 0.1f;
+    if (!(hx < 1e30f) || !(hy < 1e30f)) return 0xF;
+    int m = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float qx0 = (float)(tx0 + (q & 1) * 8), qy0 = (float)(ty0 + (q >> 1) * 8);
+        if (x + hx >= qx0 && x - hx <= qx0 + 7.f && y + hy >= qy0 && y - hy <= qy0 + 7.f) m |= 1 << q;
+    }
+    return m;
+}
+
 __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float bg0, float bg1,
                                                     float bg2, const Meta* __restrict__ meta,
                                                     Items it,
@@ -67,52 +92,64 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
     __shared__ float4 s_geo[256];
     __shared__ float4 s_col[256];
     __shared__ float s_bl[256];
+    __shared__ int s_mask[256];
     const int item = blockIdx.x;
     if (item >= meta->n_items) return;
     int t, K, cs, ce;
     item_range(it, tile_bins, item, t, K, cs, ce);
     const Px px = pixel_of(t, tbx, W, H);
     const float fx = (float)px.j, fy = (float)px.i;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tx0 = (t % tbx) * BLOCK, ty0 = (t / tbx) * BLOCK;
 
     float T = 1.f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
     int last = cs - 1;
     bool done = !px.inside;
-    const int tid = threadIdx.x;
     for (int b = cs; b < ce; b += 256) {
         if (__syncthreads_and(done)) break;
         const int idx = b + tid;
+        int mask = 0;
         if (idx < ce) {
+            const float4 g = pk.geo[idx];
             float4 c = pk.col[idx];
+            mask = quad_mask(g.x, g.y, g.z, g.w, c.x, c.y, tx0, ty0);
             c.z = fmaxf(c.z + 0.5f, 0.f);
             c.w = fmaxf(c.w + 0.5f, 0.f);
-            s_geo[tid] = pk.geo[idx];
+            s_geo[tid] = g;
             s_col[tid] = c;
             s_bl[tid] = fmaxf(pk.bl[idx] + 0.5f, 0.f);
         }
+        s_mask[tid] = mask;
         __syncthreads();
-        if (!done) {
-            const int nb = min(256, ce - b);
-            for (int q = 0; q < nb; ++q) {
-                const float4 g = s_geo[q];
-                const float4 c = s_col[q];
+        const int nb = min(256, ce - b);
+        for (int ch = 0; ch < nb; ch += 64) {
+            const int q = ch + lane;
+            uint64_t m = __ballot(q < nb && ((s_mask[q] >> w) & 1));
+            while (m) {
+                const int qq = ch + __builtin_ctzll(m);
+                m &= m - 1;
+                if (done) continue;
+                const float4 g = s_geo[qq];
+                const float4 c = s_col[qq];
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-                if (sigma < 0.f || sigma >= 5.55f) continue;
-                const float alpha = fminf(0.999f, c.y * exp_cw(-sigma));
-                if (alpha < 1.f / 255.f) continue;
+                const bool in_range = !(sigma < 0.f || sigma >= 5.55f);
+                const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
+                if (!in_range || alpha < 1.f / 255.f) continue;
                 const float nT = T * (1.f - alpha);
                 if (nT <= 1e-4f) {
-                    last = b + q - 1;
+                    last = b + qq - 1;
                     done = true;
-                    break;
+                    continue;
                 }
                 const float vis = alpha * T;
                 C0 = fmaf(c.z, vis, C0);
                 C1 = fmaf(c.w, vis, C1);
-                C2 = fmaf(s_bl[q], vis, C2);
+                C2 = fmaf(s_bl[qq], vis, C2);
                 T = nT;
-                last = b + q;
+                last = b + qq;
             }
+            if (__ballot(!done) == 0) break;
         }
     }
     if (!px.inside) return;
@@ -203,6 +240,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     __shared__ float4 s_col[256];
     __shared__ float s_bl[256];
     __shared__ int s_id[256];
+    __shared__ int s_mask[256];
     __shared__ int s_max;
     const int item = blockIdx.x;
     if (item >= meta->n_items) return;
@@ -210,7 +248,8 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     item_range(it, tile_bins, item, t, K, cs, ce);
     const Px px = pixel_of(t, tbx, W, H);
     const float fx = (float)px.j, fy = (float)px.i;
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tx0 = (t % tbx) * BLOCK, ty0 = (t / tbx) * BLOCK;
 
     float T = 1.f, Tfin = 1.f, B0 = 0.f, B1 = 0.f, B2 = 0.f, vo0 = 0.f, vo1 = 0.f, vo2 = 0.f;
     int bf = cs - 1;
@@ -243,77 +282,75 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     for (int top = hi; top >= cs; top -= 256) {
         __syncthreads();
         const int idx = top - tid;
+        int mask = 0;
         if (idx >= cs) {
-            s_geo[tid] = pk.geo[idx];
-            s_col[tid] = pk.col[idx];
+            const float4 g = pk.geo[idx];
+            const float4 c = pk.col[idx];
+            mask = quad_mask(g.x, g.y, g.z, g.w, c.x, c.y, tx0, ty0);
+            s_geo[tid] = g;
+            s_col[tid] = c;
             s_bl[tid] = pk.bl[idx];
             s_id[tid] = pk.ids[idx];
         }
+        s_mask[tid] = mask;
         __syncthreads();
         const int nb = min(256, top - cs + 1);
-        for (int q = max(0, top - wave_bf); q < nb; ++q) {
-            const int e_idx = top - q;
-            const float4 g = s_geo[q];
-            const float4 c = s_col[q];
-            const float braw = s_bl[q];
-            const float dx = g.x - fx, dy = g.y - fy;
-            bool valid = px.inside && e_idx <= bf;
-            float alpha = 0.f;
-            if (valid) {
+        const int q0 = max(0, top - wave_bf);
+        for (int ch = (q0 / 64) * 64; ch < nb; ch += 64) {
+            const int q = ch + lane;
+            uint64_t m = __ballot(q >= q0 && q < nb && ((s_mask[q] >> w) & 1));
+            while (m) {
+                const int qq = ch + __builtin_ctzll(m);
+                m &= m - 1;
+                const int e_idx = top - qq;
+                const float4 g = s_geo[qq];
+                const float4 c = s_col[qq];
+                const float braw = s_bl[qq];
+                const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-                if (sigma < 0.f || sigma >= 5.55f) {
-                    valid = false;
-                } else {
-                    alpha = fminf(0.999f, c.y * exp_cw(-sigma));
-                    if (alpha < 1.f / 255.f) valid = false;
+                const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
+                const bool valid = px.inside && e_idx <= bf && !(sigma < 0.f || sigma >= 5.55f) &&
+                                   !(alpha < 1.f / 255.f);
+                if (__ballot(valid) == 0) continue;
+                float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                float vop = 0.f;
+                if (valid && alpha < 0.999f) {
+                    const float ra = 1.f / (1.f - alpha);
+                    T *= ra;
+                    const float fac = alpha * T;
+                    v[5] = fac * vo0;
+                    v[6] = fac * vo1;
+                    v[7] = fac * vo2;
+                    const float r0 = fmaxf(c.z + 0.5f, 0.f), r1 = fmaxf(c.w + 0.5f, 0.f),
+                                r2 = fmaxf(braw + 0.5f, 0.f);
+                    const float t0 = fmaf(r0, T, fmaf(-B0, ra, -ra * tb0));
+                    const float t1 = fmaf(r1, T, fmaf(-B1, ra, -ra * tb1));
+                    const float t2 = fmaf(r2, T, fmaf(-B2, ra, -ra * tb2));
+                    const float v_alpha = 0.f + (t0 * vo0 + t1 * vo1 + t2 * vo2);
+                    B0 = fmaf(r0, fac, B0);
+                    B1 = fmaf(r1, fac, B1);
+                    B2 = fmaf(r2, fac, B2);
+                    const float v_sigma = -alpha * v_alpha;
+                    const float hv = 0.5f * v_sigma;
+                    v[2] = hv * (dx * dx);
+                    v[3] = hv * (dx * dy);
+                    v[4] = hv * (dy * dy);
+                    v[0] = v_sigma * fmaf(g.z, dx, g.w * dy);
+                    v[1] = v_sigma * fmaf(g.w, dx, c.x * dy);
+                    vop = -v_sigma * (1.f - c.y);
                 }
-            }
-            if (__ballot(valid) == 0) continue;
-            float vx = 0.f, vy = 0.f, va = 0.f, vb = 0.f, vc = 0.f, vr = 0.f, vg = 0.f, vbl = 0.f,
-                  vop = 0.f;
-            if (valid && alpha < 0.999f) {
-                const float ra = 1.f / (1.f - alpha);
-                T *= ra;
-                const float fac = alpha * T;
-                vr = fac * vo0;
-                vg = fac * vo1;
-                vbl = fac * vo2;
-                const float r0 = fmaxf(c.z + 0.5f, 0.f), r1 = fmaxf(c.w + 0.5f, 0.f),
-                            r2 = fmaxf(braw + 0.5f, 0.f);
-                const float t0 = fmaf(r0, T, fmaf(-B0, ra, -ra * tb0));
-                const float t1 = fmaf(r1, T, fmaf(-B1, ra, -ra * tb1));
-                const float t2 = fmaf(r2, T, fmaf(-B2, ra, -ra * tb2));
-                const float v_alpha = 0.f + (t0 * vo0 + t1 * vo1 + t2 * vo2);
-                B0 = fmaf(r0, fac, B0);
-                B1 = fmaf(r1, fac, B1);
-                B2 = fmaf(r2, fac, B2);
-                const float v_sigma = -alpha * v_alpha;
-                const float hv = 0.5f * v_sigma;
-                va = hv * (dx * dx);
-                vb = hv * (dx * dy);
-                vc = hv * (dy * dy);
-                vx = v_sigma * fmaf(g.z, dx, g.w * dy);
-                vy = v_sigma * fmaf(g.w, dx, c.x * dy);
-                vop = -v_sigma * (1.f - c.y);
-            }
-            const float s0 = wave_sum(vx), s1 = wave_sum(vy), s2 = wave_sum(va), s3 = wave_sum(vb),
-                        s4 = wave_sum(vc), s5 = wave_sum(vr), s6 = wave_sum(vg),
-                        s7 = wave_sum(vbl), s8 = wave_sum(vop);
-            if (lane < 9) {
-                float val = s8;
-                bool ok = true;
-                switch (lane) {
-                    case 0: val = s0; break;
-                    case 1: val = s1; break;
-                    case 2: val = s2; break;
-                    case 3: val = s3; break;
-                    case 4: val = s4; break;
-                    case 5: val = s5; ok = c.z + 0.5f >= 0.f; break;
-                    case 6: val = s6; ok = c.w + 0.5f >= 0.f; break;
-                    case 7: val = s7; ok = braw + 0.5f >= 0.f; break;
-                    default: break;
+                const float u = wave_sum8_transposed(v, lane);
+                const float s8 = wave_sum(vop);
+                // lanes 0, 8, ..., 56 hold the eight sums; lane 1 adds the ninth
+                int k = -1;
+                if ((lane & 7) == 0) k = sum8_value_of_lane(lane);
+                else if (lane == 1) k = 8;
+                if (k >= 0) {
+                    const bool ok = k == 5 ? c.z + 0.5f >= 0.f
+                                  : k == 6 ? c.w + 0.5f >= 0.f
+                                  : k == 7 ? braw + 0.5f >= 0.f : true;
+                    if (ok) atomicAdd(&gacc[(size_t)s_id[qq] * 9 + k], k == 8 ? s8 : u);
                 }
-                if (ok) atomicAdd(&gacc[(size_t)s_id[q] * 9 + lane], val);
             }
         }
     }
