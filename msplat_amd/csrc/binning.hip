@@ -46,9 +46,9 @@ __global__ __launch_bounds__(256) void k_emit(int N, int tbx, int tby, GaussOut 
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= N || hits[r] == 0) return;
     const int g = (int)order[r];
-    const float2 xy = go.xy[g], ext = go.aabb[g];
+    const float4 r0 = go.rec[4 * (size_t)g], r2 = go.rec[4 * (size_t)g + 2];
     int x0, y0, x1, y1;
-    tile_rect(xy.x, xy.y, ext.x, ext.y, tbx, tby, x0, y0, x1, y1);
+    tile_rect(r0.x, r0.y, r2.y, r2.z, tbx, tby, x0, y0, x1, y1);
     int e = eoff[r];
     for (int ty = y0; ty < y1; ++ty)
         for (int tx = x0; tx < x1; ++tx, ++e) {
@@ -140,13 +140,13 @@ __global__ __launch_bounds__(256) void k_pack(int64_t I, const uint32_t* __restr
     const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= I) return;
     const int g = (int)tval[p];
-    const float2 xy = go.xy[g];
-    const float4 c = go.conic[g];
-    const float4 rgb = go.rgb[g];
+    const float4* rec = go.rec + 4 * (size_t)g;
+    const float4 r0 = rec[0], r1 = rec[1];
+    const float bl = rec[2].x;
     pk.ids[p] = g;
-    pk.geo[p] = make_float4(xy.x, xy.y, c.x, c.y);
-    pk.col[p] = make_float4(c.z, c.w, rgb.x, rgb.y);
-    pk.bl[p] = rgb.z;
+    pk.geo[p] = r0;
+    pk.col[p] = r1;
+    pk.bl[p] = bl;
 }
 
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }

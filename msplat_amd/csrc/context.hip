@@ -56,7 +56,7 @@ struct Ctx {
     int64_t calls = 0;
 
     // per gaussian
-    Buf xy, conic, rgb, depth, radii, aabb, tiles_hit, gacc;
+    Buf rec, radii, tiles_hit, gacc;
     Buf dkey, dval, dkey2, dval2, hits, eoff, dtemp, stemp;
     // per tile
     Buf tstart, tend, tile_bins, tile_K, tile_item0, l_chunked;
@@ -133,7 +133,7 @@ template <typename T>
 T* P(Buf& b) { return reinterpret_cast<T*>(b.p); }
 
 void free_all(Ctx* c) {
-    Buf* bufs[] = {&c->xy, &c->conic, &c->rgb, &c->depth, &c->radii, &c->aabb, &c->tiles_hit,
+    Buf* bufs[] = {&c->rec, &c->radii, &c->tiles_hit,
                    &c->gacc, &c->dkey, &c->dval, &c->dkey2, &c->dval2, &c->hits, &c->eoff,
                    &c->dtemp, &c->stemp, &c->tstart, &c->tend, &c->tile_bins, &c->tile_K,
                    &c->tile_item0, &c->l_chunked, &c->tkey, &c->tval, &c->tkey2, &c->tval2,
@@ -156,12 +156,8 @@ void free_all(Ctx* c) {
 
 GaussOut gauss_out(Ctx* c) {
     GaussOut go;
-    go.xy = P<float2>(c->xy);
-    go.conic = P<float4>(c->conic);
-    go.rgb = P<float4>(c->rgb);
-    go.depth = P<float>(c->depth);
+    go.rec = P<float4>(c->rec);
     go.radii = P<int>(c->radii);
-    go.aabb = P<float2>(c->aabb);
     go.tiles_hit = P<int>(c->tiles_hit);
     return go;
 }
@@ -275,12 +271,8 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
     const int N = p.N, T = p.tbx * p.tby;
     const size_t Px = (size_t)p.W * p.H;
     const size_t Nn = (size_t)std::max(N, 1);
-    ENSURE(c->xy, Nn * 8);
-    ENSURE(c->conic, Nn * 16);
-    ENSURE(c->rgb, Nn * 16);
-    ENSURE(c->depth, Nn * 4);
+    ENSURE(c->rec, Nn * 64);
     ENSURE(c->radii, Nn * 4);
-    ENSURE(c->aabb, Nn * 8);
     ENSURE(c->tiles_hit, Nn * 4);
     ENSURE(c->gacc, Nn * 36);
     ENSURE(c->dkey, Nn * 4);
@@ -650,8 +642,7 @@ int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes) {
     // Direct copies.
     struct D { const char* name; Buf* b; size_t bytes; };
     const D direct[] = {
-        {"xys", &c->xy, N * 8},           {"depths", &c->depth, N * 4},
-        {"radii", &c->radii, N * 4},      {"aabb", &c->aabb, N * 8},
+        {"radii", &c->radii, N * 4},
         {"num_tiles_hit", &c->tiles_hit, N * 4}, {"tile_bins", &c->tile_bins, T * 8},
         {"gaussian_ids", &c->pk_ids, I * 4}, {"final_Ts", &c->final_T, Px * 4},
         {"final_index", &c->final_idx, Px * 4}, {"out_img", &c->out_img, Px * 12},
@@ -671,26 +662,24 @@ int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes) {
         return MSPLAT_OK;
     }
     // Repacked views of the internal layouts.
-    auto fetch4 = [&](Buf& b, std::vector<float>& h) -> int {
-        h.resize(N * 4);
-        if (N == 0) return MSPLAT_OK;
-        HIP_TRY(hipMemcpyAsync(h.data(), b.p, N * 16, hipMemcpyDeviceToHost, c->stream));
-        HIP_TRY(hipStreamSynchronize(c->stream));
-        return MSPLAT_OK;
-    };
     std::vector<float> h;
-    if (n == "conics" || n == "colors" || n == "opacity_sigmoid") {
-        const bool op = n == "opacity_sigmoid";
-        const size_t per = op ? 1 : 3;
-        *nbytes = N * per * 4;
+    // Fields of the 64-byte projection records: (name, floats, record offsets).
+    struct F { const char* name; int per; int off[3]; };
+    const F fields[] = {{"xys", 2, {0, 1, 0}},       {"conics", 3, {2, 3, 4}},
+                        {"opacity_sigmoid", 1, {5, 0, 0}}, {"colors", 3, {6, 7, 8}},
+                        {"aabb", 2, {9, 10, 0}},    {"depths", 1, {11, 0, 0}}};
+    for (const F& f : fields) {
+        if (n != f.name) continue;
+        *nbytes = N * f.per * 4;
         if (!dst) return MSPLAT_OK;
-        int r = fetch4(n == "colors" ? c->rgb : c->conic, h);
-        if (r != MSPLAT_OK) return r;
-        float* o = static_cast<float*>(dst);
-        for (size_t g = 0; g < N; ++g) {
-            if (op) o[g] = h[4 * g + 3];
-            else for (int k = 0; k < 3; ++k) o[3 * g + k] = h[4 * g + k];
+        h.resize(N * 16);
+        if (N) {
+            HIP_TRY(hipMemcpyAsync(h.data(), c->rec.p, N * 64, hipMemcpyDeviceToHost, c->stream));
+            HIP_TRY(hipStreamSynchronize(c->stream));
         }
+        float* o = static_cast<float*>(dst);
+        for (size_t g = 0; g < N; ++g)
+            for (int k = 0; k < f.per; ++k) o[g * f.per + k] = h[16 * g + f.off[k]];
         return MSPLAT_OK;
     }
     const int q0 = n == "v_xy" ? 0 : n == "v_conic" ? 2 : n == "v_rgb" ? 5 : n == "v_opacity" ? 8 : -1;

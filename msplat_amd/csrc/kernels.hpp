@@ -24,14 +24,15 @@ struct CamParams {
     float bg[3];
 };
 
-// Per-gaussian outputs of the projection (internal layout).
+// Per-gaussian outputs of the projection (internal layout).  One 64-byte
+// record per gaussian so that the per-intersection gathers touch one cache
+// line:  rec[4g+0] = (x, y, conic_a, conic_b)
+//        rec[4g+1] = (conic_c, sigmoid(opacity), r, g)   raw SH colour
+//        rec[4g+2] = (b, extent_x, extent_y, depth)
+//        rec[4g+3] = unused
 struct GaussOut {
-    float2* xy;          // pixel centre
-    float4* conic;       // (a, b, c, sigmoid(opacity))
-    float4* rgb;         // (r, g, b, 0) raw SH colour (no +0.5)
-    float* depth;
+    float4* rec;
     int* radii;
-    float2* aabb;        // per-axis pixel extents
     int* tiles_hit;
 };
 

@@ -99,6 +99,10 @@ __device__ __forceinline__ float sh_basis(int b, float x, float y, float z) {
     }
 }
 
+// Element-parallel Adam on features_rest, four consecutive floats per thread
+// (16-byte loads and stores).  Elements of culled gaussians and of bands above
+// degrees_to_use keep their values (the reference updates visible gaussians'
+// used bands only, .metal:1846-1848, 1931-1985).
 __global__ __launch_bounds__(256) void k_sh_rest_adam(int64_t n, int rest_per, int n_used,
                                                       const float* __restrict__ means,
                                                       float cx, float cy, float cz,
@@ -107,20 +111,54 @@ __global__ __launch_bounds__(256) void k_sh_rest_adam(int64_t n, int rest_per, i
                                                       float* __restrict__ f_rest,
                                                       float* __restrict__ m, float* __restrict__ v,
                                                       AdamHP hp) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= n) return;
-    const int g = (int)(e / rest_per);
-    const int rem = (int)(e - (int64_t)g * rest_per);
-    const int b = rem / 3, c = rem - 3 * (rem / 3);
-    if (b >= n_used || radii[g] <= 0) return;
-    const float dx = means[3 * g] - cx, dy = means[3 * g + 1] - cy, dz = means[3 * g + 2] - cz;
-    const float inv = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
-    const float grad = sh_basis(b, dx * inv, dy * inv, dz * inv) * gacc[(size_t)g * 9 + 5 + c];
-    float p = f_rest[e], mm = m[e], vv = v[e];
-    adam_elem(p, mm, vv, grad, hp.step[4], hp.b1, hp.b2, hp.bc2[4], hp.eps);
-    f_rest[e] = p;
-    m[e] = mm;
-    v[e] = vv;
+    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (e0 >= n) return;
+    int g = (int)(e0 / rest_per);
+    int rem = (int)(e0 - (int64_t)g * rest_per);
+    const int cnt = (int)min((int64_t)4, n - e0);
+    // Gaussians covered by these elements (at most two: rest_per >= 9).
+    const int g_last = (int)((e0 + cnt - 1) / rest_per);
+    const bool vis0 = radii[g] > 0, vis1 = radii[g_last] > 0;
+    if (!vis0 && !vis1) return;
+    float pv[4], mv[4], vv[4];
+    const bool full = cnt == 4;
+    if (full) {
+        const float4 a = *reinterpret_cast<const float4*>(f_rest + e0);
+        const float4 b = *reinterpret_cast<const float4*>(m + e0);
+        const float4 c = *reinterpret_cast<const float4*>(v + e0);
+        pv[0] = a.x; pv[1] = a.y; pv[2] = a.z; pv[3] = a.w;
+        mv[0] = b.x; mv[1] = b.y; mv[2] = b.z; mv[3] = b.w;
+        vv[0] = c.x; vv[1] = c.y; vv[2] = c.z; vv[3] = c.w;
+    } else {
+        for (int k = 0; k < cnt; ++k) { pv[k] = f_rest[e0 + k]; mv[k] = m[e0 + k]; vv[k] = v[e0 + k]; }
+    }
+    int gd = -1;
+    float dxn = 0.f, dyn = 0.f, dzn = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (k < cnt) {
+            const int b = rem / 3, c = rem - 3 * (rem / 3);
+            if (b < n_used && (g == g_last ? vis1 : vis0)) {
+                if (gd != g) {
+                    gd = g;
+                    const float dx = means[3 * g] - cx, dy = means[3 * g + 1] - cy,
+                                dz = means[3 * g + 2] - cz;
+                    const float inv = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
+                    dxn = dx * inv; dyn = dy * inv; dzn = dz * inv;
+                }
+                const float grad = sh_basis(b, dxn, dyn, dzn) * gacc[(size_t)g * 9 + 5 + c];
+                adam_elem(pv[k], mv[k], vv[k], grad, hp.step[4], hp.b1, hp.b2, hp.bc2[4], hp.eps);
+            }
+        }
+        if (++rem == rest_per) { rem = 0; ++g; }
+    }
+    if (full) {
+        *reinterpret_cast<float4*>(f_rest + e0) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+        *reinterpret_cast<float4*>(m + e0) = make_float4(mv[0], mv[1], mv[2], mv[3]);
+        *reinterpret_cast<float4*>(v + e0) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+    } else {
+        for (int k = 0; k < cnt; ++k) { f_rest[e0 + k] = pv[k]; m[e0 + k] = mv[k]; v[e0 + k] = vv[k]; }
+    }
 }
 
 struct BwdPtrs {
@@ -168,8 +206,8 @@ __global__ __launch_bounds__(256) void k_proj_bwd_adam(CamParams p, BwdPtrs P, A
         // cov2d_to_conic_vjp: v_Sigma = -X G X.
         float vc2[3];
         {
-            const float4 cn = go.conic[g];
-            const float X[2][2] = {{cn.x, cn.y}, {cn.y, cn.z}};
+            const float4 r0 = go.rec[4 * (size_t)g], r1 = go.rec[4 * (size_t)g + 1];
+            const float X[2][2] = {{r0.z, r0.w}, {r0.w, r1.x}};
             const float G[2][2] = {{ga[2], ga[3]}, {ga[3], ga[4]}};
             float nX[2][2], T1[2][2], S[2][2];
 #pragma unroll
@@ -352,7 +390,8 @@ void launch_sh_rest_adam(hipStream_t s, const CamParams& p, const float* means,
     const int n_used = dtu >= 3 ? 15 : dtu == 2 ? 8 : dtu == 1 ? 3 : 0;
     if (n_used == 0 || p.rest_per == 0 || p.N <= 0) return;
     const int64_t n = (int64_t)p.N * p.rest_per;
-    hipLaunchKernelGGL(k_sh_rest_adam, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, n,
+    const int64_t threads = (n + 3) / 4;
+    hipLaunchKernelGGL(k_sh_rest_adam, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, n,
                        p.rest_per, n_used, means, p.cam[0], p.cam[1], p.cam[2], radii, gacc,
                        f_rest, m, v, hp);
 }

@@ -81,12 +81,28 @@ __device__ __forceinline__ void sh_color(int degree, V3 d, const float* dc, cons
     }
 }
 
-__global__ __launch_bounds__(256) void k_project_fwd(
+constexpr int PROJ_T = 128;   // gaussians per workgroup
+
+__global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     CamParams p, const float* __restrict__ means, const float* __restrict__ scales,
     const float* __restrict__ quats, const float* __restrict__ f_dc,
     const float* __restrict__ f_rest, const float* __restrict__ opac_logits, GaussOut go,
     uint32_t* __restrict__ dkey, uint32_t* __restrict__ dval, float* __restrict__ gacc) {
-    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    // Stage this workgroup's features_rest rows (PROJ_T * rest_per contiguous
+    // floats, 16-byte aligned) through LDS with coalesced 16-byte loads.
+    extern __shared__ float s_rest[];
+    const int g0 = blockIdx.x * PROJ_T;
+    if (p.dtu > 0) {
+        const int64_t base = (int64_t)g0 * p.rest_per;
+        const int64_t total = (int64_t)p.N * p.rest_per;
+        const int cnt = (int)min((int64_t)PROJ_T * p.rest_per, total - base);
+        const float4* src4 = reinterpret_cast<const float4*>(f_rest + base);
+        float4* dst4 = reinterpret_cast<float4*>(s_rest);
+        for (int i = threadIdx.x; i < cnt / 4; i += PROJ_T) dst4[i] = src4[i];
+        for (int i = (cnt / 4) * 4 + threadIdx.x; i < cnt; i += PROJ_T) s_rest[i] = f_rest[base + i];
+        __syncthreads();
+    }
+    const int g = g0 + threadIdx.x;
     if (g >= p.N) return;
 #pragma unroll
     for (int q = 0; q < 9; ++q) gacc[(size_t)g * 9 + q] = 0.f;
@@ -152,19 +168,18 @@ __global__ __launch_bounds__(256) void k_project_fwd(
     if (area <= 0) return;
 
     go.tiles_hit[g] = area;
-    go.depth[g] = pv.z;
     go.radii[g] = f2i(radius);
-    go.xy[g] = make_float2(px, py);
-    go.aabb[g] = make_float2(ex, ey);
 
     // SH colour along normalize(p - cam_pos).
     const float dx = pw.x - p.cam[0], dy = pw.y - p.cam[1], dz = pw.z - p.cam[2];
     const float inv = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
     const V3 dir{dx * inv, dy * inv, dz * inv};
     float col[3];
-    sh_color(p.dtu, dir, f_dc + 3 * (size_t)g, f_rest + (size_t)p.rest_per * g, col);
-    go.conic[g] = make_float4(ca, cb, cc, sigmoid(opac_logits[g]));
-    go.rgb[g] = make_float4(col[0], col[1], col[2], 0.f);
+    sh_color(p.dtu, dir, f_dc + 3 * (size_t)g, s_rest + (size_t)p.rest_per * threadIdx.x, col);
+    float4* rec = go.rec + 4 * (size_t)g;
+    rec[0] = make_float4(px, py, ca, cb);
+    rec[1] = make_float4(cc, sigmoid(opac_logits[g]), col[0], col[1]);
+    rec[2] = make_float4(col[2], ex, ey, pv.z);
     dkey[g] = __float_as_uint(pv.z);
 }
 
@@ -175,8 +190,9 @@ void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
                         const float* f_rest, const float* opac_logits, GaussOut go,
                         uint32_t* dkey, uint32_t* dval, float* gacc) {
     if (p.N <= 0) return;
-    const int blocks = (p.N + 255) / 256;
-    hipLaunchKernelGGL(k_project_fwd, dim3(blocks), dim3(256), 0, s, p, means, scales, quats,
+    const int blocks = (p.N + PROJ_T - 1) / PROJ_T;
+    const size_t lds = p.dtu > 0 ? (size_t)PROJ_T * p.rest_per * sizeof(float) : 0;
+    hipLaunchKernelGGL(k_project_fwd, dim3(blocks), dim3(PROJ_T), lds, s, p, means, scales, quats,
                        f_dc, f_rest, opac_logits, go, dkey, dval, gacc);
 }
 

@@ -315,7 +315,8 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
                 float vop = 0.f;
                 if (valid && alpha < 0.999f) {
-                    const float ra = 1.f / (1.f - alpha);
+                    // hardware reciprocal (1 ulp): the backward is compared with a tolerance
+                    const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
                     T *= ra;
                     const float fac = alpha * T;
                     v[5] = fac * vo0;
