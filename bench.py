@@ -30,6 +30,22 @@ METRIC = "train iters/sec + render FPS, 1.5M Gaussians SH3 @1297×840, 1×MI355X
 HBM_PEAK = 8.0e12
 FP32_PEAK = 157.3e12
 
+# Algorithmic fp32 operations per (pixel, entry) pair of the reference's
+# per-pixel raster loops (.metal:472-585 forward, 898-1099 backward), counted
+# as add/sub/mul/min/max = 1, fma = 2, exp and reciprocal = 1 each:
+#   every evaluated pair   d = xy - p (2), sigma = 0.5 (a dx^2 + c dy^2) +
+#                          b dx dy (9), alpha = min(0.999, o exp(-sigma)) (3)
+#   forward, composited    next_T, vis, three colour fmas (9)
+#   backward, with grad    1/(1-a), T, fac, v_rgb, three clamped colour terms,
+#                          v_alpha, buffer fmas, v_sigma, v_conic, v_xy,
+#                          v_opacity (55) + the nine gradient sums (9)
+# Only pairs that composite (forward) or carry a gradient (backward) are
+# counted, as the rasteriser's own GPU counters report them; pairs that are
+# tested and rejected add nothing, so the figure is a lower bound.
+FWD_PAIR_FLOPS = 11 + 3 + 9
+BWD_PAIR_FLOPS = 11 + 3 + 64
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "raster_bwd_config3_traffic.json")
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -94,6 +110,76 @@ def cpu_baseline(params_dev, cams, targets, degree, bg, n_steps):
     return n_steps / dt, int(orc.lib().orc_num_threads()), dt
 
 
+def rocprof_summary(d: str, last: int, command: str) -> str:
+    """Markdown summary of a `rocprofv3 --kernel-trace --stats -f csv` output
+    directory: kernels by total time, and the raster backward's average
+    duration over all its dispatches and over the last `last` (the timed
+    train steps of a default run, which end with no further backward)."""
+    import csv
+    import glob
+    import re
+    stats = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)
+    trace = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+    if not stats or not trace:
+        raise SystemExit(f"no kernel_stats / kernel_trace csv under {d}")
+
+    def short(name):
+        m = re.search(r"(k_\w+)", name)
+        return m.group(1) if m else name.split("(")[0][:60]
+
+    rows = sorted(csv.DictReader(open(stats[0])), key=lambda r: -float(r["TotalDurationNs"]))
+    out = [f"Command: `{command}`", "",
+           "| kernel | calls | avg us | min us | max us | % time |", "|---|---:|---:|---:|---:|---:|"]
+    for r in rows[:20]:
+        out.append(f"| {short(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                   f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.2f} |")
+    tr = [r for r in csv.DictReader(open(trace[0])) if "k_raster_bwd" in r["Kernel_Name"]]
+    tr.sort(key=lambda r: int(r["Start_Timestamp"]))
+    dur = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in tr]
+    if dur:
+        tail = dur[-last:] if last > 0 else dur
+        out += ["", f"k_raster_bwd: {len(dur)} dispatches, average {sum(dur) / len(dur):.1f} us; "
+                    f"last {len(tail)} dispatches (the timed steps) average {sum(tail) / len(tail):.1f} us"]
+    return "\n".join(out) + "\n"
+
+
+def _pmc_mean(d: str, kernel_re: str, counter: str, last: int) -> tuple:
+    """Mean of one counter over the dispatches of the kernels matching kernel_re
+    (the last `last` of them when last > 0) in a `rocprofv3 --pmc -f csv` directory."""
+    import csv
+    import glob
+    import re
+    f = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not f:
+        raise SystemExit(f"no counter_collection csv under {d}")
+    rows = [r for r in csv.DictReader(open(f[0]))
+            if re.search(kernel_re, r["Kernel_Name"]) and r["Counter_Name"] == counter]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    v = [float(r["Counter_Value"]) for r in rows]
+    if last > 0:
+        v = v[-last:]
+    if not v:
+        raise SystemExit(f"no {counter} samples for /{kernel_re}/ under {d}")
+    return sum(v) / len(v), len(v)
+
+
+def traffic_summary(dirs: list, copy_mib: int, last: int, commands: str) -> dict:
+    """HBM bytes per k_raster_bwd launch from FETCH_SIZE / WRITE_SIZE runs
+    (KiB per dispatch), each scaled so that a plain device copy of copy_mib MiB
+    reads and writes exactly copy_mib MiB."""
+    fetch_dir, write_dir, copy_fetch_dir, copy_write_dir = dirs
+    fk, nf = _pmc_mean(fetch_dir, "k_raster_bwd", "FETCH_SIZE", last)
+    wk, nw = _pmc_mean(write_dir, "k_raster_bwd", "WRITE_SIZE", last)
+    cf, _ = _pmc_mean(copy_fetch_dir, "copyBuffer", "FETCH_SIZE", 0)
+    cw, _ = _pmc_mean(copy_write_dir, "copyBuffer", "WRITE_SIZE", 0)
+    fs, ws = copy_mib * 1024 / cf, copy_mib * 1024 / cw
+    return {"kernel": "k_raster_bwd", "dispatches": [nf, nw],
+            "fetch_kib_per_dispatch": fk, "write_kib_per_dispatch": wk,
+            "copy_fetch_kib": cf, "copy_write_kib": cw, "copy_mib": copy_mib,
+            "fetch_scale": fs, "write_scale": ws,
+            "hbm_bytes_per_launch": 1024 * (fk * fs + wk * ws), "commands": commands}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,13 +187,40 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--frames", type=int, default=200)
     ap.add_argument("--n", type=int, default=1_500_000)
-    ap.add_argument("--cpu-steps", type=int, default=2)
+    ap.add_argument("--cpu-steps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB five times (calibrates "
+                         "the FETCH_SIZE / WRITE_SIZE counters against known traffic) and exit")
+    ap.add_argument("--rocprof-summary", default="",
+                    help="only print a markdown summary of this rocprofv3 csv output directory and exit")
+    ap.add_argument("--rocprof-command", default="", help="command line quoted in the summary")
+    ap.add_argument("--traffic-summary", nargs=4, default=None,
+                    metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
+                    help="only print the HBM traffic JSON of the raster backward from four "
+                         "rocprofv3 --pmc csv directories (the copy runs use --copy-mib) and exit")
     args = ap.parse_args()
+    if args.traffic_summary:
+        print(json.dumps(traffic_summary(args.traffic_summary, args.copy_mib or 1024, args.steps,
+                                         args.rocprof_command), indent=1))
+        return
+    if args.rocprof_summary:
+        print(rocprof_summary(args.rocprof_summary, args.steps, args.rocprof_command), end="")
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
               "this build has no multi-GPU path.", file=sys.stderr)
         sys.exit(2)
+    if args.copy_mib > 0:
+        import torch
+        n = args.copy_mib * (1 << 20) // 4
+        a = torch.ones(n, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copied {args.copy_mib} MiB x5")
+        return
 
     import torch
     from msplat_amd import camera, device, synthetic
@@ -141,6 +254,7 @@ def main():
     device.sync()
     t1 = time.perf_counter()
     stages, calls = stage_times(lib)
+    train_pairs = device.drain_raster_counters()
     train_s = t1 - t0
     its = args.steps / train_s
     log(f"train: {args.steps} steps in {train_s:.3f}s = {its:.1f} it/s; gaussians {n_start} -> {tr.splat_count()}")
@@ -162,11 +276,34 @@ def main():
     device.sync()
     r1 = time.perf_counter()
     rstages, _ = stage_times(lib)
+    render_pairs = device.drain_raster_counters()
     fps = args.frames / (r1 - r0)
     log(f"render: {args.frames} frames in {r1 - r0:.3f}s = {fps:.1f} FPS at N={tr.splat_count()}")
     for k, (ms, c) in rstages.items():
         if c:
             log(f"  {k:18s} {ms / c:8.3f} ms/call")
+
+    # Roofline of the dominant kernel (raster backward): algorithmic flops from
+    # the GPU pair counters over exactly the timed launches, divided by those
+    # launches' HIP-event durations on the context stream.
+    bwd_ms, bwd_n = stages["rast_bwd"][0] / max(stages["rast_bwd"][1], 1), stages["rast_bwd"][1]
+    bwd_flops = BWD_PAIR_FLOPS * train_pairs[1] / max(bwd_n, 1)
+    achieved = bwd_flops / (bwd_ms * 1e-3)
+    fwd_ms, fwd_n = rstages["rast_fwd"][0] / max(rstages["rast_fwd"][1], 1), rstages["rast_fwd"][1]
+    fwd_flops = FWD_PAIR_FLOPS * render_pairs[0] / max(fwd_n, 1)
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    roofline = {"bound": "mfma", "achieved": achieved / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
+                "frac": achieved / FP32_PEAK, "traffic": traffic,
+                "kernel": "k_raster_bwd", "roof": "fp32 vector ALU (the kernel has no matrix-shaped work)",
+                "launches": bwd_n, "launch_ms": bwd_ms, "flops_per_launch": bwd_flops,
+                "grad_pairs_per_launch": train_pairs[1] / max(bwd_n, 1)}
+    log(f"roofline k_raster_bwd: {bwd_flops / 1e9:.2f} GFLOP/launch ({train_pairs[1] / max(bwd_n, 1) / 1e6:.1f}M "
+        f"gradient pairs) in {bwd_ms:.3f} ms = {achieved / 1e12:.2f} TFLOP/s ({100 * achieved / FP32_PEAK:.1f}% "
+        f"of fp32 peak); render forward {fwd_flops / 1e9:.2f} GFLOP in {fwd_ms:.3f} ms = "
+        f"{fwd_flops / fwd_ms / 1e9:.2f} TFLOP/s")
 
     cpu = None
     if not args.no_cpu and args.cpu_steps > 0:
@@ -184,6 +321,9 @@ def main():
                    "gaussians_start": n_start, "gaussians_end": tr.splat_count(), "render_frames": args.frames},
         "render_fps": fps,
         "stage_ms": {k: ms / c for k, (ms, c) in stages.items() if c},
+        "render_stage_ms": {k: ms / c for k, (ms, c) in rstages.items() if c},
+        "rast_fwd_render_tflops": fwd_flops / fwd_ms / 1e9,
+        "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)

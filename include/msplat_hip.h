@@ -156,12 +156,27 @@ int msplat_hip_enable_stage_timing(int enable);
 int msplat_hip_drain_stage_times(double* ms, int64_t* counts, const char** names, int max_stages,
                                  int* n_stages, int64_t* n_calls);
 
+/* While stage timing is enabled the rasteriser also counts, on the GPU,
+ * counts[0] (pixel, entry) pairs composited by the forward and counts[1]
+ * pairs that carry a gradient in the backward, summed over the timed calls.
+ * drain returns them (zeros when timing is off) and restarts the sums.  Part
+ * of the profiler interface above; the reference has no counterpart. */
+int msplat_hip_drain_raster_counters(int64_t counts[2]);
+
 /* Copy a named intermediate of the last render / train step to host memory.
  * Names: xys, depths, radii, conics, colors, aabb, num_tiles_hit,
  * tile_bins, gaussian_ids, final_Ts, final_index, out_img, v_rendered,
  * v_xy, v_conic, v_rgb, v_opacity, meta.  *nbytes is set to the size; pass
  * dst == NULL to query it. */
 int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes);
+
+/* Algorithmic rasteriser work of the last render / train step, counted on the
+ * GPU per (pixel, entry) pair in the order of the reference's per-pixel loops
+ * (no culling): counts[0..2] forward pairs tested / with sigma in [0, 5.55) /
+ * composited; counts[3..5] backward pairs tested / in range / carrying a
+ * gradient (meaningful after a train step).  Measurement aid with no
+ * counterpart in the reference; it changes no state. */
+int msplat_hip_raster_work(int64_t counts[6]);
 
 #ifdef __cplusplus
 }

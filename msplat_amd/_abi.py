@@ -111,6 +111,8 @@ SIGNATURES = [
     ("msplat_hip_drain_stage_times", c_int,
      [POINTER(c_double), POINTER(c_int64), POINTER(c_char_p), c_int, POINTER(c_int), POINTER(c_int64)]),
     ("msplat_hip_copy_intermediate", c_int, [c_char_p, c_void_p, POINTER(c_size_t)]),
+    ("msplat_hip_raster_work", c_int, [POINTER(c_int64)]),
+    ("msplat_hip_drain_raster_counters", c_int, [POINTER(c_int64)]),
 ]
 
 _lib = None

@@ -67,7 +67,7 @@ struct Ctx {
     // per pixel
     Buf final_T, final_idx, out_img, hbuf, dbuf, v_rendered, loss_part;
     // scalars
-    Buf meta_d, loss_d, count_d;
+    Buf meta_d, loss_d, count_d, work_d;
     Meta* meta_h = nullptr;
     float* loss_h = nullptr;
     int* count_h = nullptr;
@@ -141,7 +141,7 @@ void free_all(Ctx* c) {
                    &c->pk_col, &c->pk_bl, &c->pk_ids, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
                    &c->hbuf, &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
-                   &c->count_d, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
+                   &c->count_d, &c->work_d, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
                    &c->d_tot, &c->d_scratch, &c->d_rnd};
     for (Buf* b : bufs)
         if (b->p) { (void)hipFree(b->p); b->p = nullptr; b->bytes = 0; }
@@ -191,6 +191,12 @@ ChunkBufs chunks(Ctx* c) {
 }
 
 int sh_bases(int degree) { return degree == 0 ? 1 : degree == 1 ? 4 : degree == 2 ? 9 : degree == 3 ? 16 : 25; }
+
+// Raster pair counters (composited forward, gradient-carrying backward),
+// accumulated while stage timing is enabled.
+unsigned long long* work_counters(Ctx* c) {
+    return c->timing ? P<unsigned long long>(c->work_d) : nullptr;
+}
 
 // Record the start of stage `st` (S_END closes the call).
 void stage_mark(Ctx* c, int st) {
@@ -348,7 +354,8 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
     stage_mark(c, S_RFWD);
     ChunkBufs cb = chunks(c);
     launch_raster_fwd(c->stream, p, max_items, P<Meta>(c->meta_d), it, P<int>(c->tile_bins), pk,
-                      P<float>(c->final_T), P<int>(c->final_idx), P<float>(c->out_img), cb);
+                      P<float>(c->final_T), P<int>(c->final_idx), P<float>(c->out_img), cb,
+                      work_counters(c));
     launch_raster_merge(c->stream, p, P<Meta>(c->meta_d), P<int>(c->l_chunked), it,
                         P<float>(c->final_T), P<int>(c->final_idx), P<float>(c->out_img), cb,
                         training);
@@ -509,7 +516,7 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
     launch_raster_bwd(c->stream, p, c->max_items, P<Meta>(c->meta_d), items(c),
                       P<int>(c->tile_bins), packed(c),
                       P<float>(c->final_T), P<int>(c->final_idx), chunks(c),
-                      P<float>(c->v_rendered), P<float>(c->gacc));
+                      P<float>(c->v_rendered), P<float>(c->gacc), work_counters(c));
     AdamHP hp;
     for (int g = 0; g < 6; ++g) { hp.step[g] = a->adam_step_sizes[g]; hp.bc2[g] = a->adam_bc2_sqrts[g]; }
     hp.b1 = a->adam_beta1;
@@ -599,6 +606,10 @@ int msplat_hip_enable_stage_timing(int enable) {
     Ctx* c = g_ctx;
     if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
     c->timing = enable != 0;
+    if (c->timing) {
+        ENSURE(c->work_d, 16);
+        HIP_TRY(hipMemsetAsync(c->work_d.p, 0, 16, c->stream));
+    }
     c->n_marks[0] = c->n_marks[1] = 0;
     for (int i = 0; i < kNumStages; ++i) { c->stage_sum[i] = 0.0; c->stage_cnt[i] = 0; }
     c->calls = 0;
@@ -623,6 +634,43 @@ int msplat_hip_drain_stage_times(double* ms, int64_t* counts, const char** names
     if (n_stages) *n_stages = n;
     if (n_calls) *n_calls = c->calls;
     c->calls = 0;
+    return MSPLAT_OK;
+}
+
+int msplat_hip_drain_raster_counters(int64_t counts[2]) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!counts) return fail(MSPLAT_ERR_ARG, "null counts");
+    counts[0] = counts[1] = 0;
+    if (!c->timing) return MSPLAT_OK;
+    unsigned long long h[2];
+    HIP_TRY(hipMemcpyAsync(h, c->work_d.p, sizeof(h), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    HIP_TRY(hipMemsetAsync(c->work_d.p, 0, 16, c->stream));
+    counts[0] = (int64_t)h[0];
+    counts[1] = (int64_t)h[1];
+    return MSPLAT_OK;
+}
+
+int msplat_hip_raster_work(int64_t counts[6]) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!counts) return fail(MSPLAT_ERR_ARG, "null counts");
+    ENSURE(c->count_d, 64);
+    HIP_TRY(hipMemsetAsync(c->count_d.p, 0, 48, c->stream));
+    CamParams p{};
+    p.W = c->last_W;
+    p.H = c->last_H;
+    p.tbx = (p.W + BLOCK - 1) / BLOCK;
+    p.tby = (p.H + BLOCK - 1) / BLOCK;
+    unsigned long long* d = P<unsigned long long>(c->count_d);
+    if (c->last_N > 0 && c->meta_d.p)
+        launch_raster_work(c->stream, p, c->max_items, P<Meta>(c->meta_d), items(c),
+                           P<int>(c->tile_bins), packed(c), P<int>(c->final_idx), chunks(c), d);
+    unsigned long long h[6];
+    HIP_TRY(hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    for (int k = 0; k < 6; ++k) counts[k] = (int64_t)h[k];
     return MSPLAT_OK;
 }
 

@@ -108,16 +108,23 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go
 inline int64_t items_bound(int64_t T, int64_t I) { return T + I / 512 + I / 2048 + 1; }
 
 // Rasterisation (raster.hip); grids are sized by items_bound / T and the
-// kernels read the exact counts from meta.
+// kernels read the exact counts from meta.  A non-null `work` makes the
+// forward add its composited (pixel, entry) pairs to work[0] and the
+// backward its pairs that carry a gradient to work[1].
 void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Packed pk, float* final_T, int* final_idx,
-                       float* out_img, ChunkBufs cb);
+                       float* out_img, ChunkBufs cb, unsigned long long* work);
 void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
                          Items it, float* final_T, int* final_idx, float* out_img, ChunkBufs cb,
                          bool with_suffix);
 void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Packed pk, const float* final_T,
-                       const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc);
+                       const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc,
+                       unsigned long long* work);
+// Adds the six pair counts of the most recent forward/backward into out[6].
+void launch_raster_work(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
+                        Items it, const int* tile_bins, Packed pk, const int* final_idx,
+                        ChunkBufs cb, unsigned long long* out);
 
 void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
                  float inv_n, float* hbuf, float* dbuf, float* v_rendered, float* loss_part,

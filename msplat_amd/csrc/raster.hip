@@ -44,6 +44,13 @@ __device__ __forceinline__ Px pixel_of(int t, int tbx, int W, int H) {
     return p;
 }
 
+// Adds the sum of v over the wave into *dst (one atomic per wave).
+__device__ __forceinline__ void wave_count_add(unsigned long long* dst, unsigned v) {
+    unsigned long long x = v;
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+    if ((threadIdx.x & 63) == 0 && x) atomicAdd(dst, x);
+}
+
 __device__ __forceinline__ void item_range(const Items& it, const int* tile_bins, int item,
                                            int& t, int& K, int& cs, int& ce) {
     t = it.tile[item];
@@ -88,7 +95,8 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
                                                     const int* __restrict__ tile_bins, Packed pk,
                                                     float* __restrict__ final_T,
                                                     int* __restrict__ final_idx,
-                                                    float* __restrict__ out_img, ChunkBufs cb) {
+                                                    float* __restrict__ out_img, ChunkBufs cb,
+                                                    unsigned long long* __restrict__ work) {
     __shared__ float4 s_geo[256];
     __shared__ float4 s_col[256];
     __shared__ float s_bl[256];
@@ -104,6 +112,7 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
 
     float T = 1.f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
     int last = cs - 1;
+    unsigned ncomp = 0;     // pairs composited by this pixel
     bool done = !px.inside;
     for (int b = cs; b < ce; b += 256) {
         if (__syncthreads_and(done)) break;
@@ -148,10 +157,12 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
                 C2 = fmaf(s_bl[qq], vis, C2);
                 T = nT;
                 last = b + qq;
+                ++ncomp;
             }
             if (__ballot(!done) == 0) break;
         }
     }
+    if (work) wave_count_add(work, ncomp);
     if (!px.inside) return;
     if (K == 1) {
         const size_t pix = (size_t)px.i * W + px.j;
@@ -235,7 +246,8 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                                                     const float* __restrict__ final_T,
                                                     const int* __restrict__ final_idx,
                                                     ChunkBufs cb, const float* __restrict__ v_out,
-                                                    float* __restrict__ gacc) {
+                                                    float* __restrict__ gacc,
+                                                    unsigned long long* __restrict__ work) {
     __shared__ float4 s_geo[256];
     __shared__ float4 s_col[256];
     __shared__ float s_bl[256];
@@ -253,6 +265,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
 
     float T = 1.f, Tfin = 1.f, B0 = 0.f, B1 = 0.f, B2 = 0.f, vo0 = 0.f, vo1 = 0.f, vo2 = 0.f;
     int bf = cs - 1;
+    unsigned ngrad = 0;     // pairs of this pixel that carry a gradient
     if (px.inside) {
         const size_t pix = (size_t)px.i * W + px.j;
         Tfin = final_T[pix];
@@ -315,6 +328,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
                 float vop = 0.f;
                 if (valid && alpha < 0.999f) {
+                    ++ngrad;
                     // hardware reciprocal (1 ulp): the backward is compared with a tolerance
                     const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
                     T *= ra;
@@ -355,17 +369,85 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
             }
         }
     }
+    if (work) wave_count_add(work + 1, ngrad);
+}
+
+// Algorithmic work of the most recent forward (+ backward): one thread per
+// pixel walks its item's entries in the order of the per-pixel loops of the
+// reference kernels, without quadrant culling or lockstep, and counts
+// (pixel, entry) pairs: forward tested / sigma in range / composited,
+// backward tested / sigma in range / carrying a gradient.  The counts
+// define the algorithmic flops of the roofline; they change no state.
+__global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
+                                                     const Meta* __restrict__ meta, Items it,
+                                                     const int* __restrict__ tile_bins, Packed pk,
+                                                     const int* __restrict__ final_idx,
+                                                     ChunkBufs cb,
+                                                     unsigned long long* __restrict__ out) {
+    const int item = blockIdx.x;
+    if (item >= meta->n_items) return;
+    int t, K, cs, ce;
+    item_range(it, tile_bins, item, t, K, cs, ce);
+    const Px px = pixel_of(t, tbx, W, H);
+    unsigned n[6] = {0u, 0u, 0u, 0u, 0u, 0u};
+    if (px.inside) {
+        const float fx = (float)px.j, fy = (float)px.i;
+        float T = 1.f;
+        for (int i = cs; i < ce; ++i) {
+            ++n[0];
+            const float4 g = pk.geo[i];
+            const float4 c = pk.col[i];
+            const float dx = g.x - fx, dy = g.y - fy;
+            const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
+            if (sigma < 0.f || sigma >= 5.55f) continue;
+            ++n[1];
+            const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
+            if (alpha < 1.f / 255.f) continue;
+            const float nT = T * (1.f - alpha);
+            if (nT <= 1e-4f) break;
+            ++n[2];
+            T = nT;
+        }
+        const int bf = K == 1 ? final_idx[(size_t)px.i * W + px.j]
+                              : cb.cidx[(size_t)item * TILE_PIX + px.lp];
+        for (int i = min(bf, ce - 1); i >= cs; --i) {
+            ++n[3];
+            const float4 g = pk.geo[i];
+            const float4 c = pk.col[i];
+            const float dx = g.x - fx, dy = g.y - fy;
+            const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
+            if (sigma < 0.f || sigma >= 5.55f) continue;
+            ++n[4];
+            const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
+            if (alpha < 1.f / 255.f || !(alpha < 0.999f)) continue;
+            ++n[5];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        unsigned long long v = n[k];
+        for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+        if ((threadIdx.x & 63) == 0) atomicAdd(&out[k], v);
+    }
 }
 
 }  // namespace
 
+void launch_raster_work(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
+                        Items it, const int* tile_bins, Packed pk, const int* final_idx,
+                        ChunkBufs cb, unsigned long long* out) {
+    if (max_items <= 0) return;
+    hipLaunchKernelGGL(k_raster_work, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
+                       meta, it, tile_bins, pk, final_idx, cb, out);
+}
+
 void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Packed pk, float* final_T, int* final_idx,
-                       float* out_img, ChunkBufs cb) {
+                       float* out_img, ChunkBufs cb, unsigned long long* work) {
     if (max_items <= 0) return;
     hipLaunchKernelGGL(k_raster_fwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
                        p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx,
-                       out_img, cb);
+                       out_img, cb, work);
 }
 
 void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
@@ -379,11 +461,12 @@ void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, co
 
 void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Packed pk, const float* final_T,
-                       const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc) {
+                       const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc,
+                       unsigned long long* work) {
     if (max_items <= 0) return;
     hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
                        p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx, cb,
-                       v_out, gacc);
+                       v_out, gacc, work);
 }
 
 }  // namespace msp

@@ -198,6 +198,28 @@ def intermediate(name: str, dtype=np.float32, shape=None) -> np.ndarray:
     return out.reshape(shape) if shape is not None else out
 
 
+RASTER_WORK_KEYS = ("fwd_tested", "fwd_in_range", "fwd_composited",
+                    "bwd_tested", "bwd_in_range", "bwd_with_grad")
+
+
+def raster_work() -> dict:
+    """(pixel, entry) pair counts of the last render / train step's rasteriser
+    (msplat_hip_raster_work): the algorithmic work behind its flop count."""
+    lib = init()
+    out = (ctypes.c_int64 * 6)()
+    _abi.check(lib.msplat_hip_raster_work(out))
+    return dict(zip(RASTER_WORK_KEYS, (int(v) for v in out)))
+
+
+def drain_raster_counters() -> tuple:
+    """(forward pairs composited, backward pairs with gradient) summed over the
+    calls made while stage timing was on; restarts the sums."""
+    lib = init()
+    out = (ctypes.c_int64 * 2)()
+    _abi.check(lib.msplat_hip_drain_raster_counters(out))
+    return int(out[0]), int(out[1])
+
+
 def meta() -> dict:
     raw = intermediate("meta", np.uint8)
     total = int(np.frombuffer(raw[:8].tobytes(), np.int64)[0])

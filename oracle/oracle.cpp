@@ -426,22 +426,31 @@ inline void adam_elem(float& p, float& m, float& v, float g, float step, float b
 
 struct Entry { float x, y, a, b, c, o, r, g, bl; int id; };
 
+// Work counters of the last orc_rasterize call: (pixel, entry) pairs tested,
+// pairs with sigma in [0, 5.55), pairs that composite (forward) or carry a
+// gradient (backward).  Used only to state the algorithmic work of a step.
+struct Counts { int64_t e = 0, r = 0, s = 0; };
+Counts g_fwd_counts, g_bwd_counts;
+
 // Forward over entries [s, e) for one pixel with local transmittance start 1
 // (.metal:510-572 / 2691-2731).  Returns T; fills C and last.
 inline float raster_pixel_fwd(const Entry* ent, int s, int e, float px, float py, float* C,
-                              int* last) {
+                              int* last, Counts* cnt) {
     float T = 1.f;
     C[0] = C[1] = C[2] = 0.f;
     int lc = s - 1;
     for (int i = s; i < e; ++i) {
         const Entry& en = ent[i];
+        ++cnt->e;
         const float dx = en.x - px, dy = en.y - py;
         const float sigma = std::fma(0.5f, std::fma(en.a, dx * dx, en.c * dy * dy), en.b * dx * dy);
         if (sigma < 0.f || sigma >= 5.55f) continue;
+        ++cnt->r;
         const float alpha = std::fmin(0.999f, en.o * oexp(-sigma));
         if (alpha < 1.f / 255.f) continue;
         const float next_T = T * (1.f - alpha);
         if (next_T <= 1e-4f) { lc = i - 1; break; }
+        ++cnt->s;
         const float vis = alpha * T;
         const float rgb[3] = {std::fmax(en.r + 0.5f, 0.f), std::fmax(en.g + 0.5f, 0.f),
                               std::fmax(en.bl + 0.5f, 0.f)};
@@ -457,19 +466,22 @@ inline float raster_pixel_fwd(const Entry* ent, int s, int e, float px, float py
 // (.metal:1015-1096 / 2963-3028).  Accumulates per-entry gradients into acc[i*9..].
 inline void raster_pixel_bwd(const Entry* ent, int s, int bin_final, float px, float py,
                              float T, const float* buf0, float T_final, const float* bg,
-                             const float* v_out, double* acc, int acc_base) {
+                             const float* v_out, double* acc, int acc_base, Counts* cnt) {
     float buffer[3] = {buf0[0], buf0[1], buf0[2]};
     const float Tfb[3] = {T_final * bg[0], T_final * bg[1], T_final * bg[2]};
     for (int i = bin_final; i >= s; --i) {
         const Entry& en = ent[i];
+        ++cnt->e;
         const float opac = en.o;
         const float dx = en.x - px, dy = en.y - py;
         const float sigma = std::fma(0.5f, std::fma(en.a, dx * dx, en.c * dy * dy), en.b * dx * dy);
         if (sigma < 0.f || sigma >= 5.55f) continue;
+        ++cnt->r;
         const float vis = oexp(-sigma);
         const float alpha = std::fmin(0.999f, opac * vis);
         if (alpha < 1.f / 255.f) continue;
         if (!(alpha < 0.999f)) continue;
+        ++cnt->s;
         const float ra = 1.f / (1.f - alpha);
         T *= ra;
         const float fac = alpha * T;
@@ -516,6 +528,11 @@ int32_t orc_num_threads(void) {
 }
 
 float orc_expf(float x) { return oexp(x); }
+
+void orc_raster_counts(int64_t out[6]) {
+    out[0] = g_fwd_counts.e; out[1] = g_fwd_counts.r; out[2] = g_fwd_counts.s;
+    out[3] = g_bwd_counts.e; out[4] = g_bwd_counts.r; out[5] = g_bwd_counts.s;
+}
 
 void orc_sh_consts(float out[25]) {
     out[0] = SH_C0; out[1] = SH_C1;
@@ -657,9 +674,11 @@ void orc_rasterize(const OrcCamera* cam, int32_t N, const float* xys, const floa
     }
     std::vector<double> acc;
     if (v_out) acc.assign((size_t)I * 9, 0.0);
+    int64_t fe = 0, fr = 0, fs = 0, be = 0, br = 0, bs = 0;
 
-#pragma omp parallel for schedule(dynamic, 4)
+#pragma omp parallel for schedule(dynamic, 4) reduction(+ : fe, fr, fs, be, br, bs)
     for (int t = 0; t < T; ++t) {
+        Counts cf, cbk;
         const int s = tile_bins[2 * t], e = tile_bins[2 * t + 1], n = e - s;
         const int K = orc_tile_chunks(n, T);
         const int tx0 = (t % tbx) * BLOCK, ty0 = (t / tbx) * BLOCK;
@@ -674,21 +693,21 @@ void orc_rasterize(const OrcCamera* cam, int32_t N, const float* xys, const floa
                 float Tfin, Cfin[3];
                 int last;
                 if (K == 1) {
-                    Tfin = raster_pixel_fwd(ent.data(), s, e, px, py, Cfin, &last);
+                    Tfin = raster_pixel_fwd(ent.data(), s, e, px, py, Cfin, &last, &cf);
                 } else {
                     for (int k = 0; k < K; ++k) {
                         const int cs = s + k * CHUNK, ce = std::min(s + (k + 1) * CHUNK, e);
-                        cT[k] = raster_pixel_fwd(ent.data(), cs, ce, px, py, &cC[3 * k], &cidx[k]);
+                        cT[k] = raster_pixel_fwd(ent.data(), cs, ce, px, py, &cC[3 * k], &cidx[k], &cf);
                     }
                     // rasterize_forward_merge_kernel (.metal:2764-2799)
                     float Tr = 1.f, Cr[3] = {0.f, 0.f, 0.f};
                     int li = -1, cutoff = K;
                     for (int k = 0; k < K; ++k) {
-                        const int cf = cidx[k];
-                        if (cf < 0 && k > 0) break;
+                        const int ck = cidx[k];
+                        if (ck < 0 && k > 0) break;
                         for (int c = 0; c < 3; ++c) Cr[c] = std::fma(cC[3 * k + c], Tr, Cr[c]);
                         Tr *= cT[k];
-                        if (cf >= 0) li = cf;
+                        if (ck >= 0) li = ck;
                         if (Tr <= 1e-4f) { cutoff = k + 1; break; }
                     }
                     for (int k = cutoff; k < K; ++k) cidx[k] = -1;
@@ -705,7 +724,7 @@ void orc_rasterize(const OrcCamera* cam, int32_t N, const float* xys, const floa
                 if (K == 1) {
                     const float zero[3] = {0.f, 0.f, 0.f};
                     raster_pixel_bwd(ent.data(), s, last, px, py, Tfin, zero, Tfin, bg, vo,
-                                     acc.data(), 0);
+                                     acc.data(), 0, &cbk);
                 } else {
                     // compute_chunk_prefix_suffix_kernel (.metal:2820-2839)
                     float p = 1.f;
@@ -721,12 +740,16 @@ void orc_rasterize(const OrcCamera* cam, int32_t N, const float* xys, const floa
                         const int bf = cidx[k];
                         if (cs >= ce || bf < cs) continue;
                         raster_pixel_bwd(ent.data(), cs, std::min(bf, ce - 1), px, py,
-                                         pT[k] * cT[k], &aC[3 * k], Tfin, bg, vo, acc.data(), 0);
+                                         pT[k] * cT[k], &aC[3 * k], Tfin, bg, vo, acc.data(), 0, &cbk);
                     }
                 }
             }
         }
+        fe += cf.e; fr += cf.r; fs += cf.s;
+        be += cbk.e; br += cbk.r; bs += cbk.s;
     }
+    g_fwd_counts.e = fe; g_fwd_counts.r = fr; g_fwd_counts.s = fs;
+    g_bwd_counts.e = be; g_bwd_counts.r = br; g_bwd_counts.s = bs;
     if (!v_out) return;
     // Fixed-order reduction of per-entry gradients into per-gaussian gradients.
     std::vector<double> g9((size_t)N * 9, 0.0);

@@ -96,6 +96,12 @@ void orc_rasterize(const OrcCamera* cam, int32_t N,
                    const float* v_out,
                    float* v_xy, float* v_conic, float* v_rgb, float* v_opacity);
 
+/* Work of the last orc_rasterize call: forward (pairs tested, sigma in
+ * range, composited), backward (pairs tested, sigma in range, with
+ * gradient).  Counts are per (pixel, entry) pair, algorithmic (no lockstep
+ * overshoot).  The backward counts are zero when it did not run. */
+void orc_raster_counts(int64_t out[6]);
+
 /* ---- a7: separable SSIM + L1, training semantics (.metal:3053-3115, 3226-3313, 3396-3464) ----
  * Returns the loss sum over pixels (divide by H*W for msplat's loss value). */
 double orc_ssim_loss(int32_t H, int32_t W, const float* img, const float* gt,

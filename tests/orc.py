@@ -143,6 +143,13 @@ def rasterize(cam: OrcCamera, proj: dict, opac_logits, tile_bins, ids, v_out=Non
     return out
 
 
+def raster_counts():
+    """Pair counts of the last orc_rasterize call (fwd tested/in range/composited, bwd tested/in range/grad)."""
+    out = (c_int64 * 6)()
+    lib().orc_raster_counts(out)
+    return [int(v) for v in out]
+
+
 def ssim_loss(img, gt, ssim_weight=0.2, inv_n=None, want_bufs=False):
     H, W = img.shape[:2]
     if inv_n is None:

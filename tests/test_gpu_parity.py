@@ -54,6 +54,8 @@ def _render_and_compare(dev, scene, dtu=None, cam_idx=0):
     assert_bits_equal(dev.intermediate("final_Ts").reshape(H, W), r["final_Ts"], "final_Ts")
     assert_bits_equal(dev.intermediate("final_index", np.int32).reshape(H, W), r["final_index"], "final_index")
     assert_bits_equal(img, r["out_img"], "out_img")
+    work = dev.raster_work()
+    assert [work[k] for k in dev.RASTER_WORK_KEYS[:3]] == orc.raster_counts()[:3], (work, orc.raster_counts())
     return dev.meta(), counts
 
 
@@ -132,6 +134,8 @@ def _train_compare(dev, scene, steps=1, dtu=None, check_grads=True):
                                    want=want)
         assert abs(loss_g - loss_o) <= 1e-5 * abs(loss_o), (loss_g, loss_o)
         if step == 1:
+            work = dev.raster_work()
+            assert [work[k] for k in dev.RASTER_WORK_KEYS] == orc.raster_counts(), (work, orc.raster_counts())
             assert_bits_equal(dev.intermediate("out_img").reshape(H, W, 3), o["out_img"], "out_img")
             assert_bits_equal(dev.intermediate("v_rendered").reshape(H, W, 3), o["v_rendered"], "v_rendered")
             assert_bits_equal(dev.intermediate("radii", np.int32), o["radii"], "radii")
@@ -163,6 +167,27 @@ def test_train_step_chunked(dev):
 
 def test_train_step_monolithic(dev):
     _train_compare(dev, small_scene(n=12000, width=336, height=208, seed_off=82))
+
+
+def test_raster_counters_match_work(dev):
+    """The rasteriser's in-kernel pair counters (used for the roofline) equal
+    the per-pixel work walk, which the train tests pin against the oracle."""
+    torch = pytest.importorskip("torch")
+    for sc in (small_scene(n=3000, seed_off=84), small_scene(n=30000, width=96, height=64, seed_off=85, spread=0.6)):
+        su = camera.prepare_cam(sc.cameras[0])
+        gt = dev.to_dev(target_for(sc, (su.height, su.width)))
+        g = dev.DeviceGaussians.from_arrays(sc.params(), 3, capacity=sc.n)
+        lib = dev.init()
+        dev._abi.check(lib.msplat_hip_enable_stage_timing(1))
+        try:
+            dev.train_step(g, su, 3, BG, gt, 0.2, LRS, 1)
+            counters = dev.drain_raster_counters()
+            work = dev.raster_work()
+        finally:
+            dev._abi.check(lib.msplat_hip_enable_stage_timing(0))
+        assert counters == (work["fwd_composited"], work["bwd_with_grad"]), (counters, work)
+        assert counters[1] > 0
+        torch.cuda.synchronize()
 
 
 def test_train_three_steps(dev):
