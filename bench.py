@@ -299,11 +299,16 @@ def main():
                 "frac": achieved / FP32_PEAK, "traffic": traffic,
                 "kernel": "k_raster_bwd", "roof": "fp32 vector ALU (the kernel has no matrix-shaped work)",
                 "launches": bwd_n, "launch_ms": bwd_ms, "flops_per_launch": bwd_flops,
-                "grad_pairs_per_launch": train_pairs[1] / max(bwd_n, 1)}
+                "grad_pairs_per_launch": train_pairs[1] / max(bwd_n, 1),
+                "lane_use": train_pairs[1] / max(64 * train_pairs[3], 1)}
     log(f"roofline k_raster_bwd: {bwd_flops / 1e9:.2f} GFLOP/launch ({train_pairs[1] / max(bwd_n, 1) / 1e6:.1f}M "
         f"gradient pairs) in {bwd_ms:.3f} ms = {achieved / 1e12:.2f} TFLOP/s ({100 * achieved / FP32_PEAK:.1f}% "
         f"of fp32 peak); render forward {fwd_flops / 1e9:.2f} GFLOP in {fwd_ms:.3f} ms = "
         f"{fwd_flops / fwd_ms / 1e9:.2f} TFLOP/s")
+    log(f"  wave steps/launch: bwd {train_pairs[3] / max(bwd_n, 1) / 1e6:.2f}M (lanes with gradient "
+        f"{100 * train_pairs[1] / max(64 * train_pairs[3], 1):.1f}%), render fwd "
+        f"{render_pairs[2] / max(fwd_n, 1) / 1e6:.2f}M (lanes compositing "
+        f"{100 * render_pairs[0] / max(64 * render_pairs[2], 1):.1f}%)")
 
     cpu = None
     if not args.no_cpu and args.cpu_steps > 0:

@@ -157,11 +157,13 @@ int msplat_hip_drain_stage_times(double* ms, int64_t* counts, const char** names
                                  int* n_stages, int64_t* n_calls);
 
 /* While stage timing is enabled the rasteriser also counts, on the GPU,
- * counts[0] (pixel, entry) pairs composited by the forward and counts[1]
- * pairs that carry a gradient in the backward, summed over the timed calls.
- * drain returns them (zeros when timing is off) and restarts the sums.  Part
- * of the profiler interface above; the reference has no counterpart. */
-int msplat_hip_drain_raster_counters(int64_t counts[2]);
+ * counts[0] (pixel, entry) pairs composited by the forward, counts[1] pairs
+ * that carry a gradient in the backward, and counts[2] / counts[3] the
+ * entries evaluated per 64-pixel wave in the forward / backward (each one
+ * wave-wide step), summed over the timed calls.  drain returns them (zeros
+ * when timing is off) and restarts the sums.  Part of the profiler interface
+ * above; the reference has no counterpart. */
+int msplat_hip_drain_raster_counters(int64_t counts[4]);
 
 /* Copy a named intermediate of the last render / train step to host memory.
  * Names: xys, depths, radii, conics, colors, aabb, num_tiles_hit,

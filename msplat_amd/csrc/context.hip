@@ -21,6 +21,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 namespace {
 
@@ -607,8 +608,9 @@ int msplat_hip_enable_stage_timing(int enable) {
     if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
     c->timing = enable != 0;
     if (c->timing) {
-        ENSURE(c->work_d, 16);
-        HIP_TRY(hipMemsetAsync(c->work_d.p, 0, 16, c->stream));
+        const size_t wb = (size_t)WORK_SLOTS * WORK_SLOT_U64 * sizeof(unsigned long long);
+        ENSURE(c->work_d, wb);
+        HIP_TRY(hipMemsetAsync(c->work_d.p, 0, wb, c->stream));
     }
     c->n_marks[0] = c->n_marks[1] = 0;
     for (int i = 0; i < kNumStages; ++i) { c->stage_sum[i] = 0.0; c->stage_cnt[i] = 0; }
@@ -637,18 +639,19 @@ int msplat_hip_drain_stage_times(double* ms, int64_t* counts, const char** names
     return MSPLAT_OK;
 }
 
-int msplat_hip_drain_raster_counters(int64_t counts[2]) {
+int msplat_hip_drain_raster_counters(int64_t counts[4]) {
     Ctx* c = g_ctx;
     if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
     if (!counts) return fail(MSPLAT_ERR_ARG, "null counts");
-    counts[0] = counts[1] = 0;
+    for (int k = 0; k < 4; ++k) counts[k] = 0;
     if (!c->timing) return MSPLAT_OK;
-    unsigned long long h[2];
-    HIP_TRY(hipMemcpyAsync(h, c->work_d.p, sizeof(h), hipMemcpyDeviceToHost, c->stream));
+    std::vector<unsigned long long> h((size_t)WORK_SLOTS * WORK_SLOT_U64);
+    const size_t bytes = h.size() * sizeof(unsigned long long);
+    HIP_TRY(hipMemcpyAsync(h.data(), c->work_d.p, bytes, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
-    HIP_TRY(hipMemsetAsync(c->work_d.p, 0, 16, c->stream));
-    counts[0] = (int64_t)h[0];
-    counts[1] = (int64_t)h[1];
+    HIP_TRY(hipMemsetAsync(c->work_d.p, 0, bytes, c->stream));
+    for (int sl = 0; sl < WORK_SLOTS; ++sl)
+        for (int k = 0; k < 4; ++k) counts[k] += (int64_t)h[(size_t)sl * WORK_SLOT_U64 + k];
     return MSPLAT_OK;
 }
 

@@ -104,13 +104,20 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go
                        int* tstart, int* tend, int* tile_bins, Items it, TileLists tl, Meta* meta,
                        Packed pk);
 
+// Raster pair counters: WORK_SLOTS sets of four u64 counters, each set in
+// its own 128-byte line (WORK_SLOT_U64 apart); totals are the sums over sets.
+constexpr int WORK_SLOTS = 64;
+constexpr int WORK_SLOT_U64 = 16;
+
 // Upper bound of the number of (tile, chunk) work items for I intersections.
 inline int64_t items_bound(int64_t T, int64_t I) { return T + I / 512 + I / 2048 + 1; }
 
 // Rasterisation (raster.hip); grids are sized by items_bound / T and the
-// kernels read the exact counts from meta.  A non-null `work` makes the
-// forward add its composited (pixel, entry) pairs to work[0] and the
-// backward its pairs that carry a gradient to work[1].
+// kernels read the exact counts from meta.  A non-null `work` (the counter
+// sets above) makes the forward add its composited (pixel, entry) pairs to
+// counter 0 and its wave-wide entry steps to counter 2, the backward its
+// pairs that carry a gradient to counter 1 and its wave-wide entry steps to
+// counter 3.
 void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Packed pk, float* final_T, int* final_idx,
                        float* out_img, ChunkBufs cb, unsigned long long* work);

@@ -44,6 +44,13 @@ __device__ __forceinline__ Px pixel_of(int t, int tbx, int W, int H) {
     return p;
 }
 
+// Pair counters: WORK_SLOTS copies of the counter set, one 128-byte line
+// each, picked by block id, so that the atomics of concurrent workgroups do
+// not serialise on one address; the host sums the slots.
+__device__ __forceinline__ unsigned long long* work_slot(unsigned long long* work) {
+    return work + (size_t)(blockIdx.x % WORK_SLOTS) * WORK_SLOT_U64;
+}
+
 // Adds the sum of v over the wave into *dst (one atomic per wave).
 __device__ __forceinline__ void wave_count_add(unsigned long long* dst, unsigned v) {
     unsigned long long x = v;
@@ -66,25 +73,44 @@ __device__ __forceinline__ void item_range(const Items& it, const int* tile_bins
     }
 }
 
+// Minimum over the segment X = const, Y in [y0, y1] of
+// q(X, Y) = 0.5 (a X^2 + c Y^2) + b X Y  (c > 0, ic = 1 / c).
+__device__ __forceinline__ float qmin_edge(float a, float b, float c, float ic, float X, float y0,
+                                           float y1) {
+    const float Y = fminf(fmaxf(-b * X * ic, y0), y1);
+    return 0.5f * (a * X * X + c * Y * Y) + b * X * Y;
+}
+
 // Conservative quadrant mask of one entry: bit w is set when the entry can
 // reach alpha >= 1/255 at a pixel of wave w's 8x8 quadrant of the tile at
-// (tx0, ty0).  The reach is the ellipse sigma < min(5.55, ln(255 o)) with
-// margins; entries outside a quadrant are exactly the ones the per-pixel
-// tests would skip there, so culling them changes no result.
+// (tx0, ty0).  The reach is sigma < min(5.55, ln(255 o)); the test takes the
+// exact minimum of the convex quadratic sigma over the quadrant's pixel
+// rectangle (zero when the centre lies inside, else the least of the four
+// edge minima) and compares it with the threshold plus a margin far above
+// fp32 rounding.  Entries outside a quadrant are exactly the ones the
+// per-pixel tests would skip there, so culling them changes no result.
 __device__ __forceinline__ int quad_mask(float x, float y, float a, float b, float c, float o,
                                          int tx0, int ty0) {
     if (!(o >= 0.0039f)) return o == o ? 0 : 0xF;      // alpha <= o < 1/255 everywhere
     const float det = a * c - b * b;
-    if (!(det > 0.f) || !(fabsf(x) < 1e30f) || !(fabsf(y) < 1e30f)) return 0xF;
-    const float thr = fminf(5.55f, __logf(255.f * o) + 0.05f);
-    const float hx = sqrtf(2.f * thr * c / det) * 1.002f + 0.1f;
-    const float hy = sqrtf(2.f * thr * a / det) * 1.002f + 0.1f;
-    if (!(hx < 1e30f) || !(hy < 1e30f)) return 0xF;
+    if (!(det > 0.f) || !(a > 0.f) || !(c > 0.f) || !(a < 1e30f) || !(c < 1e30f) ||
+        !(fabsf(b) < 1e30f) || !(fabsf(x) < 1e30f) || !(fabsf(y) < 1e30f))
+        return 0xF;
+    const float thr = fminf(5.55f, __logf(255.f * o) + 0.05f) * 1.002f + 1e-3f;
+    const float ia = 1.f / a, ic = 1.f / c;
     int m = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const float qx0 = (float)(tx0 + (q & 1) * 8), qy0 = (float)(ty0 + (q >> 1) * 8);
-        if (x + hx >= qx0 && x - hx <= qx0 + 7.f && y + hy >= qy0 && y - hy <= qy0 + 7.f) m |= 1 << q;
+        // offsets d = centre - pixel over the quadrant's pixels
+        const float dx0 = x - (qx0 + 7.f), dx1 = x - qx0;
+        const float dy0 = y - (qy0 + 7.f), dy1 = y - qy0;
+        const bool inside = dx0 <= 0.f && dx1 >= 0.f && dy0 <= 0.f && dy1 >= 0.f;
+        const float e = fminf(fminf(qmin_edge(a, b, c, ic, dx0, dy0, dy1),
+                                    qmin_edge(a, b, c, ic, dx1, dy0, dy1)),
+                              fminf(qmin_edge(c, b, a, ia, dy0, dx0, dx1),
+                                    qmin_edge(c, b, a, ia, dy1, dx0, dx1)));
+        if (inside || e < thr) m |= 1 << q;
     }
     return m;
 }
@@ -113,6 +139,7 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
     float T = 1.f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
     int last = cs - 1;
     unsigned ncomp = 0;     // pairs composited by this pixel
+    unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
     bool done = !px.inside;
     for (int b = cs; b < ce; b += 256) {
         if (__syncthreads_and(done)) break;
@@ -134,6 +161,7 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
         for (int ch = 0; ch < nb; ch += 64) {
             const int q = ch + lane;
             uint64_t m = __ballot(q < nb && ((s_mask[q] >> w) & 1));
+            nwit += __popcll(m);
             while (m) {
                 const int qq = ch + __builtin_ctzll(m);
                 m &= m - 1;
@@ -162,7 +190,11 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
             if (__ballot(!done) == 0) break;
         }
     }
-    if (work) wave_count_add(work, ncomp);
+    if (work) {
+        unsigned long long* ws = work_slot(work);
+        wave_count_add(ws, ncomp);
+        if (lane == 0 && nwit) atomicAdd(ws + 2, (unsigned long long)nwit);
+    }
     if (!px.inside) return;
     if (K == 1) {
         const size_t pix = (size_t)px.i * W + px.j;
@@ -266,6 +298,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     float T = 1.f, Tfin = 1.f, B0 = 0.f, B1 = 0.f, B2 = 0.f, vo0 = 0.f, vo1 = 0.f, vo2 = 0.f;
     int bf = cs - 1;
     unsigned ngrad = 0;     // pairs of this pixel that carry a gradient
+    unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
     if (px.inside) {
         const size_t pix = (size_t)px.i * W + px.j;
         Tfin = final_T[pix];
@@ -312,6 +345,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
         for (int ch = (q0 / 64) * 64; ch < nb; ch += 64) {
             const int q = ch + lane;
             uint64_t m = __ballot(q >= q0 && q < nb && ((s_mask[q] >> w) & 1));
+            nwit += __popcll(m);
             while (m) {
                 const int qq = ch + __builtin_ctzll(m);
                 m &= m - 1;
@@ -369,7 +403,11 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
             }
         }
     }
-    if (work) wave_count_add(work + 1, ngrad);
+    if (work) {
+        unsigned long long* ws = work_slot(work);
+        wave_count_add(ws + 1, ngrad);
+        if (lane == 0 && nwit) atomicAdd(ws + 3, (unsigned long long)nwit);
+    }
 }
 
 // Algorithmic work of the most recent forward (+ backward): one thread per

@@ -212,12 +212,13 @@ def raster_work() -> dict:
 
 
 def drain_raster_counters() -> tuple:
-    """(forward pairs composited, backward pairs with gradient) summed over the
-    calls made while stage timing was on; restarts the sums."""
+    """(forward pairs composited, backward pairs with gradient, forward wave
+    steps, backward wave steps) summed over the calls made while stage timing
+    was on; restarts the sums."""
     lib = init()
-    out = (ctypes.c_int64 * 2)()
+    out = (ctypes.c_int64 * 4)()
     _abi.check(lib.msplat_hip_drain_raster_counters(out))
-    return int(out[0]), int(out[1])
+    return tuple(int(v) for v in out)
 
 
 def meta() -> dict:

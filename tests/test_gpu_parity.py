@@ -185,8 +185,8 @@ def test_raster_counters_match_work(dev):
             work = dev.raster_work()
         finally:
             dev._abi.check(lib.msplat_hip_enable_stage_timing(0))
-        assert counters == (work["fwd_composited"], work["bwd_with_grad"]), (counters, work)
-        assert counters[1] > 0
+        assert counters[:2] == (work["fwd_composited"], work["bwd_with_grad"]), (counters, work)
+        assert counters[1] > 0 and 64 * counters[3] >= counters[1] and 64 * counters[2] >= counters[0]
         torch.cuda.synchronize()
 
 
