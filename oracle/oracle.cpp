@@ -528,6 +528,9 @@ int32_t orc_num_threads(void) {
 }
 
 float orc_expf(float x) { return oexp(x); }
+void orc_expf_n(int64_t n, const float* x, float* y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = oexp(x[i]);
+}
 
 void orc_raster_counts(int64_t out[6]) {
     out[0] = g_fwd_counts.e; out[1] = g_fwd_counts.r; out[2] = g_fwd_counts.s;

@@ -12,7 +12,9 @@ from ctypes import POINTER, c_double, c_float, c_int32, c_int64, c_uint32
 import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB = os.path.join(ROOT, "oracle", "liboracle.so")
+# MSPLAT_ORACLE_LIB points the tests at another build of the oracle (used to
+# check that the pins fail on a deliberately mutated copy).
+LIB = os.environ.get("MSPLAT_ORACLE_LIB") or os.path.join(ROOT, "oracle", "liboracle.so")
 
 
 class OrcCamera(ctypes.Structure):
