@@ -262,17 +262,16 @@ def main():
         if c:
             log(f"  {k:18s} {ms / c:8.3f} ms/call  ({c} calls, {100 * ms / (train_s * 1e3):5.1f}% of wall)")
 
-    # render FPS over the 32 camera poses
-    setups = [camera.prepare_cam(c) for c in cams]
-    out = torch.empty((setups[0].height, setups[0].width, 3), dtype=torch.float32, device="cuda")
-    g = tr.model.g
+    # render FPS over the 32 camera poses (render_from_pose into a device buffer)
+    out = torch.empty((cams[0].height, cams[0].width, 3), dtype=torch.float32, device="cuda")
+    poses = [np.asarray(c.cam_to_world, np.float32) for c in cams]
     for i in range(5):
-        device.render(g, setups[i % len(setups)], degree, bg, out=out)
+        tr.render_pose_device(poses[i % len(poses)], i % len(poses), out)
     _abi.check(lib.msplat_hip_enable_stage_timing(1))
     device.sync()
     r0 = time.perf_counter()
     for i in range(args.frames):
-        device.render(g, setups[i % len(setups)], degree, bg, out=out)
+        tr.render_pose_device(poses[i % len(poses)], i % len(poses), out)
     device.sync()
     r1 = time.perf_counter()
     rstages, _ = stage_times(lib)

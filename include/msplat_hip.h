@@ -137,6 +137,13 @@ int msplat_hip_render(const MsplatRenderArgs* a, float* out_img);
  * msplat_metal.mm:1328). */
 int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* loss_out);
 
+/* Loss value (sum of per-pixel losses / (H W)) of the most recent train step
+ * called with loss_out == NULL.  wait == 0 returns the value of the latest
+ * step known to have finished without waiting (NaN if none) — the reference
+ * likewise reads its loss buffer without waiting (msplat_metal.mm:1328);
+ * wait != 0 first waits for the latest step. */
+int msplat_hip_last_loss(float* loss, int wait);
+
 /* msplat_densify (bindings.h:69-84).  Waits for the result and returns the
  * new gaussian count in *new_count. */
 int msplat_hip_densify(const MsplatDensifyArgs* a, int32_t* new_count);
@@ -145,6 +152,10 @@ int msplat_hip_densify(const MsplatDensifyArgs* a, int32_t* new_count);
  * (the reference fills random_samples with mt19937 on the host,
  * model.cpp:248-253). */
 int msplat_hip_randn(float* dst, int64_t n, uint64_t seed);
+
+/* p[i] = min(p[i], hi) for i < n on the context stream: the opacity reset of
+ * afterTrain (model.cpp:280-287 clamps the logits on the host). */
+int msplat_hip_clamp_max(float* p, int64_t n, float hi);
 
 /* Per-stage GPU timing (msplat_enable_gpu_timing / msplat_drain_stage_times,
  * bindings.h:28-33).  When enabled every stage of every render / train call is

@@ -1,0 +1,154 @@
+/*
+ * msplat_trainer.h — C API of the host-side trainer (libmsplat_hip.so).
+ *
+ * Mirrors the trainer part of the reference's C API
+ * (core/include/msplat_c_api.h:16-118: MsplatConfig, MsplatStats,
+ * MsplatPixelBuffer, msplat_trainer_step / render / render_pose /
+ * render_pose_to_buffer / splat_count / iteration / destroy) and of
+ * GaussianTrainer (python/bindings.cpp:101-280).  The reference builds a
+ * trainer from a Dataset (COLMAP / Nerfstudio loading, out of scope here);
+ * this one is built from gaussian parameter arrays, cameras and target
+ * images, host or device resident.  Everything runs through the C ABI of
+ * msplat_hip.h; call msplat_hip_init first.
+ */
+#ifndef MSPLAT_TRAINER_H
+#define MSPLAT_TRAINER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* MsplatConfig (msplat_c_api.h:16-33) without the dataset-only fields
+ * (keepCrs, downscaleFactor), plus the cull thresholds model.cpp:263
+ * hard-codes, the camera order and its seed. */
+typedef struct MsplatTrainerConfig {
+    int32_t iterations;
+    int32_t shDegree;
+    int32_t shDegreeInterval;   /* <= 0: all bands from the first step */
+    float ssimWeight;
+    int32_t numDownscales;
+    int32_t resolutionSchedule;
+    int32_t refineEvery;
+    int32_t warmupLength;
+    int32_t resetAlphaEvery;
+    float densifyGradThresh;
+    float densifySizeThresh;
+    int32_t stopScreenSizeAt;
+    float splitScreenSize;
+    float bgColor[3];
+    float cullAlphaThresh;      /* model.cpp:263: 0.1 */
+    float cullScaleThresh;      /* 0.5 */
+    float cullScreenSize;       /* 0.15 */
+    int32_t shuffleCameras;     /* 1: std::shuffle with mt19937(seed) per epoch (bindings.cpp:127-137) */
+    uint32_t seed;              /* 42 in the reference */
+} MsplatTrainerConfig;
+
+static inline MsplatTrainerConfig msplat_trainer_default_config(void) {
+    MsplatTrainerConfig c;
+    c.iterations = 30000; c.shDegree = 3; c.shDegreeInterval = 1000; c.ssimWeight = 0.2f;
+    c.numDownscales = 2; c.resolutionSchedule = 3000; c.refineEvery = 100; c.warmupLength = 500;
+    c.resetAlphaEvery = 30; c.densifyGradThresh = 0.0002f; c.densifySizeThresh = 0.01f;
+    c.stopScreenSizeAt = 4000; c.splitScreenSize = 0.05f;
+    c.bgColor[0] = 0.6130f; c.bgColor[1] = 0.0101f; c.bgColor[2] = 0.3984f;
+    c.cullAlphaThresh = 0.1f; c.cullScaleThresh = 0.5f; c.cullScreenSize = 0.15f;
+    c.shuffleCameras = 1; c.seed = 42;
+    return c;
+}
+
+/* A pinhole training camera (input_data.hpp:20-38); camToWorld is a
+ * row-major 4x4 OpenGL pose. */
+typedef struct MsplatTrainerCamera {
+    int32_t width, height;
+    float fx, fy, cx, cy;
+    float camToWorld[16];
+} MsplatTrainerCamera;
+
+/* Model::CamSetup plus the matrices prepareCam caches (model.hpp:33-38,
+ * model.cpp:490-534): viewmat = [R^T | -R^T T] of the OpenCV-flipped pose,
+ * projmat = P V (near 0.001, far 1000), both row-major. */
+typedef struct MsplatCamSetup {
+    float fx, fy, cx, cy;
+    int32_t width, height;
+    float viewmat[16];
+    float projmat[16];
+    float cam_pos[3];
+    int32_t tile_bounds[3];
+} MsplatCamSetup;
+
+/* prepareCam for one camera at an integer downscale factor (host only, no
+ * device work).  Returns 0 or a negative code. */
+int32_t msplat_prepare_cam(const MsplatTrainerCamera* cam, int32_t downscale, MsplatCamSetup* out);
+
+/* MsplatStats (msplat_c_api.h:58-62). */
+typedef struct MsplatStats {
+    int32_t iteration;
+    int32_t splatCount;
+    float msPerStep;
+} MsplatStats;
+
+/* MsplatPixelBuffer (msplat_c_api.h:74-78): RGB float32 HWC, caller free()s. */
+typedef struct MsplatPixelBuffer {
+    float* data;
+    int32_t width;
+    int32_t height;
+} MsplatPixelBuffer;
+
+typedef void* MsplatTrainer;
+
+/* Builds a trainer.  params[6] = means[N,3], scales[N,3] (log), quats[N,4]
+ * (w,x,y,z), f_dc[N,3], f_rest[N,(shDegree+1)^2-1,3], opacities[N] (logits);
+ * targets[i] is the full-resolution [H,W,3] image of cameras[i] (images for
+ * downscaled steps are box-filtered from it once, on the host).
+ * on_device: 1 if params and targets are device pointers.  Returns NULL on
+ * error (message in msplat_trainer_last_error). */
+MsplatTrainer msplat_trainer_create(const MsplatTrainerConfig* config, int64_t n,
+                                    const float* const params[6], int32_t n_cameras,
+                                    const MsplatTrainerCamera* cameras,
+                                    const float* const* targets, int32_t on_device);
+void msplat_trainer_destroy(MsplatTrainer t);
+const char* msplat_trainer_last_error(void);
+
+/* One training iteration (GaussianTrainer::step, bindings.cpp:144-167):
+ * fullIteration, schedulersStep, afterTrain, commit.  msPerStep is host
+ * time of the enqueue (the reference measures the same span). */
+MsplatStats msplat_trainer_step(MsplatTrainer t);
+
+/* Loss of the most recent step known to have completed (wait = 0) or of
+ * the latest step (wait = 1). */
+float msplat_trainer_last_loss(MsplatTrainer t, int32_t wait);
+
+/* Render camera cameraIndex at the current step's resolution (host copy). */
+MsplatPixelBuffer msplat_trainer_render(MsplatTrainer t, int32_t cameraIndex);
+
+/* Render an arbitrary pose with the intrinsics of refCameraIndex
+ * (render_from_pose, bindings.cpp:236-259; msplat_c_api.h:101). */
+MsplatPixelBuffer msplat_trainer_render_pose(MsplatTrainer t, const float camToWorld[16],
+                                             int32_t refCameraIndex);
+
+/* Same into a caller-provided RGBA8 host buffer (msplat_c_api.h:106-108):
+ * call with outRGBA = NULL to get the size.  Returns 0 or a negative code. */
+int32_t msplat_trainer_render_pose_to_buffer(MsplatTrainer t, const float camToWorld[16],
+                                             int32_t refCameraIndex, uint8_t* outRGBA,
+                                             int32_t* outWidth, int32_t* outHeight);
+
+/* Same into a caller-provided device buffer of H*W*3 floats (no host copy,
+ * no synchronisation): the display-loop form of renderFromPoseToBuffer. */
+int32_t msplat_trainer_render_pose_device(MsplatTrainer t, const float camToWorld[16],
+                                          int32_t refCameraIndex, float* outDevice,
+                                          int32_t* outWidth, int32_t* outHeight);
+
+int32_t msplat_trainer_splat_count(MsplatTrainer t);
+int32_t msplat_trainer_iteration(MsplatTrainer t);
+
+/* Device pointer and row count of parameter group g (0..5) or of its Adam
+ * moments (which = 0 params, 1 exp_avg, 2 exp_avg_sq); the first
+ * splat_count rows are active.  Valid until the next step. */
+int32_t msplat_trainer_group(MsplatTrainer t, int32_t g, int32_t which, float** devPtr,
+                             int64_t* rows, int64_t* rowFloats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -88,7 +88,49 @@ class DensifyArgs(ctypes.Structure):
     ]
 
 
+class TrainerConfig(ctypes.Structure):
+    """MsplatTrainerConfig (include/msplat_trainer.h)."""
+
+    _fields_ = [
+        ("iterations", c_int32), ("shDegree", c_int32), ("shDegreeInterval", c_int32),
+        ("ssimWeight", c_float), ("numDownscales", c_int32), ("resolutionSchedule", c_int32),
+        ("refineEvery", c_int32), ("warmupLength", c_int32), ("resetAlphaEvery", c_int32),
+        ("densifyGradThresh", c_float), ("densifySizeThresh", c_float), ("stopScreenSizeAt", c_int32),
+        ("splitScreenSize", c_float), ("bgColor", c_float * 3),
+        ("cullAlphaThresh", c_float), ("cullScaleThresh", c_float), ("cullScreenSize", c_float),
+        ("shuffleCameras", c_int32), ("seed", c_uint32),
+    ]
+
+
+class TrainerCamera(ctypes.Structure):
+    """MsplatTrainerCamera (include/msplat_trainer.h)."""
+
+    _fields_ = [("width", c_int32), ("height", c_int32), ("fx", c_float), ("fy", c_float),
+                ("cx", c_float), ("cy", c_float), ("camToWorld", c_float * 16)]
+
+
+class CamSetupC(ctypes.Structure):
+    """MsplatCamSetup (include/msplat_trainer.h)."""
+
+    _fields_ = [("fx", c_float), ("fy", c_float), ("cx", c_float), ("cy", c_float),
+                ("width", c_int32), ("height", c_int32), ("viewmat", c_float * 16), ("projmat", c_float * 16),
+                ("cam_pos", c_float * 3), ("tile_bounds", c_int32 * 3)]
+
+
+class Stats(ctypes.Structure):
+    """MsplatStats (include/msplat_trainer.h)."""
+
+    _fields_ = [("iteration", c_int32), ("splatCount", c_int32), ("msPerStep", c_float)]
+
+
+class PixelBuffer(ctypes.Structure):
+    """MsplatPixelBuffer (include/msplat_trainer.h)."""
+
+    _fields_ = [("data", POINTER(c_float)), ("width", c_int32), ("height", c_int32)]
+
+
 # (name, restype, argtypes) for every symbol declared in include/msplat_hip.h
+# and include/msplat_trainer.h
 SIGNATURES = [
     ("msplat_hip_init", c_int, [c_int]),
     ("msplat_hip_shutdown", c_int, []),
@@ -105,14 +147,34 @@ SIGNATURES = [
     ("msplat_hip_sync", c_int, []),
     ("msplat_hip_render", c_int, [POINTER(RenderArgs), c_void_p]),
     ("msplat_hip_train_step", c_int, [POINTER(TrainArgs), c_void_p, POINTER(c_float)]),
+    ("msplat_hip_last_loss", c_int, [POINTER(c_float), c_int]),
     ("msplat_hip_densify", c_int, [POINTER(DensifyArgs), POINTER(c_int32)]),
     ("msplat_hip_randn", c_int, [c_void_p, c_int64, c_uint64]),
+    ("msplat_hip_clamp_max", c_int, [c_void_p, c_int64, c_float]),
     ("msplat_hip_enable_stage_timing", c_int, [c_int]),
     ("msplat_hip_drain_stage_times", c_int,
      [POINTER(c_double), POINTER(c_int64), POINTER(c_char_p), c_int, POINTER(c_int), POINTER(c_int64)]),
     ("msplat_hip_copy_intermediate", c_int, [c_char_p, c_void_p, POINTER(c_size_t)]),
     ("msplat_hip_raster_work", c_int, [POINTER(c_int64)]),
     ("msplat_hip_drain_raster_counters", c_int, [POINTER(c_int64)]),
+    # include/msplat_trainer.h
+    ("msplat_trainer_create", c_void_p,
+     [POINTER(TrainerConfig), c_int64, c_void_p * 6, c_int32, POINTER(TrainerCamera), POINTER(c_void_p), c_int32]),
+    ("msplat_trainer_destroy", None, [c_void_p]),
+    ("msplat_trainer_last_error", c_char_p, []),
+    ("msplat_trainer_step", Stats, [c_void_p]),
+    ("msplat_trainer_last_loss", c_float, [c_void_p, c_int32]),
+    ("msplat_trainer_render", PixelBuffer, [c_void_p, c_int32]),
+    ("msplat_trainer_render_pose", PixelBuffer, [c_void_p, POINTER(c_float), c_int32]),
+    ("msplat_trainer_render_pose_to_buffer", c_int32,
+     [c_void_p, POINTER(c_float), c_int32, c_void_p, POINTER(c_int32), POINTER(c_int32)]),
+    ("msplat_trainer_render_pose_device", c_int32,
+     [c_void_p, POINTER(c_float), c_int32, c_void_p, POINTER(c_int32), POINTER(c_int32)]),
+    ("msplat_prepare_cam", c_int32, [POINTER(TrainerCamera), c_int32, POINTER(CamSetupC)]),
+    ("msplat_trainer_splat_count", c_int32, [c_void_p]),
+    ("msplat_trainer_iteration", c_int32, [c_void_p]),
+    ("msplat_trainer_group", c_int32,
+     [c_void_p, c_int32, c_int32, POINTER(c_void_p), POINTER(c_int64), POINTER(c_int64)]),
 ]
 
 _lib = None

@@ -1,9 +1,9 @@
 """Camera set-up: OpenGL camera-to-world pose -> view / projection matrices.
 
-Mirrors Model::prepareCam (/root/reference/core/src/model.cpp:490-534): the
-OpenGL -> OpenCV column flip, viewmat = [R^T | -R^T T], projection with near
-0.001 / far 1000 and FOV from W / (2 fx), projmat = P @ V accumulated in fp32,
-tile bounds ceil(W/16) x ceil(H/16).
+Model::prepareCam (core/src/model.cpp:490-534) lives in the C++ host layer
+(msplat_amd/host/model.cpp): the OpenGL -> OpenCV column flip, viewmat =
+[R^T | -R^T T], projection with near 0.001 / far 1000 and FOV from W / (2 fx),
+projmat = P V accumulated in fp32, tile bounds ceil(W/16) x ceil(H/16).
 """
 from __future__ import annotations
 
@@ -49,42 +49,24 @@ class CamSetup:
 
 
 def prepare_cam(cam: Camera, downscale: int = 1) -> CamSetup:
-    f32 = np.float32
-    sf = f32(downscale)
-    fx, fy, cx, cy = f32(cam.fx) / sf, f32(cam.fy) / sf, f32(cam.cx) / sf, f32(cam.cy) / sf
-    height, width = int(cam.height / float(sf)), int(cam.width / float(sf))
-    fov_x = f32(2.0) * f32(math.atan(float(f32(width) / (f32(2.0) * fx))))
-    fov_y = f32(2.0) * f32(math.atan(float(f32(height) / (f32(2.0) * fy))))
-    d = np.asarray(cam.cam_to_world, dtype=f32).reshape(16)
-    R = np.empty((3, 3), f32)
-    T = np.empty(3, f32)
-    for i in range(3):
-        R[i, 0], R[i, 1], R[i, 2], T[i] = d[i * 4 + 0], -d[i * 4 + 1], -d[i * 4 + 2], d[i * 4 + 3]
-    Rinv = R.T.copy()
-    Tinv = np.empty(3, f32)
-    for i in range(3):
-        Tinv[i] = -(Rinv[i, 0] * T[0] + Rinv[i, 1] * T[1] + Rinv[i, 2] * T[2])
-    vm = np.array([Rinv[0, 0], Rinv[0, 1], Rinv[0, 2], Tinv[0],
-                   Rinv[1, 0], Rinv[1, 1], Rinv[1, 2], Tinv[1],
-                   Rinv[2, 0], Rinv[2, 1], Rinv[2, 2], Tinv[2],
-                   0, 0, 0, 1], dtype=f32)
-    t_p = f32(0.001) * f32(math.tan(float(f32(0.5) * fov_y)))
-    r_p = f32(0.001) * f32(math.tan(float(f32(0.5) * fov_x)))
-    n, fa = f32(0.001), f32(1000.0)
-    pm = np.array([n / r_p, 0, 0, 0,
-                   0, n / t_p, 0, 0,
-                   0, 0, (fa + n) / (fa - n), -fa * n / (fa - n),
-                   0, 0, 1, 0], dtype=f32)
-    pvm = np.zeros(16, dtype=f32)
-    for i in range(4):
-        for j in range(4):
-            acc = f32(0.0)
-            for k in range(4):
-                acc = f32(acc + f32(pm[i * 4 + k] * vm[k * 4 + j]))
-            pvm[i * 4 + j] = acc
-    tb = ((width + BLOCK - 1) // BLOCK, (height + BLOCK - 1) // BLOCK, 1)
-    return CamSetup(float(fx), float(fy), float(cx), float(cy), height, width,
-                    vm.reshape(4, 4), pvm.reshape(4, 4), T.copy(), tb)
+    """Model::prepareCam through the host library (msplat_prepare_cam in
+    include/msplat_trainer.h), so that every caller gets the matrices the C++
+    trainer uses, bit for bit.  Host-only: no device is touched."""
+    import ctypes
+
+    from . import _abi
+    lib = _abi.load()
+    k = _abi.TrainerCamera()
+    k.width, k.height = int(cam.width), int(cam.height)
+    k.fx, k.fy, k.cx, k.cy = float(cam.fx), float(cam.fy), float(cam.cx), float(cam.cy)
+    k.camToWorld[:] = [float(v) for v in np.asarray(cam.cam_to_world, np.float32).reshape(16)]
+    out = _abi.CamSetupC()
+    if lib.msplat_prepare_cam(ctypes.byref(k), int(downscale), ctypes.byref(out)) != 0:
+        raise ValueError("prepare_cam: bad camera or downscale factor")
+    vm = np.array(out.viewmat[:], np.float32).reshape(4, 4)
+    pm = np.array(out.projmat[:], np.float32).reshape(4, 4)
+    return CamSetup(out.fx, out.fy, out.cx, out.cy, out.height, out.width, vm, pm,
+                    np.array(out.cam_pos[:], np.float32), tuple(out.tile_bounds[:]))
 
 
 def look_at(position, target=(0.0, 0.0, 0.0), up=(0.0, 1.0, 0.0)) -> np.ndarray:

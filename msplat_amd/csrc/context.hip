@@ -77,6 +77,11 @@ struct Ctx {
 
     Meta meta{};
     bool meta_valid = false;
+    // Loss of the most recent train step known to have completed (NaN before
+    // any); each step copies its loss to loss_h[1] asynchronously.
+    float last_loss = __builtin_nanf("");
+    float loss_scale = 1.f;
+    bool loss_pending = false;
     int64_t max_items = 0;
     int last_N = 0, last_T = 0, last_W = 0, last_H = 0;
     bool have_bwd = false;
@@ -317,6 +322,10 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
     HIP_TRY(hipMemcpyAsync(c->meta_h, c->meta_d.p, sizeof(Meta), hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     if (c->timing) stage_fold(c, c->cur ^ 1);   // the previous call has completed
+    if (c->loss_pending) {                       // so has its loss copy
+        c->last_loss = c->loss_h[1] * c->loss_scale;
+        c->loss_pending = false;
+    }
     const int64_t I64 = c->meta_h->total_isect;
     if (I64 > (int64_t)0x7FFFFFFF - 4096)
         return fail(MSPLAT_ERR_ARG, "%lld tile intersections exceed the 32-bit index range",
@@ -459,8 +468,13 @@ int msplat_hip_memcpy_d2d(void* dst, const void* src, size_t bytes) {
 int msplat_hip_commit(void) { return g_ctx ? MSPLAT_OK : fail(MSPLAT_ERR_NOINIT, "not initialised"); }
 
 int msplat_hip_sync(void) {
-    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
-    HIP_TRY(hipStreamSynchronize(g_ctx->stream));
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (c->loss_pending) {
+        c->last_loss = c->loss_h[1] * c->loss_scale;
+        c->loss_pending = false;
+    }
     return MSPLAT_OK;
 }
 
@@ -541,7 +555,34 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
         HIP_TRY(hipMemcpyAsync(c->loss_h, c->loss_d.p, 4, hipMemcpyDeviceToHost, c->stream));
         HIP_TRY(hipStreamSynchronize(c->stream));
         *loss_out = c->loss_h[0] / (float)(p.H * p.W);
+        c->last_loss = *loss_out;
+        c->loss_pending = false;
+    } else {
+        c->loss_scale = 1.f / (float)(p.H * p.W);
+        HIP_TRY(hipMemcpyAsync(c->loss_h + 1, c->loss_d.p, 4, hipMemcpyDeviceToHost, c->stream));
+        c->loss_pending = true;
     }
+    return MSPLAT_OK;
+}
+
+int msplat_hip_last_loss(float* loss, int wait) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!loss) return fail(MSPLAT_ERR_ARG, "null loss");
+    if (c->loss_pending && wait) {
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        c->last_loss = c->loss_h[1] * c->loss_scale;
+        c->loss_pending = false;
+    }
+    *loss = c->last_loss;
+    return MSPLAT_OK;
+}
+
+int msplat_hip_clamp_max(float* p, int64_t n, float hi) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (n < 0 || (n > 0 && !p)) return fail(MSPLAT_ERR_ARG, "bad clamp arguments");
+    launch_clamp_max(g_ctx->stream, p, n, hi);
+    HIP_TRY(hipGetLastError());
     return MSPLAT_OK;
 }
 

@@ -172,6 +172,12 @@ __global__ __launch_bounds__(256) void k_copy_back(const float* __restrict__ src
 
 __global__ void k_read_count(const int* kp, int64_t last, int* out) { out[0] = kp[last]; }
 
+// Opacity reset of afterTrain (model.cpp:280-287): logits above hi become hi.
+__global__ __launch_bounds__(256) void k_clamp_max(float* __restrict__ p, int64_t n, float hi) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = p[i] > hi ? hi : p[i];
+}
+
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -179,6 +185,11 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 void launch_randn(hipStream_t s, float* dst, int64_t n, uint64_t seed) {
     if (n <= 0) return;
     hipLaunchKernelGGL(k_randn, dim3(blocks_for(n)), dim3(256), 0, s, dst, n, seed);
+}
+
+void launch_clamp_max(hipStream_t s, float* p, int64_t n, float hi) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_clamp_max, dim3(blocks_for(n)), dim3(256), 0, s, p, n, hi);
 }
 
 void launch_densify(hipStream_t s, const DensifyHP& hp, const float* gnorm, const float* vis,

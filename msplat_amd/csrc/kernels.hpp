@@ -166,6 +166,7 @@ struct DensifyHP {
     int fr;
 };
 void launch_randn(hipStream_t s, float* dst, int64_t n, uint64_t seed);
+void launch_clamp_max(hipStream_t s, float* p, int64_t n, float hi);
 void launch_densify(hipStream_t s, const DensifyHP& hp, const float* gnorm, const float* vis,
                     const float* max2d, float* const bufs[6], float* const m[6],
                     float* const v[6], const float* rnd, int* split, int* dup, int* sp,

@@ -20,12 +20,17 @@ from msplat_amd import _abi
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "msplat_hip.h")
+TRAINER_HEADER = os.path.join(ROOT, "include", "msplat_trainer.h")
 
 
 def _declared():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(msplat_hip_\w+)\s*\(", text)))
+    """Functions declared in both headers (static inline helpers excluded)."""
+    names = set()
+    for h in (HEADER, TRAINER_HEADER):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        text = re.sub(r"static inline[^{]*\{.*?\n\}", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(msplat_(?:hip_|trainer_|prepare_cam)\w*)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_and_ctypes_signatures_agree():
@@ -41,19 +46,23 @@ def test_library_exports_every_declared_symbol():
     nm = shutil.which("nm")
     if nm:
         out = subprocess.check_output([nm, "-D", "--defined-only", _abi.LIB_PATH], text=True)
-        exported = set(re.findall(r"\bT (msplat_hip_\w+)", out))
+        exported = set(re.findall(r"\bT (msplat_(?:hip_|trainer_|prepare_cam)\w*)", out))
         assert set(_declared()) <= exported
 
 
 STRUCTS = {"MsplatRenderArgs": _abi.RenderArgs, "MsplatTrainArgs": _abi.TrainArgs,
-           "MsplatDensifyArgs": _abi.DensifyArgs}
+           "MsplatDensifyArgs": _abi.DensifyArgs, "MsplatTrainerConfig": _abi.TrainerConfig,
+           "MsplatTrainerCamera": _abi.TrainerCamera, "MsplatStats": _abi.Stats,
+           "MsplatCamSetup": _abi.CamSetupC,
+           "MsplatPixelBuffer": _abi.PixelBuffer}
 
 
 def test_struct_layouts_match_header(tmp_path):
     cc = shutil.which("gcc") or shutil.which("cc")
     if not cc:
         pytest.skip("no host C compiler")
-    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"',
+             f'#include "{TRAINER_HEADER}"', "int main(void) {"]
     for cname, py in STRUCTS.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in py._fields_:

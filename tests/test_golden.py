@@ -1,0 +1,107 @@
+"""Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
+
+CPU: the oracle still reproduces every stored stage output (forward stages
+bit for bit, gradients and Adam state to fp32 rounding), so a change of the
+checker shows up here.  GPU: the HIP path reproduces the stored outputs
+directly (forward bit for bit, gradients and updated parameters within the
+parity tolerance), without running the oracle.
+"""
+from __future__ import annotations
+
+import glob
+import os
+
+import numpy as np
+import pytest
+
+import orc
+from helpers import assert_bits_equal, grad_close
+from msplat_amd import camera
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+FIXTURES = sorted(glob.glob(os.path.join(HERE, "golden", "*.npz")))
+
+
+def _load(path):
+    with np.load(path, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _setup(f):
+    W, H = int(f["width"]), int(f["height"])
+    return camera.CamSetup(float(f["fx"]), float(f["fy"]), float(f["cx"]), float(f["cy"]), H, W,
+                           f["viewmat"], f["projmat"], f["cam_pos"], ((W + 15) // 16, (H + 15) // 16, 1))
+
+
+def _params(f):
+    return [f[k] for k in ("means", "scales", "quats", "f_dc", "f_rest", "opacities")]
+
+
+def test_fixtures_present():
+    names = {os.path.basename(p) for p in FIXTURES}
+    assert {"sh3_small.npz", "sh1_dense.npz"} <= names
+
+
+@pytest.mark.parametrize("path", FIXTURES, ids=lambda p: os.path.basename(p))
+def test_oracle_reproduces_golden(path):
+    f = _load(path)
+    su, deg = _setup(f), int(f["degree"])
+    cam = orc.camera(su, deg, deg, f["background"])
+    p = orc.project(cam, f["means"], f["scales"], f["quats"], f["f_dc"], f["f_rest"])
+    vis = p["radii"] > 0
+    assert_bits_equal(p["radii"], f["radii"], "radii")
+    for k in ("xys", "depths", "conics", "colors", "aabb"):
+        assert_bits_equal(p[k][vis], f[k][vis], k)
+    counts, tb, ids = orc.bin_sort(cam, p)
+    assert_bits_equal(tb, f["tile_bins"], "tile_bins")
+    assert_bits_equal(ids, f["gaussian_ids"], "gaussian_ids")
+    r = orc.rasterize(cam, p, f["opacities"], tb, ids)
+    for k in ("final_Ts", "final_index", "out_img"):
+        assert_bits_equal(r[k], f[k], k)
+    params = [np.ascontiguousarray(a, np.float32).copy() for a in _params(f)]
+    m = [np.zeros_like(a) for a in params]
+    v = [np.zeros_like(a) for a in params]
+    n = params[0].shape[0]
+    vc, gn, mx = (np.zeros(n, np.float32) for _ in range(3))
+    loss, o = orc.train_step(cam, params, m, v, orc.adam_hparams(list(f["lrs"]), 1), f["gt"], 0.2, vc, gn, mx,
+                             want=("v_rendered", "v_xy", "v_conic", "v_rgb", "v_opacity"))
+    assert np.float32(loss) == f["loss"]
+    assert_bits_equal(o["v_rendered"], f["v_rendered"], "v_rendered")
+    for k in ("v_xy", "v_conic", "v_rgb", "v_opacity"):
+        grad_close(o[k], f[k], rtol=1e-6, floor=1e-7, what=k)
+    for i in range(6):
+        grad_close(params[i], f[f"param{i}_after"], rtol=1e-6, floor=1e-7, what=f"param{i}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", FIXTURES, ids=lambda p: os.path.basename(p))
+def test_gpu_matches_golden(path):
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from msplat_amd import device
+    device.init(0)
+    f = _load(path)
+    su, deg = _setup(f), int(f["degree"])
+    bg = f["background"]
+    n = f["means"].shape[0]
+    g = device.DeviceGaussians.from_arrays(_params(f), deg, capacity=n)
+    img = device.render(g, su, deg, bg).cpu().numpy()
+    assert_bits_equal(img, f["out_img"], "out_img")
+    assert_bits_equal(device.intermediate("tile_bins", np.int32).reshape(-1, 2), f["tile_bins"], "tile_bins")
+    assert_bits_equal(device.intermediate("gaussian_ids", np.int32), f["gaussian_ids"], "gaussian_ids")
+    H, W = su.height, su.width
+    assert_bits_equal(device.intermediate("final_index", np.int32).reshape(H, W), f["final_index"], "final_index")
+    grads = {k: torch.zeros((n, d), dtype=torch.float32, device="cuda") for k, d in
+             (("v_mean3d", 3), ("v_scale", 3), ("v_quat", 4))}
+    loss = device.train_step(g, su, deg, bg, device.to_dev(f["gt"]), 0.2, list(f["lrs"]), 1, grads_out=grads)
+    assert abs(loss - float(f["loss"])) <= 1e-5 * abs(float(f["loss"]))
+    assert_bits_equal(device.intermediate("v_rendered").reshape(H, W, 3), f["v_rendered"], "v_rendered")
+    for k, d in (("v_xy", 2), ("v_conic", 3), ("v_rgb", 3), ("v_opacity", 1)):
+        got = device.intermediate(k)
+        grad_close(got.reshape(n, d) if d > 1 else got, f[k], what=k)
+    for k in ("v_mean3d", "v_scale", "v_quat"):
+        grad_close(grads[k].cpu().numpy(), f[k], what=k)
+    gp = g.numpy()
+    for i in range(6):
+        grad_close(gp[i], f[f"param{i}_after"], rtol=1e-3, floor=1e-6, what=f"param{i}")
