@@ -165,27 +165,26 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
             while (m) {
                 const int qq = ch + __builtin_ctzll(m);
                 m &= m - 1;
-                if (done) continue;
+                // Branch-free per lane: a pair that is skipped, stops the pixel
+                // or composites only selects what it writes (colour sums get
+                // + c * 0 when not compositing, which leaves them unchanged).
                 const float4 g = s_geo[qq];
                 const float4 c = s_col[qq];
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-                const bool in_range = !(sigma < 0.f || sigma >= 5.55f);
                 const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
-                if (!in_range || alpha < 1.f / 255.f) continue;
+                const bool hit = !done && !(sigma < 0.f || sigma >= 5.55f) && !(alpha < 1.f / 255.f);
                 const float nT = T * (1.f - alpha);
-                if (nT <= 1e-4f) {
-                    last = b + qq - 1;
-                    done = true;
-                    continue;
-                }
-                const float vis = alpha * T;
+                const bool stop = hit && nT <= 1e-4f;
+                const bool comp = hit && !stop;
+                const float vis = comp ? alpha * T : 0.f;
                 C0 = fmaf(c.z, vis, C0);
                 C1 = fmaf(c.w, vis, C1);
                 C2 = fmaf(s_bl[qq], vis, C2);
-                T = nT;
-                last = b + qq;
-                ++ncomp;
+                T = comp ? nT : T;
+                last = comp ? b + qq : (stop ? b + qq - 1 : last);
+                done = done || stop;
+                ncomp += comp ? 1u : 0u;
             }
             if (__ballot(!done) == 0) break;
         }
