@@ -297,6 +297,9 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     float T = 1.f, Tfin = 1.f, B0 = 0.f, B1 = 0.f, B2 = 0.f, vo0 = 0.f, vo1 = 0.f, vo2 = 0.f;
     int bf = cs - 1;
     unsigned ngrad = 0;     // pairs of this pixel that carry a gradient
+    // gradient value this lane writes after the reductions: lanes 0, 8, ...,
+    // 56 hold the eight transposed sums, lane 1 the ninth; -1 for the others
+    const int kslot = (lane & 7) == 0 ? sum8_value_of_lane(lane) : lane == 1 ? 8 : -1;
     unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
     if (px.inside) {
         const size_t pix = (size_t)px.i * W + px.j;
@@ -358,46 +361,43 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 const bool valid = px.inside && e_idx <= bf && !(sigma < 0.f || sigma >= 5.55f) &&
                                    !(alpha < 1.f / 255.f);
                 if (__ballot(valid) == 0) continue;
-                float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-                float vop = 0.f;
-                if (valid && alpha < 0.999f) {
-                    ++ngrad;
-                    // hardware reciprocal (1 ulp): the backward is compared with a tolerance
-                    const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
-                    T *= ra;
-                    const float fac = alpha * T;
-                    v[5] = fac * vo0;
-                    v[6] = fac * vo1;
-                    v[7] = fac * vo2;
-                    const float r0 = fmaxf(c.z + 0.5f, 0.f), r1 = fmaxf(c.w + 0.5f, 0.f),
-                                r2 = fmaxf(braw + 0.5f, 0.f);
-                    const float t0 = fmaf(r0, T, fmaf(-B0, ra, -ra * tb0));
-                    const float t1 = fmaf(r1, T, fmaf(-B1, ra, -ra * tb1));
-                    const float t2 = fmaf(r2, T, fmaf(-B2, ra, -ra * tb2));
-                    const float v_alpha = 0.f + (t0 * vo0 + t1 * vo1 + t2 * vo2);
-                    B0 = fmaf(r0, fac, B0);
-                    B1 = fmaf(r1, fac, B1);
-                    B2 = fmaf(r2, fac, B2);
-                    const float v_sigma = -alpha * v_alpha;
-                    const float hv = 0.5f * v_sigma;
-                    v[2] = hv * (dx * dx);
-                    v[3] = hv * (dx * dy);
-                    v[4] = hv * (dy * dy);
-                    v[0] = v_sigma * fmaf(g.z, dx, g.w * dy);
-                    v[1] = v_sigma * fmaf(g.w, dx, c.x * dy);
-                    vop = -v_sigma * (1.f - c.y);
-                }
+                // Branch-free per lane: lanes without a gradient compute the
+                // same terms and select zeros / their old state.
+                const bool grad = valid && alpha < 0.999f;
+                ngrad += grad ? 1u : 0u;
+                // hardware reciprocal (1 ulp): the backward is compared with a tolerance
+                const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
+                const float Tn = T * ra;
+                const float fac = grad ? alpha * Tn : 0.f;
+                const float r0 = fmaxf(c.z + 0.5f, 0.f), r1 = fmaxf(c.w + 0.5f, 0.f),
+                            r2 = fmaxf(braw + 0.5f, 0.f);
+                const float t0 = fmaf(r0, Tn, fmaf(-B0, ra, -ra * tb0));
+                const float t1 = fmaf(r1, Tn, fmaf(-B1, ra, -ra * tb1));
+                const float t2 = fmaf(r2, Tn, fmaf(-B2, ra, -ra * tb2));
+                const float v_alpha = 0.f + (t0 * vo0 + t1 * vo1 + t2 * vo2);
+                B0 = fmaf(r0, fac, B0);
+                B1 = fmaf(r1, fac, B1);
+                B2 = fmaf(r2, fac, B2);
+                T = grad ? Tn : T;
+                const float v_sigma = -alpha * v_alpha;
+                const float hv = 0.5f * v_sigma;
+                float v[8];
+                v[0] = grad ? v_sigma * fmaf(g.z, dx, g.w * dy) : 0.f;
+                v[1] = grad ? v_sigma * fmaf(g.w, dx, c.x * dy) : 0.f;
+                v[2] = grad ? hv * (dx * dx) : 0.f;
+                v[3] = grad ? hv * (dx * dy) : 0.f;
+                v[4] = grad ? hv * (dy * dy) : 0.f;
+                v[5] = fac * vo0;
+                v[6] = fac * vo1;
+                v[7] = fac * vo2;
+                const float vop = grad ? -v_sigma * (1.f - c.y) : 0.f;
                 const float u = wave_sum8_transposed(v, lane);
                 const float s8 = wave_sum(vop);
-                // lanes 0, 8, ..., 56 hold the eight sums; lane 1 adds the ninth
-                int k = -1;
-                if ((lane & 7) == 0) k = sum8_value_of_lane(lane);
-                else if (lane == 1) k = 8;
-                if (k >= 0) {
-                    const bool ok = k == 5 ? c.z + 0.5f >= 0.f
-                                  : k == 6 ? c.w + 0.5f >= 0.f
-                                  : k == 7 ? braw + 0.5f >= 0.f : true;
-                    if (ok) atomicAdd(&gacc[(size_t)s_id[qq] * 9 + k], k == 8 ? s8 : u);
+                if (kslot >= 0) {
+                    const bool ok = kslot == 5 ? c.z + 0.5f >= 0.f
+                                  : kslot == 6 ? c.w + 0.5f >= 0.f
+                                  : kslot == 7 ? braw + 0.5f >= 0.f : true;
+                    if (ok) atomicAdd(&gacc[(size_t)s_id[qq] * 9 + kslot], kslot == 8 ? s8 : u);
                 }
             }
         }
