@@ -11,7 +11,8 @@
 //   4. emit one (tile id, gaussian id) pair per intersection, depth order
 //   5. stable radix sort by tile id               (depth order kept per tile)
 //   6. run edges -> per-tile counts; scan -> tile_bins, chunk work items
-//   7. pack the sorted gaussians' raster records (.metal:2128-2137)
+// The rasteriser gathers each entry's projection record by id, in place of
+// the reference's packed per-entry copies (.metal:2128-2137).
 // Equal depths keep ascending id order because both sorts are stable and the
 // first one starts from id order.  Tiles have no size limit (the reference
 // drops entries beyond 2048 per tile).
@@ -32,9 +33,22 @@ __global__ __launch_bounds__(256) void k_gather_hits(int N, const uint32_t* __re
     hits_sorted[r] = tiles_hit[order[r]];
 }
 
-__global__ void k_total(int N, const int* __restrict__ eoff, const int* __restrict__ hits,
-                        Meta* __restrict__ meta) {
-    meta->total_isect = N > 0 ? (int64_t)eoff[N - 1] + hits[N - 1] : 0;
+// Sum of tiles hit over all gaussians (the intersection total), accumulated
+// into meta->total_isect (zeroed before) with one atomic per workgroup.
+constexpr int TOTAL_BLOCKS = 128;
+__global__ __launch_bounds__(256) void k_total_hits(int N, const int* __restrict__ tiles_hit,
+                                                    Meta* __restrict__ meta) {
+    long long v = 0;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < N; i += TOTAL_BLOCKS * 256) v += tiles_hit[i];
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    __shared__ long long sh[4];
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const long long t = sh[0] + sh[1] + sh[2] + sh[3];
+        if (t) atomicAdd(reinterpret_cast<unsigned long long*>(&meta->total_isect),
+                         (unsigned long long)t);
+    }
 }
 
 __global__ __launch_bounds__(256) void k_emit(int N, int tbx, int tby, GaussOut go,
@@ -135,27 +149,19 @@ __global__ __launch_bounds__(256) void k_build_items(int T, Items it) {
     }
 }
 
-__global__ __launch_bounds__(256) void k_pack(int64_t I, const uint32_t* __restrict__ tval,
-                                              GaussOut go, Packed pk) {
-    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= I) return;
-    const int g = (int)tval[p];
-    const float4* rec = go.rec + 4 * (size_t)g;
-    const float4 r0 = rec[0], r1 = rec[1];
-    const float bl = rec[2].x;
-    pk.ids[p] = g;
-    pk.geo[p] = r0;
-    pk.col[p] = r1;
-    pk.bl[p] = bl;
-}
-
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
 
+void launch_total_hits(hipStream_t s, int N, const int* tiles_hit, Meta* meta) {
+    (void)hipMemsetAsync(&meta->total_isect, 0, sizeof(int64_t), s);
+    if (N > 0)
+        hipLaunchKernelGGL(k_total_hits, dim3(TOTAL_BLOCKS), dim3(256), 0, s, N, tiles_hit, meta);
+}
+
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
                         uint32_t* dval2, int* radix_temp, const int* tiles_hit, int* hits_sorted,
-                        int* eoff, int* scan_temp, Meta* meta, uint32_t** order_out) {
+                        int* eoff, int* scan_temp, uint32_t** order_out) {
     const bool flip = launch_radix_sort(s, dkey, dval, dkey2, dval2, N, 32, radix_temp);
     uint32_t* order = flip ? dval2 : dval;
     *order_out = order;
@@ -164,16 +170,15 @@ void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, ui
                            (const uint32_t*)order, tiles_hit, hits_sorted);
         launch_exclusive_scan_i32(s, hits_sorted, eoff, N, scan_temp);
     }
-    hipLaunchKernelGGL(k_total, dim3(1), dim3(1), 0, s, N, (const int*)eoff,
-                       (const int*)hits_sorted, meta);
 }
 
-void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go,
-                       const uint32_t* order, const int* eoff, const int* hits, uint32_t* tkey,
-                       uint32_t* tval, uint32_t* tkey2, uint32_t* tval2, int* radix_temp,
-                       int* tstart, int* tend, int* tile_bins, Items it, TileLists tl, Meta* meta,
-                       Packed pk) {
+const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go,
+                                  const uint32_t* order, const int* eoff, const int* hits,
+                                  uint32_t* tkey, uint32_t* tval, uint32_t* tkey2, uint32_t* tval2,
+                                  int* radix_temp, int* tstart, int* tend, int* tile_bins, Items it,
+                                  TileLists tl, Meta* meta) {
     const int T = p.tbx * p.tby;
+    const uint32_t* sorted_ids = tval;
     (void)hipMemsetAsync(tstart, 0, (size_t)T * 4, s);
     (void)hipMemsetAsync(tend, 0, (size_t)T * 4, s);
     if (I > 0) {
@@ -183,13 +188,13 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go
         while ((1 << bits) < T) ++bits;
         const bool flip = launch_radix_sort(s, tkey, tval, tkey2, tval2, I, bits, radix_temp);
         const uint32_t* sk = flip ? tkey2 : tkey;
-        const uint32_t* sv = flip ? tval2 : tval;
+        sorted_ids = flip ? tval2 : tval;
         hipLaunchKernelGGL(k_tile_edges, dim3(blocks_for(I)), dim3(256), 0, s, I, sk, tstart, tend);
-        hipLaunchKernelGGL(k_pack, dim3(blocks_for(I)), dim3(256), 0, s, I, sv, go, pk);
     }
     hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(SCAN_T), 0, s, T, (const int*)tstart,
                        (const int*)tend, tile_bins, it, tl, meta);
     hipLaunchKernelGGL(k_build_items, dim3(blocks_for(T)), dim3(256), 0, s, T, it);
+    return sorted_ids;
 }
 
 }  // namespace msp

@@ -55,6 +55,7 @@ struct Ctx {
     double stage_sum[kNumStages] = {};
     int64_t stage_cnt[kNumStages] = {};
     int64_t calls = 0;
+    hipEvent_t ev_total = nullptr;   // recorded after the intersection total's copy to the host
 
     // per gaussian
     Buf rec, radii, tiles_hit, gacc;
@@ -62,7 +63,7 @@ struct Ctx {
     // per tile
     Buf tstart, tend, tile_bins, tile_K, tile_item0, l_chunked;
     // per intersection
-    Buf tkey, tval, tkey2, tval2, ttemp, pk_geo, pk_col, pk_bl, pk_ids;
+    Buf tkey, tval, tkey2, tval2, ttemp;
     // per item
     Buf it_tile, it_k, c_T, c_C, c_idx, c_pT, c_aC;
     // per pixel
@@ -75,6 +76,7 @@ struct Ctx {
     // densify scratch
     Buf d_split, d_dup, d_sp, d_dp, d_keep, d_kp, d_tot, d_scratch, d_rnd;
 
+    const uint32_t* sorted_ids = nullptr;   // tile-sorted gaussian ids (tval or tval2)
     Meta meta{};
     bool meta_valid = false;
     // Loss of the most recent train step known to have completed (NaN before
@@ -143,8 +145,7 @@ void free_all(Ctx* c) {
                    &c->gacc, &c->dkey, &c->dval, &c->dkey2, &c->dval2, &c->hits, &c->eoff,
                    &c->dtemp, &c->stemp, &c->tstart, &c->tend, &c->tile_bins, &c->tile_K,
                    &c->tile_item0, &c->l_chunked, &c->tkey, &c->tval, &c->tkey2, &c->tval2,
-                   &c->ttemp, &c->pk_geo,
-                   &c->pk_col, &c->pk_bl, &c->pk_ids, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
+                   &c->ttemp, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
                    &c->hbuf, &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
                    &c->count_d, &c->work_d, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
@@ -157,6 +158,7 @@ void free_all(Ctx* c) {
     for (auto& row : c->ev)
         for (auto& e : row)
             if (e) (void)hipEventDestroy(e);
+    if (c->ev_total) (void)hipEventDestroy(c->ev_total);
     if (c->own) (void)hipStreamDestroy(c->own);
 }
 
@@ -177,12 +179,10 @@ Items items(Ctx* c) {
     return it;
 }
 
-Packed packed(Ctx* c) {
-    Packed pk;
-    pk.geo = P<float4>(c->pk_geo);
-    pk.col = P<float4>(c->pk_col);
-    pk.bl = P<float>(c->pk_bl);
-    pk.ids = P<int>(c->pk_ids);
+Entries packed(Ctx* c) {
+    Entries pk;
+    pk.ids = c->sorted_ids;
+    pk.rec = P<float4>(c->rec);
     return pk;
 }
 
@@ -313,14 +313,18 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
     launch_project_fwd(c->stream, p, a->means3d, a->scales, a->quats, a->features_dc,
                        a->features_rest, a->opacities, go, P<uint32_t>(c->dkey),
                        P<uint32_t>(c->dval), P<float>(c->gacc));
+    // The intersection total goes to the host while the GPU sorts by depth:
+    // the host waits on an event recorded after the copy, not on the stream.
+    launch_total_hits(c->stream, N, P<int>(c->tiles_hit), P<Meta>(c->meta_d));
+    HIP_TRY(hipMemcpyAsync(c->meta_h, c->meta_d.p, sizeof(Meta), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipEventRecord(c->ev_total, c->stream));
     stage_mark(c, S_DEPTH);
     uint32_t* order = nullptr;
     launch_depth_order(c->stream, N, P<uint32_t>(c->dkey), P<uint32_t>(c->dval),
                        P<uint32_t>(c->dkey2), P<uint32_t>(c->dval2), P<int>(c->dtemp),
                        P<int>(c->tiles_hit), P<int>(c->hits), P<int>(c->eoff), P<int>(c->stemp),
-                       P<Meta>(c->meta_d), &order);
-    HIP_TRY(hipMemcpyAsync(c->meta_h, c->meta_d.p, sizeof(Meta), hipMemcpyDeviceToHost, c->stream));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+                       &order);
+    HIP_TRY(hipEventSynchronize(c->ev_total));
     if (c->timing) stage_fold(c, c->cur ^ 1);   // the previous call has completed
     if (c->loss_pending) {                       // so has its loss copy
         c->last_loss = c->loss_h[1] * c->loss_scale;
@@ -336,10 +340,6 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
     ENSURE(c->tkey2, I * 4);
     ENSURE(c->tval2, I * 4);
     ENSURE(c->ttemp, (size_t)radix_temp_ints((int64_t)I) * 4);
-    ENSURE(c->pk_geo, I * 16);
-    ENSURE(c->pk_col, I * 16);
-    ENSURE(c->pk_bl, I * 4);
-    ENSURE(c->pk_ids, I * 4);
     const int64_t max_items = items_bound(T, I64);
     ENSURE(c->it_tile, (size_t)max_items * 4);
     ENSURE(c->it_k, (size_t)max_items * 4);
@@ -356,11 +356,12 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
     stage_mark(c, S_TILES);
     TileLists tl{P<int>(c->l_chunked), nullptr, nullptr};
     Items it = items(c);
-    Packed pk = packed(c);
-    launch_tile_lists(c->stream, p, I64, go, order, P<int>(c->eoff), P<int>(c->hits),
-                      P<uint32_t>(c->tkey), P<uint32_t>(c->tval), P<uint32_t>(c->tkey2),
-                      P<uint32_t>(c->tval2), P<int>(c->ttemp), P<int>(c->tstart), P<int>(c->tend),
-                      P<int>(c->tile_bins), it, tl, P<Meta>(c->meta_d), pk);
+    c->sorted_ids = launch_tile_lists(c->stream, p, I64, go, order, P<int>(c->eoff),
+                                      P<int>(c->hits), P<uint32_t>(c->tkey), P<uint32_t>(c->tval),
+                                      P<uint32_t>(c->tkey2), P<uint32_t>(c->tval2),
+                                      P<int>(c->ttemp), P<int>(c->tstart), P<int>(c->tend),
+                                      P<int>(c->tile_bins), it, tl, P<Meta>(c->meta_d));
+    Entries pk = packed(c);
     stage_mark(c, S_RFWD);
     ChunkBufs cb = chunks(c);
     launch_raster_fwd(c->stream, p, max_items, P<Meta>(c->meta_d), it, P<int>(c->tile_bins), pk,
@@ -401,6 +402,7 @@ int msplat_hip_init(int device) {
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->count_h), 16));
     for (auto& row : c->ev)
         for (auto& e : row) HIP_TRY(hipEventCreate(&e));
+    HIP_TRY(hipEventCreateWithFlags(&c->ev_total, hipEventDisableTiming));
     return MSPLAT_OK;
 }
 
@@ -736,7 +738,7 @@ int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes) {
     const D direct[] = {
         {"radii", &c->radii, N * 4},
         {"num_tiles_hit", &c->tiles_hit, N * 4}, {"tile_bins", &c->tile_bins, T * 8},
-        {"gaussian_ids", &c->pk_ids, I * 4}, {"final_Ts", &c->final_T, Px * 4},
+        {"final_Ts", &c->final_T, Px * 4},
         {"final_index", &c->final_idx, Px * 4}, {"out_img", &c->out_img, Px * 12},
         {"v_rendered", &c->v_rendered, Px * 12}, {"gacc", &c->gacc, N * 36},
     };
@@ -745,6 +747,13 @@ int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes) {
         *nbytes = d.bytes;
         if (!dst || d.bytes == 0) return MSPLAT_OK;
         HIP_TRY(hipMemcpyAsync(dst, d.b->p, d.bytes, hipMemcpyDeviceToHost, c->stream));
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        return MSPLAT_OK;
+    }
+    if (n == "gaussian_ids") {
+        *nbytes = I * 4;
+        if (!dst || I == 0) return MSPLAT_OK;
+        HIP_TRY(hipMemcpyAsync(dst, c->sorted_ids, I * 4, hipMemcpyDeviceToHost, c->stream));
         HIP_TRY(hipStreamSynchronize(c->stream));
         return MSPLAT_OK;
     }

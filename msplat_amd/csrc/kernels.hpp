@@ -36,12 +36,11 @@ struct GaussOut {
     int* tiles_hit;
 };
 
-// Per-entry (tile-sorted) packed records.
-struct Packed {
-    float4* geo;         // (x, y, conic_a, conic_b)
-    float4* col;         // (conic_c, opacity, r_raw, g_raw)
-    float* bl;           // b_raw
-    int* ids;            // gaussian id
+// Tile-sorted entries: ids[i] is the gaussian of entry i; the rasteriser
+// gathers its projection record rec[4 id .. 4 id + 2] (one 64-byte line).
+struct Entries {
+    const uint32_t* ids;
+    const float4* rec;
 };
 
 // Work items of the rasteriser: item i covers chunk item_k[i] of tile item_tile[i].
@@ -93,16 +92,20 @@ int64_t radix_temp_ints(int64_t n);
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
                        int64_t n, int bits, int* temp);
 
-// Binning (binning.hip).  launch_depth_order leaves the intersection total in
-// meta->total_isect; launch_tile_lists needs it on the host.
+// Binning (binning.hip).  launch_total_hits writes the intersection total to
+// meta->total_isect (needed on the host before launch_tile_lists);
+// launch_depth_order orders the gaussians by depth and scans their tile
+// counts in that order.
+void launch_total_hits(hipStream_t s, int N, const int* tiles_hit, Meta* meta);
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
                         uint32_t* dval2, int* radix_temp, const int* tiles_hit, int* hits_sorted,
-                        int* eoff, int* scan_temp, Meta* meta, uint32_t** order_out);
-void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go,
-                       const uint32_t* order, const int* eoff, const int* hits, uint32_t* tkey,
-                       uint32_t* tval, uint32_t* tkey2, uint32_t* tval2, int* radix_temp,
-                       int* tstart, int* tend, int* tile_bins, Items it, TileLists tl, Meta* meta,
-                       Packed pk);
+                        int* eoff, int* scan_temp, uint32_t** order_out);
+// Returns the buffer (tval or tval2) that holds the tile-sorted gaussian ids.
+const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go,
+                                  const uint32_t* order, const int* eoff, const int* hits,
+                                  uint32_t* tkey, uint32_t* tval, uint32_t* tkey2, uint32_t* tval2,
+                                  int* radix_temp, int* tstart, int* tend, int* tile_bins, Items it,
+                                  TileLists tl, Meta* meta);
 
 // Raster pair counters: WORK_SLOTS sets of four u64 counters, each set in
 // its own 128-byte line (WORK_SLOT_U64 apart); totals are the sums over sets.
@@ -119,18 +122,18 @@ inline int64_t items_bound(int64_t T, int64_t I) { return T + I / 512 + I / 2048
 // pairs that carry a gradient to counter 1 and its wave-wide entry steps to
 // counter 3.
 void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
-                       Items it, const int* tile_bins, Packed pk, float* final_T, int* final_idx,
+                       Items it, const int* tile_bins, Entries pk, float* final_T, int* final_idx,
                        float* out_img, ChunkBufs cb, unsigned long long* work);
 void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
                          Items it, float* final_T, int* final_idx, float* out_img, ChunkBufs cb,
                          bool with_suffix);
 void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
-                       Items it, const int* tile_bins, Packed pk, const float* final_T,
+                       Items it, const int* tile_bins, Entries pk, const float* final_T,
                        const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc,
                        unsigned long long* work);
 // Adds the six pair counts of the most recent forward/backward into out[6].
 void launch_raster_work(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
-                        Items it, const int* tile_bins, Packed pk, const int* final_idx,
+                        Items it, const int* tile_bins, Entries pk, const int* final_idx,
                         ChunkBufs cb, unsigned long long* out);
 
 void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,

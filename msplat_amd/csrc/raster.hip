@@ -2,8 +2,9 @@
 //
 // Work decomposition: one 256-thread workgroup (four wave64) per (tile,
 // chunk) item; each wave owns one 8x8 quadrant of the 16x16 tile, one lane per
-// pixel.  Sorted entries are staged through LDS 256 at a time and read by all
-// lanes as broadcasts.  A tile that is rasterised in one piece writes the
+// pixel.  Sorted entries (gaussian ids; each entry's projection record is
+// gathered by id) are staged through LDS 256 at a time and read by all lanes
+// as broadcasts.  A tile that is rasterised in one piece writes the
 // final image directly; a chunked tile writes per-pixel chunk state that the
 // merge kernel folds front to back.
 //
@@ -118,7 +119,7 @@ __device__ __forceinline__ int quad_mask(float x, float y, float a, float b, flo
 __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float bg0, float bg1,
                                                     float bg2, const Meta* __restrict__ meta,
                                                     Items it,
-                                                    const int* __restrict__ tile_bins, Packed pk,
+                                                    const int* __restrict__ tile_bins, Entries pk,
                                                     float* __restrict__ final_T,
                                                     int* __restrict__ final_idx,
                                                     float* __restrict__ out_img, ChunkBufs cb,
@@ -146,14 +147,16 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
         const int idx = b + tid;
         int mask = 0;
         if (idx < ce) {
-            const float4 g = pk.geo[idx];
-            float4 c = pk.col[idx];
+            const float4* r = pk.rec + 4 * (size_t)pk.ids[idx];
+            const float4 g = r[0];
+            float4 c = r[1];
+            const float bl = r[2].x;
             mask = quad_mask(g.x, g.y, g.z, g.w, c.x, c.y, tx0, ty0);
             c.z = fmaxf(c.z + 0.5f, 0.f);
             c.w = fmaxf(c.w + 0.5f, 0.f);
             s_geo[tid] = g;
             s_col[tid] = c;
-            s_bl[tid] = fmaxf(pk.bl[idx] + 0.5f, 0.f);
+            s_bl[tid] = fmaxf(bl + 0.5f, 0.f);
         }
         s_mask[tid] = mask;
         __syncthreads();
@@ -273,7 +276,7 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
 __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float bg0, float bg1,
                                                     float bg2, const Meta* __restrict__ meta,
                                                     Items it,
-                                                    const int* __restrict__ tile_bins, Packed pk,
+                                                    const int* __restrict__ tile_bins, Entries pk,
                                                     const float* __restrict__ final_T,
                                                     const int* __restrict__ final_idx,
                                                     ChunkBufs cb, const float* __restrict__ v_out,
@@ -332,13 +335,15 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
         const int idx = top - tid;
         int mask = 0;
         if (idx >= cs) {
-            const float4 g = pk.geo[idx];
-            const float4 c = pk.col[idx];
+            const int gid = (int)pk.ids[idx];
+            const float4* r = pk.rec + 4 * (size_t)gid;
+            const float4 g = r[0];
+            const float4 c = r[1];
             mask = quad_mask(g.x, g.y, g.z, g.w, c.x, c.y, tx0, ty0);
             s_geo[tid] = g;
             s_col[tid] = c;
-            s_bl[tid] = pk.bl[idx];
-            s_id[tid] = pk.ids[idx];
+            s_bl[tid] = r[2].x;
+            s_id[tid] = gid;
         }
         s_mask[tid] = mask;
         __syncthreads();
@@ -417,7 +422,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
 // define the algorithmic flops of the roofline; they change no state.
 __global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
                                                      const Meta* __restrict__ meta, Items it,
-                                                     const int* __restrict__ tile_bins, Packed pk,
+                                                     const int* __restrict__ tile_bins, Entries pk,
                                                      const int* __restrict__ final_idx,
                                                      ChunkBufs cb,
                                                      unsigned long long* __restrict__ out) {
@@ -432,8 +437,9 @@ __global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
         float T = 1.f;
         for (int i = cs; i < ce; ++i) {
             ++n[0];
-            const float4 g = pk.geo[i];
-            const float4 c = pk.col[i];
+            const float4* r = pk.rec + 4 * (size_t)pk.ids[i];
+            const float4 g = r[0];
+            const float4 c = r[1];
             const float dx = g.x - fx, dy = g.y - fy;
             const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
             if (sigma < 0.f || sigma >= 5.55f) continue;
@@ -449,8 +455,9 @@ __global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
                               : cb.cidx[(size_t)item * TILE_PIX + px.lp];
         for (int i = min(bf, ce - 1); i >= cs; --i) {
             ++n[3];
-            const float4 g = pk.geo[i];
-            const float4 c = pk.col[i];
+            const float4* r = pk.rec + 4 * (size_t)pk.ids[i];
+            const float4 g = r[0];
+            const float4 c = r[1];
             const float dx = g.x - fx, dy = g.y - fy;
             const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
             if (sigma < 0.f || sigma >= 5.55f) continue;
@@ -471,7 +478,7 @@ __global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
 }  // namespace
 
 void launch_raster_work(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
-                        Items it, const int* tile_bins, Packed pk, const int* final_idx,
+                        Items it, const int* tile_bins, Entries pk, const int* final_idx,
                         ChunkBufs cb, unsigned long long* out) {
     if (max_items <= 0) return;
     hipLaunchKernelGGL(k_raster_work, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
@@ -479,7 +486,7 @@ void launch_raster_work(hipStream_t s, const CamParams& p, int64_t max_items, co
 }
 
 void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
-                       Items it, const int* tile_bins, Packed pk, float* final_T, int* final_idx,
+                       Items it, const int* tile_bins, Entries pk, float* final_T, int* final_idx,
                        float* out_img, ChunkBufs cb, unsigned long long* work) {
     if (max_items <= 0) return;
     hipLaunchKernelGGL(k_raster_fwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
@@ -497,7 +504,7 @@ void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, co
 }
 
 void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
-                       Items it, const int* tile_bins, Packed pk, const float* final_T,
+                       Items it, const int* tile_bins, Entries pk, const float* final_T,
                        const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc,
                        unsigned long long* work) {
     if (max_items <= 0) return;
