@@ -1,13 +1,15 @@
 // radix.hip — device-wide scans and a stable LSD radix sort of (u32 key, u32
 // value) pairs, used by the binning to order intersections without atomics.
 //
-// Sort: 8-bit digits, reduce-then-scan per pass over 2048-key blocks
-// (256 threads x 8 keys):
+// Sort: digits of up to 8 bits, reduce-then-scan per pass over 4096-key
+// blocks (256 threads x 16 keys):
 //   1. per-block digit histograms in LDS -> hist[digit][block]
 //   2. exclusive scan of hist in digit-major order -> scatter offsets
-//   3. per-block stable ranks: each wave ranks 512 consecutive keys in eight
-//      64-key rounds with an 8-ballot match of equal digits, keeping per-digit
-//      running counts in LDS; wave counts are combined in wave order.
+//   3. per-block stable ranks: each wave ranks 1024 consecutive keys in
+//      sixteen 64-key rounds with a ballot match of equal digits, keeping
+//      per-digit running counts in LDS; wave counts are combined in wave
+//      order; the block is reordered by digit in LDS and written out in digit
+//      runs (coalesced stores).
 // Stability makes the result independent of how work is scheduled: equal keys
 // keep their input order.
 #include "common.hpp"
@@ -18,8 +20,9 @@ namespace msp {
 namespace {
 
 constexpr int RT = 256;            // threads per block
-constexpr int RK = 8;              // keys per thread
+constexpr int RK = 16;             // keys per thread
 constexpr int RB = RT * RK;        // keys per block
+constexpr int WK = RB / 4;         // keys per wave (RK rounds of 64)
 constexpr int SB = 1024;           // elements per scan block
 
 __device__ __forceinline__ int block_sum_256(int v, int* sh) {
@@ -103,47 +106,73 @@ __global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
 }
 
 __global__ __launch_bounds__(RT) void k_radix_hist(const uint32_t* __restrict__ keys, int64_t n,
-                                                   int shift, int nblocks, int* __restrict__ hist) {
+                                                   int shift, uint32_t mask, int nblocks,
+                                                   int* __restrict__ hist) {
     __shared__ int h[256];
     h[threadIdx.x] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * RB;
-#pragma unroll
+#pragma unroll 4
     for (int k = 0; k < RK; ++k) {
         const int64_t i = base + k * RT + threadIdx.x;
-        if (i < n) atomicAdd(&h[(keys[i] >> shift) & 0xFF], 1);
+        if (i < n) atomicAdd(&h[(keys[i] >> shift) & mask], 1);
     }
     __syncthreads();
-    hist[(size_t)threadIdx.x * nblocks + blockIdx.x] = h[threadIdx.x];
+    if (threadIdx.x <= mask) hist[(size_t)threadIdx.x * nblocks + blockIdx.x] = h[threadIdx.x];
 }
 
+// Exclusive scan of one value per thread over the 256 threads of a block.
+__device__ __forceinline__ int block_exclusive_scan_256(int v, int* sh) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) sh[w] = x;
+    __syncthreads();
+    int wofs = 0;
+    for (int k = 0; k < w; ++k) wofs += sh[k];
+    __syncthreads();
+    return wofs + x - v;
+}
+
+// One LSD pass over the digit (key >> shift) & mask (nbits bits, <= 8).
+// Keys are ranked stably inside the block (each wave ranks its RB/4
+// consecutive keys in 64-key rounds by ballot-matching the digit bits and
+// keeps per-digit running counts), reordered by digit in LDS, and written out
+// in digit runs so that neighbouring lanes store neighbouring addresses.
 __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict__ kin,
                                                       const uint32_t* __restrict__ vin,
                                                       uint32_t* __restrict__ kout,
                                                       uint32_t* __restrict__ vout, int64_t n,
-                                                      int shift, int nblocks,
-                                                      const int* __restrict__ offs) {
+                                                      int shift, uint32_t mask, int nbits,
+                                                      int nblocks, const int* __restrict__ offs) {
+    __shared__ uint32_t s_key[RB];
+    __shared__ uint32_t s_val[RB];
     __shared__ int wcnt[4][256];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    for (int i = threadIdx.x; i < 4 * 256; i += RT) (&wcnt[0][0])[i] = 0;
+    __shared__ int dstart[256];
+    __shared__ int gofs[256];
+    __shared__ int scan_sh[4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    for (int i = tid; i < 4 * 256; i += RT) (&wcnt[0][0])[i] = 0;
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * RB + (int64_t)w * (RB / 4);
+    const int64_t wbase = (int64_t)blockIdx.x * RB + (int64_t)w * WK;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     uint32_t key[RK], val[RK];
     int dig[RK], rank[RK];
 #pragma unroll
     for (int j = 0; j < RK; ++j) {
-        const int64_t i = base + j * 64 + lane;
+        const int64_t i = wbase + j * 64 + lane;
         const bool ok = i < n;
         key[j] = ok ? kin[i] : 0u;
         val[j] = ok ? vin[i] : 0u;
-        const int d = ok ? (int)((key[j] >> shift) & 0xFF) : 256;
+        const int d = ok ? (int)((key[j] >> shift) & mask) : 256;
         dig[j] = d;
-        // lanes holding the same digit in this 64-key round
         uint64_t peers = __ballot(ok);
         if (!ok) peers = ~peers;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
+        for (int b = 0; b < nbits; ++b) {
             const uint64_t bb = __ballot((d >> b) & 1);
             peers &= ((d >> b) & 1) ? bb : ~bb;
         }
@@ -155,25 +184,37 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
         if (ok && before == 0) wcnt[w][dd] = base_cnt + __popcll(peers);
     }
     __syncthreads();
-    // digit offsets of each wave inside the block: counts of earlier waves
+    // per digit: offsets of the four waves, the block's count and its start
+    int cnt = 0;
     {
-        const int d = threadIdx.x;
-        int run = 0;
+        const int d = tid;
 #pragma unroll
         for (int ww = 0; ww < 4; ++ww) {
             const int c = wcnt[ww][d];
-            wcnt[ww][d] = run;
-            run += c;
+            wcnt[ww][d] = cnt;
+            cnt += c;
         }
+        gofs[d] = (uint32_t)d <= mask ? offs[(size_t)d * nblocks + blockIdx.x] : 0;
     }
+    const int start = block_exclusive_scan_256(cnt, scan_sh);
+    dstart[tid] = start;
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < RK; ++j) {
         const int d = dig[j];
         if (d > 255) continue;
-        const int64_t pos = (int64_t)offs[(size_t)d * nblocks + blockIdx.x] + wcnt[w][d] + rank[j];
-        kout[pos] = key[j];
-        vout[pos] = val[j];
+        const int p = dstart[d] + wcnt[w][d] + rank[j];
+        s_key[p] = key[j];
+        s_val[p] = val[j];
+    }
+    __syncthreads();
+    const int nvalid = (int)min((int64_t)RB, n - (int64_t)blockIdx.x * RB);
+    for (int p = tid; p < nvalid; p += RT) {
+        const uint32_t k = s_key[p];
+        const int d = (int)((k >> shift) & mask);
+        const int64_t pos = (int64_t)gofs[d] + (p - dstart[d]);
+        kout[pos] = k;
+        vout[pos] = s_val[p];
     }
 }
 
@@ -205,25 +246,33 @@ int64_t radix_temp_ints(int64_t n) {
 }
 
 // Sorts (k0, v0) by the bits [0, bits) of the keys; ping-pongs with (k1, v1).
-// Returns true when the result ends up in (k1, v1).
+// The bits are split into ceil(bits / 8) passes of equal width (fewer digit
+// values give longer runs per digit and block).  Returns true when the result
+// ends up in (k1, v1).
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
                        int64_t n, int bits, int* temp) {
     if (n <= 0 || bits <= 0) return false;
     const int nb = (int)((n + RB - 1) / RB);
+    const int passes = (bits + 7) / 8;
     int* hist = temp;
     int* tot = temp + 256 * (int64_t)nb;
     bool flip = false;
-    for (int shift = 0; shift < bits; shift += 8) {
+    int shift = 0;
+    for (int pass = 0; pass < passes; ++pass) {
+        const int width = (bits - shift + (passes - pass) - 1) / (passes - pass);
+        const uint32_t mask = (1u << width) - 1u;
         uint32_t* ki = flip ? k1 : k0;
         uint32_t* vi = flip ? v1 : v0;
         uint32_t* ko = flip ? k0 : k1;
         uint32_t* vo = flip ? v0 : v1;
-        hipLaunchKernelGGL(k_radix_hist, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki, n, shift, nb,
-                           hist);
-        launch_exclusive_scan_i32(s, hist, hist, 256 * (int64_t)nb, tot);
+        hipLaunchKernelGGL(k_radix_hist, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki, n, shift,
+                           mask, nb, hist);
+        launch_exclusive_scan_i32(s, hist, hist, (int64_t)(mask + 1) * nb, tot);
         hipLaunchKernelGGL(k_radix_scatter, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki,
-                           (const uint32_t*)vi, ko, vo, n, shift, nb, (const int*)hist);
+                           (const uint32_t*)vi, ko, vo, n, shift, mask, width, nb,
+                           (const int*)hist);
         flip = !flip;
+        shift += width;
     }
     return flip;
 }
