@@ -51,24 +51,58 @@ __global__ __launch_bounds__(256) void k_total_hits(int N, const int* __restrict
     }
 }
 
+// Emission of the (tile id, gaussian id) pairs of 64 depth-consecutive
+// gaussians by one wave.  Their pairs occupy one contiguous output range (the
+// emit offsets are a scan in depth order); the wave walks that range 64
+// slots at a time, each lane finding the gaussian that owns its slot by a
+// binary search over the lanes' start offsets, so every store is coalesced.
 __global__ __launch_bounds__(256) void k_emit(int N, int tbx, int tby, GaussOut go,
                                               const uint32_t* __restrict__ order,
                                               const int* __restrict__ eoff,
                                               const int* __restrict__ hits,
                                               uint32_t* __restrict__ tkey,
                                               uint32_t* __restrict__ tval) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= N || hits[r] == 0) return;
-    const int g = (int)order[r];
-    const float4 r0 = go.rec[4 * (size_t)g], r2 = go.rec[4 * (size_t)g + 2];
-    int x0, y0, x1, y1;
-    tile_rect(r0.x, r0.y, r2.y, r2.z, tbx, tby, x0, y0, x1, y1);
-    int e = eoff[r];
-    for (int ty = y0; ty < y1; ++ty)
-        for (int tx = x0; tx < x1; ++tx, ++e) {
-            tkey[e] = (uint32_t)(ty * tbx + tx);
-            tval[e] = (uint32_t)g;
+    const int lane = threadIdx.x & 63;
+    const int base = blockIdx.x * blockDim.x + threadIdx.x - lane;   // wave-uniform
+    if (base >= N) return;
+    const int r = base + lane;
+    int start = 0x7FFFFFFF, end = 0, x0 = 0, y0 = 0, w = 1;
+    int g = 0;
+    if (r < N) {
+        start = eoff[r];
+        const int h = hits[r];
+        end = start + h;
+        if (h > 0) {
+            g = (int)order[r];
+            const float4 r0 = go.rec[4 * (size_t)g], r2 = go.rec[4 * (size_t)g + 2];
+            int x1, y1;
+            tile_rect(r0.x, r0.y, r2.y, r2.z, tbx, tby, x0, y0, x1, y1);
+            w = x1 - x0;
         }
+    }
+    const int last = min(63, N - 1 - base);
+    const int e0 = __shfl(start, 0, 64);
+    const int e1 = __shfl(end, last, 64);
+    for (int eb = e0; eb < e1; eb += 64) {
+        const int e = eb + lane;
+        // owner: the last lane whose start is <= e (lanes without pairs share
+        // their start with the next lane and lose the tie)
+        int lo = 0;
+#pragma unroll
+        for (int step = 32; step >= 1; step >>= 1) {
+            const int cand = lo + step;
+            if (__shfl(start, cand, 64) <= e) lo = cand;
+        }
+        const int k = e - __shfl(start, lo, 64);
+        const int ow = __shfl(w, lo, 64);
+        const int ox = __shfl(x0, lo, 64), oy = __shfl(y0, lo, 64);
+        const int og = __shfl(g, lo, 64);
+        if (e < e1) {
+            const int q = k / ow;
+            tkey[e] = (uint32_t)((oy + q) * tbx + ox + (k - q * ow));
+            tval[e] = (uint32_t)og;
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void k_tile_edges(int64_t I, const uint32_t* __restrict__ tkey,
