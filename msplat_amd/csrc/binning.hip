@@ -52,10 +52,14 @@ __global__ __launch_bounds__(256) void k_total_hits(int N, const int* __restrict
 }
 
 // Emission of the (tile id, gaussian id) pairs of 64 depth-consecutive
-// gaussians by one wave.  Their pairs occupy one contiguous output range (the
-// emit offsets are a scan in depth order); the wave walks that range 64
-// slots at a time, each lane finding the gaussian that owns its slot by a
-// binary search over the lanes' start offsets, so every store is coalesced.
+// gaussians by one wave, with coalesced stores.  Gaussians with fewer than
+// EMIT_BIG pairs are written together: their pairs are numbered 0..S-1 in
+// wave order and each lane finds the owner of its slot by a binary search
+// over the lanes' running offsets.  Larger ones (close to the camera, so
+// often several in one wave) are then written one at a time by the whole
+// wave, 64 pairs per step.
+constexpr int EMIT_BIG = 64;
+
 __global__ __launch_bounds__(256) void k_emit(int N, int tbx, int tby, GaussOut go,
                                               const uint32_t* __restrict__ order,
                                               const int* __restrict__ eoff,
@@ -66,13 +70,11 @@ __global__ __launch_bounds__(256) void k_emit(int N, int tbx, int tby, GaussOut 
     const int base = blockIdx.x * blockDim.x + threadIdx.x - lane;   // wave-uniform
     if (base >= N) return;
     const int r = base + lane;
-    int start = 0x7FFFFFFF, end = 0, x0 = 0, y0 = 0, w = 1;
-    int g = 0;
+    int start = 0, h = 0, x0 = 0, y0 = 0, w = 1, g = 0;
     if (r < N) {
-        start = eoff[r];
-        const int h = hits[r];
-        end = start + h;
+        h = hits[r];
         if (h > 0) {
+            start = eoff[r];
             g = (int)order[r];
             const float4 r0 = go.rec[4 * (size_t)g], r2 = go.rec[4 * (size_t)g + 2];
             int x1, y1;
@@ -80,27 +82,49 @@ __global__ __launch_bounds__(256) void k_emit(int N, int tbx, int tby, GaussOut 
             w = x1 - x0;
         }
     }
-    const int last = min(63, N - 1 - base);
-    const int e0 = __shfl(start, 0, 64);
-    const int e1 = __shfl(end, last, 64);
-    for (int eb = e0; eb < e1; eb += 64) {
-        const int e = eb + lane;
-        // owner: the last lane whose start is <= e (lanes without pairs share
-        // their start with the next lane and lose the tie)
+    // small gaussians: wave-wide numbering of their pairs
+    const bool big = h >= EMIT_BIG;
+    const int hs = big ? 0 : h;
+    int incl = hs;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+    }
+    const int sstart = incl - hs;
+    const int S = __shfl(incl, 63, 64);
+    for (int sb = 0; sb < S; sb += 64) {
+        const int sl = sb + lane;
+        // owner: the last lane whose first slot is <= sl (lanes without small
+        // pairs share their first slot with the next lane and lose the tie)
         int lo = 0;
 #pragma unroll
         for (int step = 32; step >= 1; step >>= 1) {
             const int cand = lo + step;
-            if (__shfl(start, cand, 64) <= e) lo = cand;
+            if (__shfl(sstart, cand, 64) <= sl) lo = cand;
         }
-        const int k = e - __shfl(start, lo, 64);
+        const int k = sl - __shfl(sstart, lo, 64);
+        const int oe = __shfl(start, lo, 64);
         const int ow = __shfl(w, lo, 64);
         const int ox = __shfl(x0, lo, 64), oy = __shfl(y0, lo, 64);
         const int og = __shfl(g, lo, 64);
-        if (e < e1) {
+        if (sl < S) {
             const int q = k / ow;
-            tkey[e] = (uint32_t)((oy + q) * tbx + ox + (k - q * ow));
-            tval[e] = (uint32_t)og;
+            tkey[oe + k] = (uint32_t)((oy + q) * tbx + ox + (k - q * ow));
+            tval[oe + k] = (uint32_t)og;
+        }
+    }
+    // large gaussians: one at a time, the whole wave writing 64 pairs per step
+    uint64_t bigm = __ballot(big);
+    while (bigm) {
+        const int L = __builtin_ctzll(bigm);
+        bigm &= bigm - 1;
+        const int be = __shfl(start, L, 64), bh = __shfl(h, L, 64), bw = __shfl(w, L, 64);
+        const int bx = __shfl(x0, L, 64), by = __shfl(y0, L, 64), bg = __shfl(g, L, 64);
+        for (int k = lane; k < bh; k += 64) {
+            const int q = k / bw;
+            tkey[be + k] = (uint32_t)((by + q) * tbx + bx + (k - q * bw));
+            tval[be + k] = (uint32_t)bg;
         }
     }
 }
