@@ -541,8 +541,8 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
     hp.eps = a->adam_eps;
     GaussOut go = gauss_out(c);
     stage_mark(c, S_SHADAM);
-    launch_sh_rest_adam(c->stream, p, a->r.means3d, go.radii, P<float>(c->gacc),
-                        a->adam_params[4], a->adam_exp_avg[4], a->adam_exp_avg_sq[4], hp);
+    launch_sh_rest_adam(c->stream, p, go.rec, go.radii, P<float>(c->gacc), a->adam_params[4],
+                        a->adam_exp_avg[4], a->adam_exp_avg_sq[4], hp);
     stage_mark(c, S_PBWD);
     launch_proj_bwd_adam(c->stream, p, a->adam_params, a->adam_exp_avg, a->adam_exp_avg_sq, hp, go,
                          P<float>(c->gacc), a->vis_counts, a->xys_grad_norm, a->max_2d_size,

@@ -29,7 +29,7 @@ struct CamParams {
 // line:  rec[4g+0] = (x, y, conic_a, conic_b)
 //        rec[4g+1] = (conic_c, sigmoid(opacity), r, g)   raw SH colour
 //        rec[4g+2] = (b, extent_x, extent_y, depth)
-//        rec[4g+3] = unused
+//        rec[4g+3] = (view direction normalize(p - cam), 0)
 struct GaussOut {
     float4* rec;
     int* radii;
@@ -146,9 +146,8 @@ struct AdamHP {
     float b1, b2, eps;
 };
 
-void launch_sh_rest_adam(hipStream_t s, const CamParams& p, const float* means,
-                         const int* radii, const float* gacc, float* f_rest, float* m,
-                         float* v, const AdamHP& hp);
+void launch_sh_rest_adam(hipStream_t s, const CamParams& p, const float4* rec, const int* radii,
+                         const float* gacc, float* f_rest, float* m, float* v, const AdamHP& hp);
 void launch_proj_bwd_adam(hipStream_t s, const CamParams& p, float* const params[6],
                           float* const m[6], float* const v[6], const AdamHP& hp,
                           GaussOut go, const float* gacc, float* vis, float* gnorm,

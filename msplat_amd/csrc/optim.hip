@@ -14,8 +14,8 @@
 // quats, opacity and f_dc directly (dense for the first four, visible-only for
 // f_dc, as in the reference), plus the densify statistics.  The 45 floats of
 // f_rest per gaussian are updated by a separate element-parallel kernel whose
-// loads and stores are contiguous across the wave; it runs first because it
-// reads the pre-update means for the view direction.
+// loads and stores are contiguous across the wave; it takes the view
+// direction the projection stored with each gaussian's record.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -77,49 +77,73 @@ __device__ __forceinline__ void adam_elem(float& p, float& m, float& v, float g,
     v = vn;
 }
 
-// SH basis value b (0-based over the rest coefficients) along d (.metal:1936-1977).
-__device__ __forceinline__ float sh_basis(int b, float x, float y, float z) {
-    const float xx = x * x, xy = x * y, xz = x * z, yy = y * y, yz = y * z, zz = z * z;
-    switch (b) {
-        case 0: return -SH_C1 * y;
-        case 1: return SH_C1 * z;
-        case 2: return -SH_C1 * x;
-        case 3: return SH_C2_0 * xy;
-        case 4: return SH_C2_1 * yz;
-        case 5: return SH_C2_2 * (2.f * zz - xx - yy);
-        case 6: return SH_C2_3 * xz;
-        case 7: return SH_C2_4 * (xx - yy);
-        case 8: return SH_C3_0 * y * (3.f * xx - yy);
-        case 9: return SH_C3_1 * xy * z;
-        case 10: return SH_C3_2 * y * (4.f * zz - xx - yy);
-        case 11: return SH_C3_3 * z * (2.f * zz - 3.f * xx - 3.f * yy);
-        case 12: return SH_C3_4 * x * (4.f * zz - xx - yy);
-        case 13: return SH_C3_5 * z * (xx - yy);
-        default: return SH_C3_6 * x * (xx - 3.f * yy);
-    }
-}
 
 // Element-parallel Adam on features_rest, four consecutive floats per thread
-// (16-byte loads and stores).  Elements of culled gaussians and of bands above
-// degrees_to_use keep their values (the reference updates visible gaussians'
-// used bands only, .metal:1846-1848, 1931-1985).
-__global__ __launch_bounds__(256) void k_sh_rest_adam(int64_t n, int rest_per, int n_used,
-                                                      const float* __restrict__ means,
-                                                      float cx, float cy, float cz,
-                                                      const int* __restrict__ radii,
-                                                      const float* __restrict__ gacc,
-                                                      float* __restrict__ f_rest,
-                                                      float* __restrict__ m, float* __restrict__ v,
-                                                      AdamHP hp) {
-    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+// (16-byte loads and stores).  Each 256-thread block covers 1024 consecutive
+// elements; the gradient of element (gaussian g, basis b, channel c) is
+// basis_b(dir_g) * v_rgb[g][c], so the block first evaluates the basis once
+// per gaussian it touches (view direction from the projection record) into
+// LDS.  Elements of culled gaussians and of bands above degrees_to_use keep
+// their values (the reference updates visible gaussians' used bands only,
+// .metal:1846-1848, 1931-1985).
+constexpr int SHA_T = 256;
+constexpr int SHA_E = 4 * SHA_T;
+constexpr int SHA_MAXG = SHA_E / 9 + 2;   // rest_per >= 9
+
+__device__ __forceinline__ void sh_basis15(float x, float y, float z, float* o) {
+    const float xx = x * x, xy = x * y, xz = x * z, yy = y * y, yz = y * z, zz = z * z;
+    o[0] = -SH_C1 * y;
+    o[1] = SH_C1 * z;
+    o[2] = -SH_C1 * x;
+    o[3] = SH_C2_0 * xy;
+    o[4] = SH_C2_1 * yz;
+    o[5] = SH_C2_2 * (2.f * zz - xx - yy);
+    o[6] = SH_C2_3 * xz;
+    o[7] = SH_C2_4 * (xx - yy);
+    o[8] = SH_C3_0 * y * (3.f * xx - yy);
+    o[9] = SH_C3_1 * xy * z;
+    o[10] = SH_C3_2 * y * (4.f * zz - xx - yy);
+    o[11] = SH_C3_3 * z * (2.f * zz - 3.f * xx - 3.f * yy);
+    o[12] = SH_C3_4 * x * (4.f * zz - xx - yy);
+    o[13] = SH_C3_5 * z * (xx - yy);
+    o[14] = SH_C3_6 * x * (xx - 3.f * yy);
+}
+
+__global__ __launch_bounds__(SHA_T) void k_sh_rest_adam(int64_t n, int rest_per, int n_used,
+                                                        const float4* __restrict__ rec,
+                                                        const int* __restrict__ radii,
+                                                        const float* __restrict__ gacc,
+                                                        float* __restrict__ f_rest,
+                                                        float* __restrict__ m,
+                                                        float* __restrict__ v, AdamHP hp) {
+    __shared__ float s_basis[SHA_MAXG][16];
+    __shared__ float s_vrgb[SHA_MAXG][3];
+    __shared__ int s_vis[SHA_MAXG];
+    const int64_t eb = (int64_t)blockIdx.x * SHA_E;
+    const int gA = (int)(eb / rest_per);
+    const int gB = (int)((min(eb + SHA_E, n) - 1) / rest_per);
+    for (int t = threadIdx.x; t <= gB - gA; t += SHA_T) {
+        const int g = gA + t;
+        const bool vis = radii[g] > 0;
+        s_vis[t] = vis;
+        if (vis) {
+            const float4 d = rec[4 * (size_t)g + 3];
+            float bs[15];
+            sh_basis15(d.x, d.y, d.z, bs);
+#pragma unroll
+            for (int b = 0; b < 15; ++b) s_basis[t][b] = bs[b];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) s_vrgb[t][c] = gacc[(size_t)g * 9 + 5 + c];
+        }
+    }
+    __syncthreads();
+    const int64_t e0 = eb + 4 * threadIdx.x;
     if (e0 >= n) return;
     int g = (int)(e0 / rest_per);
     int rem = (int)(e0 - (int64_t)g * rest_per);
     const int cnt = (int)min((int64_t)4, n - e0);
-    // Gaussians covered by these elements (at most two: rest_per >= 9).
     const int g_last = (int)((e0 + cnt - 1) / rest_per);
-    const bool vis0 = radii[g] > 0, vis1 = radii[g_last] > 0;
-    if (!vis0 && !vis1) return;
+    if (!s_vis[g - gA] && !s_vis[g_last - gA]) return;
     float pv[4], mv[4], vv[4];
     const bool full = cnt == 4;
     if (full) {
@@ -132,21 +156,12 @@ __global__ __launch_bounds__(256) void k_sh_rest_adam(int64_t n, int rest_per, i
     } else {
         for (int k = 0; k < cnt; ++k) { pv[k] = f_rest[e0 + k]; mv[k] = m[e0 + k]; vv[k] = v[e0 + k]; }
     }
-    int gd = -1;
-    float dxn = 0.f, dyn = 0.f, dzn = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         if (k < cnt) {
-            const int b = rem / 3, c = rem - 3 * (rem / 3);
-            if (b < n_used && (g == g_last ? vis1 : vis0)) {
-                if (gd != g) {
-                    gd = g;
-                    const float dx = means[3 * g] - cx, dy = means[3 * g + 1] - cy,
-                                dz = means[3 * g + 2] - cz;
-                    const float inv = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
-                    dxn = dx * inv; dyn = dy * inv; dzn = dz * inv;
-                }
-                const float grad = sh_basis(b, dxn, dyn, dzn) * gacc[(size_t)g * 9 + 5 + c];
+            const int li = g - gA, b = rem / 3, c = rem - 3 * (rem / 3);
+            if (b < n_used && s_vis[li]) {
+                const float grad = s_basis[li][b] * s_vrgb[li][c];
                 adam_elem(pv[k], mv[k], vv[k], grad, hp.step[4], hp.b1, hp.b2, hp.bc2[4], hp.eps);
             }
         }
@@ -383,17 +398,15 @@ __global__ __launch_bounds__(256) void k_split_gacc(int N, const float* __restri
 
 }  // namespace
 
-void launch_sh_rest_adam(hipStream_t s, const CamParams& p, const float* means,
-                         const int* radii, const float* gacc, float* f_rest, float* m, float* v,
-                         const AdamHP& hp) {
+void launch_sh_rest_adam(hipStream_t s, const CamParams& p, const float4* rec, const int* radii,
+                         const float* gacc, float* f_rest, float* m, float* v, const AdamHP& hp) {
     const int dtu = p.dtu < 3 ? p.dtu : 3;
     const int n_used = dtu >= 3 ? 15 : dtu == 2 ? 8 : dtu == 1 ? 3 : 0;
     if (n_used == 0 || p.rest_per == 0 || p.N <= 0) return;
     const int64_t n = (int64_t)p.N * p.rest_per;
-    const int64_t threads = (n + 3) / 4;
-    hipLaunchKernelGGL(k_sh_rest_adam, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, n,
-                       p.rest_per, n_used, means, p.cam[0], p.cam[1], p.cam[2], radii, gacc,
-                       f_rest, m, v, hp);
+    const int64_t blocks = (n + SHA_E - 1) / SHA_E;
+    hipLaunchKernelGGL(k_sh_rest_adam, dim3((unsigned)blocks), dim3(SHA_T), 0, s, n, p.rest_per,
+                       n_used, rec, radii, gacc, f_rest, m, v, hp);
 }
 
 void launch_proj_bwd_adam(hipStream_t s, const CamParams& p, float* const params[6],

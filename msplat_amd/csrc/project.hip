@@ -180,6 +180,7 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     rec[0] = make_float4(px, py, ca, cb);
     rec[1] = make_float4(cc, sigmoid(opac_logits[g]), col[0], col[1]);
     rec[2] = make_float4(col[2], ex, ey, pv.z);
+    rec[3] = make_float4(dir.x, dir.y, dir.z, 0.f);
     dkey[g] = __float_as_uint(pv.z);
 }
 
