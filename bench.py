@@ -309,6 +309,36 @@ def main():
         f"{render_pairs[2] / max(fwd_n, 1) / 1e6:.2f}M (lanes compositing "
         f"{100 * render_pairs[0] / max(64 * render_pairs[2], 1):.1f}%)")
 
+    # HBM-bound stages: algorithmic bytes per launch (visible / culled
+    # gaussians counted separately, from the last step's radii) over the
+    # stages' HIP-event times in the timed train steps.
+    radii = device.intermediate("radii", np.int32)
+    n_all = int(radii.size)
+    n_vis = int((radii > 0).sum())
+    n_cul = n_all - n_vis
+    px = cams[0].width * cams[0].height
+    algo_bytes = {
+        # read means, log-scales, quats, f_dc, f_rest (45), opacity = 236 B; write the
+        # 64-byte record, radii, tiles hit, depth key / value and the zeroed
+        # 36-byte gradient accumulator = 116 B (culled: 12 B read, 52 B written)
+        "proj_sh_fwd": n_vis * (236 + 116) + n_cul * (12 + 52),
+        # f_rest, its two moments read and written (1080 B), direction 16 B,
+        # v_rgb 12 B, radii 4 B (culled: radii only)
+        "sh_rest_adam": n_vis * (1080 + 16 + 12 + 4) + n_cul * 4,
+        # dense Adam on means / scales / quats / opacity (11 floats x p, m, v
+        # read + written = 264 B), f_dc Adam for visible (72 B), record 48 B,
+        # gradient accumulator 36 B, radii 4 B, three statistics r + w 24 B
+        "proj_sh_bwd_adam": n_vis * (264 + 72 + 48 + 36 + 4 + 24) + n_cul * (264 + 4),
+        # read render + target, write the loss gradient image: 36 B per pixel
+        "loss_fwd_bwd": 36 * px,
+    }
+    hbm = {}
+    for k, b in algo_bytes.items():
+        ms = stages[k][0] / max(stages[k][1], 1)
+        hbm[k] = {"ms": ms, "bytes": b, "GBps": b / (ms * 1e-3) / 1e9, "frac": b / (ms * 1e-3) / HBM_PEAK}
+        log(f"  {k:18s} {b / 1e6:8.1f} MB algorithmic in {ms:.3f} ms = {hbm[k]['GBps']:7.0f} GB/s "
+            f"({100 * hbm[k]['frac']:.1f}% of HBM peak)")
+
     cpu = None
     if not args.no_cpu and args.cpu_steps > 0:
         rate, cores, dt = cpu_baseline(device_params, cams, targets, degree, bg, args.cpu_steps)
@@ -327,6 +357,8 @@ def main():
         "stage_ms": {k: ms / c for k, (ms, c) in stages.items() if c},
         "render_stage_ms": {k: ms / c for k, (ms, c) in rstages.items() if c},
         "rast_fwd_render_tflops": fwd_flops / fwd_ms / 1e9,
+        "hbm_stages": hbm,
+        "visible_gaussians": n_vis,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

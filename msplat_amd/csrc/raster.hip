@@ -303,6 +303,8 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     // gradient value this lane writes after the reductions: lanes 0, 8, ...,
     // 56 hold the eight transposed sums, lane 1 the ninth; -1 for the others
     const int kslot = (lane & 7) == 0 ? sum8_value_of_lane(lane) : lane == 1 ? 8 : -1;
+    // the entry mask bit that keeps this lane's value (v_rgb channels only)
+    const int kbit = kslot >= 5 && kslot <= 7 ? 16 << (kslot - 5) : 0;
     unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
     if (px.inside) {
         const size_t pix = (size_t)px.i * W + px.j;
@@ -338,11 +340,17 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
             const int gid = (int)pk.ids[idx];
             const float4* r = pk.rec + 4 * (size_t)gid;
             const float4 g = r[0];
-            const float4 c = r[1];
+            float4 c = r[1];
+            const float braw = r[2].x;
             mask = quad_mask(g.x, g.y, g.z, g.w, c.x, c.y, tx0, ty0);
+            // bits 4..6: the channel's raw colour + 0.5 >= 0 (its v_rgb is kept)
+            mask |= (c.z + 0.5f >= 0.f ? 16 : 0) | (c.w + 0.5f >= 0.f ? 32 : 0) |
+                    (braw + 0.5f >= 0.f ? 64 : 0);
+            c.z = fmaxf(c.z + 0.5f, 0.f);
+            c.w = fmaxf(c.w + 0.5f, 0.f);
             s_geo[tid] = g;
             s_col[tid] = c;
-            s_bl[tid] = r[2].x;
+            s_bl[tid] = fmaxf(braw + 0.5f, 0.f);
             s_id[tid] = gid;
         }
         s_mask[tid] = mask;
@@ -359,7 +367,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 const int e_idx = top - qq;
                 const float4 g = s_geo[qq];
                 const float4 c = s_col[qq];
-                const float braw = s_bl[qq];
+                const float r0 = c.z, r1 = c.w, r2 = s_bl[qq];   // max(raw + 0.5, 0)
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
                 const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
@@ -374,21 +382,21 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
                 const float Tn = T * ra;
                 const float fac = grad ? alpha * Tn : 0.f;
-                const float r0 = fmaxf(c.z + 0.5f, 0.f), r1 = fmaxf(c.w + 0.5f, 0.f),
-                            r2 = fmaxf(braw + 0.5f, 0.f);
                 const float t0 = fmaf(r0, Tn, fmaf(-B0, ra, -ra * tb0));
                 const float t1 = fmaf(r1, Tn, fmaf(-B1, ra, -ra * tb1));
                 const float t2 = fmaf(r2, Tn, fmaf(-B2, ra, -ra * tb2));
-                const float v_alpha = 0.f + (t0 * vo0 + t1 * vo1 + t2 * vo2);
+                const float v_alpha = t0 * vo0 + t1 * vo1 + t2 * vo2;
                 B0 = fmaf(r0, fac, B0);
                 B1 = fmaf(r1, fac, B1);
                 B2 = fmaf(r2, fac, B2);
                 T = grad ? Tn : T;
                 const float v_sigma = -alpha * v_alpha;
                 const float hv = 0.5f * v_sigma;
+                const float gx = v_sigma * fmaf(g.z, dx, g.w * dy);
+                const float gy = v_sigma * fmaf(g.w, dx, c.x * dy);
                 float v[8];
-                v[0] = grad ? v_sigma * fmaf(g.z, dx, g.w * dy) : 0.f;
-                v[1] = grad ? v_sigma * fmaf(g.w, dx, c.x * dy) : 0.f;
+                v[0] = grad ? gx : 0.f;
+                v[1] = grad ? gy : 0.f;
                 v[2] = grad ? hv * (dx * dx) : 0.f;
                 v[3] = grad ? hv * (dx * dy) : 0.f;
                 v[4] = grad ? hv * (dy * dy) : 0.f;
@@ -398,12 +406,8 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 const float vop = grad ? -v_sigma * (1.f - c.y) : 0.f;
                 const float u = wave_sum8_transposed(v, lane);
                 const float s8 = wave_sum(vop);
-                if (kslot >= 0) {
-                    const bool ok = kslot == 5 ? c.z + 0.5f >= 0.f
-                                  : kslot == 6 ? c.w + 0.5f >= 0.f
-                                  : kslot == 7 ? braw + 0.5f >= 0.f : true;
-                    if (ok) atomicAdd(&gacc[(size_t)s_id[qq] * 9 + kslot], kslot == 8 ? s8 : u);
-                }
+                if (kslot >= 0 && (kbit == 0 || (s_mask[qq] & kbit)))
+                    atomicAdd(&gacc[(size_t)s_id[qq] * 9 + kslot], kslot == 8 ? s8 : u);
             }
         }
     }
