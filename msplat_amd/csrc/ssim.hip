@@ -1,17 +1,22 @@
 // ssim.hip — separable 11-tap SSIM + L1 loss, forward and backward, on
 // 16x16 workgroups with LDS-staged halos.
 //
-// Three passes with the reference's training semantics:
-//   h-fwd        ssim_h_fwd_kernel (.metal:3053-3115): horizontal zero-padded
-//                sums of x=gt, y=render: mu_x, mu_y, E[x^2], E[y^2], E[xy]
-//   v-fwd+h-bwd  ssim_fused_v_fwd_h_bwd_kernel (.metal:3226-3313): vertical
-//                sums -> SSIM and its derivative fields f1, f2, f3 at every
-//                centre of the tile rows, including the 5-column halo outside
-//                the image (whose zero statistics give f = (0, -2/C2, 2/C2)),
-//                then the mirrored horizontal pass
+// Two passes with the reference's training semantics:
+//   h-fwd + v-fwd + h-bwd   ssim_h_fwd_kernel (.metal:3053-3115) and
+//                ssim_fused_v_fwd_h_bwd_kernel (.metal:3226-3313) in one
+//                workgroup per 16x16 tile: the horizontal zero-padded sums of
+//                x=gt, y=render (mu_x, mu_y, E[x^2], E[y^2], E[xy]) for the
+//                tile rows +-5 and columns +-5 are computed into LDS from the
+//                input (no intermediate buffer), then the vertical sums ->
+//                SSIM and its derivative fields f1, f2, f3 at every centre of
+//                the tile rows, including the 5-column halo outside the image
+//                (whose zero statistics give f = (0, -2/C2, 2/C2)), then the
+//                mirrored horizontal pass
 //   v-bwd        ssim_v_bwd_kernel (.metal:3396-3464): mirrored vertical pass
 //                (rows outside the image contribute nothing) and the
 //                combination with the L1 sign term.
+// Every sum is accumulated in the same order as the reference's separate
+// kernels, so the fusion changes no bit of the result.
 // The loss is reduced per workgroup into (sum SSIM, sum L1, pixel count) and
 // folded by one final workgroup in a fixed order; it equals the sum over
 // pixels of w*(1 - mean_c SSIM) + (1-w)*mean_c |gt - r|.
@@ -26,72 +31,56 @@ constexpr int TG = 16;
 constexpr int HALF = 5;
 constexpr int WIN = 11;
 constexpr int TW = TG + 2 * HALF;   // 26
-
-__global__ __launch_bounds__(256) void k_ssim_h_fwd(int W, int H, const float* __restrict__ img,
-                                                    const float* __restrict__ gt,
-                                                    float* __restrict__ hbuf) {
-    __shared__ float s_gt[3][TG][TW];
-    __shared__ float s_rd[3][TG][TW];
-    const int tr = threadIdx.x, lx = tr & 15, ly = tr >> 4;
-    const int bx = blockIdx.x * TG - HALF, by = blockIdx.y * TG;
-    for (int c = 0; c < 3; ++c)
-        for (int i = tr; i < TG * TW; i += 256) {
-            const int sy = i / TW, sx = i % TW, gy = by + sy, gx = bx + sx;
-            float gv = 0.f, rv = 0.f;
-            if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
-                const size_t q = ((size_t)gy * W + gx) * 3 + c;
-                gv = gt[q];
-                rv = img[q];
-            }
-            s_gt[c][sy][sx] = gv;
-            s_rd[c][sy][sx] = rv;
-        }
-    __syncthreads();
-    const int px = blockIdx.x * TG + lx, py = blockIdx.y * TG + ly;
-    if (px >= W || py >= H) return;
-    for (int c = 0; c < 3; ++c) {
-        float mx = 0.f, my = 0.f, sx = 0.f, sy = 0.f, cxy = 0.f;
-#pragma unroll
-        for (int d = 0; d < WIN; ++d) {
-            const float w = GAUSS_1D[d];
-            const float gv = s_gt[c][ly][lx + d], rv = s_rd[c][ly][lx + d];
-            mx += w * gv;
-            my += w * rv;
-            sx += w * gv * gv;
-            sy += w * rv * rv;
-            cxy += w * gv * rv;
-        }
-        float* o = hbuf + ((size_t)py * W + px) * 15 + c * 5;
-        o[0] = mx;
-        o[1] = my;
-        o[2] = sx;
-        o[3] = sy;
-        o[4] = cxy;
-    }
-}
+constexpr int TIN = TW + 2 * HALF;  // 36
 
 __global__ __launch_bounds__(256) void k_ssim_fused(int W, int H, const float* __restrict__ img,
                                                     const float* __restrict__ gt,
-                                                    const float* __restrict__ hbuf,
                                                     float* __restrict__ dbuf,
                                                     float* __restrict__ loss_part) {
+    __shared__ float s_in[2][TW][TIN][3];   // gt / render, rows y0-5.., cols x0-10..
     __shared__ float s_hp[TW][TW][5];
     __shared__ float s_f1[TG][TW], s_f2[TG][TW], s_f3[TG][TW];
     __shared__ float s_red[3][4];
     const int tr = threadIdx.x, lx = tr & 15, ly = tr >> 4;
     const int bx = blockIdx.x * TG - HALF, by = blockIdx.y * TG - HALF;
+    // input rows by .. by+25, columns bx-5 .. bx+30, all three channels
+    for (int i = tr; i < TW * TIN * 3; i += 256) {
+        const int c = i % 3, sx = (i / 3) % TIN, sy = i / (3 * TIN);
+        const int gy = by + sy, gx = bx - HALF + sx;
+        float gv = 0.f, rv = 0.f;
+        if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
+            const size_t q = ((size_t)gy * W + gx) * 3 + c;
+            gv = gt[q];
+            rv = img[q];
+        }
+        s_in[0][sy][sx][c] = gv;
+        s_in[1][sy][sx][c] = rv;
+    }
     float ssim_sum = 0.f, l1_sum = 0.f, cnt = 0.f;
     for (int c = 0; c < 3; ++c) {
+        __syncthreads();
+        // horizontal zero-padded sums (ssim_h_fwd, .metal:3053-3115) at the
+        // in-image positions of rows by.., columns bx..; zero elsewhere
         for (int i = tr; i < TW * TW; i += 256) {
             const int sy = i / TW, sx = i % TW, gy = by + sy, gx = bx + sx;
+            float mx = 0.f, my = 0.f, sxx = 0.f, syy = 0.f, cxy = 0.f;
             if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
-                const float* h = hbuf + ((size_t)gy * W + gx) * 15 + c * 5;
 #pragma unroll
-                for (int f = 0; f < 5; ++f) s_hp[sy][sx][f] = h[f];
-            } else {
-#pragma unroll
-                for (int f = 0; f < 5; ++f) s_hp[sy][sx][f] = 0.f;
+                for (int d = 0; d < WIN; ++d) {
+                    const float w = GAUSS_1D[d];
+                    const float gv = s_in[0][sy][sx + d][c], rv = s_in[1][sy][sx + d][c];
+                    mx += w * gv;
+                    my += w * rv;
+                    sxx += w * gv * gv;
+                    syy += w * rv * rv;
+                    cxy += w * gv * rv;
+                }
             }
+            s_hp[sy][sx][0] = mx;
+            s_hp[sy][sx][1] = my;
+            s_hp[sy][sx][2] = sxx;
+            s_hp[sy][sx][3] = syy;
+            s_hp[sy][sx][4] = cxy;
         }
         __syncthreads();
         for (int i = tr; i < TG * TW; i += 256) {
@@ -227,11 +216,9 @@ __global__ __launch_bounds__(256) void k_loss_final(int nparts, const float* __r
 }  // namespace
 
 void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
-                 float inv_n, float* hbuf, float* dbuf, float* v_rendered, float* loss_part,
-                 float* loss_out) {
+                 float inv_n, float* dbuf, float* v_rendered, float* loss_part, float* loss_out) {
     const dim3 grid((W + TG - 1) / TG, (H + TG - 1) / TG);
-    hipLaunchKernelGGL(k_ssim_h_fwd, grid, dim3(256), 0, s, W, H, img, gt, hbuf);
-    hipLaunchKernelGGL(k_ssim_fused, grid, dim3(256), 0, s, W, H, img, gt, hbuf, dbuf, loss_part);
+    hipLaunchKernelGGL(k_ssim_fused, grid, dim3(256), 0, s, W, H, img, gt, dbuf, loss_part);
     hipLaunchKernelGGL(k_ssim_v_bwd, grid, dim3(256), 0, s, W, H, img, gt, dbuf, w, inv_n,
                        v_rendered);
     hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(256), 0, s, (int)(grid.x * grid.y), loss_part,
