@@ -315,10 +315,10 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
                        P<uint32_t>(c->dval), P<float>(c->gacc));
     // The intersection total goes to the host while the GPU sorts by depth:
     // the host waits on an event recorded after the copy, not on the stream.
+    stage_mark(c, S_DEPTH);
     launch_total_hits(c->stream, N, P<int>(c->tiles_hit), P<Meta>(c->meta_d));
     HIP_TRY(hipMemcpyAsync(c->meta_h, c->meta_d.p, sizeof(Meta), hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipEventRecord(c->ev_total, c->stream));
-    stage_mark(c, S_DEPTH);
     uint32_t* order = nullptr;
     launch_depth_order(c->stream, N, P<uint32_t>(c->dkey), P<uint32_t>(c->dval),
                        P<uint32_t>(c->dkey2), P<uint32_t>(c->dval2), P<int>(c->dtemp),

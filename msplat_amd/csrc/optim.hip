@@ -182,7 +182,10 @@ struct BwdPtrs {
     float* v[6];
 };
 
-__global__ __launch_bounds__(256) void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
+// At least six waves per SIMD (at most 84 VGPRs) so that the many independent
+// parameter / moment loads of neighbouring waves overlap.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6)))
+void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
                                                        GaussOut go, const float* __restrict__ gacc,
                                                        float* __restrict__ vis,
                                                        float* __restrict__ gnorm,
