@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void k_emit(int N, int tbx, int tby, GaussOut 
         }
     }
     // large gaussians: one at a time, the whole wave writing 64 pairs per step
-    uint64_t bigm = __ballot(big);
+    uint64_t bigm = wave_ballot(big);
     while (bigm) {
         const int L = __builtin_ctzll(bigm);
         bigm &= bigm - 1;

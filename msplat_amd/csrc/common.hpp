@@ -110,6 +110,22 @@ __device__ __forceinline__ float dpp(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
+// Lane mask of a predicate over the active lanes.  Takes the condition as a
+// bool so that the compare result is used directly (HIP's __ballot takes an
+// int and first turns the condition into a 0/1 value).
+__device__ __forceinline__ uint64_t wave_ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+// Lane masks of single compares (one v_cmp writing an SGPR pair), to be
+// combined with scalar ands; lane_of(mask) turns a mask back into the
+// per-lane condition without a vector instruction.  Predicates: "u"
+// versions are true for NaN operands, as !(a < b) is.
+__device__ __forceinline__ uint64_t mask_lt(float a, float b) { return __builtin_amdgcn_fcmpf(a, b, 4); }
+__device__ __forceinline__ uint64_t mask_le(float a, float b) { return __builtin_amdgcn_fcmpf(a, b, 5); }
+__device__ __forceinline__ uint64_t mask_uge(float a, float b) { return __builtin_amdgcn_fcmpf(a, b, 11); }
+__device__ __forceinline__ uint64_t mask_ult(float a, float b) { return __builtin_amdgcn_fcmpf(a, b, 12); }
+__device__ __forceinline__ uint64_t mask_ge_i(int a, int b) { return __builtin_amdgcn_sicmp(a, b, 39); }
+__device__ __forceinline__ bool lane_of(uint64_t m) { return __builtin_amdgcn_inverse_ballot_w64(m); }
+
 // Sum over the 64 lanes; every lane gets the total.  All lanes must be active.
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp<0xB1>(v);    // quad_perm [1,0,3,2]
@@ -124,10 +140,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Transposed sum over the 64 lanes of eight values v[0..7]: afterwards lane l
-// holds the total of value  4 * ((l >> 3) & 1) + {0, 2, 1, 3}[l >> 4].
+// holds the total of value  4 * ((l >> 2) & 1) + {0, 2, 1, 3}[l >> 4].
 // Halves and rows are exchanged with gfx950's permlane32/16 swaps, the rest
-// with row DPP; about 21 VALU operations for the eight sums.  All lanes must
-// be active.
+// with row DPP; 18 VALU operations for the eight sums.  All lanes must be
+// active.
 __device__ __forceinline__ float swap_add32(float a, float b) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -141,20 +157,61 @@ __device__ __forceinline__ float wave_sum8_transposed(const float* v, int lane) 
     const float r1 = swap_add32(v[2], v[3]);
     const float r2 = swap_add32(v[4], v[5]);
     const float r3 = swap_add32(v[6], v[7]);
+    // s0 holds values {0,2,1,3}[row] summed over the four rows, s1 {4,6,5,7}
     const float s0 = swap_add16(r0, r1);
     const float s1 = swap_add16(r2, r3);
-    const float t0 = s0 + dpp<0x128>(s0);   // row_ror:8 == lane ^ 8
-    const float t1 = s1 + dpp<0x128>(s1);
-    float u = (lane & 8) ? t1 : t0;
+    // Lane l keeps the set of its bit 2 and receives that set's partial from
+    // lane (l - 4) mod 16 (row_ror:4), whose bit 2 is the opposite one; the
+    // two lanes plus the xor-1/2/8 partners below cover the 16 lanes once.
+    const bool hi = (lane & 4) != 0;
+    const float keep = hi ? s1 : s0;
+    const float send = hi ? s0 : s1;
+    float u = keep + dpp<0x124>(send);      // row_ror:4
     u += dpp<0xB1>(u);                      // quad_perm [1,0,3,2]
     u += dpp<0x4E>(u);                      // quad_perm [2,3,0,1]
-    const float from_lo = dpp<0x124>(u);    // row_ror:4  -> value of lane (l - 4) mod 16
-    const float from_hi = dpp<0x12C>(u);    // row_ror:12 -> value of lane (l + 4) mod 16
-    return u + ((lane & 4) ? from_lo : from_hi);
+    u += dpp<0x128>(u);                     // row_ror:8 == lane ^ 8
+    return u;
 }
+// Value index held by lane l after wave_sum8_transposed; the eight lanes with
+// bits 0, 1 and 3 clear hold the eight distinct totals.
 __device__ __forceinline__ int sum8_value_of_lane(int lane) {
     const int row = lane >> 4;
-    return 4 * ((lane >> 3) & 1) + (row == 1 ? 2 : row == 2 ? 1 : row);
+    return 4 * ((lane >> 2) & 1) + (row == 1 ? 2 : row == 2 ? 1 : row);
+}
+__device__ __forceinline__ bool sum8_owner_lane(int lane) { return (lane & 11) == 0; }
+
+// Sum over the 64 lanes, total in lane 63: row sums by row DPP, then the
+// gfx9 row_bcast:15 / row_bcast:31 adds carry rows 0..2 into row 3 (rows
+// outside the row mask keep their value).  The two masked adds are written
+// as assembly because the compiler does not fold a row-masked DPP move into
+// the add; the s_nop 1 before each covers the VALU-write -> DPP-read hazard
+// (two wait states) and the one after covers a DPP reader that may follow.
+// All lanes must be active.
+__device__ __forceinline__ float wave_sum_to_last(float v) {
+    v += dpp<0xB1>(v);                 // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);                 // quad_perm [2,3,0,1]
+    v += dpp<0x124>(v);                // row_ror:4
+    v += dpp<0x128>(v);                // row_ror:8  -> row sums
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+        "s_nop 1"
+        : "+v"(v));
+    return v;
+}
+
+// Sum over the 64 lanes with the total in every lane, without lane reads:
+// half and row swaps, then four row DPP steps.  All lanes must be active.
+__device__ __forceinline__ float wave_sum_bcast(float v) {
+    v = swap_add32(v, v);
+    v = swap_add16(v, v);
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x124>(v);
+    v += dpp<0x128>(v);
+    return v;
 }
 
 __device__ __forceinline__ int wave_max_i(int v) {

@@ -170,10 +170,10 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
         val[j] = ok ? vin[i] : 0u;
         const int d = ok ? (int)((key[j] >> shift) & mask) : 256;
         dig[j] = d;
-        uint64_t peers = __ballot(ok);
+        uint64_t peers = wave_ballot(ok);
         if (!ok) peers = ~peers;
         for (int b = 0; b < nbits; ++b) {
-            const uint64_t bb = __ballot((d >> b) & 1);
+            const uint64_t bb = wave_ballot((d >> b) & 1);
             peers &= ((d >> b) & 1) ? bb : ~bb;
         }
         const int before = __popcll(peers & lt);

@@ -52,13 +52,6 @@ __device__ __forceinline__ unsigned long long* work_slot(unsigned long long* wor
     return work + (size_t)(blockIdx.x % WORK_SLOTS) * WORK_SLOT_U64;
 }
 
-// Adds the sum of v over the wave into *dst (one atomic per wave).
-__device__ __forceinline__ void wave_count_add(unsigned long long* dst, unsigned v) {
-    unsigned long long x = v;
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-    if ((threadIdx.x & 63) == 0 && x) atomicAdd(dst, x);
-}
-
 __device__ __forceinline__ void item_range(const Items& it, const int* tile_bins, int item,
                                            int& t, int& K, int& cs, int& ce) {
     t = it.tile[item];
@@ -124,46 +117,47 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
                                                     int* __restrict__ final_idx,
                                                     float* __restrict__ out_img, ChunkBufs cb,
                                                     unsigned long long* __restrict__ work) {
-    __shared__ float4 s_geo[256];
-    __shared__ float4 s_col[256];
-    __shared__ float s_bl[256];
-    __shared__ int s_mask[256];
+    __shared__ float4 s_geo[256];    // x, y, conic a, b
+    __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
+    __shared__ float4 s_aux[256];    // clamped b, mask (bits); 16-byte stride shares the address
     const int item = blockIdx.x;
     if (item >= meta->n_items) return;
     int t, K, cs, ce;
     item_range(it, tile_bins, item, t, K, cs, ce);
     const Px px = pixel_of(t, tbx, W, H);
-    const float fx = (float)px.j, fy = (float)px.i;
+    float fx = (float)px.j, fy = (float)px.i;
+    // opaque to the compiler, so that the loop keeps the converted
+    // coordinates instead of converting the integers again every step
+    asm volatile("" : "+v"(fx), "+v"(fy));
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int tx0 = (t % tbx) * BLOCK, ty0 = (t / tbx) * BLOCK;
 
     float T = 1.f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
     int last = cs - 1;
-    unsigned ncomp = 0;     // pairs composited by this pixel
+    unsigned ncomp = 0;     // pairs composited by this wave (wave-uniform)
     unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
-    bool done = !px.inside;
+    // lanes whose pixel is still compositing (wave-uniform lane mask)
+    uint64_t live = wave_ballot(px.inside);
     for (int b = cs; b < ce; b += 256) {
-        if (__syncthreads_and(done)) break;
+        if (__syncthreads_and(live == 0)) break;
         const int idx = b + tid;
         int mask = 0;
+        float bl_raw = 0.f;
         if (idx < ce) {
             const float4* r = pk.rec + 4 * (size_t)pk.ids[idx];
             const float4 g = r[0];
-            float4 c = r[1];
-            const float bl = r[2].x;
+            const float4 c = r[1];
+            bl_raw = r[2].x;
             mask = quad_mask(g.x, g.y, g.z, g.w, c.x, c.y, tx0, ty0);
-            c.z = fmaxf(c.z + 0.5f, 0.f);
-            c.w = fmaxf(c.w + 0.5f, 0.f);
             s_geo[tid] = g;
-            s_col[tid] = c;
-            s_bl[tid] = fmaxf(bl + 0.5f, 0.f);
+            s_col[tid] = make_float4(c.x, c.y, fmaxf(c.z + 0.5f, 0.f), fmaxf(c.w + 0.5f, 0.f));
         }
-        s_mask[tid] = mask;
+        s_aux[tid] = make_float4(fmaxf(bl_raw + 0.5f, 0.f), __int_as_float(mask), 0.f, 0.f);
         __syncthreads();
         const int nb = min(256, ce - b);
         for (int ch = 0; ch < nb; ch += 64) {
             const int q = ch + lane;
-            uint64_t m = __ballot(q < nb && ((s_mask[q] >> w) & 1));
+            uint64_t m = wave_ballot(q < nb && ((__float_as_int(s_aux[q].y) >> w) & 1));
             nwit += __popcll(m);
             while (m) {
                 const int qq = ch + __builtin_ctzll(m);
@@ -176,25 +170,31 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
                 const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
-                const bool hit = !done && !(sigma < 0.f || sigma >= 5.55f) && !(alpha < 1.f / 255.f);
+                // hit: live && !(sigma < 0 || sigma >= 5.55) && !(alpha < 1/255)
+                const uint64_t hm = live & mask_uge(sigma, 0.f) & mask_ult(sigma, 5.55f) &
+                                    mask_uge(alpha, 1.f / 255.f);
                 const float nT = T * (1.f - alpha);
-                const bool stop = hit && nT <= 1e-4f;
-                const bool comp = hit && !stop;
+                const uint64_t sm = hm & mask_le(nT, 1e-4f);     // stops here
+                const uint64_t cm = hm & ~sm;                    // composites
+                const bool comp = lane_of(cm);
                 const float vis = comp ? alpha * T : 0.f;
                 C0 = fmaf(c.z, vis, C0);
                 C1 = fmaf(c.w, vis, C1);
-                C2 = fmaf(s_bl[qq], vis, C2);
+                C2 = fmaf(s_aux[qq].x, vis, C2);
                 T = comp ? nT : T;
-                last = comp ? b + qq : (stop ? b + qq - 1 : last);
-                done = done || stop;
-                ncomp += comp ? 1u : 0u;
+                last = comp ? b + qq : last;
+                ncomp += (unsigned)__popcll(cm);
+                if (sm) {      // at most once per pixel
+                    if (lane_of(sm)) last = b + qq - 1;
+                    live &= ~sm;
+                }
             }
-            if (__ballot(!done) == 0) break;
+            if (live == 0) break;
         }
     }
     if (work) {
         unsigned long long* ws = work_slot(work);
-        wave_count_add(ws, ncomp);
+        if (lane == 0 && ncomp) atomicAdd(ws, (unsigned long long)ncomp);
         if (lane == 0 && nwit) atomicAdd(ws + 2, (unsigned long long)nwit);
     }
     if (!px.inside) return;
@@ -282,11 +282,9 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                                                     ChunkBufs cb, const float* __restrict__ v_out,
                                                     float* __restrict__ gacc,
                                                     unsigned long long* __restrict__ work) {
-    __shared__ float4 s_geo[256];
-    __shared__ float4 s_col[256];
-    __shared__ float s_bl[256];
-    __shared__ int s_id[256];
-    __shared__ int s_mask[256];
+    __shared__ float4 s_geo[256];    // x, y, conic a, b
+    __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
+    __shared__ float4 s_aux[256];    // clamped b, opacity - 1, id, mask (bits)
     __shared__ int s_max;
     const int item = blockIdx.x;
     if (item >= meta->n_items) return;
@@ -298,11 +296,12 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     const int tx0 = (t % tbx) * BLOCK, ty0 = (t / tbx) * BLOCK;
 
     float T = 1.f, Tfin = 1.f, B0 = 0.f, B1 = 0.f, B2 = 0.f, vo0 = 0.f, vo1 = 0.f, vo2 = 0.f;
+    // bf = cs - 1 for pixels outside the image: no entry passes e_idx <= bf
     int bf = cs - 1;
-    unsigned ngrad = 0;     // pairs of this pixel that carry a gradient
-    // gradient value this lane writes after the reductions: lanes 0, 8, ...,
-    // 56 hold the eight transposed sums, lane 1 the ninth; -1 for the others
-    const int kslot = (lane & 7) == 0 ? sum8_value_of_lane(lane) : lane == 1 ? 8 : -1;
+    unsigned ngrad = 0;     // pairs of this wave that carry a gradient (wave-uniform)
+    // gradient value this lane writes after the reductions: the owner lanes
+    // of the eight transposed sums, lane 63 the ninth; -1 for the others
+    const int kslot = sum8_owner_lane(lane) ? sum8_value_of_lane(lane) : lane == 63 ? 8 : -1;
     // the entry mask bit that keeps this lane's value (v_rgb channels only)
     const int kbit = kslot >= 5 && kslot <= 7 ? 16 << (kslot - 5) : 0;
     unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
@@ -324,7 +323,11 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
             bf = cb.cidx[o];
         }
     }
-    const float tb0 = Tfin * bg0, tb1 = Tfin * bg1, tb2 = Tfin * bg2;
+    // The colour terms of v_alpha enter only as sum_k v_out_k (...)_k:
+    // D = sum_k v_out_k B_k (accumulated colour behind) and TB = sum_k
+    // v_out_k T_final bg_k are carried instead of the three channels.
+    const float TB = fmaf(Tfin * bg2, vo2, fmaf(Tfin * bg1, vo1, (Tfin * bg0) * vo0));
+    float D = fmaf(B2, vo2, fmaf(B1, vo1, B0 * vo0));
     const int wave_bf = wave_max_i(bf);
     if (tid == 0) s_max = cs - 1;
     __syncthreads();
@@ -346,74 +349,73 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
             // bits 4..6: the channel's raw colour + 0.5 >= 0 (its v_rgb is kept)
             mask |= (c.z + 0.5f >= 0.f ? 16 : 0) | (c.w + 0.5f >= 0.f ? 32 : 0) |
                     (braw + 0.5f >= 0.f ? 64 : 0);
-            c.z = fmaxf(c.z + 0.5f, 0.f);
-            c.w = fmaxf(c.w + 0.5f, 0.f);
             s_geo[tid] = g;
-            s_col[tid] = c;
-            s_bl[tid] = fmaxf(braw + 0.5f, 0.f);
-            s_id[tid] = gid;
+            s_col[tid] = make_float4(c.x, c.y, fmaxf(c.z + 0.5f, 0.f), fmaxf(c.w + 0.5f, 0.f));
+            s_aux[tid] = make_float4(fmaxf(braw + 0.5f, 0.f), c.y - 1.f, __int_as_float(gid),
+                                     __int_as_float(mask));
+        } else {
+            s_aux[tid].w = __int_as_float(0);
         }
-        s_mask[tid] = mask;
         __syncthreads();
         const int nb = min(256, top - cs + 1);
         const int q0 = max(0, top - wave_bf);
+        const int qlo = top - bf;      // this pixel takes entries qq >= qlo (e_idx <= bf)
         for (int ch = (q0 / 64) * 64; ch < nb; ch += 64) {
             const int q = ch + lane;
-            uint64_t m = __ballot(q >= q0 && q < nb && ((s_mask[q] >> w) & 1));
+            uint64_t m = wave_ballot(q >= q0 && q < nb &&
+                                     ((__float_as_int(s_aux[q].w) >> w) & 1));
             nwit += __popcll(m);
             while (m) {
                 const int qq = ch + __builtin_ctzll(m);
                 m &= m - 1;
-                const int e_idx = top - qq;
                 const float4 g = s_geo[qq];
                 const float4 c = s_col[qq];
-                const float r0 = c.z, r1 = c.w, r2 = s_bl[qq];   // max(raw + 0.5, 0)
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
                 const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
-                const bool valid = px.inside && e_idx <= bf && !(sigma < 0.f || sigma >= 5.55f) &&
-                                   !(alpha < 1.f / 255.f);
-                if (__ballot(valid) == 0) continue;
+                // valid: qq >= qlo && !(sigma < 0 || sigma >= 5.55) && !(alpha < 1/255)
+                const uint64_t vmask = mask_ge_i(qq, qlo) & mask_uge(sigma, 0.f) &
+                                       mask_ult(sigma, 5.55f) & mask_uge(alpha, 1.f / 255.f);
+                if (vmask == 0) continue;
                 // Branch-free per lane: lanes without a gradient compute the
                 // same terms and select zeros / their old state.
-                const bool grad = valid && alpha < 0.999f;
-                ngrad += grad ? 1u : 0u;
+                const uint64_t gmask = vmask & mask_lt(alpha, 0.999f);
+                const bool grad = lane_of(gmask);
+                ngrad += (unsigned)__popcll(gmask);
+                const float4 x = s_aux[qq];
+                const float r0 = c.z, r1 = c.w, r2 = x.x;   // max(raw + 0.5, 0)
                 // hardware reciprocal (1 ulp): the backward is compared with a tolerance
                 const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
                 const float Tn = T * ra;
                 const float fac = grad ? alpha * Tn : 0.f;
-                const float t0 = fmaf(r0, Tn, fmaf(-B0, ra, -ra * tb0));
-                const float t1 = fmaf(r1, Tn, fmaf(-B1, ra, -ra * tb1));
-                const float t2 = fmaf(r2, Tn, fmaf(-B2, ra, -ra * tb2));
-                const float v_alpha = t0 * vo0 + t1 * vo1 + t2 * vo2;
-                B0 = fmaf(r0, fac, B0);
-                B1 = fmaf(r1, fac, B1);
-                B2 = fmaf(r2, fac, B2);
+                // v_alpha = sum_k (r_k Tn - (B_k + T_final bg_k) ra) v_out_k
+                const float RV = fmaf(r2, vo2, fmaf(r1, vo1, r0 * vo0));
+                const float v_alpha = fmaf(Tn, RV, -ra * (D + TB));
+                D = fmaf(fac, RV, D);
                 T = grad ? Tn : T;
-                const float v_sigma = -alpha * v_alpha;
-                const float hv = 0.5f * v_sigma;
-                const float gx = v_sigma * fmaf(g.z, dx, g.w * dy);
-                const float gy = v_sigma * fmaf(g.w, dx, c.x * dy);
+                // v_sigma of the lanes with a gradient, zero elsewhere
+                const float vsg = grad ? -alpha * v_alpha : 0.f;
+                const float hv = 0.5f * vsg;
                 float v[8];
-                v[0] = grad ? gx : 0.f;
-                v[1] = grad ? gy : 0.f;
-                v[2] = grad ? hv * (dx * dx) : 0.f;
-                v[3] = grad ? hv * (dx * dy) : 0.f;
-                v[4] = grad ? hv * (dy * dy) : 0.f;
+                v[0] = vsg * fmaf(g.z, dx, g.w * dy);
+                v[1] = vsg * fmaf(g.w, dx, c.x * dy);
+                v[2] = hv * (dx * dx);
+                v[3] = hv * (dx * dy);
+                v[4] = hv * (dy * dy);
                 v[5] = fac * vo0;
                 v[6] = fac * vo1;
                 v[7] = fac * vo2;
-                const float vop = grad ? -v_sigma * (1.f - c.y) : 0.f;
                 const float u = wave_sum8_transposed(v, lane);
-                const float s8 = wave_sum(vop);
-                if (kslot >= 0 && (kbit == 0 || (s_mask[qq] & kbit)))
-                    atomicAdd(&gacc[(size_t)s_id[qq] * 9 + kslot], kslot == 8 ? s8 : u);
+                // opacity (logit) term -v_sigma (1 - o), total in lane 63
+                const float s8 = wave_sum_to_last(vsg * x.y);
+                if (kslot >= 0 && (kbit == 0 || (__float_as_int(x.w) & kbit)))
+                    atomicAdd(&gacc[(size_t)__float_as_int(x.z) * 9 + kslot], kslot == 8 ? s8 : u);
             }
         }
     }
     if (work) {
         unsigned long long* ws = work_slot(work);
-        wave_count_add(ws + 1, ngrad);
+        if (lane == 0 && ngrad) atomicAdd(ws + 1, (unsigned long long)ngrad);
         if (lane == 0 && nwit) atomicAdd(ws + 3, (unsigned long long)nwit);
     }
 }
