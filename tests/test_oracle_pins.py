@@ -56,6 +56,33 @@ def test_exp_against_libm():
     assert math.isnan(orc.lib().orc_expf(float("nan")))
 
 
+def test_exp_raster_against_libm():
+    """The rasteriser's exp (Remez degree-6) within 1.05 ulp of the correctly
+    rounded exp over the range of -sigma it is used on, [-5.6, 0], including
+    every float in [-1, 0] near the reduction boundaries."""
+    rng = np.random.default_rng(2)
+    x = np.concatenate([np.linspace(-5.6, 0.0, 1000001, dtype=F32),
+                        rng.uniform(-5.6, 0.0, 500000).astype(F32),
+                        # arguments around multiples of ln2/2, where k changes
+                        (np.arange(-17, 1, dtype=np.float64)[:, None] * math.log(2) / 2 +
+                         np.linspace(-1e-5, 1e-5, 2001)[None, :]).astype(F32).ravel(),
+                        np.array([0.0, -0.0, -1e-30, -5.55, -5.5499997], F32)])
+    x = x[(x >= -5.6) & (x <= 0.0)]
+    y = np.empty_like(x)
+    orc.lib().orc_expf_raster_n(x.size, orc.P(x), orc.P(y))
+    ref = np.exp(x.astype(np.float64))
+    ulp = np.spacing(ref.astype(F32)).astype(np.float64)
+    err = np.abs(y.astype(np.float64) - ref) / ulp
+    assert err.max() <= 1.05, (float(err.max()), float(x[np.argmax(err)]))
+    assert orc.lib().orc_expf_raster(0.0) == 1.0
+    assert math.isnan(orc.lib().orc_expf_raster(float("nan")))
+    # monotone over the used range (alpha thresholds are decided on it)
+    xs = np.sort(x)
+    ys = np.empty_like(xs)
+    orc.lib().orc_expf_raster_n(xs.size, orc.P(xs), orc.P(ys))
+    assert np.all(np.diff(ys.astype(np.float64)) >= 0)
+
+
 # ---------------------------------------------------------------- SH ---------
 
 SH_CLOSED = [
