@@ -328,7 +328,8 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     // v_out_k T_final bg_k are carried instead of the three channels.
     const float TB = fmaf(Tfin * bg2, vo2, fmaf(Tfin * bg1, vo1, (Tfin * bg0) * vo0));
     float D = fmaf(B2, vo2, fmaf(B1, vo1, B0 * vo0));
-    const int wave_bf = wave_max_i(bf);
+    // wave-uniform (readfirstlane): the entry loop indexes then live in scalar registers
+    const int wave_bf = __builtin_amdgcn_readfirstlane(wave_max_i(bf));
     if (tid == 0) s_max = cs - 1;
     __syncthreads();
     if (lane == 0) atomicMax(&s_max, wave_bf);
