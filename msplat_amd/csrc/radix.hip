@@ -2,11 +2,13 @@
 // value) pairs, used by the binning to order intersections without atomics.
 //
 // Sort: digits of up to 8 bits, reduce-then-scan per pass over 4096-key
-// blocks (256 threads x 16 keys):
-//   1. per-block digit histograms in LDS -> hist[digit][block]
-//   2. exclusive scan of hist in digit-major order -> scatter offsets
-//   3. per-block stable ranks: each wave ranks 1024 consecutive keys in
-//      sixteen 64-key rounds with a ballot match of equal digits, keeping
+// blocks (1024 threads x 4 keys):
+//   1. per-block digit histograms in LDS -> hist[digit][block], and the
+//      digit totals over all blocks (one global atomic per block and digit)
+//   2. one workgroup per digit scans its row of hist and adds the keys of
+//      all smaller digits -> scatter offsets
+//   3. per-block stable ranks: each wave ranks 256 consecutive keys in
+//      four 64-key rounds with a ballot match of equal digits, keeping
 //      per-digit running counts in LDS; wave counts are combined in wave
 //      order; the block is reordered by digit in LDS and written out in digit
 //      runs (coalesced stores).
@@ -19,20 +21,28 @@ namespace msp {
 
 namespace {
 
-constexpr int RT = 256;            // threads per block
-constexpr int RK = 16;             // keys per thread
+constexpr int RT = 1024;           // threads per sort block (16 waves)
+constexpr int RW = RT / 64;        // waves per sort block
+constexpr int RK = 4;              // keys per thread
 constexpr int RB = RT * RK;        // keys per block
-constexpr int WK = RB / 4;         // keys per wave (RK rounds of 64)
+constexpr int WK = RK * 64;        // keys per wave (RK rounds of 64)
 constexpr int SB = 1024;           // elements per scan block
+constexpr int MAX_PASSES = 4;      // 32-bit keys in 8-bit digits
+constexpr int DCOPIES = 16;        // copies of the digit totals (block b adds to copy b % 16)
 
-__device__ __forceinline__ int block_sum_256(int v, int* sh) {
+// Sum of v over the NT threads of a block (sh: NT / 64 ints).
+template <int NT>
+__device__ __forceinline__ int block_sum(int v, int* sh) {
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
     if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
     __syncthreads();
-    const int t = sh[0] + sh[1] + sh[2] + sh[3];
+    int t = 0;
+#pragma unroll
+    for (int k = 0; k < NT / 64; ++k) t += sh[k];
     __syncthreads();
     return t;
 }
+__device__ __forceinline__ int block_sum_256(int v, int* sh) { return block_sum<256>(v, sh); }
 
 __global__ __launch_bounds__(256) void k_block_reduce(const int* __restrict__ in, int64_t n,
                                                       int* __restrict__ tot) {
@@ -73,13 +83,24 @@ __global__ __launch_bounds__(1024) void k_scan_totals(int* __restrict__ tot, int
 }
 
 // Scan of each 1024-element block plus its offset; inclusive or exclusive.
-template <bool INCLUSIVE>
+// With PREFIX the block sums the totals of the blocks before it itself (tot
+// holds plain block totals); otherwise tot holds the scanned offsets.
+template <bool INCLUSIVE, bool PREFIX>
 __global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
                                                     int* __restrict__ out, int64_t n,
                                                     const int* __restrict__ tot) {
     __shared__ int ts[256];
+    __shared__ int sh[4];
     const int64_t base = (int64_t)blockIdx.x * SB;
     const int t = threadIdx.x;
+    int boff = 0;
+    if (PREFIX) {
+        int acc = 0;
+        for (int b = t; b < (int)blockIdx.x; b += 256) acc += tot[b];
+        boff = block_sum_256(acc, sh);
+    } else {
+        boff = tot[blockIdx.x];
+    }
     int v[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -95,7 +116,7 @@ __global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
         ts[t] += x;
         __syncthreads();
     }
-    int run = ts[t] - s4 + tot[blockIdx.x];
+    int run = ts[t] - s4 + boff;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int64_t i = base + 4 * t + k;
@@ -107,22 +128,28 @@ __global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
 
 __global__ __launch_bounds__(RT) void k_radix_hist(const uint32_t* __restrict__ keys, int64_t n,
                                                    int shift, uint32_t mask, int nblocks,
-                                                   int* __restrict__ hist) {
+                                                   int* __restrict__ hist, int* __restrict__ dtot) {
     __shared__ int h[256];
-    h[threadIdx.x] = 0;
+    if (threadIdx.x < 256) h[threadIdx.x] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * RB;
-#pragma unroll 4
+#pragma unroll
     for (int k = 0; k < RK; ++k) {
         const int64_t i = base + k * RT + threadIdx.x;
         if (i < n) atomicAdd(&h[(keys[i] >> shift) & mask], 1);
     }
     __syncthreads();
-    if (threadIdx.x <= mask) hist[(size_t)threadIdx.x * nblocks + blockIdx.x] = h[threadIdx.x];
+    if (threadIdx.x <= mask) {
+        const int c = h[threadIdx.x];
+        hist[(size_t)threadIdx.x * nblocks + blockIdx.x] = c;
+        // the digit's total over all blocks, spread over DCOPIES addresses
+        if (c) atomicAdd(&dtot[(blockIdx.x % DCOPIES) * 256 + threadIdx.x], c);
+    }
 }
 
-// Exclusive scan of one value per thread over the 256 threads of a block.
-__device__ __forceinline__ int block_exclusive_scan_256(int v, int* sh) {
+// Exclusive scan of one value per thread over the NT threads of a block.
+template <int NT>
+__device__ __forceinline__ int block_exclusive_scan(int v, int* sh) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int x = v;
 #pragma unroll
@@ -138,6 +165,30 @@ __device__ __forceinline__ int block_exclusive_scan_256(int v, int* sh) {
     return wofs + x - v;
 }
 
+// Scatter offsets of one digit (one workgroup per digit d): hist[d][b]
+// becomes the position of block b's first key with digit d, i.e. the keys
+// of all smaller digits (sum of the dtot copies over d' < d) plus those of
+// digit d in the blocks before b (exclusive scan of the row).
+__global__ __launch_bounds__(1024) void k_radix_offsets(int* __restrict__ hist, int nblocks,
+                                                        const int* __restrict__ dtot) {
+    __shared__ int sh[16];
+    const int d = blockIdx.x, t = threadIdx.x;
+    int lower = 0;
+    if (t < d) {
+#pragma unroll
+        for (int c = 0; c < DCOPIES; ++c) lower += dtot[c * 256 + t];
+    }
+    int carry = block_sum<1024>(lower, sh);
+    int* row = hist + (size_t)d * nblocks;
+    for (int c = 0; c < nblocks; c += 1024) {
+        const int i = c + t;
+        const int v = i < nblocks ? row[i] : 0;
+        const int ex = block_exclusive_scan<1024>(v, sh);
+        if (i < nblocks) row[i] = carry + ex;
+        carry += block_sum<1024>(v, sh);
+    }
+}
+
 // One LSD pass over the digit (key >> shift) & mask (nbits bits, <= 8).
 // Keys are ranked stably inside the block (each wave ranks its RB/4
 // consecutive keys in 64-key rounds by ballot-matching the digit bits and
@@ -151,12 +202,12 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
                                                       int nblocks, const int* __restrict__ offs) {
     __shared__ uint32_t s_key[RB];
     __shared__ uint32_t s_val[RB];
-    __shared__ int wcnt[4][256];
+    __shared__ int wcnt[RW][256];
     __shared__ int dstart[256];
     __shared__ int gofs[256];
-    __shared__ int scan_sh[4];
+    __shared__ int scan_sh[RW];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    for (int i = tid; i < 4 * 256; i += RT) (&wcnt[0][0])[i] = 0;
+    for (int i = tid; i < RW * 256; i += RT) (&wcnt[0][0])[i] = 0;
     __syncthreads();
     const int64_t wbase = (int64_t)blockIdx.x * RB + (int64_t)w * WK;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -184,20 +235,21 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
         if (ok && before == 0) wcnt[w][dd] = base_cnt + __popcll(peers);
     }
     __syncthreads();
-    // per digit: offsets of the four waves, the block's count and its start
+    // per digit (threads 0..255): offsets of the waves in wave order, the
+    // block's count and its start
     int cnt = 0;
-    {
+    if (tid < 256) {
         const int d = tid;
 #pragma unroll
-        for (int ww = 0; ww < 4; ++ww) {
+        for (int ww = 0; ww < RW; ++ww) {
             const int c = wcnt[ww][d];
             wcnt[ww][d] = cnt;
             cnt += c;
         }
         gofs[d] = (uint32_t)d <= mask ? offs[(size_t)d * nblocks + blockIdx.x] : 0;
     }
-    const int start = block_exclusive_scan_256(cnt, scan_sh);
-    dstart[tid] = start;
+    const int start = block_exclusive_scan<RT>(cnt, scan_sh);
+    if (tid < 256) dstart[tid] = start;
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < RK; ++j) {
@@ -224,25 +276,36 @@ inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1)
 
 int64_t scan_block_count(int64_t n) { return (n + SB - 1) / SB; }
 
-void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* tot) {
+// Up to this many blocks each scan block adds up the totals before it itself
+// (two kernels); beyond, a one-workgroup scan of the totals runs in between.
+constexpr int SCAN_DIRECT_BLOCKS = 2048;
+
+template <bool INCLUSIVE>
+void launch_scan(hipStream_t s, const int* in, int* out, int64_t n, int* tot) {
     if (n <= 0) return;
     const int nb = (int)scan_block_count(n);
     hipLaunchKernelGGL(k_block_reduce, dim3(nb), dim3(256), 0, s, in, n, tot);
-    hipLaunchKernelGGL(k_scan_totals, dim3(1), dim3(1024), 0, s, tot, nb);
-    hipLaunchKernelGGL(k_block_scan<true>, dim3(nb), dim3(256), 0, s, in, out, n, (const int*)tot);
+    if (nb <= SCAN_DIRECT_BLOCKS) {
+        hipLaunchKernelGGL((k_block_scan<INCLUSIVE, true>), dim3(nb), dim3(256), 0, s, in, out, n,
+                           (const int*)tot);
+    } else {
+        hipLaunchKernelGGL(k_scan_totals, dim3(1), dim3(1024), 0, s, tot, nb);
+        hipLaunchKernelGGL((k_block_scan<INCLUSIVE, false>), dim3(nb), dim3(256), 0, s, in, out, n,
+                           (const int*)tot);
+    }
+}
+
+void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* tot) {
+    launch_scan<true>(s, in, out, n, tot);
 }
 
 void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* tot) {
-    if (n <= 0) return;
-    const int nb = (int)scan_block_count(n);
-    hipLaunchKernelGGL(k_block_reduce, dim3(nb), dim3(256), 0, s, in, n, tot);
-    hipLaunchKernelGGL(k_scan_totals, dim3(1), dim3(1024), 0, s, tot, nb);
-    hipLaunchKernelGGL(k_block_scan<false>, dim3(nb), dim3(256), 0, s, in, out, n, (const int*)tot);
+    launch_scan<false>(s, in, out, n, tot);
 }
 
 int64_t radix_temp_ints(int64_t n) {
     const int64_t nb = (n + RB - 1) / RB;
-    return 256 * nb + scan_block_count(256 * nb) + 8;
+    return 256 * nb + DCOPIES * 256 * MAX_PASSES + 8;
 }
 
 // Sorts (k0, v0) by the bits [0, bits) of the keys; ping-pongs with (k1, v1).
@@ -255,7 +318,8 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
     const int nb = (int)((n + RB - 1) / RB);
     const int passes = (bits + 7) / 8;
     int* hist = temp;
-    int* tot = temp + 256 * (int64_t)nb;
+    int* dtot = temp + 256 * (int64_t)nb;      // per pass: DCOPIES x 256 digit totals
+    (void)hipMemsetAsync(dtot, 0, (size_t)DCOPIES * 256 * passes * sizeof(int), s);
     bool flip = false;
     int shift = 0;
     for (int pass = 0; pass < passes; ++pass) {
@@ -265,9 +329,11 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
         uint32_t* vi = flip ? v1 : v0;
         uint32_t* ko = flip ? k0 : k1;
         uint32_t* vo = flip ? v0 : v1;
+        int* dt = dtot + DCOPIES * 256 * pass;
         hipLaunchKernelGGL(k_radix_hist, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki, n, shift,
-                           mask, nb, hist);
-        launch_exclusive_scan_i32(s, hist, hist, (int64_t)(mask + 1) * nb, tot);
+                           mask, nb, hist, dt);
+        hipLaunchKernelGGL(k_radix_offsets, dim3(mask + 1), dim3(1024), 0, s, hist, nb,
+                           (const int*)dt);
         hipLaunchKernelGGL(k_radix_scatter, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki,
                            (const uint32_t*)vi, ko, vo, n, shift, mask, width, nb,
                            (const int*)hist);
