@@ -184,7 +184,7 @@ struct BwdPtrs {
 
 // At least six waves per SIMD (at most 84 VGPRs) so that the many independent
 // parameter / moment loads of neighbouring waves overlap.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
                                                        GaussOut go, const float* __restrict__ gacc,
                                                        float* __restrict__ vis,
@@ -195,15 +195,38 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
                                                        float* __restrict__ v_quat_out) {
     const int g = blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= p.N) return;
-    float* means = P.params[0];
-    float* scales = P.params[1];
-    float* quats = P.params[2];
+    // The dense parameters and moments are loaded up front, so that these
+    // loads and the gradient inputs share one memory round trip.
+    // sp / sm / sv [k]: 0-2 means, 3-5 scales, 6-9 quats, 10 opacity (the
+    // visible-only f_dc update loads its own).
+    float sp[11], sm[11], sv[11];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        sp[k] = P.params[0][3 * (size_t)g + k];
+        sm[k] = P.m[0][3 * (size_t)g + k];
+        sv[k] = P.v[0][3 * (size_t)g + k];
+        sp[3 + k] = P.params[1][3 * (size_t)g + k];
+        sm[3 + k] = P.m[1][3 * (size_t)g + k];
+        sv[3 + k] = P.v[1][3 * (size_t)g + k];
+    }
+    {
+        const float4 a = reinterpret_cast<const float4*>(P.params[2])[g];
+        const float4 b = reinterpret_cast<const float4*>(P.m[2])[g];
+        const float4 c = reinterpret_cast<const float4*>(P.v[2])[g];
+        sp[6] = a.x; sp[7] = a.y; sp[8] = a.z; sp[9] = a.w;
+        sm[6] = b.x; sm[7] = b.y; sm[8] = b.z; sm[9] = b.w;
+        sv[6] = c.x; sv[7] = c.y; sv[8] = c.z; sv[9] = c.w;
+    }
+    sp[10] = P.params[5][g];
+    sm[10] = P.m[5][g];
+    sv[10] = P.v[5][g];
     const int rad = go.radii[g];
     const float* ga = gacc + (size_t)g * 9;
     F3 vm{0.f, 0.f, 0.f};
     float vs[3] = {0.f, 0.f, 0.f}, vq[4] = {0.f, 0.f, 0.f, 0.f};
-    const F3 pw{means[3 * g], means[3 * g + 1], means[3 * g + 2]};
-    const float4 q = reinterpret_cast<const float4*>(quats)[g];
+    const F3 pw{sp[0], sp[1], sp[2]};
+    const float4 q = make_float4(sp[6], sp[7], sp[8], sp[9]);
+    const float v_op = ga[8];
     if (rad > 0) {
         const float vxy0 = ga[0], vxy1 = ga[1];
         // project_pix_vjp: x/y rows through a fixed 1/w (the w row is dropped).
@@ -245,8 +268,7 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
             vc2[2] = S[1][1];
         }
         // Recompute cov3d from scale and rotation.
-        const float es[3] = {exp_cw(scales[3 * g]), exp_cw(scales[3 * g + 1]),
-                             exp_cw(scales[3 * g + 2])};
+        const float es[3] = {exp_cw(sp[3]), exp_cw(sp[4]), exp_cw(sp[5])};
         const M3 R = quat_to_rotmat(q);
         float cov[6];
         {
@@ -368,23 +390,23 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
         v_quat_out[4 * g + 2] = vq[2]; v_quat_out[4 * g + 3] = vq[3];
     }
     // Dense Adam on means, scales, quats, opacities.
-    const float gm[3] = {vm.x, vm.y, vm.z};
+    const float gr[11] = {vm.x, vm.y, vm.z, vs[0], vs[1], vs[2], vq[0], vq[1], vq[2], vq[3], v_op};
+    const int grp[11] = {0, 0, 0, 1, 1, 1, 2, 2, 2, 2, 5};
+#pragma unroll
+    for (int k = 0; k < 11; ++k)
+        adam_elem(sp[k], sm[k], sv[k], gr[k], hp.step[grp[k]], hp.b1, hp.b2, hp.bc2[grp[k]], hp.eps);
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         const size_t i = 3 * (size_t)g + k;
-        adam_elem(P.params[0][i], P.m[0][i], P.v[0][i], gm[k], hp.step[0], hp.b1, hp.b2,
-                  hp.bc2[0], hp.eps);
-        adam_elem(P.params[1][i], P.m[1][i], P.v[1][i], vs[k], hp.step[1], hp.b1, hp.b2,
-                  hp.bc2[1], hp.eps);
+        P.params[0][i] = sp[k]; P.m[0][i] = sm[k]; P.v[0][i] = sv[k];
+        P.params[1][i] = sp[3 + k]; P.m[1][i] = sm[3 + k]; P.v[1][i] = sv[3 + k];
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const size_t i = 4 * (size_t)g + k;
-        adam_elem(P.params[2][i], P.m[2][i], P.v[2][i], vq[k], hp.step[2], hp.b1, hp.b2,
-                  hp.bc2[2], hp.eps);
-    }
-    adam_elem(P.params[5][g], P.m[5][g], P.v[5][g], ga[8], hp.step[5], hp.b1, hp.b2, hp.bc2[5],
-              hp.eps);
+    reinterpret_cast<float4*>(P.params[2])[g] = make_float4(sp[6], sp[7], sp[8], sp[9]);
+    reinterpret_cast<float4*>(P.m[2])[g] = make_float4(sm[6], sm[7], sm[8], sm[9]);
+    reinterpret_cast<float4*>(P.v[2])[g] = make_float4(sv[6], sv[7], sv[8], sv[9]);
+    P.params[5][g] = sp[10];
+    P.m[5][g] = sm[10];
+    P.v[5][g] = sv[10];
 }
 
 __global__ __launch_bounds__(256) void k_split_gacc(int N, const float* __restrict__ gacc,
