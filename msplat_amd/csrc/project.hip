@@ -88,10 +88,35 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     const float* __restrict__ quats, const float* __restrict__ f_dc,
     const float* __restrict__ f_rest, const float* __restrict__ opac_logits, GaussOut go,
     uint32_t* __restrict__ dkey, uint32_t* __restrict__ dval, float* __restrict__ gacc) {
+    const int g0 = blockIdx.x * PROJ_T;
+    const int g = g0 + threadIdx.x;
+    const bool live = g < p.N;
+    // Per-gaussian inputs first, so that their loads overlap the staging below.
+    V3 pw{0.f, 0.f, 0.f};
+    float sc[3] = {0.f, 0.f, 0.f}, dc[3] = {0.f, 0.f, 0.f}, ol = 0.f;
+    float4 q = make_float4(1.f, 0.f, 0.f, 0.f);
+    if (live) {
+        pw = V3{means[3 * g], means[3 * g + 1], means[3 * g + 2]};
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            sc[k] = scales[3 * (size_t)g + k];
+            dc[k] = f_dc[3 * (size_t)g + k];
+        }
+        q = reinterpret_cast<const float4*>(quats)[g];
+        ol = opac_logits[g];
+    }
+    // Zero this workgroup's raster gradient accumulators (PROJ_T * 9
+    // contiguous floats) with 16-byte stores.
+    {
+        const int64_t base = (int64_t)g0 * 9;
+        const int cnt = (int)min((int64_t)PROJ_T * 9, (int64_t)p.N * 9 - base);
+        float4* dst4 = reinterpret_cast<float4*>(gacc + base);
+        for (int i = threadIdx.x; i < cnt / 4; i += PROJ_T) dst4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int i = (cnt / 4) * 4 + threadIdx.x; i < cnt; i += PROJ_T) gacc[base + i] = 0.f;
+    }
     // Stage this workgroup's features_rest rows (PROJ_T * rest_per contiguous
     // floats, 16-byte aligned) through LDS with coalesced 16-byte loads.
     extern __shared__ float s_rest[];
-    const int g0 = blockIdx.x * PROJ_T;
     if (p.dtu > 0) {
         const int64_t base = (int64_t)g0 * p.rest_per;
         const int64_t total = (int64_t)p.N * p.rest_per;
@@ -102,22 +127,16 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
         for (int i = (cnt / 4) * 4 + threadIdx.x; i < cnt; i += PROJ_T) s_rest[i] = f_rest[base + i];
         __syncthreads();
     }
-    const int g = g0 + threadIdx.x;
-    if (g >= p.N) return;
-#pragma unroll
-    for (int q = 0; q < 9; ++q) gacc[(size_t)g * 9 + q] = 0.f;
+    if (!live) return;
     go.radii[g] = 0;
     go.tiles_hit[g] = 0;
     dkey[g] = 0xFFFFFFFFu;
     dval[g] = (uint32_t)g;
 
-    const V3 pw{means[3 * g], means[3 * g + 1], means[3 * g + 2]};
     const V3 pv = xf4x3(p.vm, pw);
     if (pv.z <= p.clip) return;
 
-    const float s0 = exp_cw(scales[3 * g]), s1 = exp_cw(scales[3 * g + 1]),
-                s2 = exp_cw(scales[3 * g + 2]);
-    const float4 q = reinterpret_cast<const float4*>(quats)[g];
+    const float s0 = exp_cw(sc[0]), s1 = exp_cw(sc[1]), s2 = exp_cw(sc[2]);
     float cov[6];
     cov3d_of(s0, s1, s2, p.glob_scale, q, cov);
 
@@ -175,10 +194,10 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     const float inv = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
     const V3 dir{dx * inv, dy * inv, dz * inv};
     float col[3];
-    sh_color(p.dtu, dir, f_dc + 3 * (size_t)g, s_rest + (size_t)p.rest_per * threadIdx.x, col);
+    sh_color(p.dtu, dir, dc, s_rest + (size_t)p.rest_per * threadIdx.x, col);
     float4* rec = go.rec + 4 * (size_t)g;
     rec[0] = make_float4(px, py, ca, cb);
-    rec[1] = make_float4(cc, sigmoid(opac_logits[g]), col[0], col[1]);
+    rec[1] = make_float4(cc, sigmoid(ol), col[0], col[1]);
     rec[2] = make_float4(col[2], ex, ey, pv.z);
     rec[3] = make_float4(dir.x, dir.y, dir.z, 0.f);
     dkey[g] = __float_as_uint(pv.z);
