@@ -534,7 +534,7 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
                       P<float>(c->final_T), P<int>(c->final_idx), chunks(c),
                       P<float>(c->v_rendered), P<float>(c->gacc), work_counters(c));
     AdamHP hp;
-    for (int g = 0; g < 6; ++g) { hp.step[g] = a->adam_step_sizes[g]; hp.bc2[g] = a->adam_bc2_sqrts[g]; }
+    for (int g = 0; g < 6; ++g) { hp.step[g] = a->adam_step_sizes[g]; hp.inv_bc2[g] = 1.0f / a->adam_bc2_sqrts[g]; }
     hp.b1 = a->adam_beta1;
     hp.b2 = a->adam_beta2;
     hp.eps = a->adam_eps;

@@ -141,7 +141,7 @@ void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt,
 
 struct AdamHP {
     float step[6];
-    float bc2[6];
+    float inv_bc2[6];   // 1 / sqrt(1 - beta2^t) per parameter group
     float b1, b2, eps;
 };
 

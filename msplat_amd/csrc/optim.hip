@@ -52,8 +52,16 @@ __device__ __forceinline__ M3 transpose(const M3& A) {
 }
 __device__ __forceinline__ float dot3(F3 a, F3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
 
+// The backward and Adam outputs are compared with the CPU restatement to a
+// relative tolerance, so their divisions and square roots use the hardware
+// reciprocal and square root (v_rcp_f32 / v_sqrt_f32, about 1 ulp) rather
+// than the correctly rounded multi-instruction IEEE sequences; the forward
+// stages, which must match bit for bit, keep IEEE division and sqrt.
+__device__ __forceinline__ float rcp_hw(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float sqrt_hw(float x) { return __builtin_amdgcn_sqrtf(x); }
+
 __device__ __forceinline__ M3 quat_to_rotmat(float4 q) {
-    const float s = 1.f / sqrtf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+    const float s = rcp_hw(sqrt_hw(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z));
     const float w = q.x * s, x = q.y * s, y = q.z * s, z = q.w * s;
     M3 R;
     R.m[0][0] = 1.f - 2.f * (y * y + z * z);
@@ -68,11 +76,12 @@ __device__ __forceinline__ M3 quat_to_rotmat(float4 q) {
     return R;
 }
 
+// adam_update_element (.metal:1791-1800); inv_bc2 = 1 / sqrt(1 - beta2^t).
 __device__ __forceinline__ void adam_elem(float& p, float& m, float& v, float g, float step,
-                                          float b1, float b2, float bc2, float eps) {
+                                          float b1, float b2, float inv_bc2, float eps) {
     const float mn = fmaf(b1, m, (1.0f - b1) * g);
     const float vn = fmaf(b2, v, (1.0f - b2) * g * g);
-    p -= step * mn / (sqrtf(vn) / bc2 + eps);
+    p -= step * mn * rcp_hw(sqrt_hw(vn) * inv_bc2 + eps);
     m = mn;
     v = vn;
 }
@@ -162,7 +171,7 @@ __global__ __launch_bounds__(SHA_T) void k_sh_rest_adam(int64_t n, int rest_per,
             const int li = g - gA, b = rem / 3, c = rem - 3 * (rem / 3);
             if (b < n_used && s_vis[li]) {
                 const float grad = s_basis[li][b] * s_vrgb[li][c];
-                adam_elem(pv[k], mv[k], vv[k], grad, hp.step[4], hp.b1, hp.b2, hp.bc2[4], hp.eps);
+                adam_elem(pv[k], mv[k], vv[k], grad, hp.step[4], hp.b1, hp.b2, hp.inv_bc2[4], hp.eps);
             }
         }
         if (++rem == rest_per) { rem = 0; ++g; }
@@ -182,8 +191,9 @@ struct BwdPtrs {
     float* v[6];
 };
 
-// At least six waves per SIMD (at most 84 VGPRs) so that the many independent
-// parameter / moment loads of neighbouring waves overlap.
+// At least three waves per SIMD (at most 168 VGPRs): with every load of a
+// thread issued in two batches (dense parameters and gradient inputs, then
+// the visible-only f_dc and statistics), that keeps enough bytes in flight.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
                                                        GaussOut go, const float* __restrict__ gacc,
@@ -228,12 +238,23 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
     const float4 q = make_float4(sp[6], sp[7], sp[8], sp[9]);
     const float v_op = ga[8];
     if (rad > 0) {
+        // Visible-only inputs (f_dc with its moments, the densify statistics)
+        // are loaded before the gradient arithmetic, in one round trip.
+        float dp[3], dm[3], dv[3];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            dp[c] = P.params[3][3 * (size_t)g + c];
+            dm[c] = P.m[3][3 * (size_t)g + c];
+            dv[c] = P.v[3][3 * (size_t)g + c];
+        }
+        const float st_vis = vis[g], st_gnorm = gnorm[g], st_max2d = max2d[g];
+        const float vrgb[3] = {ga[5], ga[6], ga[7]};
         const float vxy0 = ga[0], vxy1 = ga[1];
         // project_pix_vjp: x/y rows through a fixed 1/w (the w row is dropped).
         {
             const float* m = p.pm;
             const float hw = m[12] * pw.x + m[13] * pw.y + m[14] * pw.z + m[15];
-            const float rw = 1.f / (hw + 1e-6f);
+            const float rw = rcp_hw(hw + 1e-6f);
             const float vpx = 0.5f * (float)p.W * vxy0 * rw, vpy = 0.5f * (float)p.H * vxy1 * rw;
             const float vpz = 0.f;
             vm.x = m[0] * vpx + m[4] * vpy + m[8] * vpz;
@@ -292,9 +313,9 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
                   w[8] * pw.x + w[9] * pw.y + w[10] * pw.z + w[11]};
             const float tan_fovx = 0.5f * (float)p.W / p.fx, tan_fovy = 0.5f * (float)p.H / p.fy;
             const float lim_x = 1.3f * tan_fovx, lim_y = 1.3f * tan_fovy;
-            pv.x = pv.z * fminf(lim_x, fmaxf(-lim_x, pv.x / pv.z));
-            pv.y = pv.z * fminf(lim_y, fmaxf(-lim_y, pv.y / pv.z));
-            const float rz = 1.f / pv.z, rz2 = rz * rz;
+            const float rz = rcp_hw(pv.z), rz2 = rz * rz;
+            pv.x = pv.z * fminf(lim_x, fmaxf(-lim_x, pv.x * rz));
+            pv.y = pv.z * fminf(lim_y, fmaxf(-lim_y, pv.y * rz));
             M3 Wm;
             Wm.m[0][0] = w[0]; Wm.m[0][1] = w[4]; Wm.m[0][2] = w[8];
             Wm.m[1][0] = w[1]; Wm.m[1][1] = w[5]; Wm.m[1][2] = w[9];
@@ -356,7 +377,7 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
                 vs[i] = dot3(F3{R.m[i][0], R.m[i][1], R.m[i][2]},
                              F3{vM.m[i][0], vM.m[i][1], vM.m[i][2]}) * es[i];
             const M3 vR = mat_mul(vM, S);
-            const float s = 1.f / sqrtf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+            const float s = rcp_hw(sqrt_hw(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z));
             const float w = q.x * s, x = q.y * s, y = q.z * s, z = q.w * s;
             const auto& Rv = vR.m;
             vq[0] = 2.f * (x * (Rv[1][2] - Rv[2][1]) + y * (Rv[2][0] - Rv[0][2]) +
@@ -370,14 +391,18 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
         }
         // f_dc Adam (visible only) and densify statistics.
 #pragma unroll
+        for (int c = 0; c < 3; ++c)
+            adam_elem(dp[c], dm[c], dv[c], SH_C0 * vrgb[c], hp.step[3], hp.b1, hp.b2, hp.inv_bc2[3],
+                      hp.eps);
+#pragma unroll
         for (int c = 0; c < 3; ++c) {
-            const size_t i = 3 * (size_t)g + c;
-            adam_elem(P.params[3][i], P.m[3][i], P.v[3][i], SH_C0 * ga[5 + c], hp.step[3], hp.b1,
-                      hp.b2, hp.bc2[3], hp.eps);
+            P.params[3][3 * (size_t)g + c] = dp[c];
+            P.m[3][3 * (size_t)g + c] = dm[c];
+            P.v[3][3 * (size_t)g + c] = dv[c];
         }
-        vis[g] += 1.0f;
-        gnorm[g] += sqrtf(vxy0 * vxy0 + vxy1 * vxy1);
-        max2d[g] = fmaxf(max2d[g], (float)rad * inv_max_dim);
+        vis[g] = st_vis + 1.0f;
+        gnorm[g] = st_gnorm + sqrtf(vxy0 * vxy0 + vxy1 * vxy1);
+        max2d[g] = fmaxf(st_max2d, (float)rad * inv_max_dim);
     }
     if (v_mean_out) {
         v_mean_out[3 * g] = vm.x; v_mean_out[3 * g + 1] = vm.y; v_mean_out[3 * g + 2] = vm.z;
@@ -394,7 +419,7 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
     const int grp[11] = {0, 0, 0, 1, 1, 1, 2, 2, 2, 2, 5};
 #pragma unroll
     for (int k = 0; k < 11; ++k)
-        adam_elem(sp[k], sm[k], sv[k], gr[k], hp.step[grp[k]], hp.b1, hp.b2, hp.bc2[grp[k]], hp.eps);
+        adam_elem(sp[k], sm[k], sv[k], gr[k], hp.step[grp[k]], hp.b1, hp.b2, hp.inv_bc2[grp[k]], hp.eps);
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         const size_t i = 3 * (size_t)g + k;

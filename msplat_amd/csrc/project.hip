@@ -83,6 +83,9 @@ __device__ __forceinline__ void sh_color(int degree, V3 d, const float* dc, cons
 
 constexpr int PROJ_T = 128;   // gaussians per workgroup
 
+// PROJ_STAGE: 16-byte features_rest loads per thread, enough for PROJ_T rows
+// of up to 48 floats (SH degree <= 3) or 72 floats (degree 4).
+template <int PROJ_STAGE>
 __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     CamParams p, const float* __restrict__ means, const float* __restrict__ scales,
     const float* __restrict__ quats, const float* __restrict__ f_dc,
@@ -115,16 +118,32 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
         for (int i = (cnt / 4) * 4 + threadIdx.x; i < cnt; i += PROJ_T) gacc[base + i] = 0.f;
     }
     // Stage this workgroup's features_rest rows (PROJ_T * rest_per contiguous
-    // floats, 16-byte aligned) through LDS with coalesced 16-byte loads.
+    // floats, 16-byte aligned) through LDS with coalesced 16-byte loads.  All
+    // of a thread's loads are issued before the first LDS store, so the
+    // workgroup waits for one memory round trip, not one per load.
     extern __shared__ float s_rest[];
     if (p.dtu > 0) {
         const int64_t base = (int64_t)g0 * p.rest_per;
         const int64_t total = (int64_t)p.N * p.rest_per;
         const int cnt = (int)min((int64_t)PROJ_T * p.rest_per, total - base);
+        const int nv = cnt / 4;
         const float4* src4 = reinterpret_cast<const float4*>(f_rest + base);
         float4* dst4 = reinterpret_cast<float4*>(s_rest);
-        for (int i = threadIdx.x; i < cnt / 4; i += PROJ_T) dst4[i] = src4[i];
-        for (int i = (cnt / 4) * 4 + threadIdx.x; i < cnt; i += PROJ_T) s_rest[i] = f_rest[base + i];
+        if (nv > 0) {
+            // Branch-free: indexes past the block's rows re-read its last
+            // vector and store it to a spare LDS slot after the staging
+            // area, so the compiler keeps all loads in flight together.
+            float4 stage[PROJ_STAGE];
+#pragma unroll
+            for (int k = 0; k < PROJ_STAGE; ++k)
+                stage[k] = src4[min((int)threadIdx.x + k * PROJ_T, nv - 1)];
+#pragma unroll
+            for (int k = 0; k < PROJ_STAGE; ++k) {
+                const int i = threadIdx.x + k * PROJ_T;
+                dst4[i < nv ? i : PROJ_T * PROJ_STAGE] = stage[k];
+            }
+        }
+        for (int i = nv * 4 + threadIdx.x; i < cnt; i += PROJ_T) s_rest[i] = f_rest[base + i];
         __syncthreads();
     }
     if (!live) return;
@@ -211,9 +230,17 @@ void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
                         uint32_t* dkey, uint32_t* dval, float* gacc) {
     if (p.N <= 0) return;
     const int blocks = (p.N + PROJ_T - 1) / PROJ_T;
-    const size_t lds = p.dtu > 0 ? (size_t)PROJ_T * p.rest_per * sizeof(float) : 0;
-    hipLaunchKernelGGL(k_project_fwd, dim3(blocks), dim3(PROJ_T), lds, s, p, means, scales, quats,
-                       f_dc, f_rest, opac_logits, go, dkey, dval, gacc);
+    // staging area of PROJ_STAGE vectors per thread plus the spare slot
+    const int stage = p.rest_per <= 48 ? PROJ_T * 48 / 4 / PROJ_T : PROJ_T * 72 / 4 / PROJ_T;
+    const size_t lds = p.dtu > 0 ? ((size_t)PROJ_T * stage + 1) * 16 : 0;
+    if (p.rest_per <= 48)
+        hipLaunchKernelGGL(k_project_fwd<PROJ_T * 48 / 4 / PROJ_T>, dim3(blocks), dim3(PROJ_T), lds,
+                           s, p, means, scales, quats, f_dc, f_rest, opac_logits, go, dkey, dval,
+                           gacc);
+    else
+        hipLaunchKernelGGL(k_project_fwd<PROJ_T * 72 / 4 / PROJ_T>, dim3(blocks), dim3(PROJ_T), lds,
+                           s, p, means, scales, quats, f_dc, f_rest, opac_logits, go, dkey, dval,
+                           gacc);
 }
 
 }  // namespace msp
