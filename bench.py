@@ -180,6 +180,138 @@ def traffic_summary(dirs: list, copy_mib: int, last: int, commands: str) -> dict
             "hbm_bytes_per_launch": 1024 * (fk * fs + wk * ws), "commands": commands}
 
 
+def _stage_line(stages):
+    return {k: ms / c for k, (ms, c) in stages.items() if c}
+
+
+def proj_bytes(n_vis, n_cul):
+    """Algorithmic bytes of the projection: read means, log-scales, quats,
+    f_dc, f_rest (45), opacity = 236 B; write the 64-byte record, radii,
+    tiles hit, depth key / value and the zeroed 36-byte gradient accumulator
+    = 116 B (culled: 12 B read, 52 B written)."""
+    return n_vis * (236 + 116) + n_cul * (12 + 52)
+
+
+def bench_config4(args):
+    """Config 4, heavy-tile stress: 1M SH3 gaussians (70% in a N(0, 0.05^2)
+    blob 1.5 units in front of the camera, 30% U[-4,4]^3), 2594x1680, full
+    train steps (forward + SSIM/L1 + backward + Adam) on one camera, target =
+    render of the means jittered by N(0, 0.02) plus N(0, 0.01) pixel noise."""
+    import torch
+    from msplat_amd import camera, device, synthetic
+    from msplat_amd.trainer import LR_INIT
+    lib = device.init(0)
+    bg = np.array([0.6130, 0.0101, 0.3984], np.float32)
+    t = time.perf_counter()
+    scene = synthetic.config4()
+    params = [device.to_dev(a) for a in scene.params()]
+    g = device.DeviceGaussians.from_tensors(params, 3)
+    su = camera.prepare_cam(scene.cameras[0])
+    seed = synthetic.BASE_SEED + 4
+    jit = device.DeviceGaussians.from_tensors(params, 3)
+    jit.bufs[0][: jit.n] += synthetic.device_randn(3 * jit.n, seed * 7 + 11, 0.0, 0.02).view(jit.n, 3)
+    gt = device.render(jit, su, 3, bg).clone()
+    gt += synthetic.device_randn(gt.numel(), seed * 13, 0.0, 0.01).view_as(gt)
+    del jit
+    torch.cuda.synchronize()
+    m = device.meta()
+    log(f"config4 setup {time.perf_counter() - t:.1f}s: {g.n} gaussians, {su.width}x{su.height}, "
+        f"{m['total_isect']} intersections, largest tile {m['max_count']} entries, "
+        f"{m['n_chunked_tiles']} chunked tiles, {m['n_items']} raster work items")
+    for s in range(args.warmup):
+        device.train_step(g, su, 3, bg, gt, 0.2, LR_INIT, s + 1, want_loss=False)
+    device.sync()
+    device.drain_raster_counters()
+    _abi_check(lib.msplat_hip_enable_stage_timing(1))
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        device.train_step(g, su, 3, bg, gt, 0.2, LR_INIT, args.warmup + s + 1, want_loss=False)
+    device.sync()
+    dt = time.perf_counter() - t0
+    stages, _ = stage_times(lib)
+    pairs = device.drain_raster_counters()
+    m = device.meta()
+    its = args.steps / dt
+    for k, v in _stage_line(stages).items():
+        log(f"  {k:18s} {v:8.3f} ms/call")
+    log(f"config4: {its:.1f} train it/s; largest tile {m['max_count']} entries")
+    return {"metric": "train iters/sec, config 4 (1M heavy-tile blob SH3 @2594x1680), 1xMI355X",
+            "value": its, "unit": "it/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": 1e3 * dt / args.steps, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "config4: 1M SH3, 70% blob 1.5 units ahead, 2594x1680, full train step",
+                       "intersections": m["total_isect"], "largest_tile": m["max_count"],
+                       "chunked_tiles": m["n_chunked_tiles"], "raster_items": m["n_items"]},
+            "stage_ms": _stage_line(stages),
+            "bwd_grad_pairs_per_step": pairs[1] / max(args.steps, 1)}
+
+
+def config5_cameras(n_poses=100, width=4946, height=3286):
+    from msplat_amd import camera, synthetic
+    st = synthetic.Stream(synthetic.BASE_SEED + 5 + 1000)
+    dirs = synthetic._sphere_dirs(st, n_poses)
+    return [camera.pinhole(width, height, 70.0, camera.look_at(5.0 * d)) for d in dirs]
+
+
+def bench_config5(args):
+    """Config 5, render only: 6M SH3 gaussians with config-2 distributions
+    (generated on the GPU), 4946x3286, 100 poses on a radius-5 sphere; render
+    FPS and the projection's HBM rate."""
+    import torch
+    from msplat_amd import camera, device, synthetic
+    lib = device.init(0)
+    bg = np.array([0.6130, 0.0101, 0.3984], np.float32)
+    t = time.perf_counter()
+    params = synthetic.device_cloud(6_000_000, 3, synthetic.BASE_SEED + 5)
+    g = device.DeviceGaussians.from_tensors(params, 3)
+    del params
+    cams = config5_cameras()
+    setups = [camera.prepare_cam(c) for c in cams]
+    out = torch.empty((setups[0].height, setups[0].width, 3), dtype=torch.float32, device="cuda")
+    for i in range(3):
+        device.render(g, setups[i], 3, bg, out)
+    torch.cuda.synchronize()
+    log(f"config5 setup {time.perf_counter() - t:.1f}s")
+    _abi_check(lib.msplat_hip_enable_stage_timing(1))
+    vis = cul = 0
+    isect = 0
+    t0 = time.perf_counter()
+    for i, su in enumerate(setups):
+        device.render(g, su, 3, bg, out)
+    device.sync()
+    dt = time.perf_counter() - t0
+    stages, _ = stage_times(lib)
+    # visible counts per pose, outside the timed loop
+    for su in setups[:10]:
+        device.render(g, su, 3, bg, out)
+        radii = device.intermediate("radii", np.int32)
+        vis += int((radii > 0).sum())
+        cul += int((radii <= 0).sum())
+        isect += device.meta()["total_isect"]
+    vis, cul, isect = vis / 10, cul / 10, isect / 10
+    fps = len(setups) / dt
+    st = _stage_line(stages)
+    pb = proj_bytes(vis, cul)
+    hbm = {"proj_sh_fwd": {"ms": st["proj_sh_fwd"], "bytes": pb,
+                           "GBps": pb / (st["proj_sh_fwd"] * 1e-3) / 1e9,
+                           "frac": pb / (st["proj_sh_fwd"] * 1e-3) / HBM_PEAK}}
+    for k, v in st.items():
+        log(f"  {k:18s} {v:8.3f} ms/call")
+    log(f"config5: {fps:.1f} render FPS; projection {hbm['proj_sh_fwd']['GBps']:.0f} GB/s")
+    return {"metric": "render FPS, config 5 (6M SH3 @4946x3286, 100 poses), 1xMI355X",
+            "value": fps, "unit": "FPS", "n_gpus": 1, "steps": len(setups), "warmup": 3,
+            "ms_per_step": 1e3 * dt / len(setups), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "config5: 6M SH3, 4946x3286, 100 poses on a radius-5 sphere, render only",
+                       "visible_gaussians_mean": vis, "intersections_mean": isect},
+            "stage_ms": st, "hbm_stages": hbm}
+
+
+def _abi_check(rc):
+    from msplat_amd import _abi
+    _abi.check(rc)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,6 +321,10 @@ def main():
     ap.add_argument("--n", type=int, default=1_500_000)
     ap.add_argument("--cpu-steps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5),
+                    help="3 (default): the headline train + render workload; 4: heavy-tile train "
+                         "steps at 2594x1680; 5: 6M-gaussian render at 4946x3286 (extra lines, "
+                         "not the headline metric)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB five times (calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counters against known traffic) and exit")
@@ -211,6 +347,12 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
               "this build has no multi-GPU path.", file=sys.stderr)
         sys.exit(2)
+    if args.config in (4, 5):
+        if args.config == 4 and args.steps == 300:
+            args.steps = 50
+        res = bench_config4(args) if args.config == 4 else bench_config5(args)
+        print(json.dumps(res), flush=True)
+        return
     if args.copy_mib > 0:
         import torch
         n = args.copy_mib * (1 << 20) // 4
@@ -318,10 +460,7 @@ def main():
     n_cul = n_all - n_vis
     px = cams[0].width * cams[0].height
     algo_bytes = {
-        # read means, log-scales, quats, f_dc, f_rest (45), opacity = 236 B; write the
-        # 64-byte record, radii, tiles hit, depth key / value and the zeroed
-        # 36-byte gradient accumulator = 116 B (culled: 12 B read, 52 B written)
-        "proj_sh_fwd": n_vis * (236 + 116) + n_cul * (12 + 52),
+        "proj_sh_fwd": proj_bytes(n_vis, n_cul),
         # f_rest, its two moments read and written (1080 B), direction 16 B,
         # v_rgb 12 B, radii 4 B (culled: radii only)
         "sh_rest_adam": n_vis * (1080 + 16 + 12 + 4) + n_cul * 4,

@@ -157,6 +157,26 @@ int msplat_hip_randn(float* dst, int64_t n, uint64_t seed);
  * afterTrain (model.cpp:280-287 clamps the logits on the host). */
 int msplat_hip_clamp_max(float* p, int64_t n, float hi);
 
+/* RGBA8 display image of an fp32 RGB render: for each of n_pixels pixels
+ * (device img[n,3] -> device rgba[n,4], 4-byte aligned) each channel is
+ * clamped to [0, 1], multiplied by 255 and truncated to a byte; alpha is 255.
+ * The conversion of Trainer::renderFromPoseToBuffer (msplat_api.mm:230-238,
+ * done there on the CPU), on the context stream. */
+int msplat_hip_image_to_rgba8(const float* img, int64_t n_pixels, uint8_t* rgba);
+
+/* Evaluation metrics of a render against its target (device [H,W,3] fp32
+ * images): PSNR = 10 log10(1 / MSE) and mean |r - g| as psnr / l1_loss
+ * (model.cpp:25-40) compute them, and SSIM averaged over pixels and channels
+ * as ssim_eval (ssim.cpp:61-123) does, with a window_size-tap Gaussian
+ * (odd, <= 11; the reference's default 11) of width sigma (default 1.5) and
+ * borders clamped to the edge pixel.  Sums are fp64, as there.  Waits for the
+ * result. */
+typedef struct MsplatImageMetrics {
+    float psnr, ssim, l1;
+} MsplatImageMetrics;
+int msplat_hip_image_metrics(const float* img, const float* gt, int32_t height, int32_t width,
+                             int32_t window_size, float sigma, MsplatImageMetrics* out);
+
 /* Per-stage GPU timing (msplat_enable_gpu_timing / msplat_drain_stage_times,
  * bindings.h:28-33).  When enabled every stage of every render / train call is
  * bracketed by HIP events on the context stream (no extra synchronisation).

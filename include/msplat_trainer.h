@@ -128,7 +128,10 @@ MsplatPixelBuffer msplat_trainer_render_pose(MsplatTrainer t, const float camToW
                                              int32_t refCameraIndex);
 
 /* Same into a caller-provided RGBA8 host buffer (msplat_c_api.h:106-108):
- * call with outRGBA = NULL to get the size.  Returns 0 or a negative code. */
+ * call with outRGBA = NULL to get the size.  Each channel is clamped to
+ * [0, 1], times 255, truncated (msplat_api.mm:230-238); the conversion runs
+ * on the GPU and 4 bytes per pixel are copied.  Returns 0 or a negative
+ * code. */
 int32_t msplat_trainer_render_pose_to_buffer(MsplatTrainer t, const float camToWorld[16],
                                              int32_t refCameraIndex, uint8_t* outRGBA,
                                              int32_t* outWidth, int32_t* outHeight);
@@ -138,6 +141,66 @@ int32_t msplat_trainer_render_pose_to_buffer(MsplatTrainer t, const float camToW
 int32_t msplat_trainer_render_pose_device(MsplatTrainer t, const float camToWorld[16],
                                           int32_t refCameraIndex, float* outDevice,
                                           int32_t* outWidth, int32_t* outHeight);
+
+/* MsplatEvalMetrics (msplat_c_api.h:64-70). */
+typedef struct MsplatEvalMetrics {
+    float psnr;
+    float ssim;
+    float l1;
+    int32_t numTest;
+    int32_t numGaussians;
+} MsplatEvalMetrics;
+
+/* Evaluation on held-out cameras (msplat_trainer_evaluate, msplat_c_api.h:99;
+ * Trainer::evaluate, msplat_api.mm:138-166): each camera is rendered at the
+ * final iteration's resolution, its full-resolution target is box-filtered
+ * to that size, and PSNR / SSIM (11 taps, sigma 1.5) / L1 are averaged over
+ * the cameras (msplat_hip_image_metrics).  The reference's test cameras come
+ * from its dataset; here they are passed in (images on the device when
+ * on_device != 0).  numTest = 0 on error. */
+MsplatEvalMetrics msplat_trainer_evaluate(MsplatTrainer t, int32_t n_test,
+                                          const MsplatTrainerCamera* cameras,
+                                          const float* const* images, int32_t on_device);
+
+/* Scene files (msplat_c_api.h:109-110; Trainer::exportPly / exportSplat,
+ * msplat_api.mm:240-246; layouts of save_gaussians.cpp).  0 or a negative
+ * code (message in msplat_trainer_last_error). */
+int32_t msplat_trainer_export_ply(MsplatTrainer t, const char* path);
+int32_t msplat_trainer_export_splat(MsplatTrainer t, const char* path);
+
+/* Checkpoints in the reference's .msplat byte format (msplat_c_api.h:111-112;
+ * Model::saveCheckpoint / loadCheckpoint, model.cpp:361-488).  load returns
+ * the saved step (>= 0; training continues after it, with the camera order
+ * reshuffled as Trainer::loadCheckpoint does) or a negative code. */
+int32_t msplat_trainer_save_checkpoint(MsplatTrainer t, const char* path);
+int32_t msplat_trainer_load_checkpoint(MsplatTrainer t, const char* path);
+
+/* Resume from an exported PLY (the CLI's --resume, cli/msplat.cpp:132;
+ * Model::loadPly, model.cpp:319-330): replaces the gaussians, restarts the
+ * optimiser and returns the step recorded in the file (0 if none) or a
+ * negative code.  The iteration counter is left to the caller, as there. */
+int32_t msplat_trainer_load_ply(MsplatTrainer t, const char* path);
+
+/* Dataset normalisation the scene files undo (export) or apply (load) when
+ * keep != 0: world = stored / scale + translation (keepCrs,
+ * loaders.hpp:38-43).  Identity by default. */
+int32_t msplat_trainer_set_crs(MsplatTrainer t, float scale, const float translation[3],
+                               int32_t keep);
+
+/* Host-memory scene files (no GPU call): the writers and the reader behind
+ * the trainer's exports, for parameter arrays already in host memory
+ * (params[6] as for msplat_trainer_create; opacities [n]).  read: call with
+ * params == NULL for *n and *rest_bases, then with six buffers of those
+ * sizes.  0 or a negative code (message in msplat_trainer_last_error). */
+int32_t msplat_scene_write_ply(const char* path, int64_t n, int32_t rest_bases,
+                               const float* const params[6], float crs_scale,
+                               const float crs_translation[3], int32_t keep_crs, int32_t step);
+int32_t msplat_scene_write_splat(const char* path, int64_t n, int32_t rest_bases,
+                                 const float* const params[6], float crs_scale,
+                                 const float crs_translation[3], int32_t keep_crs);
+int32_t msplat_scene_read_ply(const char* path, float crs_scale, const float crs_translation[3],
+                              int32_t keep_crs, int64_t* n, int32_t* rest_bases, int32_t* step,
+                              float* const params[6]);
 
 int32_t msplat_trainer_splat_count(MsplatTrainer t);
 int32_t msplat_trainer_iteration(MsplatTrainer t);

@@ -129,6 +129,19 @@ class PixelBuffer(ctypes.Structure):
     _fields_ = [("data", POINTER(c_float)), ("width", c_int32), ("height", c_int32)]
 
 
+class ImageMetrics(ctypes.Structure):
+    """MsplatImageMetrics (include/msplat_hip.h)."""
+
+    _fields_ = [("psnr", c_float), ("ssim", c_float), ("l1", c_float)]
+
+
+class EvalMetrics(ctypes.Structure):
+    """MsplatEvalMetrics (include/msplat_trainer.h)."""
+
+    _fields_ = [("psnr", c_float), ("ssim", c_float), ("l1", c_float), ("numTest", c_int32),
+                ("numGaussians", c_int32)]
+
+
 # (name, restype, argtypes) for every symbol declared in include/msplat_hip.h
 # and include/msplat_trainer.h
 SIGNATURES = [
@@ -157,6 +170,9 @@ SIGNATURES = [
     ("msplat_hip_copy_intermediate", c_int, [c_char_p, c_void_p, POINTER(c_size_t)]),
     ("msplat_hip_raster_work", c_int, [POINTER(c_int64)]),
     ("msplat_hip_drain_raster_counters", c_int, [POINTER(c_int64)]),
+    ("msplat_hip_image_to_rgba8", c_int, [c_void_p, c_int64, c_void_p]),
+    ("msplat_hip_image_metrics", c_int,
+     [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, POINTER(ImageMetrics)]),
     # include/msplat_trainer.h
     ("msplat_trainer_create", c_void_p,
      [POINTER(TrainerConfig), c_int64, c_void_p * 6, c_int32, POINTER(TrainerCamera), POINTER(c_void_p), c_int32]),
@@ -171,6 +187,21 @@ SIGNATURES = [
     ("msplat_trainer_render_pose_device", c_int32,
      [c_void_p, POINTER(c_float), c_int32, c_void_p, POINTER(c_int32), POINTER(c_int32)]),
     ("msplat_prepare_cam", c_int32, [POINTER(TrainerCamera), c_int32, POINTER(CamSetupC)]),
+    ("msplat_trainer_evaluate", EvalMetrics,
+     [c_void_p, c_int32, POINTER(TrainerCamera), POINTER(c_void_p), c_int32]),
+    ("msplat_trainer_export_ply", c_int32, [c_void_p, c_char_p]),
+    ("msplat_trainer_export_splat", c_int32, [c_void_p, c_char_p]),
+    ("msplat_trainer_save_checkpoint", c_int32, [c_void_p, c_char_p]),
+    ("msplat_trainer_load_checkpoint", c_int32, [c_void_p, c_char_p]),
+    ("msplat_trainer_load_ply", c_int32, [c_void_p, c_char_p]),
+    ("msplat_trainer_set_crs", c_int32, [c_void_p, c_float, POINTER(c_float), c_int32]),
+    ("msplat_scene_write_ply", c_int32,
+     [c_char_p, c_int64, c_int32, c_void_p * 6, c_float, POINTER(c_float), c_int32, c_int32]),
+    ("msplat_scene_write_splat", c_int32,
+     [c_char_p, c_int64, c_int32, c_void_p * 6, c_float, POINTER(c_float), c_int32]),
+    ("msplat_scene_read_ply", c_int32,
+     [c_char_p, c_float, POINTER(c_float), c_int32, POINTER(c_int64), POINTER(c_int32),
+      POINTER(c_int32), POINTER(c_void_p)]),
     ("msplat_trainer_splat_count", c_int32, [c_void_p]),
     ("msplat_trainer_iteration", c_int32, [c_void_p]),
     ("msplat_trainer_group", c_int32,

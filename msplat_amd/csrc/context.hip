@@ -17,6 +17,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -70,6 +71,8 @@ struct Ctx {
     Buf final_T, final_idx, out_img, dbuf, v_rendered, loss_part;
     // scalars
     Buf meta_d, loss_d, count_d, work_d;
+    // evaluation: per-workgroup fp64 partials and the three sums
+    Buf eval_part, eval_out;
     Meta* meta_h = nullptr;
     float* loss_h = nullptr;
     int* count_h = nullptr;
@@ -148,7 +151,7 @@ void free_all(Ctx* c) {
                    &c->ttemp, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
                    &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
-                   &c->count_d, &c->work_d, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
+                   &c->count_d, &c->work_d, &c->eval_part, &c->eval_out, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
                    &c->d_tot, &c->d_scratch, &c->d_rnd};
     for (Buf* b : bufs)
         if (b->p) { (void)hipFree(b->p); b->p = nullptr; b->bytes = 0; }
@@ -584,6 +587,55 @@ int msplat_hip_clamp_max(float* p, int64_t n, float hi) {
     if (n < 0 || (n > 0 && !p)) return fail(MSPLAT_ERR_ARG, "bad clamp arguments");
     launch_clamp_max(g_ctx->stream, p, n, hi);
     HIP_TRY(hipGetLastError());
+    return MSPLAT_OK;
+}
+
+int msplat_hip_image_to_rgba8(const float* img, int64_t n_pixels, uint8_t* rgba) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (n_pixels < 0 || (n_pixels > 0 && (!img || !rgba)))
+        return fail(MSPLAT_ERR_ARG, "bad rgba8 arguments");
+    if (reinterpret_cast<uintptr_t>(rgba) % 4 != 0)
+        return fail(MSPLAT_ERR_ARG, "rgba must be 4-byte aligned");
+    launch_to_rgba8(g_ctx->stream, img, n_pixels, reinterpret_cast<uint32_t*>(rgba));
+    HIP_TRY(hipGetLastError());
+    return MSPLAT_OK;
+}
+
+int msplat_hip_image_metrics(const float* img, const float* gt, int32_t height, int32_t width,
+                             int32_t window_size, float sigma, MsplatImageMetrics* out) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!img || !gt || !out) return fail(MSPLAT_ERR_ARG, "null metrics argument");
+    if (height <= 0 || width <= 0 || (int64_t)height * width > (int64_t)1 << 30)
+        return fail(MSPLAT_ERR_ARG, "bad image size %dx%d", width, height);
+    if (window_size < 1 || window_size > 11 || window_size % 2 == 0)
+        return fail(MSPLAT_ERR_ARG, "window size %d: odd and at most 11", window_size);
+    if (!(sigma > 0.f)) return fail(MSPLAT_ERR_ARG, "sigma must be positive");
+    // the window exactly as ssim_eval builds it (ssim.cpp:68-75), in fp32
+    EvalWindow win;
+    win.ws = window_size;
+    win.pad = window_size / 2;
+    float ksum = 0.f;
+    for (int i = 0; i < window_size; ++i) {
+        const float x = (float)(i - window_size / 2);
+        win.w[i] = std::exp(-(x * x) / (2.0f * sigma * sigma));
+        ksum += win.w[i];
+    }
+    for (int i = 0; i < window_size; ++i) win.w[i] /= ksum;
+    for (int i = window_size; i < 11; ++i) win.w[i] = 0.f;
+    ENSURE(c->eval_part, (size_t)eval_partial_count(height, width) * 3 * sizeof(double));
+    ENSURE(c->eval_out, 3 * sizeof(double));
+    launch_image_metrics(c->stream, img, gt, height, width, win, P<double>(c->eval_part),
+                         P<double>(c->eval_out));
+    HIP_TRY(hipGetLastError());
+    double sums[3];
+    HIP_TRY(hipMemcpyAsync(sums, c->eval_out.p, sizeof(sums), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    const double n = (double)height * (double)width * 3.0;
+    const double mse = sums[1] / n;
+    out->psnr = (float)(10.0f * std::log10(1.0 / mse));
+    out->ssim = (float)(sums[0] / (double)((int64_t)height * width * 3));
+    out->l1 = (float)(sums[2] / n);
     return MSPLAT_OK;
 }
 

@@ -174,4 +174,14 @@ void launch_densify(hipStream_t s, const DensifyHP& hp, const float* gnorm, cons
                     int* dp, int* keep, int* kp, int* block_tot, float* scratch,
                     int* count_out);
 
+// Evaluation images: RGBA8 display conversion and PSNR / L1 / SSIM.
+struct EvalWindow {
+    int ws, pad;      // taps (odd, <= 11) and ws / 2
+    float w[11];      // normalised Gaussian taps, computed on the host in fp32
+};
+int64_t eval_partial_count(int H, int W);
+void launch_to_rgba8(hipStream_t s, const float* img, int64_t n, uint32_t* rgba);
+void launch_image_metrics(hipStream_t s, const float* img, const float* gt, int H, int W,
+                          const EvalWindow& win, double* part, double* out3);
+
 }  // namespace msp

@@ -146,6 +146,29 @@ def render(g: DeviceGaussians, setup, degrees_to_use: int, background, out=None)
     return out
 
 
+def image_metrics(img, gt, window_size: int = 11, sigma: float = 1.5) -> dict:
+    """PSNR / SSIM / L1 of two (H, W, 3) float32 CUDA images (msplat_hip_image_metrics)."""
+    lib = init()
+    torch().cuda.synchronize()
+    H, W = int(img.shape[0]), int(img.shape[1])
+    m = _abi.ImageMetrics()
+    _abi.check(lib.msplat_hip_image_metrics(ptr(img.contiguous()), ptr(gt.contiguous()), H, W,
+                                            window_size, sigma, ctypes.byref(m)))
+    return {"psnr": m.psnr, "ssim": m.ssim, "l1": m.l1}
+
+
+def image_to_rgba8(img):
+    """(H, W, 4) uint8 CUDA tensor of a (H, W, 3) float32 CUDA image (msplat_hip_image_to_rgba8)."""
+    T = torch()
+    lib = init()
+    T.cuda.synchronize()
+    out = T.empty(img.shape[:-1] + (4,), dtype=T.uint8, device="cuda")
+    n = int(img.numel() // 3)
+    _abi.check(lib.msplat_hip_image_to_rgba8(ptr(img.contiguous()), n, ptr(out)))
+    sync()
+    return out
+
+
 def adam_constants(lrs, step: int, beta1=0.9, beta2=0.999):
     """Bias corrections of fullIteration (model.cpp:558-571), in fp32."""
     f = np.float32

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <fstream>
 
 namespace msplat {
 
@@ -41,9 +42,13 @@ void Model::setupOptimizers(const float* const params[6], bool onDevice) {
         adam_exp_avg_sq_buf[g] = gpu_zeros(shape, DType::Float32);
         adam_lr[g] = lr_init[g];
     }
-    for (auto& s : stats_buf) s = gpu_zeros({buf_capacity}, DType::Float32);
+    allocStats();
     adam_step_count = 0;
     refreshViews();
+}
+
+void Model::allocStats() {
+    for (auto& s : stats_buf) s = gpu_zeros({buf_capacity}, DType::Float32);
 }
 
 void Model::refreshViews() {
@@ -237,6 +242,175 @@ MTensor Model::render(Camera& cam, int step) {   // model.cpp:536-544
                          cam.cachedProjViewMat, s.fx, s.fy, s.cx, s.cy, s.height, s.width,
                          s.tileBounds, 0.01f, s.degree, s.degreesToUse, s.cam_pos, featuresDc,
                          featuresRest, opacities, cfg_.bgColor);
+}
+
+// ---- scene files and checkpoints ----
+
+HostGaussians Model::toHost() const {
+    msplat_gpu_sync();
+    HostGaussians g;
+    g.n = num_active;
+    g.rest_bases = (int)(featuresRest.stride0() / 3);
+    auto get = [](const MTensor& t, std::vector<float>& dst) {
+        dst.resize((size_t)t.numel());
+        t.copy_to_host(dst.data(), dst.size() * sizeof(float));
+    };
+    get(means, g.means);
+    get(scales, g.scales);
+    get(quats, g.quats);
+    get(featuresDc, g.f_dc);
+    get(featuresRest, g.f_rest);
+    get(opacities, g.opacities);
+    return g;
+}
+
+void Model::save(const std::string& filename, int step) {   // model.cpp:298-305
+    const size_t dot = filename.rfind('.');
+    if (dot != std::string::npos && filename.substr(dot) == ".splat") saveSplat(filename);
+    else savePly(filename, step);
+}
+
+void Model::savePly(const std::string& filename, int step) {
+    save_gaussian_ply(filename, toHost(), crs, step);
+}
+
+void Model::saveSplat(const std::string& filename) { save_gaussian_splat(filename, toHost(), crs); }
+
+int Model::loadPly(const std::string& filename) {   // model.cpp:319-330
+    int step = 0;
+    HostGaussians g = load_gaussian_ply(filename, crs, &step);
+    const int K1 = (cfg_.shDegree + 1) * (cfg_.shDegree + 1) - 1;
+    if (g.rest_bases != K1)
+        throw std::runtime_error("PLY has " + std::to_string(g.rest_bases) +
+                                 " higher-order SH bases, the model's degree needs " +
+                                 std::to_string(K1));
+    num_active = g.n;
+    const float* params[6] = {g.means.data(), g.scales.data(), g.quats.data(),
+                              g.f_dc.data(), g.f_rest.data(), g.opacities.data()};
+    setupOptimizers(params, false);
+    return step;
+}
+
+namespace {
+
+constexpr uint32_t CKPT_MAGIC = 0x4C50534D;   // "MSPL"
+constexpr uint32_t CKPT_VERSION = 1;
+
+template <typename T>
+void put(std::ofstream& f, const T& v) { f.write(reinterpret_cast<const char*>(&v), sizeof(T)); }
+template <typename T>
+T take(std::ifstream& f) {
+    T v{};
+    f.read(reinterpret_cast<char*>(&v), sizeof(T));
+    if (!f) throw std::runtime_error("checkpoint is truncated");
+    return v;
+}
+
+// writeTensor (model.cpp:336-346): ndim, int64 shape, byte count, data.
+void write_tensor(std::ofstream& f, const MTensor& t) {
+    put<uint32_t>(f, (uint32_t)t.dim());
+    for (int64_t d = 0; d < t.dim(); ++d) put<int64_t>(f, t.size((int)d));
+    const uint64_t bytes = t.nbytes();
+    put<uint64_t>(f, bytes);
+    std::vector<char> host(bytes);
+    t.copy_to_host(host.data(), bytes);
+    f.write(host.data(), (std::streamsize)bytes);
+}
+
+struct HostTensor {
+    std::vector<int64_t> shape;
+    std::vector<float> data;
+};
+
+HostTensor read_tensor(std::ifstream& f) {   // readTensor (model.cpp:348-359)
+    HostTensor t;
+    const uint32_t ndim = take<uint32_t>(f);
+    if (ndim == 0 || ndim > 8) throw std::runtime_error("checkpoint tensor has a bad rank");
+    int64_t numel = 1;
+    for (uint32_t i = 0; i < ndim; ++i) {
+        t.shape.push_back(take<int64_t>(f));
+        if (t.shape.back() < 0) throw std::runtime_error("checkpoint tensor has a bad shape");
+        numel *= t.shape.back();
+    }
+    const uint64_t bytes = take<uint64_t>(f);
+    if (bytes != (uint64_t)numel * 4) throw std::runtime_error("checkpoint tensor size mismatch");
+    t.data.resize((size_t)numel);
+    f.read(reinterpret_cast<char*>(t.data.data()), (std::streamsize)bytes);
+    if (!f) throw std::runtime_error("checkpoint is truncated");
+    return t;
+}
+
+}  // namespace
+
+void Model::saveCheckpoint(const std::string& filename, int step) {   // model.cpp:361-399
+    msplat_gpu_sync();
+    std::ofstream f(filename, std::ios::binary);
+    if (!f.is_open()) throw std::runtime_error("Cannot open checkpoint file for writing: " + filename);
+    put(f, CKPT_MAGIC);
+    put(f, CKPT_VERSION);
+    put<uint32_t>(f, (uint32_t)step);
+    put<uint32_t>(f, (uint32_t)num_active);
+    put<uint32_t>(f, (uint32_t)cfg_.shDegree);
+    put<uint32_t>(f, (uint32_t)adam_step_count);
+    f.write(reinterpret_cast<const char*>(adam_lr), sizeof(adam_lr));
+    put(f, means_lr_init);
+    put(f, means_lr_final);
+    const MTensor* p[6] = {&means, &scales, &quats, &featuresDc, &featuresRest, &opacities};
+    for (const MTensor* t : p) write_tensor(f, *t);
+    for (int g = 0; g < N_ADAM_GROUPS; ++g) write_tensor(f, adam_exp_avg[g]);
+    for (int g = 0; g < N_ADAM_GROUPS; ++g) write_tensor(f, adam_exp_avg_sq[g]);
+    if (!f) throw std::runtime_error("write failed: " + filename);
+}
+
+int Model::loadCheckpoint(const std::string& filename) {   // model.cpp:401-488
+    std::ifstream f(filename, std::ios::binary);
+    if (!f.is_open()) throw std::runtime_error("Cannot open checkpoint file: " + filename);
+    if (take<uint32_t>(f) != CKPT_MAGIC) throw std::runtime_error("Not a valid msplat checkpoint file");
+    const uint32_t version = take<uint32_t>(f);
+    if (version != CKPT_VERSION)
+        throw std::runtime_error("Unsupported checkpoint version: " + std::to_string(version));
+    const uint32_t step = take<uint32_t>(f);
+    const uint32_t n = take<uint32_t>(f);
+    const uint32_t deg = take<uint32_t>(f);
+    const uint32_t adam_steps = take<uint32_t>(f);
+    float lr[N_ADAM_GROUPS];
+    for (float& v : lr) v = take<float>(f);
+    const float lr_init = take<float>(f), lr_final = take<float>(f);
+    if ((int)deg != cfg_.shDegree)
+        throw std::runtime_error("checkpoint SH degree " + std::to_string(deg) +
+                                 " differs from the model's " + std::to_string(cfg_.shDegree));
+    if (n == 0) throw std::runtime_error("checkpoint holds no gaussians");
+    HostTensor t[3 * N_ADAM_GROUPS];
+    for (auto& x : t) x = read_tensor(f);
+    const int64_t K1 = (int64_t)(cfg_.shDegree + 1) * (cfg_.shDegree + 1) - 1;
+    const std::vector<int64_t> tail[6] = {{3}, {3}, {4}, {3}, {K1, 3}, {1}};
+    for (int k = 0; k < 3 * N_ADAM_GROUPS; ++k) {
+        std::vector<int64_t> want{(int64_t)n};
+        want.insert(want.end(), tail[k % 6].begin(), tail[k % 6].end());
+        if (t[k].shape != want) throw std::runtime_error("checkpoint tensor has an unexpected shape");
+    }
+    // Fresh backing buffers of 4x the count holding the loaded rows.
+    num_active = n;
+    buf_capacity = 4 * (int64_t)n;
+    MTensor* bufs[6] = {&means_buf, &scales_buf, &quats_buf, &featuresDc_buf, &featuresRest_buf,
+                        &opacities_buf};
+    for (int g = 0; g < 6; ++g) {
+        std::vector<int64_t> shape{buf_capacity};
+        shape.insert(shape.end(), tail[g].begin(), tail[g].end());
+        MTensor* dst[3] = {bufs[g], &adam_exp_avg_buf[g], &adam_exp_avg_sq_buf[g]};
+        const HostTensor* src[3] = {&t[g], &t[6 + g], &t[12 + g]};
+        for (int k = 0; k < 3; ++k) {
+            *dst[k] = gpu_zeros(shape, DType::Float32);
+            dst[k]->copy_from_host(src[k]->data.data(), src[k]->data.size() * sizeof(float));
+        }
+    }
+    allocStats();
+    std::memcpy(adam_lr, lr, sizeof(adam_lr));
+    means_lr_init = lr_init;
+    means_lr_final = lr_final;
+    adam_step_count = (int)adam_steps;
+    refreshViews();
+    return (int)step;
 }
 
 }  // namespace msplat

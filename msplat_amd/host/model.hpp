@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "bindings.hpp"
+#include "gaussian_io.hpp"
 
 namespace msplat {
 
@@ -94,6 +95,26 @@ public:
     int bufCapacity() const { return buf_capacity; }
     float lastLoss() const { return last_loss; }
 
+    // Scene files (model.cpp:298-330): PLY or .splat by extension, and a
+    // PLY import that replaces the gaussians and restarts the optimiser;
+    // loadPly returns the iteration recorded in the file (0 if none).
+    void save(const std::string& filename, int step);
+    void savePly(const std::string& filename, int step);
+    void saveSplat(const std::string& filename);
+    int loadPly(const std::string& filename);
+    // Checkpoint (model.cpp:333-488), the reference's byte format: "MSPL"
+    // magic, version 1, step, gaussian count, SH degree, Adam step count,
+    // learning rates, then the six parameter tensors and the twelve Adam
+    // moment tensors (ndim, shape, byte count, data).  loadCheckpoint
+    // returns the saved step.
+    void saveCheckpoint(const std::string& filename, int step);
+    int loadCheckpoint(const std::string& filename);
+    // Active gaussians copied to host memory.
+    HostGaussians toHost() const;
+    // Dataset normalisation applied by the scene files when crs.keep is set
+    // (identity by default: a model built from given arrays).
+    Crs crs;
+
     // parameter / moment views of the active rows
     MTensor means, scales, quats, featuresDc, featuresRest, opacities;
     MTensor adam_exp_avg[N_ADAM_GROUPS], adam_exp_avg_sq[N_ADAM_GROUPS];
@@ -104,6 +125,7 @@ public:
 
 private:
     void setupOptimizers(const float* const params[6], bool onDevice);
+    void allocStats();
     void refreshViews();
     void ensureCapacity(int64_t needed);
 

@@ -117,6 +117,52 @@ public:
         return model->render(cam, current_step);
     }
 
+    // Trainer::evaluate (msplat_api.mm:138-166): render at the final
+    // iteration's resolution against the target box-filtered to it.
+    MsplatEvalMetrics evaluate(int n, const MsplatTrainerCamera* cams, const float* const* images,
+                               bool on_device) {
+        if (n <= 0 || !cams || !images) throw std::runtime_error("no test cameras");
+        const int ds = model->getDownscaleFactor(cfg.iterations);
+        double sp = 0.0, ss = 0.0, sl = 0.0;
+        for (int i = 0; i < n; ++i) {
+            Camera cam;
+            cam.width = cams[i].width; cam.height = cams[i].height;
+            cam.fx = cams[i].fx; cam.fy = cams[i].fy; cam.cx = cams[i].cx; cam.cy = cams[i].cy;
+            std::memcpy(cam.camToWorld, cams[i].camToWorld, sizeof(cam.camToWorld));
+            if (!images[i]) throw std::runtime_error("missing test image");
+            const size_t full = (size_t)cam.width * cam.height * 3;
+            std::vector<float> host(full);
+            if (on_device) check(msplat_hip_memcpy_d2h(host.data(), images[i], full * 4), "copy");
+            else std::memcpy(host.data(), images[i], full * 4);
+            int w2 = cam.width, h2 = cam.height;
+            if (ds > 1) host = box_downscale(host, cam.width, cam.height, ds, w2, h2);
+            MTensor gt = gpu_empty({h2, w2, 3}, DType::Float32);
+            gt.copy_from_host(host.data(), host.size() * sizeof(float));
+            MTensor img = model->render(cam, cfg.iterations);
+            if (img.size(0) != h2 || img.size(1) != w2)
+                throw std::runtime_error("render and target sizes differ");
+            MsplatImageMetrics m;
+            check(msplat_hip_image_metrics(img.data<float>(), gt.data<float>(), h2, w2, 11, 1.5f, &m),
+                  "image metrics");
+            sp += m.psnr;
+            ss += m.ssim;
+            sl += m.l1;
+        }
+        MsplatEvalMetrics out;
+        out.psnr = (float)(sp / n);
+        out.ssim = (float)(ss / n);
+        out.l1 = (float)(sl / n);
+        out.numTest = n;
+        out.numGaussians = (int32_t)model->numActive();
+        return out;
+    }
+
+    int load_checkpoint(const std::string& path) {   // Trainer::loadCheckpoint (msplat_api.mm:252-257)
+        current_step = model->loadCheckpoint(path);
+        shuffle_cameras();
+        return current_step;
+    }
+
     MTensor render_camera(int i) {
         if (i < 0 || i >= (int)cameras.size()) throw std::runtime_error("camera index out of range");
         return model->render(cameras[i], current_step);
@@ -240,15 +286,10 @@ int32_t msplat_trainer_render_pose_to_buffer(MsplatTrainer t, const float camToW
         if (outWidth) *outWidth = w;
         if (outHeight) *outHeight = h;
         if (!outRGBA) return MSPLAT_OK;
-        std::vector<float> host((size_t)img.numel());
-        img.copy_to_host(host.data(), img.nbytes());
-        for (size_t p = 0; p < (size_t)w * h; ++p) {
-            for (int c = 0; c < 3; ++c) {
-                const float v = std::min(std::max(host[3 * p + c], 0.f), 1.f);
-                outRGBA[4 * p + c] = (uint8_t)std::lround(v * 255.f);
-            }
-            outRGBA[4 * p + 3] = 255;
-        }
+        const int64_t n = (int64_t)w * h;
+        msplat::MTensor rgba = msplat::gpu_empty({n}, msplat::DType::Int32);   // 4 bytes per pixel
+        msplat::check(msplat_hip_image_to_rgba8(img.data<float>(), n, rgba.data<uint8_t>()), "rgba8");
+        rgba.copy_to_host(outRGBA, (size_t)n * 4);
         return MSPLAT_OK;
     }, (int32_t)MSPLAT_ERR_ARG);
 }
@@ -283,6 +324,129 @@ int32_t msplat_prepare_cam(const MsplatTrainerCamera* cam, int32_t downscale, Ms
     out->tile_bounds[1] = (h + msplat::TILE - 1) / msplat::TILE;
     out->tile_bounds[2] = 1;
     return MSPLAT_OK;
+}
+
+MsplatEvalMetrics msplat_trainer_evaluate(MsplatTrainer t, int32_t n_test,
+                                          const MsplatTrainerCamera* cameras,
+                                          const float* const* images, int32_t on_device) {
+    MsplatEvalMetrics bad{0.f, 0.f, 0.f, 0, 0};
+    if (!t) return bad;
+    return guarded([&]() { return T(t)->evaluate(n_test, cameras, images, on_device != 0); }, bad);
+}
+
+int32_t msplat_trainer_export_ply(MsplatTrainer t, const char* path) {
+    if (!t || !path) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t {
+        T(t)->model->savePly(path, T(t)->current_step);
+        return MSPLAT_OK;
+    }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+int32_t msplat_trainer_export_splat(MsplatTrainer t, const char* path) {
+    if (!t || !path) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t {
+        T(t)->model->saveSplat(path);
+        return MSPLAT_OK;
+    }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+int32_t msplat_trainer_save_checkpoint(MsplatTrainer t, const char* path) {
+    if (!t || !path) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t {
+        T(t)->model->saveCheckpoint(path, T(t)->current_step);
+        return MSPLAT_OK;
+    }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+int32_t msplat_trainer_load_checkpoint(MsplatTrainer t, const char* path) {
+    if (!t || !path) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t { return T(t)->load_checkpoint(path); }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+int32_t msplat_trainer_load_ply(MsplatTrainer t, const char* path) {
+    if (!t || !path) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t { return T(t)->model->loadPly(path); }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+int32_t msplat_trainer_set_crs(MsplatTrainer t, float scale, const float translation[3],
+                               int32_t keep) {
+    if (!t || !translation || !(scale > 0.f)) return MSPLAT_ERR_ARG;
+    msplat::Crs& c = T(t)->model->crs;
+    c.scale = scale;
+    for (int i = 0; i < 3; ++i) c.translation[i] = translation[i];
+    c.keep = keep != 0;
+    return MSPLAT_OK;
+}
+
+namespace {
+msplat::HostGaussians host_gaussians(int64_t n, int32_t rest_bases, const float* const params[6]) {
+    if (n < 0 || rest_bases < 0 || !params) throw std::runtime_error("bad scene arguments");
+    const size_t per[6] = {3, 3, 4, 3, (size_t)rest_bases * 3, 1};
+    for (int g = 0; g < 6; ++g)
+        if (!params[g] && (per[g] > 0 && n > 0)) throw std::runtime_error("null parameter array");
+    msplat::HostGaussians h;
+    h.n = n;
+    h.rest_bases = rest_bases;
+    std::vector<float>* dst[6] = {&h.means, &h.scales, &h.quats, &h.f_dc, &h.f_rest, &h.opacities};
+    for (int g = 0; g < 6; ++g)
+        dst[g]->assign(params[g], params[g] + (size_t)n * per[g]);
+    return h;
+}
+msplat::Crs make_crs(float scale, const float translation[3], int32_t keep) {
+    msplat::Crs c;
+    if (keep) {
+        if (!(scale > 0.f) || !translation) throw std::runtime_error("bad coordinate normalisation");
+        c.scale = scale;
+        for (int i = 0; i < 3; ++i) c.translation[i] = translation[i];
+    }
+    c.keep = keep != 0;
+    return c;
+}
+}  // namespace
+
+int32_t msplat_scene_write_ply(const char* path, int64_t n, int32_t rest_bases,
+                               const float* const params[6], float crs_scale,
+                               const float crs_translation[3], int32_t keep_crs, int32_t step) {
+    if (!path) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t {
+        msplat::save_gaussian_ply(path, host_gaussians(n, rest_bases, params),
+                                  make_crs(crs_scale, crs_translation, keep_crs), step);
+        return MSPLAT_OK;
+    }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+int32_t msplat_scene_write_splat(const char* path, int64_t n, int32_t rest_bases,
+                                 const float* const params[6], float crs_scale,
+                                 const float crs_translation[3], int32_t keep_crs) {
+    if (!path) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t {
+        msplat::save_gaussian_splat(path, host_gaussians(n, rest_bases, params),
+                                    make_crs(crs_scale, crs_translation, keep_crs));
+        return MSPLAT_OK;
+    }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+int32_t msplat_scene_read_ply(const char* path, float crs_scale, const float crs_translation[3],
+                              int32_t keep_crs, int64_t* n, int32_t* rest_bases, int32_t* step,
+                              float* const params[6]) {
+    if (!path) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t {
+        int st = 0;
+        msplat::HostGaussians g =
+            msplat::load_gaussian_ply(path, make_crs(crs_scale, crs_translation, keep_crs), &st);
+        if (n) *n = g.n;
+        if (rest_bases) *rest_bases = g.rest_bases;
+        if (step) *step = st;
+        if (params) {
+            const std::vector<float>* src[6] = {&g.means, &g.scales, &g.quats,
+                                                &g.f_dc, &g.f_rest, &g.opacities};
+            for (int k = 0; k < 6; ++k) {
+                if (!params[k]) throw std::runtime_error("null parameter buffer");
+                std::memcpy(params[k], src[k]->data(), src[k]->size() * sizeof(float));
+            }
+        }
+        return MSPLAT_OK;
+    }, (int32_t)MSPLAT_ERR_ARG);
 }
 
 int32_t msplat_trainer_splat_count(MsplatTrainer t) { return t ? (int32_t)T(t)->model->numActive() : -1; }

@@ -175,6 +175,69 @@ class GaussianTrainer:
         if rc != 0:
             raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())
 
+    def render_from_pose_rgba8(self, cam_to_world, ref_cam_idx: int = 0) -> np.ndarray:
+        """renderFromPoseToBuffer: (H, W, 4) uint8 display image (converted on the GPU)."""
+        _, p = _pose(cam_to_world)
+        w, h = ctypes.c_int32(0), ctypes.c_int32(0)
+        rc = self._lib.msplat_trainer_render_pose_to_buffer(self._h, p, ref_cam_idx, None,
+                                                            ctypes.byref(w), ctypes.byref(h))
+        if rc != 0:
+            raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())
+        out = np.empty((h.value, w.value, 4), np.uint8)
+        rc = self._lib.msplat_trainer_render_pose_to_buffer(self._h, p, ref_cam_idx, out.ctypes.data,
+                                                            ctypes.byref(w), ctypes.byref(h))
+        if rc != 0:
+            raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())
+        return out
+
+    def evaluate(self, cameras: List[Camera], images) -> dict:
+        """Metrics on held-out cameras (GaussianTrainer.evaluate, python/bindings.cpp:180-205):
+        dict with psnr, ssim, l1, num_test, num_gaussians.  images: one
+        full-resolution (H, W, 3) float32 target per camera (numpy)."""
+        if len(cameras) != len(images) or not cameras:
+            raise ValueError("one image per test camera is needed")
+        ims = [np.ascontiguousarray(im, np.float32) for im in images]
+        for cam, im in zip(cameras, ims):
+            if im.shape != (cam.height, cam.width, 3):
+                raise ValueError("test image shape does not match its camera")
+        cams = (_abi.TrainerCamera * len(cameras))(*[_c_camera(c) for c in cameras])
+        ptrs = (ctypes.c_void_p * len(ims))(*[im.ctypes.data for im in ims])
+        m = self._lib.msplat_trainer_evaluate(self._h, len(cameras), cams,
+                                              ctypes.cast(ptrs, ctypes.POINTER(ctypes.c_void_p)), 0)
+        if m.numTest == 0:
+            raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())
+        return {"psnr": m.psnr, "ssim": m.ssim, "l1": m.l1, "num_test": m.numTest,
+                "num_gaussians": m.numGaussians}
+
+    def _path_call(self, fn, path: str) -> int:
+        rc = fn(self._h, str(path).encode())
+        if rc < 0:
+            raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())
+        return int(rc)
+
+    def export_ply(self, path: str) -> None:
+        self._path_call(self._lib.msplat_trainer_export_ply, path)
+
+    def export_splat(self, path: str) -> None:
+        self._path_call(self._lib.msplat_trainer_export_splat, path)
+
+    def save_checkpoint(self, path: str) -> None:
+        self._path_call(self._lib.msplat_trainer_save_checkpoint, path)
+
+    def load_checkpoint(self, path: str) -> int:
+        """Restore a checkpoint; returns its step (training continues after it)."""
+        return self._path_call(self._lib.msplat_trainer_load_checkpoint, path)
+
+    def load_ply(self, path: str) -> int:
+        """Replace the gaussians by an exported PLY (restarting the optimiser);
+        returns the step recorded in the file."""
+        return self._path_call(self._lib.msplat_trainer_load_ply, path)
+
+    def set_crs(self, scale: float, translation, keep: bool = True) -> None:
+        t = (ctypes.c_float * 3)(*[float(v) for v in translation])
+        if self._lib.msplat_trainer_set_crs(self._h, float(scale), t, int(keep)) != 0:
+            raise ValueError("bad coordinate normalisation")
+
     def group(self, g: int, which: int = 0) -> np.ndarray:
         """Host copy of the active rows of parameter group g (which=0) or of its
         Adam moments (1, 2)."""

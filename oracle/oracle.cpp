@@ -1203,4 +1203,93 @@ int32_t orc_densify(const OrcDensifyArgs* a, const float* gnorm, const float* vi
     return out;
 }
 
+// ---- evaluation metrics (model.cpp:25-40, ssim.cpp:26-123) ----
+
+namespace {
+// gaussianBlur (ssim.cpp:26-59): horizontal pass into tmp, then vertical,
+// taps summed from the first, borders clamped.
+void blur_clamped(const float* in, float* out, float* tmp, int H, int W, const float* k, int ks) {
+    const int pad = ks / 2;
+    for (int y = 0; y < H; ++y)
+        for (int x = 0; x < W; ++x) {
+            float sum = 0.f;
+            for (int i = 0; i < ks; ++i) {
+                const int sx = std::min(std::max(x + i - pad, 0), W - 1);
+                sum += in[(size_t)y * W + sx] * k[i];
+            }
+            tmp[(size_t)y * W + x] = sum;
+        }
+    for (int y = 0; y < H; ++y)
+        for (int x = 0; x < W; ++x) {
+            float sum = 0.f;
+            for (int i = 0; i < ks; ++i) {
+                const int sy = std::min(std::max(y + i - pad, 0), H - 1);
+                sum += tmp[(size_t)sy * W + x] * k[i];
+            }
+            out[(size_t)y * W + x] = sum;
+        }
+}
+}  // namespace
+
+void orc_image_metrics(int32_t H, int32_t W, const float* img, const float* gt,
+                       int32_t window_size, float sigma, float out[3]) {
+    const int64_t n = (int64_t)H * W * 3;
+    // psnr (model.cpp:25-32): fp64 mean of the squared fp32 differences
+    double mse = 0.0, l1 = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+        const double d = img[i] - gt[i];
+        mse += d * d;
+        l1 += std::fabs(img[i] - gt[i]);
+    }
+    mse /= (double)n;
+    out[0] = (float)(10.0f * std::log10(1.0 / mse));
+    out[2] = (float)(l1 / (double)n);
+    // ssim_eval (ssim.cpp:61-123)
+    std::vector<float> k(window_size);
+    float ksum = 0.f;
+    for (int i = 0; i < window_size; ++i) {
+        const float x = (float)(i - window_size / 2);
+        k[i] = std::exp(-(x * x) / (2.0f * sigma * sigma));
+        ksum += k[i];
+    }
+    for (int i = 0; i < window_size; ++i) k[i] /= ksum;
+    const size_t HW = (size_t)H * W;
+    std::vector<float> r(HW), g(HW), rr(HW), gg(HW), rg(HW), mu1(HW), mu2(HW), s11(HW), s22(HW),
+        s12(HW), tmp(HW);
+    const float C1 = 0.01f * 0.01f, C2 = 0.03f * 0.03f;
+    double sum = 0.0;
+    int64_t count = 0;
+    for (int c = 0; c < 3; ++c) {
+        for (size_t i = 0; i < HW; ++i) {
+            r[i] = img[3 * i + c];
+            g[i] = gt[3 * i + c];
+            rr[i] = r[i] * r[i];
+            gg[i] = g[i] * g[i];
+            rg[i] = r[i] * g[i];
+        }
+        blur_clamped(r.data(), mu1.data(), tmp.data(), H, W, k.data(), window_size);
+        blur_clamped(g.data(), mu2.data(), tmp.data(), H, W, k.data(), window_size);
+        blur_clamped(rr.data(), s11.data(), tmp.data(), H, W, k.data(), window_size);
+        blur_clamped(gg.data(), s22.data(), tmp.data(), H, W, k.data(), window_size);
+        blur_clamped(rg.data(), s12.data(), tmp.data(), H, W, k.data(), window_size);
+        for (size_t i = 0; i < HW; ++i) {
+            const float m1sq = mu1[i] * mu1[i], m2sq = mu2[i] * mu2[i], m12 = mu1[i] * mu2[i];
+            const float sig1sq = s11[i] - m1sq, sig2sq = s22[i] - m2sq, sig12 = s12[i] - m12;
+            const float num = (2.0f * m12 + C1) * (2.0f * sig12 + C2);
+            const float den = (m1sq + m2sq + C1) * (sig1sq + sig2sq + C2);
+            sum += num / den;
+            ++count;
+        }
+    }
+    out[1] = (float)(sum / (double)count);
+}
+
+void orc_image_to_rgba8(int64_t n_pixels, const float* img, uint8_t* rgba) {
+    for (int64_t p = 0; p < n_pixels; ++p) {
+        for (int c = 0; c < 3; ++c)
+            rgba[4 * p + c] = (uint8_t)(std::fmin(std::fmax(img[3 * p + c], 0.f), 1.f) * 255.f);
+        rgba[4 * p + 3] = 255;
+    }
+}
+
 }  // extern "C"

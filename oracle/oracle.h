@@ -176,6 +176,16 @@ int32_t orc_densify(const OrcDensifyArgs* a, const float* xys_grad_norm,
                     const float* random_samples,
                     int32_t* split_flag_out, int32_t* dup_flag_out, int32_t* keep_flag_out);
 
+/* ---- next to the path: evaluation metrics and the RGBA8 display image ----
+ * psnr / l1_loss (model.cpp:25-40) and ssim_eval (ssim.cpp:61-123) of an
+ * [H,W,3] render against its target: out[0] = PSNR, out[1] = SSIM with a
+ * window_size-tap Gaussian of width sigma and edge-clamped borders,
+ * out[2] = mean |r - g|.  rgba8: renderFromPoseToBuffer's conversion
+ * (msplat_api.mm:230-238). */
+void orc_image_metrics(int32_t H, int32_t W, const float* img, const float* gt,
+                       int32_t window_size, float sigma, float out[3]);
+void orc_image_to_rgba8(int64_t n_pixels, const float* img, uint8_t* rgba);
+
 #ifdef __cplusplus
 }
 #endif

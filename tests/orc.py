@@ -176,6 +176,23 @@ def render(cam: OrcCamera, means, scales, quats, f_dc, f_rest, opac_logits):
     return img, Ts, idx
 
 
+def image_metrics(img, gt, window_size=11, sigma=1.5) -> dict:
+    """psnr / ssim_eval / l1_loss of two (H, W, 3) float32 images."""
+    img, gt = f32(img), f32(gt)
+    out = np.zeros(3, np.float32)
+    lib().orc_image_metrics(c_int32(img.shape[0]), c_int32(img.shape[1]), P(img), P(gt),
+                            c_int32(window_size), c_float(sigma), P(out))
+    return {"psnr": float(out[0]), "ssim": float(out[1]), "l1": float(out[2])}
+
+
+def image_to_rgba8(img) -> np.ndarray:
+    img = f32(img)
+    n = img.size // 3
+    out = np.zeros(img.shape[:-1] + (4,), np.uint8)
+    lib().orc_image_to_rgba8(c_int64(n), P(img), P(out))
+    return out
+
+
 def adam_hparams(lrs, step: int, beta1=0.9, beta2=0.999, eps=1e-8) -> OrcAdam:
     """fullIteration's bias corrections (model.cpp:558-571), fp32 like the reference."""
     a = OrcAdam()
