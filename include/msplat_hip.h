@@ -177,6 +177,14 @@ typedef struct MsplatImageMetrics {
 int msplat_hip_image_metrics(const float* img, const float* gt, int32_t height, int32_t width,
                              int32_t window_size, float sigma, MsplatImageMetrics* out);
 
+/* Initial gaussian scale of every point of a cloud: the mean distance to its
+ * three nearest other points (device xyz[n,3] -> device mean_dist[n]),
+ * exactly as the reference's nanoflann kd-tree query gives it
+ * (PointsTensor::scales, kdtree_tensor.hpp:26-40; Model::Model takes its log,
+ * model.cpp:63-73).  n >= 4.  Reads the points back once for their bounding
+ * box; the result is ready when the stream is. */
+int msplat_hip_knn_mean_dist(const float* xyz, int64_t n, float* mean_dist);
+
 /* Per-stage GPU timing (msplat_enable_gpu_timing / msplat_drain_stage_times,
  * bindings.h:28-33).  When enabled every stage of every render / train call is
  * bracketed by HIP events on the context stream (no extra synchronisation).

@@ -202,6 +202,33 @@ int32_t msplat_scene_read_ply(const char* path, float crs_scale, const float crs
                               int32_t keep_crs, int64_t* n, int32_t* rest_bases, int32_t* step,
                               float* const params[6]);
 
+/* A COLMAP dataset (msplat_dataset_create, msplat_c_api.h:84-89; loadColmap,
+ * load_colmap.cpp:121-164): cameras.bin / images.bin / points3D.bin (or
+ * points3D.ply) under path or path/sparse/0, cameras sorted by image name,
+ * OpenGL camera-to-world poses, then autoScaleAndCenter
+ * (input_data.cpp:79-125).  image_dir NULL: path/images if present, else
+ * path.  Images are not decoded: each camera carries its image path and the
+ * caller supplies pixels to msplat_trainer_create.  NULL on error. */
+typedef void* MsplatDataset;
+MsplatDataset msplat_dataset_create(const char* path, const char* image_dir);
+void msplat_dataset_destroy(MsplatDataset ds);
+int32_t msplat_dataset_num_cameras(MsplatDataset ds);
+/* Camera i: intrinsics and pose (cam), distortion k1 k2 p1 p2 (nullable),
+ * image path (nullable; valid while ds lives). */
+int32_t msplat_dataset_camera(MsplatDataset ds, int32_t i, MsplatTrainerCamera* cam,
+                              float distortion[4], const char** image_path);
+/* msplat_dataset_camera_pose (msplat_c_api.h:115). */
+int32_t msplat_dataset_camera_pose(MsplatDataset ds, int32_t i, float camToWorld[16]);
+int64_t msplat_dataset_num_points(MsplatDataset ds);
+/* Normalised points [n,3] and colours [n,3] (either nullable). */
+int32_t msplat_dataset_points(MsplatDataset ds, float* xyz, uint8_t* rgb);
+/* world = normalised / scale + translation. */
+int32_t msplat_dataset_normalisation(MsplatDataset ds, float* scale, float translation[3]);
+/* Initial gaussians of the point cloud into six host buffers sized for
+ * num_points (Model::Model, model.cpp:59-110): the nearest-neighbour scales
+ * run on the GPU (msplat_hip_knn_mean_dist). */
+int32_t msplat_dataset_init_gaussians(MsplatDataset ds, int32_t sh_degree, float* const params[6]);
+
 int32_t msplat_trainer_splat_count(MsplatTrainer t);
 int32_t msplat_trainer_iteration(MsplatTrainer t);
 

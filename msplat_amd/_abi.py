@@ -171,6 +171,7 @@ SIGNATURES = [
     ("msplat_hip_raster_work", c_int, [POINTER(c_int64)]),
     ("msplat_hip_drain_raster_counters", c_int, [POINTER(c_int64)]),
     ("msplat_hip_image_to_rgba8", c_int, [c_void_p, c_int64, c_void_p]),
+    ("msplat_hip_knn_mean_dist", c_int, [c_void_p, c_int64, c_void_p]),
     ("msplat_hip_image_metrics", c_int,
      [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, POINTER(ImageMetrics)]),
     # include/msplat_trainer.h
@@ -202,6 +203,16 @@ SIGNATURES = [
     ("msplat_scene_read_ply", c_int32,
      [c_char_p, c_float, POINTER(c_float), c_int32, POINTER(c_int64), POINTER(c_int32),
       POINTER(c_int32), POINTER(c_void_p)]),
+    ("msplat_dataset_create", c_void_p, [c_char_p, c_char_p]),
+    ("msplat_dataset_destroy", None, [c_void_p]),
+    ("msplat_dataset_num_cameras", c_int32, [c_void_p]),
+    ("msplat_dataset_camera", c_int32,
+     [c_void_p, c_int32, POINTER(TrainerCamera), POINTER(c_float), POINTER(c_char_p)]),
+    ("msplat_dataset_camera_pose", c_int32, [c_void_p, c_int32, POINTER(c_float)]),
+    ("msplat_dataset_num_points", c_int64, [c_void_p]),
+    ("msplat_dataset_points", c_int32, [c_void_p, c_void_p, c_void_p]),
+    ("msplat_dataset_normalisation", c_int32, [c_void_p, POINTER(c_float), POINTER(c_float)]),
+    ("msplat_dataset_init_gaussians", c_int32, [c_void_p, c_int32, c_void_p * 6]),
     ("msplat_trainer_splat_count", c_int32, [c_void_p]),
     ("msplat_trainer_iteration", c_int32, [c_void_p]),
     ("msplat_trainer_group", c_int32,

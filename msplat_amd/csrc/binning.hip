@@ -211,6 +211,12 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
 
+void launch_run_edges(hipStream_t s, int64_t n, const uint32_t* sorted_keys, int* start, int* end) {
+    if (n > 0)
+        hipLaunchKernelGGL(k_tile_edges, dim3(blocks_for(n)), dim3(256), 0, s, n, sorted_keys, start,
+                           end);
+}
+
 void launch_total_hits(hipStream_t s, int N, const int* tiles_hit, Meta* meta) {
     (void)hipMemsetAsync(&meta->total_isect, 0, sizeof(int64_t), s);
     if (N > 0)

@@ -73,6 +73,9 @@ struct Ctx {
     Buf meta_d, loss_d, count_d, work_d;
     // evaluation: per-workgroup fp64 partials and the three sums
     Buf eval_part, eval_out;
+    // nearest-neighbour scales: cell keys / point ids (ping-pong), sort
+    // scratch, cell ranges
+    Buf knn_k, knn_v, knn_k2, knn_v2, knn_tmp, knn_s, knn_e;
     Meta* meta_h = nullptr;
     float* loss_h = nullptr;
     int* count_h = nullptr;
@@ -151,7 +154,8 @@ void free_all(Ctx* c) {
                    &c->ttemp, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
                    &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
-                   &c->count_d, &c->work_d, &c->eval_part, &c->eval_out, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
+                   &c->count_d, &c->work_d, &c->eval_part, &c->eval_out, &c->knn_k, &c->knn_v, &c->knn_k2, &c->knn_v2,
+                   &c->knn_tmp, &c->knn_s, &c->knn_e, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
                    &c->d_tot, &c->d_scratch, &c->d_rnd};
     for (Buf* b : bufs)
         if (b->p) { (void)hipFree(b->p); b->p = nullptr; b->bytes = 0; }
@@ -636,6 +640,78 @@ int msplat_hip_image_metrics(const float* img, const float* gt, int32_t height, 
     out->psnr = (float)(10.0f * std::log10(1.0 / mse));
     out->ssim = (float)(sums[0] / (double)((int64_t)height * width * 3));
     out->l1 = (float)(sums[2] / n);
+    return MSPLAT_OK;
+}
+
+int msplat_hip_knn_mean_dist(const float* xyz, int64_t n, float* mean_dist) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!xyz || !mean_dist) return fail(MSPLAT_ERR_ARG, "null knn argument");
+    if (n < 4) return fail(MSPLAT_ERR_ARG, "%lld points: at least 4 are needed", (long long)n);
+    if (n > 0x7FFFFFFF) return fail(MSPLAT_ERR_ARG, "too many points");
+    // bounding box on the host (an initialisation-time call)
+    std::vector<float> host((size_t)n * 3);
+    HIP_TRY(hipMemcpyAsync(host.data(), xyz, host.size() * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    float lo[3], hi[3];
+    for (int k = 0; k < 3; ++k) { lo[k] = INFINITY; hi[k] = -INFINITY; }
+    for (int64_t i = 0; i < n; ++i)
+        for (int k = 0; k < 3; ++k) {
+            const float v = host[3 * i + k];
+            if (!std::isfinite(v)) return fail(MSPLAT_ERR_ARG, "point %lld is not finite", (long long)i);
+            lo[k] = std::min(lo[k], v);
+            hi[k] = std::max(hi[k], v);
+        }
+    // cell edge: about one point per cell, at most 4 n cells and 1024 per axis
+    double ext[3], emax = 0.0, amax = 0.0;
+    for (int k = 0; k < 3; ++k) {
+        ext[k] = (double)hi[k] - (double)lo[k];
+        emax = std::max(emax, ext[k]);
+        amax = std::max(amax, std::max(std::fabs((double)lo[k]), std::fabs((double)hi[k])));
+    }
+    KnnGrid g;
+    double h = emax > 0.0 ? emax / std::cbrt((double)n) : 1.0;
+    auto dims_for = [&](double hh, int* d) {
+        double cells = 1.0;
+        for (int k = 0; k < 3; ++k) {
+            d[k] = (int)std::min(1024.0, std::max(1.0, std::ceil(ext[k] / hh)));
+            cells *= d[k];
+        }
+        return cells;
+    };
+    for (int it = 0; it < 40 && dims_for(h, g.dim) < 0.5 * (double)n; ++it) {
+        if (std::max(g.dim[0], std::max(g.dim[1], g.dim[2])) >= 1024) break;
+        h *= 0.8;
+    }
+    while (dims_for(h, g.dim) > 4.0 * (double)n) h *= 1.25;
+    if (emax > 0.0) h = std::max(h, emax / 1024.0);
+    dims_for(h, g.dim);
+    for (int k = 0; k < 3; ++k) g.lo[k] = lo[k];
+    g.h = (float)h;
+    g.inv_h = (float)(1.0 / h);
+    g.margin = (float)(1e-3 * h + 1e-6 * amax);
+    const int64_t cells = (int64_t)g.dim[0] * g.dim[1] * g.dim[2];
+    int bits = 1;
+    while (((int64_t)1 << bits) < cells) ++bits;
+    const size_t N = (size_t)n;
+    ENSURE(c->knn_k, N * 4);
+    ENSURE(c->knn_v, N * 4);
+    ENSURE(c->knn_k2, N * 4);
+    ENSURE(c->knn_v2, N * 4);
+    ENSURE(c->knn_tmp, (size_t)radix_temp_ints(n) * 4);
+    ENSURE(c->knn_s, (size_t)cells * 4);
+    ENSURE(c->knn_e, (size_t)cells * 4);
+    HIP_TRY(hipMemsetAsync(c->knn_s.p, 0, (size_t)cells * 4, c->stream));
+    HIP_TRY(hipMemsetAsync(c->knn_e.p, 0, (size_t)cells * 4, c->stream));
+    launch_knn_cells(c->stream, n, xyz, g, P<uint32_t>(c->knn_k), P<uint32_t>(c->knn_v));
+    const bool flip = launch_radix_sort(c->stream, P<uint32_t>(c->knn_k), P<uint32_t>(c->knn_v),
+                                        P<uint32_t>(c->knn_k2), P<uint32_t>(c->knn_v2), n, bits,
+                                        P<int>(c->knn_tmp));
+    const uint32_t* sk = flip ? P<uint32_t>(c->knn_k2) : P<uint32_t>(c->knn_k);
+    const uint32_t* order = flip ? P<uint32_t>(c->knn_v2) : P<uint32_t>(c->knn_v);
+    launch_run_edges(c->stream, n, sk, P<int>(c->knn_s), P<int>(c->knn_e));
+    launch_knn_search(c->stream, n, xyz, g, order, P<int>(c->knn_s), P<int>(c->knn_e), mean_dist);
+    HIP_TRY(hipGetLastError());
     return MSPLAT_OK;
 }
 

@@ -184,4 +184,18 @@ void launch_to_rgba8(hipStream_t s, const float* img, int64_t n, uint32_t* rgba)
 void launch_image_metrics(hipStream_t s, const float* img, const float* gt, int H, int W,
                           const EvalWindow& win, double* part, double* out3);
 
+// Nearest-neighbour scales of a point cloud (uniform grid).
+struct KnnGrid {
+    float lo[3];
+    float h, inv_h;     // cell edge and its reciprocal
+    float margin;       // bound on the cell-assignment rounding, in distance
+    int dim[3];
+};
+void launch_knn_cells(hipStream_t s, int64_t n, const float* xyz, const KnnGrid& g,
+                      uint32_t* key, uint32_t* val);
+void launch_knn_search(hipStream_t s, int64_t n, const float* xyz, const KnnGrid& g,
+                       const uint32_t* order, const int* cstart, const int* cend,
+                       float* mean_dist);
+void launch_run_edges(hipStream_t s, int64_t n, const uint32_t* sorted_keys, int* start, int* end);
+
 }  // namespace msp

@@ -14,6 +14,7 @@
 #include <string>
 #include <vector>
 
+#include "dataset.hpp"
 #include "model.hpp"
 
 namespace msplat {
@@ -444,6 +445,86 @@ int32_t msplat_scene_read_ply(const char* path, float crs_scale, const float crs
                 if (!params[k]) throw std::runtime_error("null parameter buffer");
                 std::memcpy(params[k], src[k]->data(), src[k]->size() * sizeof(float));
             }
+        }
+        return MSPLAT_OK;
+    }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+MsplatDataset msplat_dataset_create(const char* path, const char* image_dir) {
+    if (!path) return nullptr;
+    return guarded([&]() -> MsplatDataset {
+        return new msplat::Dataset(msplat::load_colmap(path, image_dir ? image_dir : ""));
+    }, nullptr);
+}
+
+void msplat_dataset_destroy(MsplatDataset ds) { delete static_cast<msplat::Dataset*>(ds); }
+
+namespace {
+msplat::Dataset* D(MsplatDataset ds) { return static_cast<msplat::Dataset*>(ds); }
+const msplat::DatasetCamera& dcam(MsplatDataset ds, int32_t i) {
+    if (!ds || i < 0 || i >= (int32_t)D(ds)->cameras.size())
+        throw std::runtime_error("camera index out of range");
+    return D(ds)->cameras[i];
+}
+}  // namespace
+
+int32_t msplat_dataset_num_cameras(MsplatDataset ds) {
+    return ds ? (int32_t)D(ds)->cameras.size() : -1;
+}
+
+int32_t msplat_dataset_camera(MsplatDataset ds, int32_t i, MsplatTrainerCamera* cam,
+                              float distortion[4], const char** image_path) {
+    return guarded([&]() -> int32_t {
+        const msplat::DatasetCamera& c = dcam(ds, i);
+        if (cam) {
+            cam->width = c.width; cam->height = c.height;
+            cam->fx = c.fx; cam->fy = c.fy; cam->cx = c.cx; cam->cy = c.cy;
+            std::memcpy(cam->camToWorld, c.camToWorld, sizeof(c.camToWorld));
+        }
+        if (distortion) {
+            distortion[0] = c.k1; distortion[1] = c.k2; distortion[2] = c.p1; distortion[3] = c.p2;
+        }
+        if (image_path) *image_path = c.filePath.c_str();
+        return MSPLAT_OK;
+    }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+int32_t msplat_dataset_camera_pose(MsplatDataset ds, int32_t i, float camToWorld[16]) {
+    if (!camToWorld) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t {
+        std::memcpy(camToWorld, dcam(ds, i).camToWorld, 16 * sizeof(float));
+        return MSPLAT_OK;
+    }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+int64_t msplat_dataset_num_points(MsplatDataset ds) {
+    return ds ? (int64_t)(D(ds)->xyz.size() / 3) : -1;
+}
+
+int32_t msplat_dataset_points(MsplatDataset ds, float* xyz, uint8_t* rgb) {
+    if (!ds) return MSPLAT_ERR_ARG;
+    if (xyz) std::memcpy(xyz, D(ds)->xyz.data(), D(ds)->xyz.size() * sizeof(float));
+    if (rgb) std::memcpy(rgb, D(ds)->rgb.data(), D(ds)->rgb.size());
+    return MSPLAT_OK;
+}
+
+int32_t msplat_dataset_normalisation(MsplatDataset ds, float* scale, float translation[3]) {
+    if (!ds) return MSPLAT_ERR_ARG;
+    if (scale) *scale = D(ds)->scale;
+    if (translation)
+        for (int k = 0; k < 3; ++k) translation[k] = D(ds)->translation[k];
+    return MSPLAT_OK;
+}
+
+int32_t msplat_dataset_init_gaussians(MsplatDataset ds, int32_t sh_degree, float* const params[6]) {
+    if (!ds || !params) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t {
+        msplat::HostGaussians g = msplat::init_gaussians(D(ds)->xyz, D(ds)->rgb, sh_degree);
+        const std::vector<float>* src[6] = {&g.means, &g.scales, &g.quats,
+                                            &g.f_dc, &g.f_rest, &g.opacities};
+        for (int k = 0; k < 6; ++k) {
+            if (!params[k]) throw std::runtime_error("null parameter buffer");
+            std::memcpy(params[k], src[k]->data(), src[k]->size() * sizeof(float));
         }
         return MSPLAT_OK;
     }, (int32_t)MSPLAT_ERR_ARG);

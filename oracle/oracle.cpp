@@ -1292,4 +1292,26 @@ void orc_image_to_rgba8(int64_t n_pixels, const float* img, uint8_t* rgba) {
     }
 }
 
+void orc_knn_mean_dist(int64_t n, const float* xyz, float* out) {
+#pragma omp parallel for schedule(dynamic, 64)
+    for (int64_t i = 0; i < n; ++i) {
+        float b[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+        for (int64_t j = 0; j < n; ++j) {
+            float d = 0.f;
+            for (int k = 0; k < 3; ++k) {
+                const float diff = xyz[3 * i + k] - xyz[3 * j + k];
+                d += diff * diff;
+            }
+            if (d < b[3]) {   // insertion into the four smallest, ascending
+                int p = 3;
+                while (p > 0 && d < b[p - 1]) { b[p] = b[p - 1]; --p; }
+                b[p] = d;
+            }
+        }
+        float sum = 0.f;
+        for (int j = 1; j < 4; ++j) sum += std::sqrt(b[j]);
+        out[i] = sum / 3;
+    }
+}
+
 }  // extern "C"

@@ -186,6 +186,13 @@ void orc_image_metrics(int32_t H, int32_t W, const float* img, const float* gt,
                        int32_t window_size, float sigma, float out[3]);
 void orc_image_to_rgba8(int64_t n_pixels, const float* img, uint8_t* rgba);
 
+/* Initial scales of a point cloud (PointsTensor::scales,
+ * kdtree_tensor.hpp:26-40): for each of n points the mean of sqrt of the
+ * 2nd..4th smallest squared distances to all points (itself first), squared
+ * distances summed per axis in fp32 like nanoflann's L2_Simple_Adaptor.
+ * Brute force, O(n^2). */
+void orc_knn_mean_dist(int64_t n, const float* xyz, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -193,6 +193,13 @@ def image_to_rgba8(img) -> np.ndarray:
     return out
 
 
+def knn_mean_dist(xyz) -> np.ndarray:
+    xyz = f32(xyz)
+    out = np.zeros(xyz.shape[0], np.float32)
+    lib().orc_knn_mean_dist(c_int64(xyz.shape[0]), P(xyz), P(out))
+    return out
+
+
 def adam_hparams(lrs, step: int, beta1=0.9, beta2=0.999, eps=1e-8) -> OrcAdam:
     """fullIteration's bias corrections (model.cpp:558-571), fp32 like the reference."""
     a = OrcAdam()

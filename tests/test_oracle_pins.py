@@ -800,3 +800,22 @@ def test_densify_hand_cases():
         assert not m[0][3 * ch:3 * ch + 3].any() and not v[5][ch]
     np.testing.assert_array_equal(means[4], [3, 4, 5])        # duplicate of 1
     assert m[0][3 * 4] == 0.0 and m[0][0] == 7.0              # fresh Adam state only for new entries
+
+
+def test_knn_mean_dist_against_kdtree():
+    """orc_knn_mean_dist: the mean distance to the three nearest other points,
+    as a float64 kd-tree (scipy's cKDTree, k=4 with the point itself first)
+    gives it, on a blob with exact duplicates and on a plane; and a planted
+    mistake (averaging the 1st..3rd instead of the 2nd..4th) fails."""
+    from scipy.spatial import cKDTree
+    rng = np.random.default_rng(11)
+    blob = rng.normal(0, 1, (3000, 3))
+    blob[200:300] = blob[0:100]
+    plane = np.c_[rng.uniform(-2, 2, (2000, 2)), np.zeros(2000)]
+    for x in (blob, plane):
+        x = x.astype(np.float32)
+        got = orc.knn_mean_dist(x)
+        d, _ = cKDTree(x.astype(np.float64)).query(x.astype(np.float64), k=4)
+        want = d[:, 1:].mean(axis=1)
+        assert np.allclose(got, want, rtol=2e-6, atol=1e-7)
+        assert not np.allclose(d[:, :3].mean(axis=1), want, rtol=2e-6, atol=1e-7)
