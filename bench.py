@@ -163,17 +163,18 @@ def _pmc_mean(d: str, kernel_re: str, counter: str, last: int) -> tuple:
     return sum(v) / len(v), len(v)
 
 
-def traffic_summary(dirs: list, copy_mib: int, last: int, commands: str) -> dict:
-    """HBM bytes per k_raster_bwd launch from FETCH_SIZE / WRITE_SIZE runs
+def traffic_summary(dirs: list, copy_mib: int, last: int, commands: str,
+                    kernel: str = "k_raster_bwd") -> dict:
+    """HBM bytes per launch of `kernel` from FETCH_SIZE / WRITE_SIZE runs
     (KiB per dispatch), each scaled so that a plain device copy of copy_mib MiB
     reads and writes exactly copy_mib MiB."""
     fetch_dir, write_dir, copy_fetch_dir, copy_write_dir = dirs
-    fk, nf = _pmc_mean(fetch_dir, "k_raster_bwd", "FETCH_SIZE", last)
-    wk, nw = _pmc_mean(write_dir, "k_raster_bwd", "WRITE_SIZE", last)
+    fk, nf = _pmc_mean(fetch_dir, kernel, "FETCH_SIZE", last)
+    wk, nw = _pmc_mean(write_dir, kernel, "WRITE_SIZE", last)
     cf, _ = _pmc_mean(copy_fetch_dir, "copyBuffer", "FETCH_SIZE", 0)
     cw, _ = _pmc_mean(copy_write_dir, "copyBuffer", "WRITE_SIZE", 0)
     fs, ws = copy_mib * 1024 / cf, copy_mib * 1024 / cw
-    return {"kernel": "k_raster_bwd", "dispatches": [nf, nw],
+    return {"kernel": kernel, "dispatches": [nf, nw],
             "fetch_kib_per_dispatch": fk, "write_kib_per_dispatch": wk,
             "copy_fetch_kib": cf, "copy_write_kib": cw, "copy_mib": copy_mib,
             "fetch_scale": fs, "write_scale": ws,
@@ -335,10 +336,14 @@ def main():
                     metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="only print the HBM traffic JSON of the raster backward from four "
                          "rocprofv3 --pmc csv directories (the copy runs use --copy-mib) and exit")
+    ap.add_argument("--traffic-kernels", default="k_raster_bwd",
+                    help="comma-separated kernels for --traffic-summary (one: a flat JSON object)")
     args = ap.parse_args()
     if args.traffic_summary:
-        print(json.dumps(traffic_summary(args.traffic_summary, args.copy_mib or 1024, args.steps,
-                                         args.rocprof_command), indent=1))
+        kernels = args.traffic_kernels.split(",")
+        res = {k: traffic_summary(args.traffic_summary, args.copy_mib or 1024, args.steps,
+                                  args.rocprof_command, k) for k in kernels}
+        print(json.dumps(res[kernels[0]] if len(kernels) == 1 else res, indent=1))
         return
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary, args.steps, args.rocprof_command), end="")
