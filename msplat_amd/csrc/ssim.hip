@@ -31,44 +31,55 @@ constexpr int TG = 16;
 constexpr int HALF = 5;
 constexpr int WIN = 11;
 constexpr int TW = TG + 2 * HALF;   // 26
-constexpr int TIN = TW + 2 * HALF;  // 36
 
-__global__ __launch_bounds__(256) void k_ssim_fused(int W, int H, const float* __restrict__ img,
-                                                    const float* __restrict__ gt,
-                                                    float* __restrict__ dbuf,
-                                                    float* __restrict__ loss_part) {
-    __shared__ float s_in[2][TW][TIN][3];   // gt / render, rows y0-5.., cols x0-10..
-    __shared__ float s_hp[TW][TW][5];
-    __shared__ float s_f1[TG][TW], s_f2[TG][TW], s_f3[TG][TW];
-    __shared__ float s_red[3][4];
-    const int tr = threadIdx.x, lx = tr & 15, ly = tr >> 4;
-    const int bx = blockIdx.x * TG - HALF, by = blockIdx.y * TG - HALF;
-    // input rows by .. by+25, columns bx-5 .. bx+30, all three channels
-    for (int i = tr; i < TW * TIN * 3; i += 256) {
-        const int c = i % 3, sx = (i / 3) % TIN, sy = i / (3 * TIN);
-        const int gy = by + sy, gx = bx - HALF + sx;
-        float gv = 0.f, rv = 0.f;
-        if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
-            const size_t q = ((size_t)gy * W + gx) * 3 + c;
-            gv = gt[q];
-            rv = img[q];
-        }
-        s_in[0][sy][sx][c] = gv;
-        s_in[1][sy][sx][c] = rv;
-    }
+// Fused forward / derivative / horizontal-backward tile: FX x FY output
+// pixels per workgroup of FT threads.  The horizontal sums are needed at
+// (FY + 10) x (FX + 10) positions and the derivative fields at FY x (FX + 10),
+// so a wide tile spends less of its work on the halo than a 16 x 16 one;
+// staging one channel at a time keeps the LDS at 40 KB for three
+// workgroups (six waves per SIMD) per CU.
+constexpr int FX = 32, FY = 16, FT = FX * FY;
+constexpr int FHX = FX + 2 * HALF;   // 42: columns with horizontal sums / fields
+constexpr int FHY = FY + 2 * HALF;   // 26: rows with horizontal sums
+constexpr int FIN = FHX + 2 * HALF;  // 52: input columns
+
+__global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __restrict__ img,
+                                                   const float* __restrict__ gt,
+                                                   float* __restrict__ dbuf,
+                                                   float* __restrict__ loss_part) {
+    __shared__ float s_in[2][FHY][FIN];     // gt / render of one channel, rows y0-5.., cols x0-10..
+    __shared__ float s_hp[FHY][FHX][5];
+    __shared__ float s_f1[FY][FHX], s_f2[FY][FHX], s_f3[FY][FHX];
+    __shared__ float s_red[3][FT / 64];
+    const int tr = threadIdx.x, lx = tr % FX, ly = tr / FX;
+    const int bx = blockIdx.x * FX - HALF, by = blockIdx.y * FY - HALF;
     float ssim_sum = 0.f, l1_sum = 0.f, cnt = 0.f;
     for (int c = 0; c < 3; ++c) {
+        if (c > 0) __syncthreads();
+        // channel c of rows by .. by+25, columns bx-5 .. bx+46 (zero outside)
+        for (int i = tr; i < FHY * FIN; i += FT) {
+            const int sy = i / FIN, sx = i - sy * FIN;
+            const int gy = by + sy, gx = bx - HALF + sx;
+            float gv = 0.f, rv = 0.f;
+            if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
+                const size_t q = ((size_t)gy * W + gx) * 3 + c;
+                gv = gt[q];
+                rv = img[q];
+            }
+            s_in[0][sy][sx] = gv;
+            s_in[1][sy][sx] = rv;
+        }
         __syncthreads();
         // horizontal zero-padded sums (ssim_h_fwd, .metal:3053-3115) at the
         // in-image positions of rows by.., columns bx..; zero elsewhere
-        for (int i = tr; i < TW * TW; i += 256) {
-            const int sy = i / TW, sx = i % TW, gy = by + sy, gx = bx + sx;
+        for (int i = tr; i < FHY * FHX; i += FT) {
+            const int sy = i / FHX, sx = i - sy * FHX, gy = by + sy, gx = bx + sx;
             float mx = 0.f, my = 0.f, sxx = 0.f, syy = 0.f, cxy = 0.f;
             if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
 #pragma unroll
                 for (int d = 0; d < WIN; ++d) {
                     const float w = GAUSS_1D[d];
-                    const float gv = s_in[0][sy][sx + d][c], rv = s_in[1][sy][sx + d][c];
+                    const float gv = s_in[0][sy][sx + d], rv = s_in[1][sy][sx + d];
                     mx += w * gv;
                     my += w * rv;
                     sxx += w * gv * gv;
@@ -83,8 +94,8 @@ __global__ __launch_bounds__(256) void k_ssim_fused(int W, int H, const float* _
             s_hp[sy][sx][4] = cxy;
         }
         __syncthreads();
-        for (int i = tr; i < TG * TW; i += 256) {
-            const int dy = i / TW, dx = i % TW;
+        for (int i = tr; i < FY * FHX; i += FT) {
+            const int dy = i / FHX, dx = i - dy * FHX;
             float mx = 0.f, my = 0.f, sx = 0.f, sy = 0.f, cxy = 0.f;
 #pragma unroll
             for (int k = 0; k < WIN; ++k) {
@@ -105,18 +116,17 @@ __global__ __launch_bounds__(256) void k_ssim_fused(int W, int H, const float* _
             s_f1[dy][dx] = dmu - 2.0f * my * dsyq - mx * dsxy;
             s_f2[dy][dx] = 2.0f * dsyq;
             s_f3[dy][dx] = dsxy;
-            if (dx >= HALF && dx < HALF + TG) {
+            if (dx >= HALF && dx < HALF + FX) {
                 const int gpx = bx + dx, gpy = by + dy + HALF;
                 if (gpx >= 0 && gpx < W && gpy >= 0 && gpy < H) {
-                    const size_t q = ((size_t)gpy * W + gpx) * 3 + c;
                     ssim_sum += (A * B) / (Cd * D);
-                    l1_sum += fabsf(gt[q] - img[q]);
+                    l1_sum += fabsf(s_in[0][dy + HALF][dx + HALF] - s_in[1][dy + HALF][dx + HALF]);
                     if (c == 0) cnt += 1.f;
                 }
             }
         }
         __syncthreads();
-        const int px = blockIdx.x * TG + lx, py = blockIdx.y * TG + ly;
+        const int px = blockIdx.x * FX + lx, py = blockIdx.y * FY + ly;
         if (px < W && py < H) {
             float h1 = 0.f, h2 = 0.f, h3 = 0.f;
 #pragma unroll
@@ -131,7 +141,6 @@ __global__ __launch_bounds__(256) void k_ssim_fused(int W, int H, const float* _
             o[1] = h2;
             o[2] = h3;
         }
-        __syncthreads();
     }
     // Workgroup partials of (sum SSIM, sum L1, pixels).
     const float a = wave_sum(ssim_sum), b = wave_sum(l1_sum), n = wave_sum(cnt);
@@ -142,7 +151,9 @@ __global__ __launch_bounds__(256) void k_ssim_fused(int W, int H, const float* _
     }
     __syncthreads();
     if (tr < 3) {
-        const float v = (s_red[tr][0] + s_red[tr][1]) + (s_red[tr][2] + s_red[tr][3]);
+        float v = 0.f;
+#pragma unroll
+        for (int k = 0; k < FT / 64; ++k) v += s_red[tr][k];
         loss_part[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 3 + tr] = v;
     }
 }
@@ -217,11 +228,12 @@ __global__ __launch_bounds__(256) void k_loss_final(int nparts, const float* __r
 
 void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
                  float inv_n, float* dbuf, float* v_rendered, float* loss_part, float* loss_out) {
+    const dim3 fgrid((W + FX - 1) / FX, (H + FY - 1) / FY);
+    hipLaunchKernelGGL(k_ssim_fused, fgrid, dim3(FT), 0, s, W, H, img, gt, dbuf, loss_part);
     const dim3 grid((W + TG - 1) / TG, (H + TG - 1) / TG);
-    hipLaunchKernelGGL(k_ssim_fused, grid, dim3(256), 0, s, W, H, img, gt, dbuf, loss_part);
     hipLaunchKernelGGL(k_ssim_v_bwd, grid, dim3(256), 0, s, W, H, img, gt, dbuf, w, inv_n,
                        v_rendered);
-    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(256), 0, s, (int)(grid.x * grid.y), loss_part,
+    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(256), 0, s, (int)(fgrid.x * fgrid.y), loss_part,
                        w, loss_out);
 }
 
