@@ -7,7 +7,7 @@
 // tile's range in one contiguous list — built from stable radix sorts:
 //   1. the projection wrote key = depth bits (0xFFFFFFFF if culled), value = id
 //   2. radix sort by depth                        (order of gaussians)
-//   3. tiles-hit gathered in that order, exclusive scan -> emit offsets
+//   3. tiles hit gathered in that order by the scan -> emit offsets
 //   4. emit one (tile id, gaussian id) pair per intersection, depth order
 //   5. stable radix sort by tile id               (depth order kept per tile)
 //   6. run edges -> per-tile counts; scan -> tile_bins, chunk work items
@@ -24,32 +24,6 @@ namespace msp {
 namespace {
 
 constexpr int SCAN_T = 1024;
-
-__global__ __launch_bounds__(256) void k_gather_hits(int N, const uint32_t* __restrict__ order,
-                                                     const int* __restrict__ tiles_hit,
-                                                     int* __restrict__ hits_sorted) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= N) return;
-    hits_sorted[r] = tiles_hit[order[r]];
-}
-
-// Sum of tiles hit over all gaussians (the intersection total), accumulated
-// into meta->total_isect (zeroed before) with one atomic per workgroup.
-constexpr int TOTAL_BLOCKS = 128;
-__global__ __launch_bounds__(256) void k_total_hits(int N, const int* __restrict__ tiles_hit,
-                                                    Meta* __restrict__ meta) {
-    long long v = 0;
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < N; i += TOTAL_BLOCKS * 256) v += tiles_hit[i];
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    __shared__ long long sh[4];
-    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const long long t = sh[0] + sh[1] + sh[2] + sh[3];
-        if (t) atomicAdd(reinterpret_cast<unsigned long long*>(&meta->total_isect),
-                         (unsigned long long)t);
-    }
-}
 
 // Emission of the (tile id, gaussian id) pairs of 64 depth-consecutive
 // gaussians by one wave, with coalesced stores.  Gaussians with fewer than
@@ -73,9 +47,9 @@ __global__ __launch_bounds__(256) void k_emit(int N, int tbx, int tby, GaussOut 
     int start = 0, h = 0, x0 = 0, y0 = 0, w = 1, g = 0;
     if (r < N) {
         h = hits[r];
+        start = eoff[r];
+        g = (int)order[r];
         if (h > 0) {
-            start = eoff[r];
-            g = (int)order[r];
             const float4 r0 = go.rec[4 * (size_t)g], r2 = go.rec[4 * (size_t)g + 2];
             int x1, y1;
             tile_rect(r0.x, r0.y, r2.y, r2.z, tbx, tby, x0, y0, x1, y1);
@@ -189,6 +163,7 @@ __global__ __launch_bounds__(SCAN_T) void k_tile_scan(int T, const int* __restri
     }
     __syncthreads();
     if (tid == SCAN_T - 1) {
+        meta->total_isect = s_c[SCAN_T - 1];
         meta->max_count = s_max[0];
         meta->n_items = s_i[SCAN_T - 1];
         meta->n_chunked_tiles = s_nch;
@@ -217,23 +192,15 @@ void launch_run_edges(hipStream_t s, int64_t n, const uint32_t* sorted_keys, int
                            end);
 }
 
-void launch_total_hits(hipStream_t s, int N, const int* tiles_hit, Meta* meta) {
-    (void)hipMemsetAsync(&meta->total_isect, 0, sizeof(int64_t), s);
-    if (N > 0)
-        hipLaunchKernelGGL(k_total_hits, dim3(TOTAL_BLOCKS), dim3(256), 0, s, N, tiles_hit, meta);
-}
-
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
                         uint32_t* dval2, int* radix_temp, const int* tiles_hit, int* hits_sorted,
                         int* eoff, int* scan_temp, uint32_t** order_out) {
     const bool flip = launch_radix_sort(s, dkey, dval, dkey2, dval2, N, 32, radix_temp);
     uint32_t* order = flip ? dval2 : dval;
     *order_out = order;
-    if (N > 0) {
-        hipLaunchKernelGGL(k_gather_hits, dim3(blocks_for(N)), dim3(256), 0, s, N,
-                           (const uint32_t*)order, tiles_hit, hits_sorted);
-        launch_exclusive_scan_i32(s, hits_sorted, eoff, N, scan_temp);
-    }
+    // emission offsets: exclusive scan of the tiles hit in depth order; the
+    // scan's first kernel gathers them into hits_sorted for the emission
+    if (N > 0) launch_exclusive_scan_i32(s, tiles_hit, eoff, N, scan_temp, order, hits_sorted);
 }
 
 const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go,

@@ -71,6 +71,10 @@ struct Ctx {
     Buf final_T, final_idx, out_img, dbuf, v_rendered, loss_part;
     // scalars
     Buf meta_d, loss_d, count_d, work_d;
+    // intersection total of the projection: ISECT_SLOTS counters, one per
+    // 128-byte line (workgroup b adds to slot b % ISECT_SLOTS), summed on the host
+    Buf isect_d;
+    uint64_t* isect_h = nullptr;
     // evaluation: per-workgroup fp64 partials and the three sums
     Buf eval_part, eval_out;
     // nearest-neighbour scales: cell keys / point ids (ping-pong), sort
@@ -154,7 +158,7 @@ void free_all(Ctx* c) {
                    &c->ttemp, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
                    &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
-                   &c->count_d, &c->work_d, &c->eval_part, &c->eval_out, &c->knn_k, &c->knn_v, &c->knn_k2, &c->knn_v2,
+                   &c->count_d, &c->work_d, &c->isect_d, &c->eval_part, &c->eval_out, &c->knn_k, &c->knn_v, &c->knn_k2, &c->knn_v2,
                    &c->knn_tmp, &c->knn_s, &c->knn_e, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
                    &c->d_tot, &c->d_scratch, &c->d_rnd};
     for (Buf* b : bufs)
@@ -162,6 +166,7 @@ void free_all(Ctx* c) {
     if (c->meta_h) (void)hipHostFree(c->meta_h);
     if (c->loss_h) (void)hipHostFree(c->loss_h);
     if (c->count_h) (void)hipHostFree(c->count_h);
+    if (c->isect_h) (void)hipHostFree(c->isect_h);
     for (auto& row : c->ev)
         for (auto& e : row)
             if (e) (void)hipEventDestroy(e);
@@ -315,16 +320,20 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
     c->last_N = N; c->last_T = T; c->last_W = p.W; c->last_H = p.H;
     c->have_bwd = false;
 
+    // The projection adds up the intersection total, which goes to the host
+    // while the GPU sorts by depth: the host waits on an event recorded after
+    // the copy, not on the stream.
+    const size_t slots_bytes = (size_t)ISECT_SLOTS * ISECT_STRIDE * 8;
+    ENSURE(c->isect_d, slots_bytes);
+    HIP_TRY(hipMemsetAsync(c->isect_d.p, 0, slots_bytes, c->stream));
     stage_mark(c, S_PROJ);
     GaussOut go = gauss_out(c);
     launch_project_fwd(c->stream, p, a->means3d, a->scales, a->quats, a->features_dc,
                        a->features_rest, a->opacities, go, P<uint32_t>(c->dkey),
-                       P<uint32_t>(c->dval), P<float>(c->gacc));
-    // The intersection total goes to the host while the GPU sorts by depth:
-    // the host waits on an event recorded after the copy, not on the stream.
+                       P<uint32_t>(c->dval), P<float>(c->gacc),
+                       P<unsigned long long>(c->isect_d));
     stage_mark(c, S_DEPTH);
-    launch_total_hits(c->stream, N, P<int>(c->tiles_hit), P<Meta>(c->meta_d));
-    HIP_TRY(hipMemcpyAsync(c->meta_h, c->meta_d.p, sizeof(Meta), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->isect_h, c->isect_d.p, slots_bytes, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipEventRecord(c->ev_total, c->stream));
     uint32_t* order = nullptr;
     launch_depth_order(c->stream, N, P<uint32_t>(c->dkey), P<uint32_t>(c->dval),
@@ -337,7 +346,8 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
         c->last_loss = c->loss_h[1] * c->loss_scale;
         c->loss_pending = false;
     }
-    const int64_t I64 = c->meta_h->total_isect;
+    int64_t I64 = 0;
+    for (int k = 0; k < ISECT_SLOTS; ++k) I64 += (int64_t)c->isect_h[(size_t)k * ISECT_STRIDE];
     if (I64 > (int64_t)0x7FFFFFFF - 4096)
         return fail(MSPLAT_ERR_ARG, "%lld tile intersections exceed the 32-bit index range",
                     (long long)I64);
@@ -407,6 +417,7 @@ int msplat_hip_init(int device) {
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->meta_h), sizeof(Meta)));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->loss_h), 16));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->count_h), 16));
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->isect_h), ISECT_SLOTS * ISECT_STRIDE * 8));
     for (auto& row : c->ev)
         for (auto& e : row) HIP_TRY(hipEventCreate(&e));
     HIP_TRY(hipEventCreateWithFlags(&c->ev_total, hipEventDisableTiming));

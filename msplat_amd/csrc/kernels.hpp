@@ -79,24 +79,30 @@ struct ChunkBufs {
     float* aC;           // x3
 };
 
+// Intersection-total counters of the projection: ISECT_SLOTS u64 counters
+// ISECT_STRIDE u64 apart (one 128-byte line each); the total is their sum.
+constexpr int ISECT_SLOTS = 64;
+constexpr int ISECT_STRIDE = 16;
 void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
                         const float* scales, const float* quats, const float* f_dc,
                         const float* f_rest, const float* opac_logits, GaussOut go,
-                        uint32_t* dkey, uint32_t* dval, float* gacc);
+                        uint32_t* dkey, uint32_t* dval, float* gacc,
+                        unsigned long long* total_isect);
 
-// Scans and radix sort (radix.hip).
+// Scans and radix sort (radix.hip).  With `gather` the scanned values are
+// in[gather[i]], also stored to gathered[i] (n ints).
 int64_t scan_block_count(int64_t n);
 void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot);
-void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot);
+void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot,
+                               const uint32_t* gather = nullptr, int* gathered = nullptr);
 int64_t radix_temp_ints(int64_t n);
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
                        int64_t n, int bits, int* temp);
 
-// Binning (binning.hip).  launch_total_hits writes the intersection total to
+// Binning (binning.hip).  The projection adds the intersection total to
 // meta->total_isect (needed on the host before launch_tile_lists);
 // launch_depth_order orders the gaussians by depth and scans their tile
 // counts in that order.
-void launch_total_hits(hipStream_t s, int N, const int* tiles_hit, Meta* meta);
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
                         uint32_t* dval2, int* radix_temp, const int* tiles_hit, int* hits_sorted,
                         int* eoff, int* scan_temp, uint32_t** order_out);

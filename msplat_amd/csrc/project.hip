@@ -1,6 +1,6 @@
 // project.hip — projection + SH colour of every gaussian (one thread each),
-// fused with the depth-key output for the binning and the zeroing of the
-// raster gradient accumulators.
+// fused with the depth-key output for the binning, the intersection total
+// the host reads, and the zeroing of the raster gradient accumulators.
 //
 // Follows project_and_sh_forward_kernel (.metal:1695-1787) and its helpers
 // quat_to_rotmat (.metal:111-131), scale_rot_to_cov3d (.metal:175-188),
@@ -83,6 +83,12 @@ __device__ __forceinline__ void sh_color(int degree, V3 d, const float* dc, cons
 
 constexpr int PROJ_T = 128;   // gaussians per workgroup
 
+__device__ __forceinline__ int project_one(const CamParams& p, int g, V3 pw, const float* sc,
+                                           const float* dc, float4 q, float ol,
+                                           const float* rest, GaussOut go,
+                                           uint32_t* __restrict__ dkey,
+                                           uint32_t* __restrict__ dval);
+
 // PROJ_STAGE: 16-byte features_rest loads per thread, enough for PROJ_T rows
 // of up to 48 floats (SH degree <= 3) or 72 floats (degree 4).
 template <int PROJ_STAGE>
@@ -90,7 +96,8 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     CamParams p, const float* __restrict__ means, const float* __restrict__ scales,
     const float* __restrict__ quats, const float* __restrict__ f_dc,
     const float* __restrict__ f_rest, const float* __restrict__ opac_logits, GaussOut go,
-    uint32_t* __restrict__ dkey, uint32_t* __restrict__ dval, float* __restrict__ gacc) {
+    uint32_t* __restrict__ dkey, uint32_t* __restrict__ dval, float* __restrict__ gacc,
+    unsigned long long* __restrict__ total_isect) {
     const int g0 = blockIdx.x * PROJ_T;
     const int g = g0 + threadIdx.x;
     const bool live = g < p.N;
@@ -146,14 +153,42 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
         for (int i = nv * 4 + threadIdx.x; i < cnt; i += PROJ_T) s_rest[i] = f_rest[base + i];
         __syncthreads();
     }
-    if (!live) return;
+    int area = 0;
+    if (live)
+        area = project_one(p, g, pw, sc, dc, q, ol, s_rest + (size_t)p.rest_per * threadIdx.x, go,
+                           dkey, dval);
+    // Intersection total for the host: one atomic per workgroup, on one of
+    // ISECT_SLOTS counters so that workgroups do not queue on one address.
+    int v = area;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    __shared__ int s_tot[PROJ_T / 64];
+    if ((threadIdx.x & 63) == 0) s_tot[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        long long t = 0;
+#pragma unroll
+        for (int k = 0; k < PROJ_T / 64; ++k) t += s_tot[k];
+        if (t)
+            atomicAdd(total_isect + (size_t)(blockIdx.x % ISECT_SLOTS) * ISECT_STRIDE,
+                      (unsigned long long)t);
+    }
+}
+
+// One gaussian: writes radii, tiles hit, the record and the depth key /
+// value; returns the number of tiles hit (0 when culled).
+__device__ __forceinline__ int project_one(const CamParams& p, int g, V3 pw, const float* sc,
+                                           const float* dc, float4 q, float ol,
+                                           const float* rest, GaussOut go,
+                                           uint32_t* __restrict__ dkey,
+                                           uint32_t* __restrict__ dval) {
     go.radii[g] = 0;
     go.tiles_hit[g] = 0;
     dkey[g] = 0xFFFFFFFFu;
     dval[g] = (uint32_t)g;
 
     const V3 pv = xf4x3(p.vm, pw);
-    if (pv.z <= p.clip) return;
+    if (pv.z <= p.clip) return 0;
 
     const float s0 = exp_cw(sc[0]), s1 = exp_cw(sc[1]), s2 = exp_cw(sc[2]);
     float cov[6];
@@ -183,7 +218,7 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
 
     // Conic and 3-sigma radius.
     const float det = c2x * c2z - c2y * c2y;
-    if (det == 0.f) return;
+    if (det == 0.f) return 0;
     const float inv_det = 1.f / det;
     const float ca = c2z * inv_det, cb = -c2y * inv_det, cc = c2x * inv_det;
     const float b = 0.5f * (c2x + c2z);
@@ -203,7 +238,7 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     int x0, y0, x1, y1;
     tile_rect(px, py, ex, ey, p.tbx, p.tby, x0, y0, x1, y1);
     const int area = (x1 - x0) * (y1 - y0);
-    if (area <= 0) return;
+    if (area <= 0) return 0;
 
     go.tiles_hit[g] = area;
     go.radii[g] = f2i(radius);
@@ -213,13 +248,14 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     const float inv = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
     const V3 dir{dx * inv, dy * inv, dz * inv};
     float col[3];
-    sh_color(p.dtu, dir, dc, s_rest + (size_t)p.rest_per * threadIdx.x, col);
+    sh_color(p.dtu, dir, dc, rest, col);
     float4* rec = go.rec + 4 * (size_t)g;
     rec[0] = make_float4(px, py, ca, cb);
     rec[1] = make_float4(cc, sigmoid(ol), col[0], col[1]);
     rec[2] = make_float4(col[2], ex, ey, pv.z);
     rec[3] = make_float4(dir.x, dir.y, dir.z, 0.f);
     dkey[g] = __float_as_uint(pv.z);
+    return area;
 }
 
 }  // namespace
@@ -227,7 +263,8 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
 void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
                         const float* scales, const float* quats, const float* f_dc,
                         const float* f_rest, const float* opac_logits, GaussOut go,
-                        uint32_t* dkey, uint32_t* dval, float* gacc) {
+                        uint32_t* dkey, uint32_t* dval, float* gacc,
+                        unsigned long long* total_isect) {
     if (p.N <= 0) return;
     const int blocks = (p.N + PROJ_T - 1) / PROJ_T;
     // staging area of PROJ_STAGE vectors per thread plus the spare slot
@@ -236,11 +273,11 @@ void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
     if (p.rest_per <= 48)
         hipLaunchKernelGGL(k_project_fwd<PROJ_T * 48 / 4 / PROJ_T>, dim3(blocks), dim3(PROJ_T), lds,
                            s, p, means, scales, quats, f_dc, f_rest, opac_logits, go, dkey, dval,
-                           gacc);
+                           gacc, total_isect);
     else
         hipLaunchKernelGGL(k_project_fwd<PROJ_T * 72 / 4 / PROJ_T>, dim3(blocks), dim3(PROJ_T), lds,
                            s, p, means, scales, quats, f_dc, f_rest, opac_logits, go, dkey, dval,
-                           gacc);
+                           gacc, total_isect);
 }
 
 }  // namespace msp

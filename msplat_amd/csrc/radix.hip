@@ -44,15 +44,29 @@ __device__ __forceinline__ int block_sum(int v, int* sh) {
 }
 __device__ __forceinline__ int block_sum_256(int v, int* sh) { return block_sum<256>(v, sh); }
 
+// Value i of a scan's input: in[i], or in[gather[i]].
+__device__ __forceinline__ int scan_in(const int* __restrict__ in,
+                                       const uint32_t* __restrict__ gather, int64_t i) {
+    return gather ? in[gather[i]] : in[i];
+}
+
+// Block totals of the scan input; with `gather` the input is in[gather[i]],
+// which is also written to gathered[i] for the later passes.
 __global__ __launch_bounds__(256) void k_block_reduce(const int* __restrict__ in, int64_t n,
-                                                      int* __restrict__ tot) {
+                                                      int* __restrict__ tot,
+                                                      const uint32_t* __restrict__ gather,
+                                                      int* __restrict__ gathered) {
     __shared__ int sh[4];
     const int64_t base = (int64_t)blockIdx.x * SB;
     int v = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int64_t i = base + k * 256 + threadIdx.x;
-        if (i < n) v += in[i];
+        if (i < n) {
+            const int x = scan_in(in, gather, i);
+            if (gathered) gathered[i] = x;
+            v += x;
+        }
     }
     const int t = block_sum_256(v, sh);
     if (threadIdx.x == 0) tot[blockIdx.x] = t;
@@ -88,7 +102,8 @@ __global__ __launch_bounds__(1024) void k_scan_totals(int* __restrict__ tot, int
 template <bool INCLUSIVE, bool PREFIX>
 __global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
                                                     int* __restrict__ out, int64_t n,
-                                                    const int* __restrict__ tot) {
+                                                    const int* __restrict__ tot,
+                                                    const uint32_t* __restrict__ gather) {
     __shared__ int ts[256];
     __shared__ int sh[4];
     const int64_t base = (int64_t)blockIdx.x * SB;
@@ -105,7 +120,7 @@ __global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int64_t i = base + 4 * t + k;
-        v[k] = i < n ? in[i] : 0;
+        v[k] = i < n ? scan_in(in, gather, i) : 0;
     }
     const int s4 = v[0] + v[1] + v[2] + v[3];
     ts[t] = s4;
@@ -207,6 +222,9 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
     __shared__ int gofs[256];
     __shared__ int scan_sh[RW];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // this block's scatter offset of digit tid, loaded now so that its latency
+    // overlaps the key loads and the ranking
+    const int my_gofs = (tid < 256 && (uint32_t)tid <= mask) ? offs[(size_t)tid * nblocks + blockIdx.x] : 0;
     for (int i = tid; i < RW * 256; i += RT) (&wcnt[0][0])[i] = 0;
     __syncthreads();
     const int64_t wbase = (int64_t)blockIdx.x * RB + (int64_t)w * WK;
@@ -246,7 +264,7 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
             wcnt[ww][d] = cnt;
             cnt += c;
         }
-        gofs[d] = (uint32_t)d <= mask ? offs[(size_t)d * nblocks + blockIdx.x] : 0;
+        gofs[d] = my_gofs;
     }
     const int start = block_exclusive_scan<RT>(cnt, scan_sh);
     if (tid < 256) dstart[tid] = start;
@@ -281,26 +299,32 @@ int64_t scan_block_count(int64_t n) { return (n + SB - 1) / SB; }
 constexpr int SCAN_DIRECT_BLOCKS = 2048;
 
 template <bool INCLUSIVE>
-void launch_scan(hipStream_t s, const int* in, int* out, int64_t n, int* tot) {
+void launch_scan(hipStream_t s, const int* in, int* out, int64_t n, int* tot,
+                 const uint32_t* gather, int* gathered) {
     if (n <= 0) return;
     const int nb = (int)scan_block_count(n);
-    hipLaunchKernelGGL(k_block_reduce, dim3(nb), dim3(256), 0, s, in, n, tot);
+    hipLaunchKernelGGL(k_block_reduce, dim3(nb), dim3(256), 0, s, in, n, tot, gather, gathered);
+    if (gather) {   // the block scans read the gathered copy
+        in = gathered;
+        gather = nullptr;
+    }
     if (nb <= SCAN_DIRECT_BLOCKS) {
         hipLaunchKernelGGL((k_block_scan<INCLUSIVE, true>), dim3(nb), dim3(256), 0, s, in, out, n,
-                           (const int*)tot);
+                           (const int*)tot, gather);
     } else {
         hipLaunchKernelGGL(k_scan_totals, dim3(1), dim3(1024), 0, s, tot, nb);
         hipLaunchKernelGGL((k_block_scan<INCLUSIVE, false>), dim3(nb), dim3(256), 0, s, in, out, n,
-                           (const int*)tot);
+                           (const int*)tot, gather);
     }
 }
 
 void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* tot) {
-    launch_scan<true>(s, in, out, n, tot);
+    launch_scan<true>(s, in, out, n, tot, nullptr, nullptr);
 }
 
-void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* tot) {
-    launch_scan<false>(s, in, out, n, tot);
+void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* tot,
+                               const uint32_t* gather, int* gathered) {
+    launch_scan<false>(s, in, out, n, tot, gather, gathered);
 }
 
 int64_t radix_temp_ints(int64_t n) {
