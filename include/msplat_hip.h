@@ -126,9 +126,10 @@ int msplat_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);
 int msplat_hip_commit(void);
 int msplat_hip_sync(void);
 
-/* msplat_render (bindings.h:37-46).  Writes the image [H,W,3] to out_img
- * (device); NULL leaves it in the context's own buffer, readable with
- * msplat_hip_copy_intermediate("out_img"). */
+/* msplat_render (bindings.h:37-46).  The rasteriser writes the image
+ * [H,W,3] straight to out_img (device; the context's own image buffer is
+ * then left as it was); NULL writes it to the context's own buffer, readable
+ * with msplat_hip_copy_intermediate("out_img"). */
 int msplat_hip_render(const MsplatRenderArgs* a, float* out_img);
 
 /* msplat_train_step (bindings.h:50-67).  radii_out: optional device [N];

@@ -136,8 +136,9 @@ int32_t msplat_trainer_render_pose_to_buffer(MsplatTrainer t, const float camToW
                                              int32_t refCameraIndex, uint8_t* outRGBA,
                                              int32_t* outWidth, int32_t* outHeight);
 
-/* Same into a caller-provided device buffer of H*W*3 floats (no host copy,
- * no synchronisation): the display-loop form of renderFromPoseToBuffer. */
+/* Same, rendered straight into a caller-provided device buffer of H*W*3
+ * floats (no copy, no synchronisation; outDevice NULL: size only): the
+ * display-loop form of renderFromPoseToBuffer. */
 int32_t msplat_trainer_render_pose_device(MsplatTrainer t, const float camToWorld[16],
                                           int32_t refCameraIndex, float* outDevice,
                                           int32_t* outWidth, int32_t* outHeight);

@@ -113,8 +113,9 @@ __global__ __launch_bounds__(256) void k_tile_edges(int64_t I, const uint32_t* _
     if (p == I - 1 || tkey[p + 1] != t) tend[t] = (int)(p + 1);
 }
 
-__global__ __launch_bounds__(SCAN_T) void k_tile_scan(int T, const int* __restrict__ tstart,
-                                                      const int* __restrict__ tend,
+__global__ __launch_bounds__(SCAN_T) void k_tile_scan(int T, int* __restrict__ tstart,
+                                                      int* __restrict__ tend,
+                                                      unsigned long long* __restrict__ isect,
                                                       int* __restrict__ tile_bins, Items it,
                                                       TileLists tl, Meta* __restrict__ meta) {
     __shared__ long long s_c[SCAN_T];
@@ -152,6 +153,9 @@ __global__ __launch_bounds__(SCAN_T) void k_tile_scan(int T, const int* __restri
     int ioff = s_i[tid] - is;
     for (int t = b; t < e; ++t) {
         const int n = tend[t] - tstart[t];
+        // cleared for the next frame's run edges (they write present tiles only)
+        tstart[t] = 0;
+        tend[t] = 0;
         tile_bins[2 * t] = (int)off;
         off += n;
         tile_bins[2 * t + 1] = (int)off;
@@ -161,6 +165,9 @@ __global__ __launch_bounds__(SCAN_T) void k_tile_scan(int T, const int* __restri
         ioff += K;
         if (K > 1) tl.chunked[atomicAdd(&s_nch, 1)] = t;
     }
+    // the projection's intersection counters, copied to the host earlier
+    // on the stream, cleared for the next frame
+    if (tid < ISECT_SLOTS) isect[(size_t)tid * ISECT_STRIDE] = 0ull;
     __syncthreads();
     if (tid == SCAN_T - 1) {
         meta->total_isect = s_c[SCAN_T - 1];
@@ -207,11 +214,11 @@ const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, 
                                   const uint32_t* order, const int* eoff, const int* hits,
                                   uint32_t* tkey, uint32_t* tval, uint32_t* tkey2, uint32_t* tval2,
                                   int* radix_temp, int* tstart, int* tend, int* tile_bins, Items it,
-                                  TileLists tl, Meta* meta) {
+                                  TileLists tl, Meta* meta, unsigned long long* isect) {
     const int T = p.tbx * p.tby;
     const uint32_t* sorted_ids = tval;
-    (void)hipMemsetAsync(tstart, 0, (size_t)T * 4, s);
-    (void)hipMemsetAsync(tend, 0, (size_t)T * 4, s);
+    // tstart / tend arrive zeroed: fresh buffers are, and every tile scan
+    // clears the ones it reads
     if (I > 0) {
         hipLaunchKernelGGL(k_emit, dim3(blocks_for(p.N)), dim3(256), 0, s, p.N, p.tbx, p.tby, go,
                            order, eoff, hits, tkey, tval);
@@ -222,8 +229,8 @@ const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, 
         sorted_ids = flip ? tval2 : tval;
         hipLaunchKernelGGL(k_tile_edges, dim3(blocks_for(I)), dim3(256), 0, s, I, sk, tstart, tend);
     }
-    hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(SCAN_T), 0, s, T, (const int*)tstart,
-                       (const int*)tend, tile_bins, it, tl, meta);
+    hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(SCAN_T), 0, s, T, tstart, tend, isect,
+                       tile_bins, it, tl, meta);
     hipLaunchKernelGGL(k_build_items, dim3(blocks_for(T)), dim3(256), 0, s, T, it);
     return sorted_ids;
 }

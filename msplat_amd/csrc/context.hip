@@ -75,6 +75,7 @@ struct Ctx {
     // 128-byte line (workgroup b adds to slot b % ISECT_SLOTS), summed on the host
     Buf isect_d;
     uint64_t* isect_h = nullptr;
+    bool isect_dirty = false;   // counters written and not yet cleared by a tile scan
     // evaluation: per-workgroup fp64 partials and the three sums
     Buf eval_part, eval_out;
     // nearest-neighbour scales: cell keys / point ids (ping-pong), sort
@@ -290,7 +291,8 @@ CamParams cam_params(const MsplatRenderArgs* a) {
 }
 
 // forward_pipeline (.mm:462-750): project -> depth order -> tile lists -> raster (+merge).
-int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
+// The image goes to dst_img, or to the context's own buffer when NULL.
+int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = nullptr) {
     const CamParams p = cam_params(a);
     const int N = p.N, T = p.tbx * p.tby;
     const size_t Px = (size_t)p.W * p.H;
@@ -323,9 +325,12 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
     // The projection adds up the intersection total, which goes to the host
     // while the GPU sorts by depth: the host waits on an event recorded after
     // the copy, not on the stream.
+    // (the counters arrive zeroed: fresh buffers are, and the tile scan of
+    // the previous frame cleared them, unless that frame stopped before it)
     const size_t slots_bytes = (size_t)ISECT_SLOTS * ISECT_STRIDE * 8;
     ENSURE(c->isect_d, slots_bytes);
-    HIP_TRY(hipMemsetAsync(c->isect_d.p, 0, slots_bytes, c->stream));
+    if (c->isect_dirty) HIP_TRY(hipMemsetAsync(c->isect_d.p, 0, slots_bytes, c->stream));
+    c->isect_dirty = true;
     stage_mark(c, S_PROJ);
     GaussOut go = gauss_out(c);
     launch_project_fwd(c->stream, p, a->means3d, a->scales, a->quats, a->features_dc,
@@ -377,15 +382,18 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training) {
                                       P<int>(c->hits), P<uint32_t>(c->tkey), P<uint32_t>(c->tval),
                                       P<uint32_t>(c->tkey2), P<uint32_t>(c->tval2),
                                       P<int>(c->ttemp), P<int>(c->tstart), P<int>(c->tend),
-                                      P<int>(c->tile_bins), it, tl, P<Meta>(c->meta_d));
+                                      P<int>(c->tile_bins), it, tl, P<Meta>(c->meta_d),
+                                      P<unsigned long long>(c->isect_d));
+    c->isect_dirty = false;   // the tile scan clears the counters
     Entries pk = packed(c);
+    float* img = dst_img ? dst_img : P<float>(c->out_img);
     stage_mark(c, S_RFWD);
     ChunkBufs cb = chunks(c);
     launch_raster_fwd(c->stream, p, max_items, P<Meta>(c->meta_d), it, P<int>(c->tile_bins), pk,
-                      P<float>(c->final_T), P<int>(c->final_idx), P<float>(c->out_img), cb,
+                      P<float>(c->final_T), P<int>(c->final_idx), img, cb,
                       work_counters(c));
     launch_raster_merge(c->stream, p, P<Meta>(c->meta_d), P<int>(c->l_chunked), it,
-                        P<float>(c->final_T), P<int>(c->final_idx), P<float>(c->out_img), cb,
+                        P<float>(c->final_T), P<int>(c->final_idx), img, cb,
                         training);
     HIP_TRY(hipGetLastError());
     c->meta_valid = false;
@@ -504,12 +512,9 @@ int msplat_hip_render(const MsplatRenderArgs* a, float* out_img) {
     int r = check_render_args(a);
     if (r != MSPLAT_OK) return r;
     stage_begin(c);
-    r = forward(c, a, false);
+    r = forward(c, a, false, out_img);
     if (r != MSPLAT_OK) return r;
     stage_mark(c, S_END);
-    if (out_img)
-        HIP_TRY(hipMemcpyAsync(out_img, c->out_img.p, (size_t)a->img_width * a->img_height * 12,
-                               hipMemcpyDeviceToDevice, c->stream));
     return MSPLAT_OK;
 }
 

@@ -111,7 +111,7 @@ const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, 
                                   const uint32_t* order, const int* eoff, const int* hits,
                                   uint32_t* tkey, uint32_t* tval, uint32_t* tkey2, uint32_t* tval2,
                                   int* radix_temp, int* tstart, int* tend, int* tile_bins, Items it,
-                                  TileLists tl, Meta* meta);
+                                  TileLists tl, Meta* meta, unsigned long long* isect);
 
 // Raster pair counters: WORK_SLOTS sets of four u64 counters, each set in
 // its own 128-byte line (WORK_SLOT_U64 apart); totals are the sums over sets.

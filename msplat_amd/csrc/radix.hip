@@ -214,7 +214,12 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
                                                       uint32_t* __restrict__ kout,
                                                       uint32_t* __restrict__ vout, int64_t n,
                                                       int shift, uint32_t mask, int nbits,
-                                                      int nblocks, const int* __restrict__ offs) {
+                                                      int nblocks, const int* __restrict__ offs,
+                                                      int* __restrict__ dtot) {
+    // The pass's digit totals were last read by the offsets kernel: block 0
+    // clears them for the next sort that uses this scratch.
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < DCOPIES * 256; i += RT) dtot[i] = 0;
     __shared__ uint32_t s_key[RB];
     __shared__ uint32_t s_val[RB];
     __shared__ int wcnt[RW][256];
@@ -329,7 +334,7 @@ void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n
 
 int64_t radix_temp_ints(int64_t n) {
     const int64_t nb = (n + RB - 1) / RB;
-    return 256 * nb + DCOPIES * 256 * MAX_PASSES + 8;
+    return DCOPIES * 256 * MAX_PASSES + 256 * nb + 8;
 }
 
 // Sorts (k0, v0) by the bits [0, bits) of the keys; ping-pongs with (k1, v1).
@@ -341,9 +346,13 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
     if (n <= 0 || bits <= 0) return false;
     const int nb = (int)((n + RB - 1) / RB);
     const int passes = (bits + 7) / 8;
-    int* hist = temp;
-    int* dtot = temp + 256 * (int64_t)nb;      // per pass: DCOPIES x 256 digit totals
-    (void)hipMemsetAsync(dtot, 0, (size_t)DCOPIES * 256 * passes * sizeof(int), s);
+    // Scratch layout: the digit totals first, at a fixed place whatever n is
+    // (DCOPIES x 256 per pass; each pass's scatter clears its totals for the
+    // next sort on this scratch), then the per-block histograms.
+    int* dtot = temp;
+    int* hist = temp + DCOPIES * 256 * MAX_PASSES;
+    // the digit totals arrive zeroed: fresh scratch is, and each pass's
+    // scatter clears its own
     bool flip = false;
     int shift = 0;
     for (int pass = 0; pass < passes; ++pass) {
@@ -360,7 +369,7 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
                            (const int*)dt);
         hipLaunchKernelGGL(k_radix_scatter, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki,
                            (const uint32_t*)vi, ko, vo, n, shift, mask, width, nb,
-                           (const int*)hist);
+                           (const int*)hist, dt);
         flip = !flip;
         shift += width;
     }

@@ -87,6 +87,21 @@ MTensor msplat_render(int num_points, MTensor& means3d, MTensor& scales, float g
     return g_out_img;
 }
 
+void msplat_render_to(float* out, int num_points, MTensor& means3d, MTensor& scales,
+                      float glob_scale, MTensor& quats, const float viewmat[16],
+                      const float projmat[16], float fx, float fy, float cx, float cy,
+                      unsigned img_height, unsigned img_width,
+                      const std::tuple<int, int, int> tile_bounds, float clip_thresh,
+                      unsigned degree, unsigned degrees_to_use, const float cam_pos[3],
+                      MTensor& features_dc, MTensor& features_rest, MTensor& opacities,
+                      const float background[3]) {
+    MsplatRenderArgs a;
+    fill_render(a, num_points, means3d, scales, glob_scale, quats, viewmat, projmat, fx, fy, cx, cy,
+                img_height, img_width, tile_bounds, clip_thresh, degree, degrees_to_use, cam_pos,
+                features_dc, features_rest, opacities, background);
+    check(msplat_hip_render(&a, out), "msplat_render");
+}
+
 std::tuple<MTensor, float> msplat_train_step(
     int num_points, MTensor& means3d, MTensor& scales, float glob_scale, MTensor& quats,
     const float viewmat[16], const float projmat[16], float fx, float fy, float cx, float cy,

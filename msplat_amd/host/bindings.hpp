@@ -38,6 +38,16 @@ MTensor msplat_render(int num_points, MTensor& means3d, MTensor& scales, float g
                       unsigned degree, unsigned degrees_to_use, const float cam_pos[3],
                       MTensor& features_dc, MTensor& features_rest, MTensor& opacities,
                       const float background[3]);
+// The same render written straight into a caller's device buffer of
+// img_height * img_width * 3 floats (no copy through the cached image).
+void msplat_render_to(float* out, int num_points, MTensor& means3d, MTensor& scales,
+                      float glob_scale, MTensor& quats, const float viewmat[16],
+                      const float projmat[16], float fx, float fy, float cx, float cy,
+                      unsigned img_height, unsigned img_width,
+                      const std::tuple<int, int, int> tile_bounds, float clip_thresh,
+                      unsigned degree, unsigned degrees_to_use, const float cam_pos[3],
+                      MTensor& features_dc, MTensor& features_rest, MTensor& opacities,
+                      const float background[3]);
 
 // msplat_train_step (bindings.h:50-67): fused forward + loss + backward +
 // Adam + grad stats.  Returns (radii [N], loss value).  window2d is not

@@ -244,6 +244,17 @@ MTensor Model::render(Camera& cam, int step) {   // model.cpp:536-544
                          featuresRest, opacities, cfg_.bgColor);
 }
 
+void Model::renderTo(Camera& cam, int step, float* dst, int& width, int& height) {
+    CamSetup s = prepareCam(cam, step);
+    width = s.width;
+    height = s.height;
+    if (!dst) return;
+    msplat_render_to(dst, (int)num_active, means, scales, 1.0f, quats, cam.cachedViewMat,
+                     cam.cachedProjViewMat, s.fx, s.fy, s.cx, s.cy, s.height, s.width,
+                     s.tileBounds, 0.01f, s.degree, s.degreesToUse, s.cam_pos, featuresDc,
+                     featuresRest, opacities, cfg_.bgColor);
+}
+
 // ---- scene files and checkpoints ----
 
 HostGaussians Model::toHost() const {

@@ -84,6 +84,8 @@ public:
     void schedulersStep(int step);
     void afterTrain(int step);
     MTensor render(Camera& cam, int step);
+    // render into a caller's device buffer; returns the image size
+    void renderTo(Camera& cam, int step, float* dst, int& width, int& height);
 
     int getDownscaleFactor(int step) const;
     int degreesToUse(int step) const;

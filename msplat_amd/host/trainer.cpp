@@ -164,6 +164,15 @@ public:
         return current_step;
     }
 
+    // The same into a caller's device buffer (dst NULL: size only).
+    void render_pose_to(const float camToWorld[16], int ref, float* dst, int& w, int& h) {
+        if (ref < 0 || ref >= (int)cameras.size()) throw std::runtime_error("ref_cam_idx out of range");
+        Camera cam = cameras[ref];
+        std::memcpy(cam.camToWorld, camToWorld, sizeof(cam.camToWorld));
+        cam.cached = false;
+        model->renderTo(cam, current_step, dst, w, h);
+    }
+
     MTensor render_camera(int i) {
         if (i < 0 || i >= (int)cameras.size()) throw std::runtime_error("camera index out of range");
         return model->render(cameras[i], current_step);
@@ -300,10 +309,10 @@ int32_t msplat_trainer_render_pose_device(MsplatTrainer t, const float camToWorl
                                           int32_t* outWidth, int32_t* outHeight) {
     if (!t || !camToWorld) return MSPLAT_ERR_ARG;
     return guarded([&]() -> int32_t {
-        msplat::MTensor img = T(t)->render_pose(camToWorld, refCameraIndex);
-        if (outWidth) *outWidth = (int32_t)img.size(1);
-        if (outHeight) *outHeight = (int32_t)img.size(0);
-        if (outDevice) msplat::check(msplat_hip_memcpy_d2d(outDevice, img.data_ptr(), img.nbytes()), "copy");
+        int w = 0, h = 0;
+        T(t)->render_pose_to(camToWorld, refCameraIndex, outDevice, w, h);
+        if (outWidth) *outWidth = (int32_t)w;
+        if (outHeight) *outHeight = (int32_t)h;
         return MSPLAT_OK;
     }, (int32_t)MSPLAT_ERR_ARG);
 }

@@ -251,3 +251,17 @@ def test_randn_statistics(dev):
     h = x.cpu().numpy().astype(np.float64)
     assert abs(h.mean()) < 5e-3 and abs(h.std() - 1.0) < 5e-3
     assert abs(((h > 1.0).mean()) - 0.158655) < 3e-3
+
+
+def test_scratch_reuse_across_sizes(dev):
+    """Regression: the sort / binning scratch is cleared by the kernels that
+    use it (radix digit totals, tile run edges, intersection counters) rather
+    than by memsets, so consecutive frames with fewer gaussians, fewer
+    intersections and fewer tiles must still be bit-exact.  Renders a large
+    scene, a much smaller one, then the large one again."""
+    big = small_scene(n=6000, width=192, height=128, seed_off=820)
+    little = small_scene(n=700, width=64, height=48, seed_off=821)
+    m1, _ = _render_and_compare(dev, big)
+    m2, _ = _render_and_compare(dev, little)
+    m3, _ = _render_and_compare(dev, big)
+    assert m2["total_isect"] < m1["total_isect"] == m3["total_isect"]
