@@ -10,7 +10,10 @@ renders of the cloud with means jittered by N(0, 0.02) plus N(0, 0.01) pixel
 noise.  All inputs are synthetic and resident in HBM before timing starts.
 
 value = train iterations / s over the timed steps; render_fps = renders / s
-over `--frames` poses.  Prints one JSON line.
+over `--frames` poses.  Inside the timed loops HIP events bracket only the
+roofline kernel (raster backward in training, raster forward in rendering);
+the per-stage times come from `--stage-steps` further steps / frames with
+every stage bracketed.  Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -45,6 +48,9 @@ FP32_PEAK = 157.3e12
 FWD_PAIR_FLOPS = 11 + 3 + 9
 BWD_PAIR_FLOPS = 11 + 3 + 64
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "raster_bwd_config3_traffic.json")
+# Stage names in the order of the library's stage-timing bits.
+STAGES = ["proj_sh_fwd", "depth_sort", "tile_lists", "rast_fwd", "loss_fwd_bwd", "rast_bwd",
+          "sh_rest_adam", "proj_sh_bwd_adam"]
 
 
 def log(*a):
@@ -222,15 +228,22 @@ def bench_config4(args):
     for s in range(args.warmup):
         device.train_step(g, su, 3, bg, gt, 0.2, LR_INIT, s + 1, want_loss=False)
     device.sync()
-    device.drain_raster_counters()
-    _abi_check(lib.msplat_hip_enable_stage_timing(1))
     t0 = time.perf_counter()
     for s in range(args.steps):
         device.train_step(g, su, 3, bg, gt, 0.2, LR_INIT, args.warmup + s + 1, want_loss=False)
     device.sync()
     dt = time.perf_counter() - t0
+    # per-stage breakdown over further steps, every stage bracketed by events
+    n_staged = max(1, min(args.stage_steps, args.steps))
+    _abi_check(lib.msplat_hip_set_stage_timing_mask(0xFFFFFFFF))
+    _abi_check(lib.msplat_hip_enable_stage_timing(1))
+    for s in range(n_staged):
+        device.train_step(g, su, 3, bg, gt, 0.2, LR_INIT, args.warmup + args.steps + s + 1,
+                          want_loss=False)
+    device.sync()
     stages, _ = stage_times(lib)
     pairs = device.drain_raster_counters()
+    _abi_check(lib.msplat_hip_enable_stage_timing(0))
     m = device.meta()
     its = args.steps / dt
     for k, v in _stage_line(stages).items():
@@ -244,7 +257,7 @@ def bench_config4(args):
                        "intersections": m["total_isect"], "largest_tile": m["max_count"],
                        "chunked_tiles": m["n_chunked_tiles"], "raster_items": m["n_items"]},
             "stage_ms": _stage_line(stages),
-            "bwd_grad_pairs_per_step": pairs[1] / max(args.steps, 1)}
+            "bwd_grad_pairs_per_step": pairs[1] / n_staged}
 
 
 def config5_cameras(n_poses=100, width=4946, height=3286):
@@ -273,7 +286,6 @@ def bench_config5(args):
         device.render(g, setups[i], 3, bg, out)
     torch.cuda.synchronize()
     log(f"config5 setup {time.perf_counter() - t:.1f}s")
-    _abi_check(lib.msplat_hip_enable_stage_timing(1))
     vis = cul = 0
     isect = 0
     t0 = time.perf_counter()
@@ -281,7 +293,14 @@ def bench_config5(args):
         device.render(g, su, 3, bg, out)
     device.sync()
     dt = time.perf_counter() - t0
+    # per-stage breakdown over the same poses again, every stage bracketed
+    _abi_check(lib.msplat_hip_set_stage_timing_mask(0xFFFFFFFF))
+    _abi_check(lib.msplat_hip_enable_stage_timing(1))
+    for su in setups:
+        device.render(g, su, 3, bg, out)
+    device.sync()
     stages, _ = stage_times(lib)
+    _abi_check(lib.msplat_hip_enable_stage_timing(0))
     # visible counts per pose, outside the timed loop
     for su in setups[:10]:
         device.render(g, su, 3, bg, out)
@@ -319,6 +338,8 @@ def main():
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--frames", type=int, default=200)
+    ap.add_argument("--stage-steps", type=int, default=60,
+                    help="untimed steps / frames with every stage bracketed, for the per-stage breakdown")
     ap.add_argument("--n", type=int, default=1_500_000)
     ap.add_argument("--cpu-steps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
@@ -390,6 +411,9 @@ def main():
         tr.step()
     device.sync()
     _abi = device._abi
+    # The timed steps bracket only the raster backward (the roofline kernel)
+    # with HIP events: every event leaves the GPU idle for a few microseconds.
+    _abi.check(lib.msplat_hip_set_stage_timing_mask(1 << STAGES.index("rast_bwd")))
     _abi.check(lib.msplat_hip_enable_stage_timing(1))
     n_start = tr.splat_count()
     device.sync()
@@ -400,20 +424,31 @@ def main():
         counts.append(st.splat_count)
     device.sync()
     t1 = time.perf_counter()
-    stages, calls = stage_times(lib)
+    timed, _ = stage_times(lib)
     train_pairs = device.drain_raster_counters()
     train_s = t1 - t0
     its = args.steps / train_s
     log(f"train: {args.steps} steps in {train_s:.3f}s = {its:.1f} it/s; gaussians {n_start} -> {tr.splat_count()}")
+    # Per-stage breakdown: further steps with every stage bracketed.
+    _abi.check(lib.msplat_hip_set_stage_timing_mask(0xFFFFFFFF))
+    _abi.check(lib.msplat_hip_enable_stage_timing(1))
+    for _ in range(args.stage_steps):
+        tr.step()
+    device.sync()
+    stages, _ = stage_times(lib)
+    device.drain_raster_counters()
+    step_ms = sum(ms / c for ms, c in stages.values() if c)
+    log(f"stage breakdown over {args.stage_steps} more steps (sum {step_ms:.3f} ms/step):")
     for k, (ms, c) in stages.items():
         if c:
-            log(f"  {k:18s} {ms / c:8.3f} ms/call  ({c} calls, {100 * ms / (train_s * 1e3):5.1f}% of wall)")
+            log(f"  {k:18s} {ms / c:8.3f} ms/call  ({c} calls, {100 * ms / c / step_ms:5.1f}% of stage sum)")
 
     # render FPS over the 32 camera poses (render_from_pose into a device buffer)
     out = torch.empty((cams[0].height, cams[0].width, 3), dtype=torch.float32, device="cuda")
     poses = [np.asarray(c.cam_to_world, np.float32) for c in cams]
     for i in range(5):
         tr.render_pose_device(poses[i % len(poses)], i % len(poses), out)
+    _abi.check(lib.msplat_hip_set_stage_timing_mask(1 << STAGES.index("rast_fwd")))
     _abi.check(lib.msplat_hip_enable_stage_timing(1))
     device.sync()
     r0 = time.perf_counter()
@@ -421,10 +456,18 @@ def main():
         tr.render_pose_device(poses[i % len(poses)], i % len(poses), out)
     device.sync()
     r1 = time.perf_counter()
-    rstages, _ = stage_times(lib)
+    rtimed, _ = stage_times(lib)
     render_pairs = device.drain_raster_counters()
     fps = args.frames / (r1 - r0)
     log(f"render: {args.frames} frames in {r1 - r0:.3f}s = {fps:.1f} FPS at N={tr.splat_count()}")
+    _abi.check(lib.msplat_hip_set_stage_timing_mask(0xFFFFFFFF))
+    _abi.check(lib.msplat_hip_enable_stage_timing(1))
+    for i in range(args.stage_steps):
+        tr.render_pose_device(poses[i % len(poses)], i % len(poses), out)
+    device.sync()
+    rstages, _ = stage_times(lib)
+    device.drain_raster_counters()
+    _abi.check(lib.msplat_hip_enable_stage_timing(0))
     for k, (ms, c) in rstages.items():
         if c:
             log(f"  {k:18s} {ms / c:8.3f} ms/call")
@@ -432,10 +475,10 @@ def main():
     # Roofline of the dominant kernel (raster backward): algorithmic flops from
     # the GPU pair counters over exactly the timed launches, divided by those
     # launches' HIP-event durations on the context stream.
-    bwd_ms, bwd_n = stages["rast_bwd"][0] / max(stages["rast_bwd"][1], 1), stages["rast_bwd"][1]
+    bwd_ms, bwd_n = timed["rast_bwd"][0] / max(timed["rast_bwd"][1], 1), timed["rast_bwd"][1]
     bwd_flops = BWD_PAIR_FLOPS * train_pairs[1] / max(bwd_n, 1)
     achieved = bwd_flops / (bwd_ms * 1e-3)
-    fwd_ms, fwd_n = rstages["rast_fwd"][0] / max(rstages["rast_fwd"][1], 1), rstages["rast_fwd"][1]
+    fwd_ms, fwd_n = rtimed["rast_fwd"][0] / max(rtimed["rast_fwd"][1], 1), rtimed["rast_fwd"][1]
     fwd_flops = FWD_PAIR_FLOPS * render_pairs[0] / max(fwd_n, 1)
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

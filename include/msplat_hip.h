@@ -193,6 +193,12 @@ int msplat_hip_knn_mean_dist(const float* xyz, int64_t n, float* mean_dist);
  * milliseconds ms[i] and the number of timed instances counts[i] since the
  * last drain (or enable), its name, and the number of calls timed. */
 int msplat_hip_enable_stage_timing(int enable);
+/* Bracket only the stages whose bit (1 << stage index, in the order drain
+ * names them) is set; the default is every stage.  Each event leaves the GPU
+ * idle for a few microseconds between the kernels it separates, so a
+ * throughput run times just the stages it reports.  No counterpart in the
+ * reference (its timing is per command-buffer encoder). */
+int msplat_hip_set_stage_timing_mask(uint32_t mask);
 int msplat_hip_drain_stage_times(double* ms, int64_t* counts, const char** names, int max_stages,
                                  int* n_stages, int64_t* n_calls);
 

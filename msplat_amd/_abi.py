@@ -165,6 +165,7 @@ SIGNATURES = [
     ("msplat_hip_randn", c_int, [c_void_p, c_int64, c_uint64]),
     ("msplat_hip_clamp_max", c_int, [c_void_p, c_int64, c_float]),
     ("msplat_hip_enable_stage_timing", c_int, [c_int]),
+    ("msplat_hip_set_stage_timing_mask", c_int, [c_uint32]),
     ("msplat_hip_drain_stage_times", c_int,
      [POINTER(c_double), POINTER(c_int64), POINTER(c_char_p), c_int, POINTER(c_int), POINTER(c_int64)]),
     ("msplat_hip_copy_intermediate", c_int, [c_char_p, c_void_p, POINTER(c_size_t)]),

@@ -48,7 +48,11 @@ struct Ctx {
     // Stage timing: one event per stage boundary of the current call; the
     // previous call's intervals are folded into the running sums at the next
     // call's host synchronisation point, so timing adds no synchronisation.
+    // Each event costs the GPU a few microseconds of idle time between the
+    // kernels it sits between, so a caller may bracket only some stages.
     bool timing = false;
+    uint32_t stage_mask = ~0u;
+    bool stage_open = false;   // the latest event opened a bracketed stage
     hipEvent_t ev[2][kMaxMarks] = {};
     int mark_stage[2][kMaxMarks] = {};
     int n_marks[2] = {0, 0};
@@ -217,13 +221,17 @@ unsigned long long* work_counters(Ctx* c) {
     return c->timing ? P<unsigned long long>(c->work_d) : nullptr;
 }
 
-// Record the start of stage `st` (S_END closes the call).
+// Record the start of stage `st` (S_END closes the call).  Only stages in
+// the mask get an event, plus the one that closes a bracketed stage.
 void stage_mark(Ctx* c, int st) {
     if (!c->timing) return;
+    const bool want = st < kNumStages && ((c->stage_mask >> st) & 1u);
+    if (!want && !c->stage_open) return;
     int& n = c->n_marks[c->cur];
     if (n >= kMaxMarks) return;
     (void)hipEventRecord(c->ev[c->cur][n], c->stream);
-    c->mark_stage[c->cur][n] = st;
+    c->mark_stage[c->cur][n] = want ? st : -1;
+    c->stage_open = want;
     ++n;
 }
 
@@ -249,6 +257,7 @@ void stage_begin(Ctx* c) {
     if (!c->timing) return;
     c->cur ^= 1;
     c->n_marks[c->cur] = 0;
+    c->stage_open = false;
 }
 
 int check_render_args(const MsplatRenderArgs* a) {
@@ -801,6 +810,13 @@ int msplat_hip_enable_stage_timing(int enable) {
     c->n_marks[0] = c->n_marks[1] = 0;
     for (int i = 0; i < kNumStages; ++i) { c->stage_sum[i] = 0.0; c->stage_cnt[i] = 0; }
     c->calls = 0;
+    return MSPLAT_OK;
+}
+
+int msplat_hip_set_stage_timing_mask(uint32_t mask) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    c->stage_mask = mask;
     return MSPLAT_OK;
 }
 

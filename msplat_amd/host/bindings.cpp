@@ -139,8 +139,14 @@ std::tuple<MTensor, float> msplat_train_step(
     t.inv_max_dim = inv_max_dim;
     if (!g_radii.defined() || g_radii.size(0) < num_points)
         g_radii = MTensor::empty({(int64_t)num_points * 5 / 4 + 16}, DType::Int32);
+    // The loss returned is that of the latest completed step, read without
+    // waiting for this one, like the reference's read of loss_sum right after
+    // committing the command buffer (msplat_metal.mm:1326): a synchronous read
+    // here would drain the stream every step and leave the GPU waiting for
+    // the host to launch the next one.
+    check(msplat_hip_train_step(&t, g_radii.data<int32_t>(), nullptr), "msplat_train_step");
     float loss = 0.f;
-    check(msplat_hip_train_step(&t, g_radii.data<int32_t>(), &loss), "msplat_train_step");
+    check(msplat_hip_last_loss(&loss, 0), "msplat_train_step");
     return {g_radii.view(num_points), loss};
 }
 
