@@ -165,6 +165,28 @@ int msplat_hip_clamp_max(float* p, int64_t n, float hi);
  * done there on the CPU), on the context stream. */
 int msplat_hip_image_to_rgba8(const float* img, int64_t n_pixels, uint8_t* rgba);
 
+/* Area resize of a device [src_h, src_w, 3] fp32 image into device
+ * [dst_h, dst_w, 3]: each output pixel is the overlap-weighted mean of the
+ * source pixels its footprint covers (resizeArea, image_io.cpp:91-138; used
+ * by Camera::getImage and Camera::loadImage, input_data.cpp:17-65), equal bit
+ * for bit to the reference's CPU loop.  On the context stream. */
+int msplat_hip_resize_area(const float* src, int32_t src_w, int32_t src_h, float* dst,
+                           int32_t dst_w, int32_t dst_h);
+
+/* Undistortion of a Brown-Conrady camera image (undistortImage,
+ * image_io.cpp:203-330).  intrinsics = {fx, fy, cx, cy}, distortion =
+ * {k1, k2, p1, p2, k3}.  msplat_undistort_roi (host only, no device needed)
+ * gives the crop rectangle roi = {x, y, w, h} of the undistorted image that
+ * has no empty border; the reference's camera then has cx - x, cy - y and
+ * size w x h.  msplat_hip_undistort writes that rectangle of the undistorted
+ * device [height, width, 3] image into device dst [roi h, roi w, 3] (forward
+ * distortion of each output pixel, bilinear sampling with edge clamping), on
+ * the context stream. */
+int msplat_undistort_roi(int32_t width, int32_t height, const float intrinsics[4],
+                         const float distortion[5], int32_t roi[4]);
+int msplat_hip_undistort(const float* src, int32_t width, int32_t height, const float intrinsics[4],
+                         const float distortion[5], const int32_t roi[4], float* dst);
+
 /* Evaluation metrics of a render against its target (device [H,W,3] fp32
  * images): PSNR = 10 log10(1 / MSE) and mean |r - g| as psnr / l1_loss
  * (model.cpp:25-40) compute them, and SSIM averaged over pixels and channels

@@ -173,6 +173,10 @@ SIGNATURES = [
     ("msplat_hip_drain_raster_counters", c_int, [POINTER(c_int64)]),
     ("msplat_hip_image_to_rgba8", c_int, [c_void_p, c_int64, c_void_p]),
     ("msplat_hip_knn_mean_dist", c_int, [c_void_p, c_int64, c_void_p]),
+    ("msplat_hip_resize_area", c_int, [c_void_p, c_int32, c_int32, c_void_p, c_int32, c_int32]),
+    ("msplat_undistort_roi", c_int, [c_int32, c_int32, POINTER(c_float), POINTER(c_float), POINTER(c_int32)]),
+    ("msplat_hip_undistort", c_int,
+     [c_void_p, c_int32, c_int32, POINTER(c_float), POINTER(c_float), POINTER(c_int32), c_void_p]),
     ("msplat_hip_image_metrics", c_int,
      [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, POINTER(ImageMetrics)]),
     # include/msplat_trainer.h

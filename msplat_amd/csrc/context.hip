@@ -668,6 +668,64 @@ int msplat_hip_image_metrics(const float* img, const float* gt, int32_t height, 
     return MSPLAT_OK;
 }
 
+int msplat_hip_resize_area(const float* src, int32_t src_w, int32_t src_h, float* dst,
+                           int32_t dst_w, int32_t dst_h) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!src || !dst) return fail(MSPLAT_ERR_ARG, "null resize argument");
+    if (src_w <= 0 || src_h <= 0 || (int64_t)src_w * src_h > (int64_t)1 << 30)
+        return fail(MSPLAT_ERR_ARG, "bad source size %dx%d", src_w, src_h);
+    if (dst_w <= 0 || dst_h <= 0 || (int64_t)dst_w * dst_h > (int64_t)1 << 30)
+        return fail(MSPLAT_ERR_ARG, "bad destination size %dx%d", dst_w, dst_h);
+    launch_resize_area(g_ctx->stream, src, src_w, src_h, dst, dst_w, dst_h);
+    HIP_TRY(hipGetLastError());
+    return MSPLAT_OK;
+}
+
+namespace {
+int undistort_params(int32_t width, int32_t height, const float intr[4], const float dist[5],
+                     UndistortParams& u) {
+    if (!intr || !dist) return fail(MSPLAT_ERR_ARG, "null undistortion argument");
+    if (width <= 0 || height <= 0 || (int64_t)width * height > (int64_t)1 << 30)
+        return fail(MSPLAT_ERR_ARG, "bad image size %dx%d", width, height);
+    for (int i = 0; i < 4; ++i)
+        if (!std::isfinite(intr[i])) return fail(MSPLAT_ERR_ARG, "intrinsics must be finite");
+    for (int i = 0; i < 5; ++i)
+        if (!std::isfinite(dist[i])) return fail(MSPLAT_ERR_ARG, "distortion must be finite");
+    if (intr[0] == 0.f || intr[1] == 0.f) return fail(MSPLAT_ERR_ARG, "fx, fy must be nonzero");
+    u = UndistortParams{intr[0], intr[1], intr[2], intr[3], dist[0], dist[1], dist[2], dist[3],
+                        dist[4], 0, 0, 0, 0};
+    return MSPLAT_OK;
+}
+}  // namespace
+
+int msplat_undistort_roi(int32_t width, int32_t height, const float intrinsics[4],
+                         const float distortion[5], int32_t roi[4]) {
+    UndistortParams u;
+    const int r = undistort_params(width, height, intrinsics, distortion, u);
+    if (r != MSPLAT_OK) return r;
+    if (!roi) return fail(MSPLAT_ERR_ARG, "null roi");
+    undistort_roi(width, height, u);
+    roi[0] = u.roi_x; roi[1] = u.roi_y; roi[2] = u.roi_w; roi[3] = u.roi_h;
+    return MSPLAT_OK;
+}
+
+int msplat_hip_undistort(const float* src, int32_t width, int32_t height, const float intrinsics[4],
+                         const float distortion[5], const int32_t roi[4], float* dst) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!src || !dst || !roi) return fail(MSPLAT_ERR_ARG, "null undistortion argument");
+    UndistortParams u;
+    const int r = undistort_params(width, height, intrinsics, distortion, u);
+    if (r != MSPLAT_OK) return r;
+    if (roi[0] < 0 || roi[1] < 0 || roi[2] <= 0 || roi[3] <= 0 || roi[2] > width - roi[0] ||
+        roi[3] > height - roi[1])
+        return fail(MSPLAT_ERR_ARG, "roi (%d,%d %dx%d) outside the %dx%d image", roi[0], roi[1],
+                    roi[2], roi[3], width, height);
+    u.roi_x = roi[0]; u.roi_y = roi[1]; u.roi_w = roi[2]; u.roi_h = roi[3];
+    launch_undistort(g_ctx->stream, src, width, height, u, dst);
+    HIP_TRY(hipGetLastError());
+    return MSPLAT_OK;
+}
+
 int msplat_hip_knn_mean_dist(const float* xyz, int64_t n, float* mean_dist) {
     Ctx* c = g_ctx;
     if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");

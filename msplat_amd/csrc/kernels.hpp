@@ -204,4 +204,16 @@ void launch_knn_search(hipStream_t s, int64_t n, const float* xyz, const KnnGrid
                        float* mean_dist);
 void launch_run_edges(hipStream_t s, int64_t n, const uint32_t* sorted_keys, int* start, int* end);
 
+// Target images: area resize and Brown-Conrady undistortion (image.hip).
+struct UndistortParams {
+    float fx, fy, cx, cy;
+    float k1, k2, p1, p2, k3;
+    int roi_x, roi_y, roi_w, roi_h;   // crop rectangle of the undistorted image
+};
+void undistort_roi(int w, int h, UndistortParams& u);   // host: fills roi_*
+void launch_resize_area(hipStream_t s, const float* src, int sw, int sh, float* dst, int dw,
+                        int dh);
+void launch_undistort(hipStream_t s, const float* src, int w, int h, const UndistortParams& u,
+                      float* dst);
+
 }  // namespace msp

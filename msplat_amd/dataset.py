@@ -2,8 +2,8 @@
 msplat_dataset_*): cameras with OpenGL camera-to-world poses sorted by image
 name, the normalised sparse point cloud, its normalisation, the reference's
 train / test split and the initial gaussians of the cloud (nearest-neighbour
-scales on the GPU).  Image decoding is left to the caller: each camera
-carries its image path.
+scales on the GPU).  Each camera carries its image path; load_image decodes
+it and prepares it on the GPU like the reference's Camera::loadImage.
 """
 from __future__ import annotations
 
@@ -55,6 +55,12 @@ class Dataset:
         t = (ctypes.c_float * 3)()
         _abi.check(self._lib.msplat_dataset_normalisation(self._h, ctypes.byref(s), t))
         return float(s.value), np.array(t[:], np.float32)
+
+    def load_image(self, i: int, downscale: float = 1.0):
+        """Camera i's image decoded, downscaled and undistorted on the GPU
+        (Camera::loadImage): (updated camera, CUDA (H, W, 3) float32)."""
+        from .image_io import load_camera_image
+        return load_camera_image(self.image_paths[i], self.cameras[i], self.distortion[i], downscale)
 
     def split_train_test(self, test_every: int = 8):
         """InputData::splitTrainTest (input_data.cpp:148-158): every test_every-th camera is a test camera."""

@@ -23,25 +23,14 @@ namespace {
 
 std::string g_err;
 
-// Box filter by an integer factor d over the floor(W/d) x floor(H/d) grid:
-// the area resampling of Camera::getImage (input_data.cpp:54-65) for image
-// sizes divisible by d.
-std::vector<float> box_downscale(const std::vector<float>& img, int W, int H, int d, int& w2,
-                                 int& h2) {
-    w2 = W / d;
-    h2 = H / d;
-    std::vector<float> out((size_t)w2 * h2 * 3, 0.f);
-    const float inv = 1.f / (float)(d * d);
-    for (int y = 0; y < h2; ++y)
-        for (int x = 0; x < w2; ++x)
-            for (int c = 0; c < 3; ++c) {
-                float acc = 0.f;
-                for (int dy = 0; dy < d; ++dy)
-                    for (int dx = 0; dx < d; ++dx)
-                        acc += img[((size_t)(y * d + dy) * W + (x * d + dx)) * 3 + c];
-                out[((size_t)y * w2 + x) * 3 + c] = acc * inv;
-            }
-    return out;
+// Camera::getImage (input_data.cpp:54-65): the image at 1/ds resolution,
+// (W / ds) x (H / ds) by the reference's area resize, on the GPU.
+MTensor downscaled(const MTensor& full, int W, int H, int ds) {
+    const int w2 = W / ds, h2 = H / ds;
+    if (w2 <= 0 || h2 <= 0) throw std::runtime_error("image too small for the downscale factor");
+    MTensor t = gpu_empty({h2, w2, 3}, DType::Float32);
+    check(msplat_hip_resize_area(full.data<float>(), W, H, t.data<float>(), w2, h2), "resize");
+    return t;
 }
 
 }  // namespace
@@ -131,14 +120,11 @@ public:
             cam.fx = cams[i].fx; cam.fy = cams[i].fy; cam.cx = cams[i].cx; cam.cy = cams[i].cy;
             std::memcpy(cam.camToWorld, cams[i].camToWorld, sizeof(cam.camToWorld));
             if (!images[i]) throw std::runtime_error("missing test image");
-            const size_t full = (size_t)cam.width * cam.height * 3;
-            std::vector<float> host(full);
-            if (on_device) check(msplat_hip_memcpy_d2h(host.data(), images[i], full * 4), "copy");
-            else std::memcpy(host.data(), images[i], full * 4);
-            int w2 = cam.width, h2 = cam.height;
-            if (ds > 1) host = box_downscale(host, cam.width, cam.height, ds, w2, h2);
-            MTensor gt = gpu_empty({h2, w2, 3}, DType::Float32);
-            gt.copy_from_host(host.data(), host.size() * sizeof(float));
+            MTensor gt = gpu_empty({cam.height, cam.width, 3}, DType::Float32);
+            if (on_device) gt.copy_from_device(images[i], gt.nbytes());
+            else gt.copy_from_host(images[i], gt.nbytes());
+            if (ds > 1) gt = downscaled(gt, cam.width, cam.height, ds);
+            const int h2 = (int)gt.size(0), w2 = (int)gt.size(1);
             MTensor img = model->render(cam, cfg.iterations);
             if (img.size(0) != h2 || img.size(1) != w2)
                 throw std::runtime_error("render and target sizes differ");
@@ -197,13 +183,7 @@ private:
         auto it = cache.find(ds);
         if (it != cache.end()) return it->second;
         const Camera& k = cameras[ci];
-        MTensor& full = cache.at(1);
-        std::vector<float> host((size_t)full.numel());
-        full.copy_to_host(host.data(), full.nbytes());
-        int w2, h2;
-        std::vector<float> small = box_downscale(host, k.width, k.height, ds, w2, h2);
-        MTensor t = gpu_empty({h2, w2, 3}, DType::Float32);
-        t.copy_from_host(small.data(), small.size() * sizeof(float));
+        MTensor t = downscaled(cache.at(1), k.width, k.height, ds);
         return cache[ds] = t;
     }
 

@@ -29,6 +29,11 @@
 //   accumulate_grad_stats   .metal:1643-1664
 //   train step order        msplat_metal.mm:1141-1330
 //   densify                 .metal:3475-3729, msplat_metal.mm:1337-1592
+//   image metrics           model.cpp:25-40, ssim.cpp:26-123
+//   rgba8                   msplat_api.mm:230-238
+//   knn mean distance       kdtree_tensor.hpp:26-40 (brute force)
+//   resize_area             image_io.cpp:91-138
+//   undistort (+ roi)       image_io.cpp:140-330
 
 #include "oracle.h"
 
@@ -1312,6 +1317,158 @@ void orc_knn_mean_dist(int64_t n, const float* xyz, float* out) {
         for (int j = 1; j < 4; ++j) sum += std::sqrt(b[j]);
         out[i] = sum / 3;
     }
+}
+
+
+// ---- target images: area resize and undistortion ----
+
+void orc_resize_area(int32_t sw, int32_t sh, const float* src, int32_t dw, int32_t dh, float* dst) {
+    const float scale_x = (float)sw / (float)dw;
+    const float scale_y = (float)sh / (float)dh;
+    for (int dy = 0; dy < dh; ++dy) {
+        const float y0 = (float)dy * scale_y, y1 = (float)(dy + 1) * scale_y;
+        for (int dx = 0; dx < dw; ++dx) {
+            const float x0 = (float)dx * scale_x, x1 = (float)(dx + 1) * scale_x;
+            float sum[3] = {0.f, 0.f, 0.f};
+            float total = 0.f;
+            const int iy0 = (int)y0, iy1 = std::min((int)std::ceil(y1), (int)sh);
+            const int ix0 = (int)x0, ix1 = std::min((int)std::ceil(x1), (int)sw);
+            for (int iy = iy0; iy < iy1; ++iy) {
+                const float wy = std::min((float)(iy + 1), y1) - std::max((float)iy, y0);
+                for (int ix = ix0; ix < ix1; ++ix) {
+                    const float wx = std::min((float)(ix + 1), x1) - std::max((float)ix, x0);
+                    const float area = wx * wy;
+                    const float* q = &src[((size_t)iy * sw + ix) * 3];
+                    for (int c = 0; c < 3; ++c) sum[c] += q[c] * area;
+                    total += area;
+                }
+            }
+            const float inv = 1.0f / total;
+            float* o = &dst[((size_t)dy * dw + dx) * 3];
+            for (int c = 0; c < 3; ++c) o[c] = sum[c] * inv;
+        }
+    }
+}
+
+namespace {
+
+struct Distortion { float fx, fy, cx, cy, k1, k2, p1, p2, k3; };
+
+// distortPoint, image_io.cpp:143-153
+void orc_distort_point(float x, float y, const Distortion& d, float& xd, float& yd) {
+    const float r2 = x * x + y * y;
+    const float r4 = r2 * r2;
+    const float r6 = r4 * r2;
+    const float radial = 1.0f + d.k1 * r2 + d.k2 * r4 + d.k3 * r6;
+    xd = x * radial + 2.0f * d.p1 * x * y + d.p2 * (r2 + 2.0f * x * x);
+    yd = y * radial + d.p1 * (r2 + 2.0f * y * y) + 2.0f * d.p2 * x * y;
+}
+
+// undistortPoint, image_io.cpp:156-171
+void orc_undistort_point(float xd, float yd, const Distortion& d, float& xu, float& yu) {
+    xu = xd;
+    yu = yd;
+    for (int i = 0; i < 20; i++) {
+        const float r2 = xu * xu + yu * yu;
+        const float r4 = r2 * r2;
+        const float r6 = r4 * r2;
+        const float radial = 1.0f + d.k1 * r2 + d.k2 * r4 + d.k3 * r6;
+        const float dx = 2.0f * d.p1 * xu * yu + d.p2 * (r2 + 2.0f * xu * xu);
+        const float dy = d.p1 * (r2 + 2.0f * yu * yu) + 2.0f * d.p2 * xu * yu;
+        xu = (xd - dx) / radial;
+        yu = (yd - dy) / radial;
+    }
+}
+
+// (int)floor(v) where it is defined; beyond the int range (undefined in the
+// reference) it saturates to just outside [0, n], which the clamp that
+// follows treats like any other outside value.
+int orc_floor_int(float v, int n) {
+    const float f = std::floor(v);
+    if (!(f > -1.f)) return -1;
+    if (f > (float)n) return n;
+    return (int)f;
+}
+
+// bilinearSample, image_io.cpp:174-201
+void orc_bilinear(const float* img, int w, int h, float x, float y, float out[3]) {
+    int x0 = orc_floor_int(x, w), y0 = orc_floor_int(y, h);
+    int x1 = x0 + 1, y1 = y0 + 1;
+    x0 = std::clamp(x0, 0, w - 1);
+    x1 = std::clamp(x1, 0, w - 1);
+    y0 = std::clamp(y0, 0, h - 1);
+    y1 = std::clamp(y1, 0, h - 1);
+    const float fx = x - std::floor(x);
+    const float fy = y - std::floor(y);
+    const float* p00 = &img[((size_t)y0 * w + x0) * 3];
+    const float* p10 = &img[((size_t)y0 * w + x1) * 3];
+    const float* p01 = &img[((size_t)y1 * w + x0) * 3];
+    const float* p11 = &img[((size_t)y1 * w + x1) * 3];
+    for (int c = 0; c < 3; c++) {
+        const float top = p00[c] * (1.0f - fx) + p10[c] * fx;
+        const float bottom = p01[c] * (1.0f - fx) + p11[c] * fx;
+        out[c] = top * (1.0f - fy) + bottom * fy;
+    }
+}
+
+int orc_saturating_int(float v) {
+    if (!(v > -2.0e9f)) return -2000000000;
+    if (v > 2.0e9f) return 2000000000;
+    return (int)v;
+}
+
+Distortion orc_distortion(const float intr[4], const float dist[5]) {
+    return Distortion{intr[0], intr[1], intr[2], intr[3], dist[0], dist[1], dist[2], dist[3], dist[4]};
+}
+
+}  // namespace
+
+void orc_undistort_roi(int32_t w, int32_t h, const float intr[4], const float dist[5], int32_t roi[4]) {
+    const Distortion d = orc_distortion(intr, dist);
+    float top_max = -1e9f, bottom_min = 1e9f, left_max = -1e9f, right_min = 1e9f;
+    const int n = 200;
+    for (int i = 0; i < n; i++) {
+        const float t = (float)i / (n - 1);
+        float xu, yu;
+        float xd = (t * w - d.cx) / d.fx, yd = (0.0f - d.cy) / d.fy;
+        orc_undistort_point(xd, yd, d, xu, yu);
+        top_max = std::max(top_max, yu * d.fy + d.cy);
+        xd = (t * w - d.cx) / d.fx; yd = ((float)(h - 1) - d.cy) / d.fy;
+        orc_undistort_point(xd, yd, d, xu, yu);
+        bottom_min = std::min(bottom_min, yu * d.fy + d.cy);
+        xd = (0.0f - d.cx) / d.fx; yd = (t * h - d.cy) / d.fy;
+        orc_undistort_point(xd, yd, d, xu, yu);
+        left_max = std::max(left_max, xu * d.fx + d.cx);
+        xd = ((float)(w - 1) - d.cx) / d.fx; yd = (t * h - d.cy) / d.fy;
+        orc_undistort_point(xd, yd, d, xu, yu);
+        right_min = std::min(right_min, xu * d.fx + d.cx);
+    }
+    int rx = std::max(0, orc_saturating_int(std::ceil(left_max)));
+    int ry = std::max(0, orc_saturating_int(std::ceil(top_max)));
+    int rw = std::min((int)w, orc_saturating_int(std::floor(right_min))) - rx;
+    int rh = std::min((int)h, orc_saturating_int(std::floor(bottom_min))) - ry;
+    if (rw <= 0 || rh <= 0) { rx = 0; ry = 0; rw = w; rh = h; }
+    roi[0] = rx; roi[1] = ry; roi[2] = rw; roi[3] = rh;
+}
+
+void orc_undistort(int32_t w, int32_t h, const float* src, const float intr[4], const float dist[5],
+                   int32_t roi[4], float* dst) {
+    const Distortion d = orc_distortion(intr, dist);
+    orc_undistort_roi(w, h, intr, dist, roi);
+    // the whole image remapped, then the rectangle copied out, as the reference
+    std::vector<float> full((size_t)w * h * 3);
+    for (int oy = 0; oy < h; oy++) {
+        for (int ox = 0; ox < w; ox++) {
+            const float x = ((float)ox - d.cx) / d.fx;
+            const float y = ((float)oy - d.cy) / d.fy;
+            float xd, yd;
+            orc_distort_point(x, y, d, xd, yd);
+            orc_bilinear(src, w, h, xd * d.fx + d.cx, yd * d.fy + d.cy, &full[((size_t)oy * w + ox) * 3]);
+        }
+    }
+    for (int y = 0; y < roi[3]; y++)
+        std::memcpy(&dst[(size_t)y * roi[2] * 3], &full[((size_t)(y + roi[1]) * w + roi[0]) * 3],
+                    (size_t)roi[2] * 3 * sizeof(float));
 }
 
 }  // extern "C"

@@ -193,6 +193,17 @@ void orc_image_to_rgba8(int64_t n_pixels, const float* img, uint8_t* rgba);
  * Brute force, O(n^2). */
 void orc_knn_mean_dist(int64_t n, const float* xyz, float* out);
 
+/* Target images.  resize_area (image_io.cpp:91-138): the overlap-weighted
+ * box resample of an [sh,sw,3] image to [dh,dw,3].  undistort_roi /
+ * undistort (image_io.cpp:140-330): the crop rectangle {x, y, w, h} of a
+ * Brown-Conrady image (intr = fx fy cx cy, dist = k1 k2 p1 p2 k3) and the
+ * undistorted image cropped to it (dst holds roi w x h x 3 floats; at most
+ * w x h x 3). */
+void orc_resize_area(int32_t sw, int32_t sh, const float* src, int32_t dw, int32_t dh, float* dst);
+void orc_undistort_roi(int32_t w, int32_t h, const float intr[4], const float dist[5], int32_t roi[4]);
+void orc_undistort(int32_t w, int32_t h, const float* src, const float intr[4], const float dist[5],
+                   int32_t roi[4], float* dst);
+
 #ifdef __cplusplus
 }
 #endif

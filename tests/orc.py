@@ -200,6 +200,36 @@ def knn_mean_dist(xyz) -> np.ndarray:
     return out
 
 
+def resize_area(img, dw: int, dh: int) -> np.ndarray:
+    img = f32(img)
+    sh, sw = img.shape[:2]
+    out = np.zeros((dh, dw, 3), np.float32)
+    lib().orc_resize_area(c_int32(sw), c_int32(sh), P(img), c_int32(dw), c_int32(dh), P(out))
+    return out
+
+
+def _cam_arrays(intr, dist):
+    return np.ascontiguousarray(intr, np.float32), np.ascontiguousarray(dist, np.float32)
+
+
+def undistort_roi(w: int, h: int, intr, dist) -> np.ndarray:
+    i, d = _cam_arrays(intr, dist)
+    roi = np.zeros(4, np.int32)
+    lib().orc_undistort_roi(c_int32(w), c_int32(h), P(i), P(d), P(roi))
+    return roi
+
+
+def undistort(img, intr, dist):
+    """(cropped undistorted image, roi) of an [h,w,3] image."""
+    img = f32(img)
+    h, w = img.shape[:2]
+    i, d = _cam_arrays(intr, dist)
+    roi = np.zeros(4, np.int32)
+    buf = np.zeros(h * w * 3, np.float32)
+    lib().orc_undistort(c_int32(w), c_int32(h), P(img), P(i), P(d), P(roi), P(buf))
+    return buf[: roi[2] * roi[3] * 3].reshape(roi[3], roi[2], 3).copy(), roi
+
+
 def adam_hparams(lrs, step: int, beta1=0.9, beta2=0.999, eps=1e-8) -> OrcAdam:
     """fullIteration's bias corrections (model.cpp:558-571), fp32 like the reference."""
     a = OrcAdam()

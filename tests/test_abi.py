@@ -29,7 +29,7 @@ def _declared():
     for h in (HEADER, TRAINER_HEADER):
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
         text = re.sub(r"static inline[^{]*\{.*?\n\}", "", text, flags=re.S)
-        names |= set(re.findall(r"\b(msplat_(?:hip_|trainer_|scene_|dataset_|prepare_cam)\w*)\s*\(", text))
+        names |= set(re.findall(r"\b(msplat_(?:hip_|trainer_|scene_|dataset_|undistort_|prepare_cam)\w*)\s*\(", text))
     return sorted(names)
 
 
@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol():
     nm = shutil.which("nm")
     if nm:
         out = subprocess.check_output([nm, "-D", "--defined-only", _abi.LIB_PATH], text=True)
-        exported = set(re.findall(r"\bT (msplat_(?:hip_|trainer_|scene_|dataset_|prepare_cam)\w*)", out))
+        exported = set(re.findall(r"\bT (msplat_(?:hip_|trainer_|scene_|dataset_|undistort_|prepare_cam)\w*)", out))
         assert set(_declared()) <= exported
 
 

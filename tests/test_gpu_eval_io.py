@@ -188,3 +188,24 @@ def test_checkpoint_round_trip(mods, tmp_path):
         bad = tmp_path / "bad.msplat"
         bad.write_bytes(b"\0" * 64)
         tr2.load_checkpoint(bad)
+
+
+def test_evaluate_at_downscaled_resolution(mods):
+    """num_downscales = 2 before the first resolution step: training and
+    evaluation use the target at 1/4 by the reference's area resize
+    (Camera::getImage, input_data.cpp:54-65), here on a 163x117 image that 4
+    does not divide (40x29 cells of 4.075 x 4.034 source pixels)."""
+    _, _, trainer = mods
+    sc = small_scene(n=2000, width=163, height=117, seed_off=613)
+    tg = [target_for(sc, (117, 163), seed_off=614)]
+    cfg = trainer.TrainingConfig(iterations=10, sh_degree=3, sh_degree_interval=0, num_downscales=2,
+                                 warmup_length=10_000, shuffle_cameras=False)
+    tr = trainer.GaussianTrainer(sc.params(), sc.cameras, tg, cfg)
+    tr.step()
+    small = orc.resize_area(tg[0], 163 // 4, 117 // 4)
+    r = tr.render(0)
+    assert r.shape == small.shape
+    m = tr.evaluate(sc.cameras, tg)
+    want = orc.image_metrics(r, small)
+    for k in ("psnr", "ssim", "l1"):
+        assert abs(m[k] - want[k]) <= 1e-5 * max(1.0, abs(want[k])), (k, m[k], want[k])
