@@ -19,8 +19,9 @@
 // mask of the 8x8 wave quadrants it can reach and a wave walks only the
 // entries of its own quadrant; a workgroup-wide vote stops the forward once
 // every pixel of the item has terminated; the backward reduces each
-// gaussian's per-pixel terms across the 64 lanes of a wave with a transposed
-// permlane/DPP reduction and nine lanes issue one float atomic each.
+// gaussian's per-pixel terms across the 64 lanes of a wave (eight of them
+// transposed through LDS, the ninth by DPP) and nine lanes issue one float
+// atomic each.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -107,6 +108,33 @@ __device__ __forceinline__ int quad_mask(float x, float y, float a, float b, flo
         if (inside || e < thr) m |= 1 << q;
     }
     return m;
+}
+
+// LDS row of one reduced value: 64 lane partials plus 4 floats of padding,
+// so that the eight 8-lane groups reading 32-byte pieces of different rows
+// start on different banks.
+constexpr int RED_ROW = 68;
+
+// Sum over the 64 lanes of a wave of eight values per lane, through the
+// wave's own LDS area red[8][RED_ROW]: each lane writes its eight values to
+// red[k][lane], lane l then adds red[l >> 3][8 (l & 7) .. 8 (l & 7) + 7] and
+// the eight lanes of each group combine by DPP (xor 1, xor 2, mirror within
+// 8).  Lane 8k ends with the total of value k.  Only this wave touches red,
+// and a wave's LDS accesses are performed in order, so no barrier is needed;
+// the wave barriers keep the compiler from moving the accesses across each
+// other.  All lanes must be active.
+__device__ __forceinline__ float wave_sum8_lds(const float* v, int lane, float* red) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) red[k * RED_ROW + lane] = v[k];
+    __builtin_amdgcn_wave_barrier();
+    const float4* q = reinterpret_cast<const float4*>(red + (lane >> 3) * RED_ROW + (lane & 7) * 8);
+    const float4 a = q[0], b = q[1];
+    float u = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+    __builtin_amdgcn_wave_barrier();
+    u += dpp<0xB1>(u);     // quad_perm [1,0,3,2]
+    u += dpp<0x4E>(u);     // quad_perm [2,3,0,1]
+    u += dpp<0x141>(u);    // row_half_mirror: lane ^ 7 within each 8 lanes
+    return u;
 }
 
 __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float bg0, float bg1,
@@ -285,6 +313,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     __shared__ float4 s_geo[256];    // x, y, conic a, b
     __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
     __shared__ float4 s_aux[256];    // clamped b, opacity - 1, id, mask (bits)
+    __shared__ float4 s_red4[4 * 8 * RED_ROW / 4];   // per-wave gradient reductions
     __shared__ int s_max;
     const int item = blockIdx.x;
     if (item >= meta->n_items) return;
@@ -299,9 +328,10 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     // bf = cs - 1 for pixels outside the image: no entry passes e_idx <= bf
     int bf = cs - 1;
     unsigned ngrad = 0;     // pairs of this wave that carry a gradient (wave-uniform)
-    // gradient value this lane writes after the reductions: the owner lanes
-    // of the eight transposed sums, lane 63 the ninth; -1 for the others
-    const int kslot = sum8_owner_lane(lane) ? sum8_value_of_lane(lane) : lane == 63 ? 8 : -1;
+    // gradient value this lane writes after the reductions: lane 8k the k-th
+    // of the eight LDS sums, lane 63 the ninth; -1 for the others
+    const int kslot = (lane & 7) == 0 ? lane >> 3 : lane == 63 ? 8 : -1;
+    float* red = reinterpret_cast<float*>(s_red4) + w * 8 * RED_ROW;
     // the entry mask bit that keeps this lane's value (v_rgb channels only)
     const int kbit = kslot >= 5 && kslot <= 7 ? 16 << (kslot - 5) : 0;
     unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
@@ -326,8 +356,9 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     // The colour terms of v_alpha enter only as sum_k v_out_k (...)_k:
     // D = sum_k v_out_k B_k (accumulated colour behind) and TB = sum_k
     // v_out_k T_final bg_k are carried instead of the three channels.
+    // E = D + TB, the two carried together: D changes, TB does not
     const float TB = fmaf(Tfin * bg2, vo2, fmaf(Tfin * bg1, vo1, (Tfin * bg0) * vo0));
-    float D = fmaf(B2, vo2, fmaf(B1, vo1, B0 * vo0));
+    float E = fmaf(B2, vo2, fmaf(B1, vo1, B0 * vo0)) + TB;
     // wave-uniform (readfirstlane): the entry loop indexes then live in scalar registers
     const int wave_bf = __builtin_amdgcn_readfirstlane(wave_max_i(bf));
     if (tid == 0) s_max = cs - 1;
@@ -391,8 +422,8 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 const float fac = grad ? alpha * Tn : 0.f;
                 // v_alpha = sum_k (r_k Tn - (B_k + T_final bg_k) ra) v_out_k
                 const float RV = fmaf(r2, vo2, fmaf(r1, vo1, r0 * vo0));
-                const float v_alpha = fmaf(Tn, RV, -ra * (D + TB));
-                D = fmaf(fac, RV, D);
+                const float v_alpha = fmaf(Tn, RV, -ra * E);
+                E = fmaf(fac, RV, E);
                 T = grad ? Tn : T;
                 // v_sigma of the lanes with a gradient, zero elsewhere
                 const float vsg = grad ? -alpha * v_alpha : 0.f;
@@ -406,7 +437,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 v[5] = fac * vo0;
                 v[6] = fac * vo1;
                 v[7] = fac * vo2;
-                const float u = wave_sum8_transposed(v, lane);
+                const float u = wave_sum8_lds(v, lane, red);
                 // opacity (logit) term -v_sigma (1 - o), total in lane 63
                 const float s8 = wave_sum_to_last(vsg * x.y);
                 if (kslot >= 0 && (kbit == 0 || (__float_as_int(x.w) & kbit)))
