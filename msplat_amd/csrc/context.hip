@@ -1006,13 +1006,35 @@ int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes) {
         *nbytes = N * per * 4;
         if (!dst) return MSPLAT_OK;
         h.resize(N * 9);
+        const bool need_rec = q0 == 0 || q0 == 5;
+        std::vector<float> r(need_rec ? N * 16 : 0);
         if (N) {
             HIP_TRY(hipMemcpyAsync(h.data(), c->gacc.p, N * 36, hipMemcpyDeviceToHost, c->stream));
+            if (need_rec)
+                HIP_TRY(hipMemcpyAsync(r.data(), c->rec.p, N * 64, hipMemcpyDeviceToHost, c->stream));
             HIP_TRY(hipStreamSynchronize(c->stream));
         }
         float* o = static_cast<float*>(dst);
-        for (size_t g = 0; g < N; ++g)
-            for (int k = 0; k < per; ++k) o[g * per + k] = h[g * 9 + q0 + k];
+        for (size_t g = 0; g < N; ++g) {
+            const float* a = &h[g * 9];
+            if (q0 == 0) {
+                // v_xy from the v_sigma moments and the conic (a, b, c) of
+                // the record, as the projection backward forms it; gaussians
+                // without raster gradient (culled: stale record) give 0
+                const float* q = &r[g * 16];
+                const bool any = a[0] != 0.f || a[1] != 0.f;
+                o[2 * g] = any ? std::fma(q[3], a[1], q[2] * a[0]) : 0.f;
+                o[2 * g + 1] = any ? std::fma(q[4], a[1], q[3] * a[0]) : 0.f;
+            } else if (q0 == 2) {
+                for (int k = 0; k < 3; ++k) o[3 * g + k] = 0.5f * a[2 + k];
+            } else if (q0 == 5) {
+                // channels whose raw colour + 0.5 < 0 carry no gradient
+                const float raw[3] = {r[g * 16 + 6], r[g * 16 + 7], r[g * 16 + 8]};
+                for (int k = 0; k < 3; ++k) o[3 * g + k] = raw[k] + 0.5f >= 0.f ? a[5 + k] : 0.f;
+            } else {
+                for (int k = 0; k < per; ++k) o[g * per + k] = a[q0 + k];
+            }
+        }
         return MSPLAT_OK;
     }
     return fail(MSPLAT_ERR_ARG, "unknown intermediate '%s'", name);

@@ -159,9 +159,6 @@ void launch_proj_bwd_adam(hipStream_t s, const CamParams& p, float* const params
                           float* max2d, float inv_max_dim, float* v_mean_out,
                           float* v_scale_out, float* v_quat_out);
 
-void launch_split_gacc(hipStream_t s, int N, const float* gacc, float* v_xy, float* v_conic,
-                       float* v_rgb, float* v_opac);
-
 // Densification.
 struct DensifyHP {
     int N;

@@ -118,6 +118,22 @@ __device__ __forceinline__ void sh_basis15(float x, float y, float z, float* o) 
     o[14] = SH_C3_6 * x * (xx - 3.f * yy);
 }
 
+// v_rgb of gaussian g from its accumulators, each channel kept only where
+// the raw colour + 0.5 >= 0 (rasterize_backward_kernel masks it there,
+// .metal:1083-1086; the mask is the gaussian's, so the raster backward sums
+// every channel and the mask is applied here once).
+__device__ __forceinline__ void masked_vrgb(const float* ga, const float4* rec, size_t g,
+                                            float out[3]) {
+    // loaded unconditionally (a conditional load would be a branch and a
+    // separate memory round trip per channel)
+    const float4 r1 = rec[4 * g + 1];
+    const float rb = rec[4 * g + 2].x;
+    const float v0 = ga[5], v1 = ga[6], v2 = ga[7];
+    out[0] = r1.z + 0.5f >= 0.f ? v0 : 0.f;
+    out[1] = r1.w + 0.5f >= 0.f ? v1 : 0.f;
+    out[2] = rb + 0.5f >= 0.f ? v2 : 0.f;
+}
+
 __global__ __launch_bounds__(SHA_T) void k_sh_rest_adam(int64_t n, int rest_per, int n_used,
                                                         const float4* __restrict__ rec,
                                                         const int* __restrict__ radii,
@@ -141,8 +157,10 @@ __global__ __launch_bounds__(SHA_T) void k_sh_rest_adam(int64_t n, int rest_per,
             sh_basis15(d.x, d.y, d.z, bs);
 #pragma unroll
             for (int b = 0; b < 15; ++b) s_basis[t][b] = bs[b];
+            float vr[3];
+            masked_vrgb(gacc + (size_t)g * 9, rec, (size_t)g, vr);
 #pragma unroll
-            for (int c = 0; c < 3; ++c) s_vrgb[t][c] = gacc[(size_t)g * 9 + 5 + c];
+            for (int c = 0; c < 3; ++c) s_vrgb[t][c] = vr[c];
         }
     }
     __syncthreads();
@@ -248,8 +266,15 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
             dv[c] = P.v[3][3 * (size_t)g + c];
         }
         const float st_vis = vis[g], st_gnorm = gnorm[g], st_max2d = max2d[g];
-        const float vrgb[3] = {ga[5], ga[6], ga[7]};
-        const float vxy0 = ga[0], vxy1 = ga[1];
+        float vrgb[3];
+        masked_vrgb(ga, go.rec, (size_t)g, vrgb);
+        // The raster backward sums the moments of v_sigma over the pixels
+        // (m0 = sum v dx, m1 = sum v dy, m2..m4 = sum v (dx^2, dx dy, dy^2));
+        // with this gaussian's conic (a, b, c) they give v_xy = (a m0 + b m1,
+        // b m0 + c m1) and v_conic = (m2, m3, m4) / 2.
+        const float4 r0 = go.rec[4 * (size_t)g], r1 = go.rec[4 * (size_t)g + 1];
+        const float vxy0 = fmaf(r0.w, ga[1], r0.z * ga[0]);
+        const float vxy1 = fmaf(r1.x, ga[1], r0.w * ga[0]);
         // project_pix_vjp: x/y rows through a fixed 1/w (the w row is dropped).
         {
             const float* m = p.pm;
@@ -268,9 +293,8 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
         // cov2d_to_conic_vjp: v_Sigma = -X G X.
         float vc2[3];
         {
-            const float4 r0 = go.rec[4 * (size_t)g], r1 = go.rec[4 * (size_t)g + 1];
             const float X[2][2] = {{r0.z, r0.w}, {r0.w, r1.x}};
-            const float G[2][2] = {{ga[2], ga[3]}, {ga[3], ga[4]}};
+            const float G[2][2] = {{0.5f * ga[2], 0.5f * ga[3]}, {0.5f * ga[3], 0.5f * ga[4]}};
             float nX[2][2], T1[2][2], S[2][2];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -434,18 +458,6 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
     P.v[5][g] = sv[10];
 }
 
-__global__ __launch_bounds__(256) void k_split_gacc(int N, const float* __restrict__ gacc,
-                                                    float* v_xy, float* v_conic, float* v_rgb,
-                                                    float* v_opac) {
-    const int g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= N) return;
-    const float* a = gacc + (size_t)g * 9;
-    if (v_xy) { v_xy[2 * g] = a[0]; v_xy[2 * g + 1] = a[1]; }
-    if (v_conic) { v_conic[3 * g] = a[2]; v_conic[3 * g + 1] = a[3]; v_conic[3 * g + 2] = a[4]; }
-    if (v_rgb) { v_rgb[3 * g] = a[5]; v_rgb[3 * g + 1] = a[6]; v_rgb[3 * g + 2] = a[7]; }
-    if (v_opac) v_opac[g] = a[8];
-}
-
 }  // namespace
 
 void launch_sh_rest_adam(hipStream_t s, const CamParams& p, const float4* rec, const int* radii,
@@ -471,11 +483,5 @@ void launch_proj_bwd_adam(hipStream_t s, const CamParams& p, float* const params
                        gacc, vis, gnorm, max2d, inv_max_dim, v_mean_out, v_scale_out, v_quat_out);
 }
 
-void launch_split_gacc(hipStream_t s, int N, const float* gacc, float* v_xy, float* v_conic,
-                       float* v_rgb, float* v_opac) {
-    if (N <= 0) return;
-    hipLaunchKernelGGL(k_split_gacc, dim3((N + 255) / 256), dim3(256), 0, s, N, gacc, v_xy,
-                       v_conic, v_rgb, v_opac);
-}
 
 }  // namespace msp

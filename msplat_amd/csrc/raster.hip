@@ -312,7 +312,7 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                                                     unsigned long long* __restrict__ work) {
     __shared__ float4 s_geo[256];    // x, y, conic a, b
     __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
-    __shared__ float4 s_aux[256];    // clamped b, opacity - 1, id, mask (bits)
+    __shared__ float4 s_aux[256];    // clamped b, opacity - 1, accumulator byte offset, mask
     __shared__ float4 s_red4[4 * 8 * RED_ROW / 4];   // per-wave gradient reductions
     __shared__ int s_max;
     const int item = blockIdx.x;
@@ -328,12 +328,12 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     // bf = cs - 1 for pixels outside the image: no entry passes e_idx <= bf
     int bf = cs - 1;
     unsigned ngrad = 0;     // pairs of this wave that carry a gradient (wave-uniform)
-    // gradient value this lane writes after the reductions: lane 8k the k-th
-    // of the eight LDS sums, lane 63 the ninth; -1 for the others
-    const int kslot = (lane & 7) == 0 ? lane >> 3 : lane == 63 ? 8 : -1;
+    // After the reductions lane 8k holds the k-th of the eight LDS sums and
+    // lane 63 the ninth; each adds it at byte kofs of the gaussian's nine
+    // accumulators, all nine in one atomic instruction.
+    const bool own = (lane & 7) == 0 || lane == 63;
+    const uint32_t kofs = lane == 63 ? 32u : (uint32_t)(lane >> 3) * 4u;
     float* red = reinterpret_cast<float*>(s_red4) + w * 8 * RED_ROW;
-    // the entry mask bit that keeps this lane's value (v_rgb channels only)
-    const int kbit = kslot >= 5 && kslot <= 7 ? 16 << (kslot - 5) : 0;
     unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
     if (px.inside) {
         const size_t pix = (size_t)px.i * W + px.j;
@@ -378,12 +378,10 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
             float4 c = r[1];
             const float braw = r[2].x;
             mask = quad_mask(g.x, g.y, g.z, g.w, c.x, c.y, tx0, ty0);
-            // bits 4..6: the channel's raw colour + 0.5 >= 0 (its v_rgb is kept)
-            mask |= (c.z + 0.5f >= 0.f ? 16 : 0) | (c.w + 0.5f >= 0.f ? 32 : 0) |
-                    (braw + 0.5f >= 0.f ? 64 : 0);
             s_geo[tid] = g;
             s_col[tid] = make_float4(c.x, c.y, fmaxf(c.z + 0.5f, 0.f), fmaxf(c.w + 0.5f, 0.f));
-            s_aux[tid] = make_float4(fmaxf(braw + 0.5f, 0.f), c.y - 1.f, __int_as_float(gid),
+            // z: byte offset of the gaussian's accumulators (N * 36 < 2^31)
+            s_aux[tid] = make_float4(fmaxf(braw + 0.5f, 0.f), c.y - 1.f, __int_as_float(gid * 36),
                                      __int_as_float(mask));
         } else {
             s_aux[tid].w = __int_as_float(0);
@@ -400,8 +398,13 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
             while (m) {
                 const int qq = ch + __builtin_ctzll(m);
                 m &= m - 1;
-                const float4 g = s_geo[qq];
-                const float4 c = s_col[qq];
+                // the entry index in a VGPR once, so that every LDS read of
+                // this step uses it (instead of a copy from the SGPR each)
+                int qb = qq * (int)sizeof(float4);
+                asm volatile("" : "+v"(qb));
+                const float4 g = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_geo) + qb);
+                const float4 c = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_col) + qb);
+                const float4 x = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_aux) + qb);
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
                 const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
@@ -414,7 +417,6 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 const uint64_t gmask = vmask & mask_lt(alpha, 0.999f);
                 const bool grad = lane_of(gmask);
                 ngrad += (unsigned)__popcll(gmask);
-                const float4 x = s_aux[qq];
                 const float r0 = c.z, r1 = c.w, r2 = x.x;   // max(raw + 0.5, 0)
                 // hardware reciprocal (1 ulp): the backward is compared with a tolerance
                 const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
@@ -427,21 +429,29 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 T = grad ? Tn : T;
                 // v_sigma of the lanes with a gradient, zero elsewhere
                 const float vsg = grad ? -alpha * v_alpha : 0.f;
-                const float hv = 0.5f * vsg;
+                // v_xy = v_sigma (a dx + b dy, b dx + c dy) and v_conic =
+                // v_sigma / 2 (dx^2, dx dy, dy^2) are linear in the moments
+                // below with the gaussian's own conic, the same in every
+                // tile: the moments are summed, the projection backward
+                // applies the conic once per gaussian.
+                const float w0 = vsg * dx, w1 = vsg * dy;
                 float v[8];
-                v[0] = vsg * fmaf(g.z, dx, g.w * dy);
-                v[1] = vsg * fmaf(g.w, dx, c.x * dy);
-                v[2] = hv * (dx * dx);
-                v[3] = hv * (dx * dy);
-                v[4] = hv * (dy * dy);
+                v[0] = w0;
+                v[1] = w1;
+                v[2] = w0 * dx;
+                v[3] = w0 * dy;
+                v[4] = w1 * dy;
                 v[5] = fac * vo0;
                 v[6] = fac * vo1;
                 v[7] = fac * vo2;
                 const float u = wave_sum8_lds(v, lane, red);
                 // opacity (logit) term -v_sigma (1 - o), total in lane 63
                 const float s8 = wave_sum_to_last(vsg * x.y);
-                if (kslot >= 0 && (kbit == 0 || (__float_as_int(x.w) & kbit)))
-                    atomicAdd(&gacc[(size_t)__float_as_int(x.z) * 9 + kslot], kslot == 8 ? s8 : u);
+                // v_rgb of a channel whose raw colour + 0.5 < 0 is dropped by
+                // its consumers (the mask is per gaussian, not per pixel)
+                float* ap = reinterpret_cast<float*>(reinterpret_cast<char*>(gacc) +
+                                                     ((uint32_t)__float_as_int(x.z) + kofs));
+                if (own) atomicAdd(ap, lane == 63 ? s8 : u);
             }
         }
     }
