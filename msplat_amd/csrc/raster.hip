@@ -110,6 +110,12 @@ __device__ __forceinline__ int quad_mask(float x, float y, float a, float b, flo
     return m;
 }
 
+// Entry record at byte offset qb of an LDS array of float4.
+__device__ __forceinline__ float4 lds_f4(const float4* base, int qb) {
+    return *static_cast<const float4*>(
+        __builtin_assume_aligned(reinterpret_cast<const char*>(base) + qb, 16));
+}
+
 // LDS row of one reduced value: 64 lane partials plus 4 floats of padding,
 // so that the eight 8-lane groups reading 32-byte pieces of different rows
 // start on different banks.
@@ -190,11 +196,12 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
             while (m) {
                 const int qq = ch + __builtin_ctzll(m);
                 m &= m - 1;
-                // Branch-free per lane: a pair that is skipped, stops the pixel
-                // or composites only selects what it writes (colour sums get
-                // + c * 0 when not compositing, which leaves them unchanged).
-                const float4 g = s_geo[qq];
-                const float4 c = s_col[qq];
+                // the entry's byte offset in a VGPR once, for all its LDS reads
+                int qb = qq * (int)sizeof(float4);
+                asm volatile("" : "+v"(qb));
+                const float4 g = lds_f4(s_geo, qb);
+                const float4 c = lds_f4(s_col, qb);
+                const float cb = lds_f4(s_aux, qb).x;
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
                 const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
@@ -204,14 +211,20 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
                 const float nT = T * (1.f - alpha);
                 const uint64_t sm = hm & mask_le(nT, 1e-4f);     // stops here
                 const uint64_t cm = hm & ~sm;                    // composites
-                const bool comp = lane_of(cm);
-                const float vis = comp ? alpha * T : 0.f;
-                C0 = fmaf(c.z, vis, C0);
-                C1 = fmaf(c.w, vis, C1);
-                C2 = fmaf(s_aux[qq].x, vis, C2);
-                T = comp ? nT : T;
-                last = comp ? b + qq : last;
                 ncomp += (unsigned)__popcll(cm);
+                // the colour reads complete behind the exp above, not inside
+                // the update block
+                asm volatile("" ::"v"(c.z), "v"(c.w), "v"(cb));
+                // only the compositing lanes execute the update (an exec-masked
+                // block: no per-lane selects)
+                if (lane_of(cm)) {
+                    const float vis = alpha * T;
+                    C0 = fmaf(c.z, vis, C0);
+                    C1 = fmaf(c.w, vis, C1);
+                    C2 = fmaf(cb, vis, C2);
+                    T = nT;
+                    last = b + qq;
+                }
                 if (sm) {      // at most once per pixel
                     if (lane_of(sm)) last = b + qq - 1;
                     live &= ~sm;
@@ -402,9 +415,9 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
                 // this step uses it (instead of a copy from the SGPR each)
                 int qb = qq * (int)sizeof(float4);
                 asm volatile("" : "+v"(qb));
-                const float4 g = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_geo) + qb);
-                const float4 c = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_col) + qb);
-                const float4 x = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(s_aux) + qb);
+                const float4 g = lds_f4(s_geo, qb);
+                const float4 c = lds_f4(s_col, qb);
+                const float4 x = lds_f4(s_aux, qb);
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
                 const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
