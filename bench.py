@@ -116,11 +116,12 @@ def cpu_baseline(params_dev, cams, targets, degree, bg, n_steps):
     return n_steps / dt, int(orc.lib().orc_num_threads()), dt
 
 
-def rocprof_summary(d: str, last: int, command: str) -> str:
+def rocprof_summary(d: str, first: int, count: int, command: str) -> str:
     """Markdown summary of a `rocprofv3 --kernel-trace --stats -f csv` output
     directory: kernels by total time, and the raster backward's average
-    duration over all its dispatches and over the last `last` (the timed
-    train steps of a default run, which end with no further backward)."""
+    duration over all its dispatches and over dispatches [first, first +
+    count) (in a default run: after the warmup steps, the timed train
+    steps)."""
     import csv
     import glob
     import re
@@ -143,9 +144,10 @@ def rocprof_summary(d: str, last: int, command: str) -> str:
     tr.sort(key=lambda r: int(r["Start_Timestamp"]))
     dur = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in tr]
     if dur:
-        tail = dur[-last:] if last > 0 else dur
+        sel = dur[first:first + count] if count > 0 else dur
         out += ["", f"k_raster_bwd: {len(dur)} dispatches, average {sum(dur) / len(dur):.1f} us; "
-                    f"last {len(tail)} dispatches (the timed steps) average {sum(tail) / len(tail):.1f} us"]
+                    f"dispatches {first}..{first + len(sel) - 1} (the timed steps) average "
+                    f"{sum(sel) / max(len(sel), 1):.1f} us"]
     return "\n".join(out) + "\n"
 
 
@@ -338,6 +340,9 @@ def main():
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--frames", type=int, default=200)
+    ap.add_argument("--train-only", action="store_true",
+                    help="stop after the timed train steps (counter runs: the timed steps are then "
+                         "the last dispatches of every train kernel)")
     ap.add_argument("--stage-steps", type=int, default=60,
                     help="untimed steps / frames with every stage bracketed, for the per-stage breakdown")
     ap.add_argument("--n", type=int, default=1_500_000)
@@ -367,7 +372,7 @@ def main():
         print(json.dumps(res[kernels[0]] if len(kernels) == 1 else res, indent=1))
         return
     if args.rocprof_summary:
-        print(rocprof_summary(args.rocprof_summary, args.steps, args.rocprof_command), end="")
+        print(rocprof_summary(args.rocprof_summary, args.warmup, args.steps, args.rocprof_command), end="")
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -429,6 +434,10 @@ def main():
     train_s = t1 - t0
     its = args.steps / train_s
     log(f"train: {args.steps} steps in {train_s:.3f}s = {its:.1f} it/s; gaussians {n_start} -> {tr.splat_count()}")
+    if args.train_only:
+        print(json.dumps({"metric": METRIC, "value": its, "unit": "it/s", "steps": args.steps,
+                          "warmup": args.warmup, "train_only": True}), flush=True)
+        return
     # Per-stage breakdown: further steps with every stage bracketed.
     _abi.check(lib.msplat_hip_set_stage_timing_mask(0xFFFFFFFF))
     _abi.check(lib.msplat_hip_enable_stage_timing(1))
