@@ -54,20 +54,35 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
     const int tr = threadIdx.x, lx = tr % FX, ly = tr / FX;
     const int bx = blockIdx.x * FX - HALF, by = blockIdx.y * FY - HALF;
     float ssim_sum = 0.f, l1_sum = 0.f, cnt = 0.f;
+    // The three channels of this thread's input pixels (rows by .. by+25,
+    // columns bx-5 .. bx+46, zero outside the image) are loaded once, into
+    // registers; each channel pass copies its component into LDS.
+    constexpr int NPOS = (FHY * FIN + FT - 1) / FT;
+    float rg[NPOS][3], rr[NPOS][3];
+#pragma unroll
+    for (int k = 0; k < NPOS; ++k) {
+        const int i = tr + k * FT;
+        const int sy = i / FIN, sx = i - sy * FIN;
+        const int gy = by + sy, gx = bx - HALF + sx;
+        const bool in = i < FHY * FIN && gx >= 0 && gx < W && gy >= 0 && gy < H;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const size_t q = ((size_t)gy * W + gx) * 3 + c;
+            rg[k][c] = in ? gt[q] : 0.f;
+            rr[k][c] = in ? img[q] : 0.f;
+        }
+    }
+#pragma unroll
     for (int c = 0; c < 3; ++c) {
         if (c > 0) __syncthreads();
-        // channel c of rows by .. by+25, columns bx-5 .. bx+46 (zero outside)
-        for (int i = tr; i < FHY * FIN; i += FT) {
-            const int sy = i / FIN, sx = i - sy * FIN;
-            const int gy = by + sy, gx = bx - HALF + sx;
-            float gv = 0.f, rv = 0.f;
-            if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
-                const size_t q = ((size_t)gy * W + gx) * 3 + c;
-                gv = gt[q];
-                rv = img[q];
+#pragma unroll
+        for (int k = 0; k < NPOS; ++k) {
+            const int i = tr + k * FT;
+            if (i < FHY * FIN) {
+                const int sy = i / FIN, sx = i - sy * FIN;
+                s_in[0][sy][sx] = rg[k][c];
+                s_in[1][sy][sx] = rr[k][c];
             }
-            s_in[0][sy][sx] = gv;
-            s_in[1][sy][sx] = rv;
         }
         __syncthreads();
         // horizontal zero-padded sums (ssim_h_fwd, .metal:3053-3115) at the
