@@ -272,19 +272,42 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
     if (i >= H || j >= W) return;
     float Tr = 1.f, R0 = 0.f, R1 = 0.f, R2 = 0.f;
     int li = -1, cutoff = K;
-    for (int k = 0; k < K; ++k) {
-        const size_t o = (size_t)(i0 + k) * TILE_PIX + lp;
-        const int cf = cb.cidx[o];
-        if (cf < 0 && k > 0) break;
-        const float cT = cb.cT[o];
-        R0 = fmaf(cb.cC[3 * o + 0], Tr, R0);
-        R1 = fmaf(cb.cC[3 * o + 1], Tr, R1);
-        R2 = fmaf(cb.cC[3 * o + 2], Tr, R2);
-        Tr *= cT;
-        if (cf >= 0) li = cf;
-        if (Tr <= 1e-4f) {
-            cutoff = k + 1;
-            break;
+    // Chunks are folded front to back, stopping at an empty chunk or once
+    // T <= 1e-4.  The state of MG chunks is loaded ahead of folding them
+    // (every k < K is a valid chunk), so a tile with hundreds of chunks
+    // costs one memory round trip per MG chunks instead of two per chunk.
+    constexpr int MG = 8;
+    bool done = false;
+    for (int k0 = 0; k0 < K && !done; k0 += MG) {
+        int cf[MG];
+        float cT[MG], c0[MG], c1[MG], c2[MG];
+#pragma unroll
+        for (int u = 0; u < MG; ++u) {
+            const int k = min(k0 + u, K - 1);
+            const size_t o = (size_t)(i0 + k) * TILE_PIX + lp;
+            cf[u] = cb.cidx[o];
+            cT[u] = cb.cT[o];
+            c0[u] = cb.cC[3 * o + 0];
+            c1[u] = cb.cC[3 * o + 1];
+            c2[u] = cb.cC[3 * o + 2];
+        }
+#pragma unroll
+        for (int u = 0; u < MG; ++u) {
+            const int k = k0 + u;
+            if (k >= K || (cf[u] < 0 && k > 0)) {
+                done = true;
+                break;
+            }
+            R0 = fmaf(c0[u], Tr, R0);
+            R1 = fmaf(c1[u], Tr, R1);
+            R2 = fmaf(c2[u], Tr, R2);
+            Tr *= cT[u];
+            if (cf[u] >= 0) li = cf[u];
+            if (Tr <= 1e-4f) {
+                cutoff = k + 1;
+                done = true;
+                break;
+            }
         }
     }
     for (int k = cutoff; k < K; ++k) cb.cidx[(size_t)(i0 + k) * TILE_PIX + lp] = -1;
@@ -295,22 +318,43 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
     out_img[3 * pix + 1] = clamp01(fmaf(bg1, Tr, R1));
     out_img[3 * pix + 2] = clamp01(fmaf(bg2, Tr, R2));
     if (!with_suffix) return;
+    // prefix products of T and suffix sums of the chunk colours, each over
+    // all K chunks, with the loads of MG chunks issued ahead of their stores
     float pT = 1.f;
-    for (int k = 0; k < K; ++k) {
-        const size_t o = (size_t)(i0 + k) * TILE_PIX + lp;
-        cb.pT[o] = pT;
-        pT *= cb.cT[o];
+    for (int k0 = 0; k0 < K; k0 += MG) {
+        float t[MG];
+#pragma unroll
+        for (int u = 0; u < MG; ++u)
+            t[u] = cb.cT[(size_t)(i0 + min(k0 + u, K - 1)) * TILE_PIX + lp];
+#pragma unroll
+        for (int u = 0; u < MG; ++u) {
+            if (k0 + u >= K) break;
+            cb.pT[(size_t)(i0 + k0 + u) * TILE_PIX + lp] = pT;
+            pT *= t[u];
+        }
     }
     float a0 = 0.f, a1 = 0.f, a2 = 0.f;
-    for (int k = K - 1; k >= 0; --k) {
-        const size_t o = (size_t)(i0 + k) * TILE_PIX + lp;
-        cb.aC[3 * o + 0] = a0;
-        cb.aC[3 * o + 1] = a1;
-        cb.aC[3 * o + 2] = a2;
-        const float p = cb.pT[o];
-        a0 += p * cb.cC[3 * o + 0];
-        a1 += p * cb.cC[3 * o + 1];
-        a2 += p * cb.cC[3 * o + 2];
+    for (int k1 = K - 1; k1 >= 0; k1 -= MG) {
+        float pp[MG], q0[MG], q1[MG], q2[MG];
+#pragma unroll
+        for (int u = 0; u < MG; ++u) {
+            const size_t o = (size_t)(i0 + max(k1 - u, 0)) * TILE_PIX + lp;
+            pp[u] = cb.pT[o];
+            q0[u] = cb.cC[3 * o + 0];
+            q1[u] = cb.cC[3 * o + 1];
+            q2[u] = cb.cC[3 * o + 2];
+        }
+#pragma unroll
+        for (int u = 0; u < MG; ++u) {
+            if (k1 - u < 0) break;
+            const size_t o = (size_t)(i0 + k1 - u) * TILE_PIX + lp;
+            cb.aC[3 * o + 0] = a0;
+            cb.aC[3 * o + 1] = a1;
+            cb.aC[3 * o + 2] = a2;
+            a0 += pp[u] * q0[u];
+            a1 += pp[u] * q1[u];
+            a2 += pp[u] * q2[u];
+        }
     }
 }
 
