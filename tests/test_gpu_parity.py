@@ -190,6 +190,53 @@ def test_raster_counters_match_work(dev):
         torch.cuda.synchronize()
 
 
+def _drain_stages(dev):
+    import ctypes
+    lib = dev.init()
+    ms = (ctypes.c_double * 16)()
+    cnt = (ctypes.c_int64 * 16)()
+    names = (ctypes.c_char_p * 16)()
+    n, calls = ctypes.c_int(0), ctypes.c_int64(0)
+    dev._abi.check(lib.msplat_hip_drain_stage_times(ms, cnt, names, 16, ctypes.byref(n), ctypes.byref(calls)))
+    return {names[i].decode(): (ms[i], cnt[i]) for i in range(n.value)}
+
+
+def test_stage_timing_mask(dev):
+    """msplat_hip_set_stage_timing_mask: only the selected stages are timed
+    (one bracketing pair of events each), all eight with the full mask; the
+    step's results do not depend on what is timed."""
+    sc = small_scene(n=3000, seed_off=86)
+    su = camera.prepare_cam(sc.cameras[0])
+    gt = dev.to_dev(target_for(sc, (su.height, su.width)))
+    lib = dev.init()
+    outs = []
+    try:
+        for mask in (1 << 5, 0xFFFFFFFF, (1 << 0) | (1 << 3) | (1 << 7)):
+            g = dev.DeviceGaussians.from_arrays(sc.params(), 3, capacity=sc.n)
+            dev._abi.check(lib.msplat_hip_set_stage_timing_mask(mask))
+            dev._abi.check(lib.msplat_hip_enable_stage_timing(1))
+            dev.train_step(g, su, 3, BG, gt, 0.2, LRS, 1)
+            dev.train_step(g, su, 3, BG, gt, 0.2, LRS, 2)
+            dev.sync()
+            st = _drain_stages(dev)
+            timed = {k for k, (ms, c) in st.items() if c}
+            want = {k for i, k in enumerate(STAGE_NAMES) if (mask >> i) & 1}
+            assert timed == want, (hex(mask), timed)
+            assert all(st[k][1] == 2 and st[k][0] > 0 for k in want)
+            outs.append([b[: sc.n].cpu().numpy().copy() for b in g.bufs])
+    finally:
+        dev._abi.check(lib.msplat_hip_set_stage_timing_mask(0xFFFFFFFF))
+        dev._abi.check(lib.msplat_hip_enable_stage_timing(0))
+        dev.drain_raster_counters()
+    for o in outs[1:]:
+        for x, y in zip(outs[0], o):
+            assert np.allclose(x, y, rtol=1e-4, atol=1e-6)
+
+
+STAGE_NAMES = ["proj_sh_fwd", "depth_sort", "tile_lists", "rast_fwd", "loss_fwd_bwd", "rast_bwd",
+               "sh_rest_adam", "proj_sh_bwd_adam"]
+
+
 def test_train_three_steps(dev):
     """Adam state carried over three steps (bias corrections t = 1, 2, 3)."""
     _train_compare(dev, small_scene(n=2000, seed_off=83), steps=3, check_grads=False)
