@@ -116,25 +116,28 @@ __device__ __forceinline__ float4 lds_f4(const float4* base, int qb) {
         __builtin_assume_aligned(reinterpret_cast<const char*>(base) + qb, 16));
 }
 
-// LDS row of one reduced value: 64 lane partials plus 4 floats of padding,
-// so that the eight 8-lane groups reading 32-byte pieces of different rows
-// start on different banks.
-constexpr int RED_ROW = 68;
+// LDS row of one reduced value: the 64 lane partials.  The 8-lane groups of
+// odd rows read their two 16-byte halves in the opposite order, so that the
+// two groups served in the same LDS cycle (rows 2p and 2p + 1) read
+// disjoint banks.
+constexpr int RED_ROW = 64;
 
 // Sum over the 64 lanes of a wave of eight values per lane, through the
 // wave's own LDS area red[8][RED_ROW]: each lane writes its eight values to
-// red[k][lane], lane l then adds red[l >> 3][8 (l & 7) .. 8 (l & 7) + 7] and
-// the eight lanes of each group combine by DPP (xor 1, xor 2, mirror within
-// 8).  Lane 8k ends with the total of value k.  Only this wave touches red,
-// and a wave's LDS accesses are performed in order, so no barrier is needed;
-// the wave barriers keep the compiler from moving the accesses across each
-// other.  All lanes must be active.
+// row k, lane l then adds the eight partials 8 (l & 7) .. 8 (l & 7) + 7 of
+// row l >> 3 and the eight lanes of each group combine by DPP (xor 1, xor 2,
+// mirror within 8).  Lane 8k ends with the total of value k.  Only this wave
+// touches red, and a wave's LDS accesses are performed in order, so no
+// barrier is needed; the wave barriers keep the compiler from moving the
+// accesses across each other.  All lanes must be active.
 __device__ __forceinline__ float wave_sum8_lds(const float* v, int lane, float* red) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) red[k * RED_ROW + lane] = v[k];
     __builtin_amdgcn_wave_barrier();
-    const float4* q = reinterpret_cast<const float4*>(red + (lane >> 3) * RED_ROW + (lane & 7) * 8);
-    const float4 a = q[0], b = q[1];
+    const int g = lane >> 3, h = (g & 1) << 2;
+    const float* rb = red + g * RED_ROW + (lane & 7) * 8;
+    const float4 a = *reinterpret_cast<const float4*>(rb + h);
+    const float4 b = *reinterpret_cast<const float4*>(rb + (h ^ 4));
     float u = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
     __builtin_amdgcn_wave_barrier();
     u += dpp<0xB1>(u);     // quad_perm [1,0,3,2]
@@ -358,7 +361,7 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
     }
 }
 
-__global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float bg0, float bg1,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k_raster_bwd(int W, int H, int tbx, float bg0, float bg1,
                                                     float bg2, const Meta* __restrict__ meta,
                                                     Items it,
                                                     const int* __restrict__ tile_bins, Entries pk,
@@ -370,8 +373,10 @@ __global__ __launch_bounds__(256) void k_raster_bwd(int W, int H, int tbx, float
     __shared__ float4 s_geo[256];    // x, y, conic a, b
     __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
     __shared__ float4 s_aux[256];    // clamped b, opacity - 1, accumulator byte offset, mask
-    __shared__ float4 s_red4[4 * 8 * RED_ROW / 4];   // per-wave gradient reductions
-    __shared__ int s_max;
+    // per-wave gradient reductions; its first word holds the workgroup's
+    // largest final index before the entry loop uses the area
+    __shared__ float4 s_red4[4 * 8 * RED_ROW / 4];
+    int& s_max = *reinterpret_cast<int*>(s_red4);
     const int item = blockIdx.x;
     if (item >= meta->n_items) return;
     int t, K, cs, ce;
