@@ -171,7 +171,7 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
 
     float T = 1.f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
     int last = cs - 1;
-    unsigned ncomp = 0;     // pairs composited by this wave (wave-uniform)
+    unsigned ncl = 0;       // pairs composited by this lane
     unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
     // lanes whose pixel is still compositing (wave-uniform lane mask)
     uint64_t live = wave_ballot(px.inside);
@@ -197,8 +197,9 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
             uint64_t m = wave_ballot(q < nb && ((__float_as_int(s_aux[q].y) >> w) & 1));
             nwit += __popcll(m);
             while (m) {
-                const int qq = ch + __builtin_ctzll(m);
-                m &= m - 1;
+                const int bit = __builtin_ctzll(m);
+                const int qq = ch + bit;
+                m &= ~(1ull << bit);
                 // the entry's byte offset in a VGPR once, for all its LDS reads
                 int qb = qq * (int)sizeof(float4);
                 asm volatile("" : "+v"(qb));
@@ -214,7 +215,6 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
                 const float nT = T * (1.f - alpha);
                 const uint64_t sm = hm & mask_le(nT, 1e-4f);     // stops here
                 const uint64_t cm = hm & ~sm;                    // composites
-                ncomp += (unsigned)__popcll(cm);
                 // the colour reads complete behind the exp above, not inside
                 // the update block
                 asm volatile("" ::"v"(c.z), "v"(c.w), "v"(cb));
@@ -227,6 +227,7 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
                     C2 = fmaf(cb, vis, C2);
                     T = nT;
                     last = b + qq;
+                    ++ncl;
                 }
                 if (sm) {      // at most once per pixel
                     if (lane_of(sm)) last = b + qq - 1;
@@ -238,6 +239,8 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
     }
     if (work) {
         unsigned long long* ws = work_slot(work);
+        unsigned ncomp = ncl;
+        for (int off = 32; off >= 1; off >>= 1) ncomp += __shfl_xor(ncomp, off, 64);
         if (lane == 0 && ncomp) atomicAdd(ws, (unsigned long long)ncomp);
         if (lane == 0 && nwit) atomicAdd(ws + 2, (unsigned long long)nwit);
     }
