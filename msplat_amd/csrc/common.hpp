@@ -141,47 +141,6 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
-// Transposed sum over the 64 lanes of eight values v[0..7]: afterwards lane l
-// holds the total of value  4 * ((l >> 2) & 1) + {0, 2, 1, 3}[l >> 4].
-// Halves and rows are exchanged with gfx950's permlane32/16 swaps, the rest
-// with row DPP; 18 VALU operations for the eight sums.  All lanes must be
-// active.
-__device__ __forceinline__ float swap_add32(float a, float b) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float swap_add16(float a, float b) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float wave_sum8_transposed(const float* v, int lane) {
-    const float r0 = swap_add32(v[0], v[1]);
-    const float r1 = swap_add32(v[2], v[3]);
-    const float r2 = swap_add32(v[4], v[5]);
-    const float r3 = swap_add32(v[6], v[7]);
-    // s0 holds values {0,2,1,3}[row] summed over the four rows, s1 {4,6,5,7}
-    const float s0 = swap_add16(r0, r1);
-    const float s1 = swap_add16(r2, r3);
-    // Lane l keeps the set of its bit 2 and receives that set's partial from
-    // lane (l - 4) mod 16 (row_ror:4), whose bit 2 is the opposite one; the
-    // two lanes plus the xor-1/2/8 partners below cover the 16 lanes once.
-    const bool hi = (lane & 4) != 0;
-    const float keep = hi ? s1 : s0;
-    const float send = hi ? s0 : s1;
-    float u = keep + dpp<0x124>(send);      // row_ror:4
-    u += dpp<0xB1>(u);                      // quad_perm [1,0,3,2]
-    u += dpp<0x4E>(u);                      // quad_perm [2,3,0,1]
-    u += dpp<0x128>(u);                     // row_ror:8 == lane ^ 8
-    return u;
-}
-// Value index held by lane l after wave_sum8_transposed; the eight lanes with
-// bits 0, 1 and 3 clear hold the eight distinct totals.
-__device__ __forceinline__ int sum8_value_of_lane(int lane) {
-    const int row = lane >> 4;
-    return 4 * ((lane >> 2) & 1) + (row == 1 ? 2 : row == 2 ? 1 : row);
-}
-__device__ __forceinline__ bool sum8_owner_lane(int lane) { return (lane & 11) == 0; }
-
 // Sum over the 64 lanes, total in lane 63: row sums by row DPP, then the
 // gfx9 row_bcast:15 / row_bcast:31 adds carry rows 0..2 into row 3 (rows
 // outside the row mask keep their value).  The two masked adds are written
@@ -201,18 +160,6 @@ __device__ __forceinline__ float wave_sum_to_last(float v) {
         "v_add_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
         "s_nop 1"
         : "+v"(v));
-    return v;
-}
-
-// Sum over the 64 lanes with the total in every lane, without lane reads:
-// half and row swaps, then four row DPP steps.  All lanes must be active.
-__device__ __forceinline__ float wave_sum_bcast(float v) {
-    v = swap_add32(v, v);
-    v = swap_add16(v, v);
-    v += dpp<0xB1>(v);
-    v += dpp<0x4E>(v);
-    v += dpp<0x124>(v);
-    v += dpp<0x128>(v);
     return v;
 }
 
