@@ -571,13 +571,17 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
     hp.b2 = a->adam_beta2;
     hp.eps = a->adam_eps;
     GaussOut go = gauss_out(c);
-    stage_mark(c, S_SHADAM);
-    launch_sh_rest_adam(c->stream, p, go.rec, go.radii, P<float>(c->gacc), a->adam_params[4],
-                        a->adam_exp_avg[4], a->adam_exp_avg_sq[4], hp);
+    // The two Adam kernels are independent (same inputs, disjoint outputs).
+    // The projection backward runs first, right after the raster backward,
+    // while the records and accumulators it gathers are still in cache; the
+    // streaming f_rest Adam loses less by going second.
     stage_mark(c, S_PBWD);
     launch_proj_bwd_adam(c->stream, p, a->adam_params, a->adam_exp_avg, a->adam_exp_avg_sq, hp, go,
                          P<float>(c->gacc), a->vis_counts, a->xys_grad_norm, a->max_2d_size,
                          a->inv_max_dim, a->v_mean3d_out, a->v_scale_out, a->v_quat_out);
+    stage_mark(c, S_SHADAM);
+    launch_sh_rest_adam(c->stream, p, go.rec, go.radii, P<float>(c->gacc), a->adam_params[4],
+                        a->adam_exp_avg[4], a->adam_exp_avg_sq[4], hp);
     stage_mark(c, S_END);
     c->have_bwd = true;
     if (radii_out && p.N > 0)
