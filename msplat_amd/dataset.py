@@ -17,7 +17,15 @@ from .camera import Camera
 
 
 class Dataset:
-    def __init__(self, path: str, image_dir: Optional[str] = None):
+    """A COLMAP dataset.  downscale_factor is the load-time image downscale
+    of load_image; with eval_mode every test_every-th camera is held out
+    (num_train / num_test as the reference's Dataset, python/bindings.cpp)."""
+
+    def __init__(self, path: str, image_dir: Optional[str] = None, downscale_factor: float = 1.0,
+                 eval_mode: bool = False, test_every: int = 8):
+        self.downscale_factor = float(downscale_factor)
+        self.eval_mode = bool(eval_mode)
+        self.test_every = int(test_every)
         self._lib = _abi.load()
         self._h = self._lib.msplat_dataset_create(str(path).encode(),
                                                   str(image_dir).encode() if image_dir else None)
@@ -56,11 +64,21 @@ class Dataset:
         _abi.check(self._lib.msplat_dataset_normalisation(self._h, ctypes.byref(s), t))
         return float(s.value), np.array(t[:], np.float32)
 
-    def load_image(self, i: int, downscale: float = 1.0):
-        """Camera i's image decoded, downscaled and undistorted on the GPU
-        (Camera::loadImage): (updated camera, CUDA (H, W, 3) float32)."""
+    def load_image(self, i: int, downscale: Optional[float] = None):
+        """Camera i's image decoded, downscaled (default: the dataset's
+        downscale_factor) and undistorted on the GPU (Camera::loadImage):
+        (updated camera, CUDA (H, W, 3) float32)."""
         from .image_io import load_camera_image
-        return load_camera_image(self.image_paths[i], self.cameras[i], self.distortion[i], downscale)
+        ds = self.downscale_factor if downscale is None else downscale
+        return load_camera_image(self.image_paths[i], self.cameras[i], self.distortion[i], ds)
+
+    @property
+    def num_test(self) -> int:
+        return len(self.split_train_test(self.test_every)[1]) if self.eval_mode else 0
+
+    @property
+    def num_train(self) -> int:
+        return len(self.cameras) - self.num_test
 
     def split_train_test(self, test_every: int = 8):
         """InputData::splitTrainTest (input_data.cpp:148-158): every test_every-th camera is a test camera."""

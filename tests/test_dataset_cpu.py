@@ -175,3 +175,25 @@ def test_missing_model_raises(tmp_path):
     ds_mod = _lib_or_skip()
     with pytest.raises(_abi.MsplatError, match="Cannot open"):
         ds_mod.Dataset(str(tmp_path))
+
+
+def test_package_names_and_config_defaults(tmp_path):
+    """The reference module's top-level names and TrainingConfig defaults
+    (tests/test_msplat.py:15-52 of the reference), and load_dataset's
+    train / test split (num_test 0 unless eval_mode)."""
+    import msplat_amd as msplat
+    for name in ("GaussianTrainer", "TrainingConfig", "TrainingStats", "Dataset", "load_dataset",
+                 "sync", "cleanup"):
+        assert hasattr(msplat, name), name
+    cfg = msplat.TrainingConfig()
+    assert cfg.iterations == 30000 and cfg.sh_degree == 3 and cfg.refine_every == 100
+    assert cfg.warmup_length == 500 and abs(cfg.ssim_weight - 0.2) < 1e-9
+    cfg = msplat.TrainingConfig(iterations=100, sh_degree=1, ssim_weight=0.0)
+    assert (cfg.iterations, cfg.sh_degree, cfg.ssim_weight) == (100, 1, 0.0)
+    cfg.iterations = 500
+    assert cfg.iterations == 500
+    _write_model(str(tmp_path), n_points=200, seed=5)
+    ds = msplat.load_dataset(str(tmp_path))
+    assert ds.num_test == 0 and ds.num_train == len(ds.cameras)
+    ds = msplat.load_dataset(str(tmp_path), eval_mode=True, test_every=2)
+    assert ds.num_test == len(ds.cameras[::2]) and ds.num_train + ds.num_test == len(ds.cameras)
