@@ -91,7 +91,23 @@ class GaussianTrainer:
     tensors; targets: one (H,W,3) float32 image per camera (numpy or CUDA).
     """
 
-    def __init__(self, params, cameras: List[Camera], targets, cfg: Optional[TrainingConfig] = None):
+    def __init__(self, params, cameras=None, targets=None, cfg: Optional[TrainingConfig] = None):
+        self._dataset = None
+        if hasattr(params, "init_gaussians") and hasattr(params, "load_image"):
+            # GaussianTrainer(dataset, config) as in the reference module
+            # (python/bindings.cpp:113-167): the training cameras' images are
+            # decoded and prepared on the GPU, the gaussians start from the
+            # point cloud.
+            ds = params
+            cfg = cameras if isinstance(cameras, TrainingConfig) else cfg
+            cfg = cfg or TrainingConfig()
+            test = set(range(0, len(ds.cameras), ds.test_every)) if ds.eval_mode else set()
+            loaded = [ds.load_image(i) for i in range(len(ds.cameras)) if i not in test]
+            cameras, targets = [c for c, _ in loaded], [im for _, im in loaded]
+            params = [device.to_dev(a) for a in ds.init_gaussians(cfg.sh_degree)]
+            self._dataset = ds
+        if cameras is None or targets is None:
+            raise ValueError("cameras and targets are needed (or a Dataset)")
         self.config = cfg or TrainingConfig()
         self.cameras = list(cameras)
         lib = device.init()
@@ -145,6 +161,18 @@ class GaussianTrainer:
     def current_step(self) -> int:
         return int(self._lib.msplat_trainer_iteration(self._h))
 
+    @property
+    def iteration(self) -> int:
+        return self.current_step
+
+    def train(self, callback=None, callback_every: int = 0) -> None:
+        """Steps until config.iterations, calling callback(stats) every
+        callback_every steps (GaussianTrainer::train, python/bindings.cpp:169-177)."""
+        while self.current_step < self.config.iterations:
+            st = self.step()
+            if callback is not None and callback_every > 0 and st.iteration % callback_every == 0:
+                callback(st)
+
     def last_loss(self, wait: bool = False) -> float:
         return float(self._lib.msplat_trainer_last_loss(self._h, int(wait)))
 
@@ -190,11 +218,20 @@ class GaussianTrainer:
             raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())
         return out
 
-    def evaluate(self, cameras: List[Camera], images) -> dict:
+    def evaluate(self, cameras: Optional[List[Camera]] = None, images=None) -> dict:
         """Metrics on held-out cameras (GaussianTrainer.evaluate, python/bindings.cpp:180-205):
         dict with psnr, ssim, l1, num_test, num_gaussians.  images: one
-        full-resolution (H, W, 3) float32 target per camera (numpy)."""
-        if len(cameras) != len(images) or not cameras:
+        full-resolution (H, W, 3) float32 target per camera (numpy).  Without
+        arguments, a trainer made from a Dataset in eval mode uses its
+        held-out cameras."""
+        if cameras is None and images is None:
+            ds = self._dataset
+            if ds is None or not ds.eval_mode:
+                raise ValueError("No test cameras. Load dataset with eval_mode=True.")
+            loaded = [ds.load_image(i) for i in range(0, len(ds.cameras), ds.test_every)]
+            cameras = [c for c, _ in loaded]
+            images = [im.cpu().numpy() for _, im in loaded]
+        if cameras is None or images is None or len(cameras) != len(images) or not cameras:
             raise ValueError("one image per test camera is needed")
         ims = [np.ascontiguousarray(im, np.float32) for im in images]
         for cam, im in zip(cameras, ims):

@@ -18,6 +18,7 @@ RGBA8 display image, scene files and checkpoints through the trainer.
 """
 from __future__ import annotations
 
+import os
 import struct
 
 import numpy as np
@@ -209,3 +210,27 @@ def test_evaluate_at_downscaled_resolution(mods):
     want = orc.image_metrics(r, small)
     for k in ("psnr", "ssim", "l1"):
         assert abs(m[k] - want[k]) <= 1e-5 * max(1.0, abs(want[k])), (k, m[k], want[k])
+
+
+def test_trainer_from_dataset(mods, tmp_path):
+    """GaussianTrainer(dataset, config) and train(callback, callback_every)
+    as the reference module's tests use them (tests/test_msplat.py:77-91):
+    images decoded from disk and prepared on the GPU, gaussians from the
+    point cloud, held-out cameras evaluated without arguments."""
+    from PIL import Image
+    from test_dataset_cpu import _write_model
+    import msplat_amd as msplat
+    _write_model(str(tmp_path), n_points=3000, seed=9)
+    probe = msplat.load_dataset(str(tmp_path))
+    rng = np.random.default_rng(4)
+    for cam, path in zip(probe.cameras, probe.image_paths):
+        os.makedirs(os.path.dirname(path), exist_ok=True)
+        Image.fromarray(rng.integers(0, 256, (cam.height, cam.width, 3), dtype=np.uint8), "RGB").save(path)
+    ds = msplat.load_dataset(str(tmp_path), eval_mode=True, test_every=2)
+    cfg = msplat.TrainingConfig(iterations=6, num_downscales=0, sh_degree_interval=0)
+    tr = msplat.GaussianTrainer(ds, cfg)
+    seen = []
+    tr.train(lambda s: seen.append(s.iteration), callback_every=2)
+    assert seen == [2, 4, 6] and tr.iteration == 6 and tr.splat_count() == 3000
+    m = tr.evaluate()
+    assert m["num_test"] == ds.num_test and np.isfinite(m["psnr"]) and 0.0 <= m["l1"] <= 1.0
