@@ -83,11 +83,19 @@ __device__ __forceinline__ void sh_color(int degree, V3 d, const float* dc, cons
 
 constexpr int PROJ_T = 128;   // gaussians per workgroup
 
-__device__ __forceinline__ int project_one(const CamParams& p, int g, V3 pw, const float* sc,
-                                           const float* dc, float4 q, float ol,
-                                           const float* rest, GaussOut go,
-                                           uint32_t* __restrict__ dkey,
+// Screen-space footprint of one visible gaussian (the part of the
+// projection that does not need its SH coefficients).
+struct Geo {
+    int area;   // tiles hit; 0 when culled
+    float px, py, ca, cb, cc, ex, ey, z;
+};
+
+__device__ __forceinline__ Geo project_geo(const CamParams& p, int g, V3 pw, const float* sc,
+                                           float4 q, GaussOut go, uint32_t* __restrict__ dkey,
                                            uint32_t* __restrict__ dval);
+__device__ __forceinline__ void project_col(const CamParams& p, int g, V3 pw, const float* dc,
+                                            float ol, const float* rest, const Geo& e,
+                                            GaussOut go, uint32_t* __restrict__ dkey);
 
 // PROJ_STAGE: 16-byte features_rest loads per thread, enough for PROJ_T rows
 // of up to 48 floats (SH degree <= 3) or 72 floats (degree 4).
@@ -124,10 +132,18 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
         for (int i = threadIdx.x; i < cnt / 4; i += PROJ_T) dst4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int i = (cnt / 4) * 4 + threadIdx.x; i < cnt; i += PROJ_T) gacc[base + i] = 0.f;
     }
+    // Geometry first: which of the workgroup's gaussians are visible.
+    Geo ge{};
+    if (live) ge = project_geo(p, g, pw, sc, q, go, dkey, dval);
+    __shared__ int s_vis[PROJ_T];
+    s_vis[threadIdx.x] = ge.area > 0;
+    __syncthreads();
     // Stage this workgroup's features_rest rows (PROJ_T * rest_per contiguous
     // floats, 16-byte aligned) through LDS with coalesced 16-byte loads.  All
     // of a thread's loads are issued before the first LDS store, so the
-    // workgroup waits for one memory round trip, not one per load.
+    // workgroup waits for one memory round trip, not one per load.  A vector
+    // that touches only rows of culled gaussians re-reads the block's last
+    // vector instead (one cached line), so culled rows cost no traffic.
     extern __shared__ float s_rest[];
     if (p.dtu > 0) {
         const int64_t base = (int64_t)g0 * p.rest_per;
@@ -141,9 +157,17 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
             // vector and store it to a spare LDS slot after the staging
             // area, so the compiler keeps all loads in flight together.
             float4 stage[PROJ_STAGE];
+            // rows of the first and last float of vector i: floor((4i + 0.5) /
+            // rest_per), exact in fp32 for these sizes (the quotient is never
+            // within 0.5 / rest_per of an integer)
+            const float inv_rest = 1.f / (float)p.rest_per;
 #pragma unroll
-            for (int k = 0; k < PROJ_STAGE; ++k)
-                stage[k] = src4[min((int)threadIdx.x + k * PROJ_T, nv - 1)];
+            for (int k = 0; k < PROJ_STAGE; ++k) {
+                const int i = min((int)threadIdx.x + k * PROJ_T, nv - 1);
+                const int r0 = (int)(((float)(4 * i) + 0.5f) * inv_rest);
+                const int r1 = min((int)(((float)(4 * i) + 3.5f) * inv_rest), PROJ_T - 1);
+                stage[k] = src4[(s_vis[r0] | s_vis[r1]) ? i : nv - 1];
+            }
 #pragma unroll
             for (int k = 0; k < PROJ_STAGE; ++k) {
                 const int i = threadIdx.x + k * PROJ_T;
@@ -153,10 +177,9 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
         for (int i = nv * 4 + threadIdx.x; i < cnt; i += PROJ_T) s_rest[i] = f_rest[base + i];
         __syncthreads();
     }
-    int area = 0;
-    if (live)
-        area = project_one(p, g, pw, sc, dc, q, ol, s_rest + (size_t)p.rest_per * threadIdx.x, go,
-                           dkey, dval);
+    const int area = ge.area;
+    if (area > 0)
+        project_col(p, g, pw, dc, ol, s_rest + (size_t)p.rest_per * threadIdx.x, ge, go, dkey);
     // Intersection total for the host: one atomic per workgroup, on one of
     // ISECT_SLOTS counters so that workgroups do not queue on one address.
     int v = area;
@@ -175,20 +198,19 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     }
 }
 
-// One gaussian: writes radii, tiles hit, the record and the depth key /
-// value; returns the number of tiles hit (0 when culled).
-__device__ __forceinline__ int project_one(const CamParams& p, int g, V3 pw, const float* sc,
-                                           const float* dc, float4 q, float ol,
-                                           const float* rest, GaussOut go,
-                                           uint32_t* __restrict__ dkey,
+// One gaussian's geometry: writes the culled defaults (radii, tiles hit,
+// depth key / value), and radii / tiles hit when visible.
+__device__ __forceinline__ Geo project_geo(const CamParams& p, int g, V3 pw, const float* sc,
+                                           float4 q, GaussOut go, uint32_t* __restrict__ dkey,
                                            uint32_t* __restrict__ dval) {
+    Geo r{};
     go.radii[g] = 0;
     go.tiles_hit[g] = 0;
     dkey[g] = 0xFFFFFFFFu;
     dval[g] = (uint32_t)g;
 
     const V3 pv = xf4x3(p.vm, pw);
-    if (pv.z <= p.clip) return 0;
+    if (pv.z <= p.clip) return r;
 
     const float s0 = exp_cw(sc[0]), s1 = exp_cw(sc[1]), s2 = exp_cw(sc[2]);
     float cov[6];
@@ -218,7 +240,7 @@ __device__ __forceinline__ int project_one(const CamParams& p, int g, V3 pw, con
 
     // Conic and 3-sigma radius.
     const float det = c2x * c2z - c2y * c2y;
-    if (det == 0.f) return 0;
+    if (det == 0.f) return r;
     const float inv_det = 1.f / det;
     const float ca = c2z * inv_det, cb = -c2y * inv_det, cc = c2x * inv_det;
     const float b = 0.5f * (c2x + c2z);
@@ -238,11 +260,20 @@ __device__ __forceinline__ int project_one(const CamParams& p, int g, V3 pw, con
     int x0, y0, x1, y1;
     tile_rect(px, py, ex, ey, p.tbx, p.tby, x0, y0, x1, y1);
     const int area = (x1 - x0) * (y1 - y0);
-    if (area <= 0) return 0;
+    if (area <= 0) return r;
 
     go.tiles_hit[g] = area;
     go.radii[g] = f2i(radius);
+    r.area = area;
+    r.px = px; r.py = py; r.ca = ca; r.cb = cb; r.cc = cc; r.ex = ex; r.ey = ey; r.z = pv.z;
+    return r;
+}
 
+// Colour and record of one visible gaussian: SH along normalize(p - cam_pos).
+__device__ __forceinline__ void project_col(const CamParams& p, int g, V3 pw, const float* dc,
+                                            float ol, const float* rest, const Geo& e,
+                                            GaussOut go, uint32_t* __restrict__ dkey) {
+    const float px = e.px, py = e.py, ca = e.ca, cb = e.cb, cc = e.cc, ex = e.ex, ey = e.ey;
     // SH colour along normalize(p - cam_pos).
     const float dx = pw.x - p.cam[0], dy = pw.y - p.cam[1], dz = pw.z - p.cam[2];
     const float inv = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
@@ -252,10 +283,9 @@ __device__ __forceinline__ int project_one(const CamParams& p, int g, V3 pw, con
     float4* rec = go.rec + 4 * (size_t)g;
     rec[0] = make_float4(px, py, ca, cb);
     rec[1] = make_float4(cc, sigmoid(ol), col[0], col[1]);
-    rec[2] = make_float4(col[2], ex, ey, pv.z);
+    rec[2] = make_float4(col[2], ex, ey, e.z);
     rec[3] = make_float4(dir.x, dir.y, dir.z, 0.f);
-    dkey[g] = __float_as_uint(pv.z);
-    return area;
+    dkey[g] = __float_as_uint(e.z);
 }
 
 }  // namespace
