@@ -1,5 +1,5 @@
 // ssim.hip — separable 11-tap SSIM + L1 loss, forward and backward, on
-// 16x16 workgroups with LDS-staged halos.
+// LDS-staged tiles with halos.
 //
 // Two passes with the reference's training semantics:
 //   h-fwd + v-fwd + h-bwd   ssim_h_fwd_kernel (.metal:3053-3115) and
@@ -27,10 +27,8 @@ namespace msp {
 
 namespace {
 
-constexpr int TG = 16;
 constexpr int HALF = 5;
 constexpr int WIN = 11;
-constexpr int TW = TG + 2 * HALF;   // 26
 
 // Fused forward / derivative / horizontal-backward tile: FX x FY output
 // pixels per workgroup of FT threads.  The horizontal sums are needed at
@@ -173,48 +171,56 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
     }
 }
 
+// Vertical backward tile: VX columns x VY rows of output pixels, 256
+// threads, each thread VY / 16 rows.  The derivative fields of the tile's
+// columns are read row by row as contiguous floats (VX pixels x 9 values),
+// so the loads are coalesced; VY + 10 rows are read for VY outputs.
+constexpr int VX = 16, VY = 32, VR = VY + 2 * HALF;
+constexpr int VPLANE = VR * VX + 1;   // one (channel, field) plane; odd stride spreads the banks
+
 __global__ __launch_bounds__(256) void k_ssim_v_bwd(int W, int H, const float* __restrict__ img,
                                                     const float* __restrict__ gt,
                                                     const float* __restrict__ dbuf, float w_ssim,
                                                     float inv_n, float* __restrict__ v_rendered) {
-    __shared__ float s_h[3][3][TW][TG];
+    __shared__ float s_h[9 * VPLANE];   // plane c * 3 + field, rows by.., columns bx..
     const int tr = threadIdx.x, lx = tr & 15, ly = tr >> 4;
-    const int bx = blockIdx.x * TG, by = blockIdx.y * TG - HALF;
-    for (int c = 0; c < 3; ++c)
-        for (int i = tr; i < TW * TG; i += 256) {
-            const int sy = i / TG, sx = i % TG, gy = by + sy, gx = bx + sx;
-            float v1 = 0.f, v2 = 0.f, v3 = 0.f;
-            if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
-                const float* d = dbuf + ((size_t)gy * W + gx) * 9 + c * 3;
-                v1 = d[0];
-                v2 = d[1];
-                v3 = d[2];
-            }
-            s_h[c][0][sy][sx] = v1;
-            s_h[c][1][sy][sx] = v2;
-            s_h[c][2][sy][sx] = v3;
-        }
+    const int bx = blockIdx.x * VX, by = blockIdx.y * VY - HALF;
+    const int nf = min(VX, W - bx) * 9;   // in-image floats of a row
+    constexpr int ROWF = VX * 9;
+    for (int i = tr; i < VR * ROWF; i += 256) {
+        const int sy = i / ROWF, f = i - sy * ROWF;
+        const int sx = f / 9, j = f - sx * 9;
+        const int gy = by + sy;
+        float v = 0.f;
+        if (f < nf && gy >= 0 && gy < H) v = dbuf[((size_t)gy * W + bx) * 9 + f];
+        s_h[j * VPLANE + sy * VX + sx] = v;
+    }
     __syncthreads();
-    const int px = bx + lx, py = blockIdx.y * TG + ly;
-    if (px >= W || py >= H) return;
-    for (int c = 0; c < 3; ++c) {
-        float f1 = 0.f, f2 = 0.f, f3 = 0.f;
+    const int px = bx + lx;
+    if (px >= W) return;
 #pragma unroll
-        for (int d = 0; d < WIN; ++d) {
-            const float w = GAUSS_1D[WIN - 1 - d];
-            f1 += w * s_h[c][0][ly + d][lx];
-            f2 += w * s_h[c][1][ly + d][lx];
-            f3 += w * s_h[c][2][ly + d][lx];
+    for (int rr = 0; rr < VY / 16; ++rr) {
+        const int oy = ly + 16 * rr, py = blockIdx.y * VY + oy;
+        if (py >= H) break;
+        for (int c = 0; c < 3; ++c) {
+            const float* h1 = s_h + (c * 3) * VPLANE + oy * VX + lx;
+            float f1 = 0.f, f2 = 0.f, f3 = 0.f;
+#pragma unroll
+            for (int d = 0; d < WIN; ++d) {
+                const float w = GAUSS_1D[WIN - 1 - d];
+                f1 += w * h1[d * VX];
+                f2 += w * h1[VPLANE + d * VX];
+                f3 += w * h1[2 * VPLANE + d * VX];
+            }
+            const size_t q = ((size_t)py * W + px) * 3 + c;
+            const float r = img[q], g = gt[q];
+            const float v_ssim = f1 + r * f2 + g * f3;
+            const float v_l1 = (g > r) ? -1.0f : ((g < r) ? 1.0f : 0.0f);
+            v_rendered[q] = inv_n * (-w_ssim * v_ssim + (1.0f - w_ssim) * v_l1);
         }
-        const size_t q = ((size_t)py * W + px) * 3 + c;
-        const float r = img[q], g = gt[q];
-        const float v_ssim = f1 + r * f2 + g * f3;
-        const float v_l1 = (g > r) ? -1.0f : ((g < r) ? 1.0f : 0.0f);
-        v_rendered[q] = inv_n * (-w_ssim * v_ssim + (1.0f - w_ssim) * v_l1);
     }
 }
 
-// loss = sum_pixels [w (1 - mean SSIM) + (1-w) mean L1], folded in a fixed order.
 __global__ __launch_bounds__(256) void k_loss_final(int nparts, const float* __restrict__ part,
                                                     float w_ssim, float* __restrict__ out) {
     __shared__ double s[3][256];
@@ -245,7 +251,7 @@ void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt,
                  float inv_n, float* dbuf, float* v_rendered, float* loss_part, float* loss_out) {
     const dim3 fgrid((W + FX - 1) / FX, (H + FY - 1) / FY);
     hipLaunchKernelGGL(k_ssim_fused, fgrid, dim3(FT), 0, s, W, H, img, gt, dbuf, loss_part);
-    const dim3 grid((W + TG - 1) / TG, (H + TG - 1) / TG);
+    const dim3 grid((W + VX - 1) / VX, (H + VY - 1) / VY);
     hipLaunchKernelGGL(k_ssim_v_bwd, grid, dim3(256), 0, s, W, H, img, gt, dbuf, w, inv_n,
                        v_rendered);
     hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(256), 0, s, (int)(fgrid.x * fgrid.y), loss_part,
