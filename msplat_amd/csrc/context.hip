@@ -260,9 +260,16 @@ void stage_begin(Ctx* c) {
     c->stage_open = false;
 }
 
+constexpr int kMaxPoints = 0x7FFFFFFF / 36;
+
 int check_render_args(const MsplatRenderArgs* a) {
     if (!a) return fail(MSPLAT_ERR_ARG, "null args");
     if (a->num_points < 0) return fail(MSPLAT_ERR_ARG, "num_points < 0");
+    // the raster backward addresses a gaussian's nine accumulators at byte
+    // offset 36 * id in 32 bits
+    if (a->num_points > kMaxPoints)
+        return fail(MSPLAT_ERR_ARG, "num_points %d exceeds the limit of %d gaussians",
+                    a->num_points, kMaxPoints);
     if (a->img_width == 0 || a->img_height == 0) return fail(MSPLAT_ERR_ARG, "empty image");
     if ((uint64_t)a->img_width * a->img_height > (1ull << 31) / 16)
         return fail(MSPLAT_ERR_ARG, "image too large");
@@ -516,10 +523,11 @@ int msplat_hip_sync(void) {
 }
 
 int msplat_hip_render(const MsplatRenderArgs* a, float* out_img) {
-    Ctx* c = g_ctx;
-    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    // argument errors are reported whether or not a context exists
     int r = check_render_args(a);
     if (r != MSPLAT_OK) return r;
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
     stage_begin(c);
     r = forward(c, a, false, out_img);
     if (r != MSPLAT_OK) return r;
@@ -528,11 +536,11 @@ int msplat_hip_render(const MsplatRenderArgs* a, float* out_img) {
 }
 
 int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* loss_out) {
-    Ctx* c = g_ctx;
-    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
     if (!a) return fail(MSPLAT_ERR_ARG, "null args");
     int r = check_render_args(&a->r);
     if (r != MSPLAT_OK) return r;
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
     if (a->num_adam_groups != 6) return fail(MSPLAT_ERR_ARG, "num_adam_groups must be 6");
     if (!a->gt) return fail(MSPLAT_ERR_ARG, "null gt");
     const float* rp[6] = {a->r.means3d, a->r.scales, a->r.quats, a->r.features_dc,

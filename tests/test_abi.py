@@ -99,9 +99,10 @@ def test_calls_before_init_fail_cleanly():
     lib = _abi.load()
     assert lib.msplat_hip_sync() == -3
     assert b"not initialised" in lib.msplat_hip_last_error()
-    a = _abi.RenderArgs()
+    a = _valid_empty_render_args()
     assert lib.msplat_hip_render(ctypes.byref(a), None) == -3
     t = _abi.TrainArgs()
+    t.r = _valid_empty_render_args()
     loss = ctypes.c_float(0)
     assert lib.msplat_hip_train_step(ctypes.byref(t), None, ctypes.byref(loss)) == -3
     n = ctypes.c_int32(0)
@@ -109,3 +110,35 @@ def test_calls_before_init_fail_cleanly():
     assert lib.msplat_hip_densify(ctypes.byref(d), ctypes.byref(n)) == -3
     counts = (ctypes.c_int64 * 6)()
     assert lib.msplat_hip_raster_work(counts) == -3
+
+
+def _valid_empty_render_args(n=0, w=16, h=16):
+    a = _abi.RenderArgs()
+    a.num_points = n
+    a.img_width, a.img_height = w, h
+    a.tile_bounds[:] = [(w + 15) // 16, (h + 15) // 16, 1]
+    return a
+
+
+def test_argument_errors_without_a_device():
+    """Argument checks come before the context check: a gaussian count past
+    the 32-bit accumulator addressing limit (36 bytes per gaussian), an empty
+    image and mismatched tile bounds are rejected with MSPLAT_ERR_ARG (-1)
+    without touching a device."""
+    if not os.path.exists(_abi.LIB_PATH):
+        pytest.skip("libmsplat_hip.so not built")
+    lib = _abi.load()
+    limit = 0x7FFFFFFF // 36
+    a = _valid_empty_render_args(n=limit + 1)
+    assert lib.msplat_hip_render(ctypes.byref(a), None) == -1
+    assert b"exceeds the limit" in lib.msplat_hip_last_error()
+    t = _abi.TrainArgs()
+    t.r = _valid_empty_render_args(n=limit + 1)
+    assert lib.msplat_hip_train_step(ctypes.byref(t), None, None) == -1
+    assert b"exceeds the limit" in lib.msplat_hip_last_error()
+    a = _valid_empty_render_args(w=0)
+    assert lib.msplat_hip_render(ctypes.byref(a), None) == -1
+    a = _valid_empty_render_args(w=33)
+    a.tile_bounds[0] = 2
+    assert lib.msplat_hip_render(ctypes.byref(a), None) == -1
+    assert b"tile_bounds" in lib.msplat_hip_last_error()
