@@ -200,6 +200,20 @@ typedef struct MsplatImageMetrics {
 int msplat_hip_image_metrics(const float* img, const float* gt, int32_t height, int32_t width,
                              int32_t window_size, float sigma, MsplatImageMetrics* out);
 
+/* msplat_hip_image_metrics without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving or evaluation loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as
+ * msplat_hip_image_metrics; the per-workgroup partial sums live in a
+ * fixed 1.5 MiB device workspace inside the library (one per GPU, held until
+ * the process ends) instead of the context's grow-only buffers.  Images are
+ * limited to 65536 metric tiles of 64x16 pixels (e.g. 8192x8192); larger ones
+ * return MSPLAT_ERR_ARG.  All calls on one GPU share that workspace: calls
+ * that overlap on one GPU (from several threads or streams) race. */
+int msplat_hip_image_metrics_noalloc(const float* img, const float* gt, int32_t height,
+                                     int32_t width, int32_t window_size, float sigma,
+                                     MsplatImageMetrics* out);
+
 /* Initial gaussian scale of every point of a cloud: the mean distance to its
  * three nearest other points (device xyz[n,3] -> device mean_dist[n]),
  * exactly as the reference's nanoflann kd-tree query gives it

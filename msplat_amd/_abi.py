@@ -179,6 +179,8 @@ SIGNATURES = [
      [c_void_p, c_int32, c_int32, POINTER(c_float), POINTER(c_float), POINTER(c_int32), c_void_p]),
     ("msplat_hip_image_metrics", c_int,
      [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, POINTER(ImageMetrics)]),
+    ("msplat_hip_image_metrics_noalloc", c_int,
+     [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, POINTER(ImageMetrics)]),
     # include/msplat_trainer.h
     ("msplat_trainer_create", c_void_p,
      [POINTER(TrainerConfig), c_int64, c_void_p * 6, c_int32, POINTER(TrainerCamera), POINTER(c_void_p), c_int32]),

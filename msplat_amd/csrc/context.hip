@@ -24,9 +24,23 @@
 #include <string>
 #include <vector>
 
+// Workspace of msplat_hip_image_metrics_noalloc: the per-workgroup fp64
+// partials of the metric kernels (three per 64x16 output tile, at most
+// kNoallocEvalParts tiles) followed by the three folded sums.  One copy per
+// GPU for the life of the process (1.5 MiB).  Host code uses the address that
+// hipGetSymbolAddress returns for the current device, never the array's name.
+constexpr int kNoallocEvalParts = 65536;
+constexpr int kNoallocScratchDoubles = 3 * kNoallocEvalParts + 4;
+static __device__ __align__(256) double scratch[kNoallocScratchDoubles];
+
 namespace {
 
 using namespace msp;
+
+// Device address of `scratch` per device ordinal, resolved once per device by
+// msplat_hip_init with that device current.
+constexpr int kMaxDevices = 64;
+double* g_scratch_dev[kMaxDevices] = {};
 
 // Stage names (as msplat_metal.mm:30-34 where they coincide).
 constexpr int kNumStages = 8;
@@ -428,7 +442,14 @@ int msplat_hip_init(int device) {
     int n = 0;
     HIP_TRY(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) return fail(MSPLAT_ERR_ARG, "device %d of %d", device, n);
+    if (device >= kMaxDevices) return fail(MSPLAT_ERR_ARG, "device %d beyond %d", device, kMaxDevices);
     HIP_TRY(hipSetDevice(device));
+    if (!g_scratch_dev[device]) {
+        void* sp = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+        if (!sp) return fail(MSPLAT_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch_dev[device] = static_cast<double*>(sp);
+    }
     Ctx* c = new Ctx();
     c->device = device;
     g_ctx = c;
@@ -642,18 +663,17 @@ int msplat_hip_image_to_rgba8(const float* img, int64_t n_pixels, uint8_t* rgba)
     return MSPLAT_OK;
 }
 
-int msplat_hip_image_metrics(const float* img, const float* gt, int32_t height, int32_t width,
-                             int32_t window_size, float sigma, MsplatImageMetrics* out) {
-    Ctx* c = g_ctx;
-    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+namespace {
+// Arguments and window of the image metrics, exactly as ssim_eval builds the
+// window (ssim.cpp:68-75), in fp32.
+int metrics_setup(const float* img, const float* gt, int32_t height, int32_t width,
+                  int32_t window_size, float sigma, const MsplatImageMetrics* out, EvalWindow& win) {
     if (!img || !gt || !out) return fail(MSPLAT_ERR_ARG, "null metrics argument");
     if (height <= 0 || width <= 0 || (int64_t)height * width > (int64_t)1 << 30)
         return fail(MSPLAT_ERR_ARG, "bad image size %dx%d", width, height);
     if (window_size < 1 || window_size > 11 || window_size % 2 == 0)
         return fail(MSPLAT_ERR_ARG, "window size %d: odd and at most 11", window_size);
     if (!(sigma > 0.f)) return fail(MSPLAT_ERR_ARG, "sigma must be positive");
-    // the window exactly as ssim_eval builds it (ssim.cpp:68-75), in fp32
-    EvalWindow win;
     win.ws = window_size;
     win.pad = window_size / 2;
     float ksum = 0.f;
@@ -664,13 +684,17 @@ int msplat_hip_image_metrics(const float* img, const float* gt, int32_t height, 
     }
     for (int i = 0; i < window_size; ++i) win.w[i] /= ksum;
     for (int i = window_size; i < 11; ++i) win.w[i] = 0.f;
-    ENSURE(c->eval_part, (size_t)eval_partial_count(height, width) * 3 * sizeof(double));
-    ENSURE(c->eval_out, 3 * sizeof(double));
-    launch_image_metrics(c->stream, img, gt, height, width, win, P<double>(c->eval_part),
-                         P<double>(c->eval_out));
+    return MSPLAT_OK;
+}
+
+// Run the metric kernels with the given partials / sums buffers and read the
+// three sums back (into a stack array: no allocation).
+int metrics_run(Ctx* c, const float* img, const float* gt, int32_t height, int32_t width,
+                const EvalWindow& win, double* part, double* out3, MsplatImageMetrics* out) {
+    launch_image_metrics(c->stream, img, gt, height, width, win, part, out3);
     HIP_TRY(hipGetLastError());
     double sums[3];
-    HIP_TRY(hipMemcpyAsync(sums, c->eval_out.p, sizeof(sums), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipMemcpyAsync(sums, out3, sizeof(sums), hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     const double n = (double)height * (double)width * 3.0;
     const double mse = sums[1] / n;
@@ -678,6 +702,41 @@ int msplat_hip_image_metrics(const float* img, const float* gt, int32_t height, 
     out->ssim = (float)(sums[0] / (double)((int64_t)height * width * 3));
     out->l1 = (float)(sums[2] / n);
     return MSPLAT_OK;
+}
+}  // namespace
+
+int msplat_hip_image_metrics(const float* img, const float* gt, int32_t height, int32_t width,
+                             int32_t window_size, float sigma, MsplatImageMetrics* out) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    EvalWindow win;
+    int r = metrics_setup(img, gt, height, width, window_size, sigma, out, win);
+    if (r != MSPLAT_OK) return r;
+    ENSURE(c->eval_part, (size_t)eval_partial_count(height, width) * 3 * sizeof(double));
+    ENSURE(c->eval_out, 3 * sizeof(double));
+    return metrics_run(c, img, gt, height, width, win, P<double>(c->eval_part),
+                       P<double>(c->eval_out), out);
+}
+
+int msplat_hip_image_metrics_noalloc(const float* img, const float* gt, int32_t height,
+                                     int32_t width, int32_t window_size, float sigma,
+                                     MsplatImageMetrics* out) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    EvalWindow win;
+    int r = metrics_setup(img, gt, height, width, window_size, sigma, out, win);
+    if (r != MSPLAT_OK) return r;
+    const int64_t parts = eval_partial_count(height, width);
+    if (parts > kNoallocEvalParts)
+        return fail(MSPLAT_ERR_ARG,
+                    "%dx%d image needs %lld metric tiles; the allocation-free workspace holds %d "
+                    "(64x16 pixels each)",
+                    width, height, (long long)parts, kNoallocEvalParts);
+    double* ws = g_scratch_dev[c->device];
+    if (!ws) return fail(MSPLAT_ERR_NOINIT, "workspace address of device %d not resolved", c->device);
+    // every partial and the three sums are written before they are read: the
+    // previous call's contents need no clearing
+    return metrics_run(c, img, gt, height, width, win, ws, ws + 3 * (size_t)kNoallocEvalParts, out);
 }
 
 int msplat_hip_resize_area(const float* src, int32_t src_w, int32_t src_h, float* dst,
