@@ -57,31 +57,6 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def config3_cameras(n_cams=32, width=1297, height=840):
-    from msplat_amd import camera, synthetic
-    st = synthetic.Stream(synthetic.BASE_SEED + 3 + 1000)
-    dirs = synthetic._sphere_dirs(st, n_cams)
-    radii = 4.0 + 2.0 * st.uniform(n_cams)
-    return [camera.pinhole(width, height, 70.0, camera.look_at(r * d)) for r, d in zip(radii, dirs)]
-
-
-def make_targets(params, cams, degree, bg):
-    """Render of the cloud with means jittered by N(0,0.02) plus N(0,0.01) pixel noise."""
-    from msplat_amd import camera, device, synthetic
-    seed = synthetic.BASE_SEED + 3
-    jit = [p for p in params]
-    jit[0] = params[0] + synthetic.device_randn(params[0].numel(), seed * 7 + 11, 0.0, 0.02).view_as(params[0])
-    g = device.DeviceGaussians.from_tensors(jit, degree)
-    out = []
-    for i, c in enumerate(cams):
-        s = camera.prepare_cam(c)
-        img = device.render(g, s, degree, bg).clone()
-        img += synthetic.device_randn(img.numel(), seed * 13 + i, 0.0, 0.01).view_as(img)
-        out.append(img)
-    del g
-    return out
-
-
 def stage_times(lib):
     import ctypes
     from msplat_amd import _abi
@@ -262,13 +237,6 @@ def bench_config4(args):
             "bwd_grad_pairs_per_step": pairs[1] / n_staged}
 
 
-def config5_cameras(n_poses=100, width=4946, height=3286):
-    from msplat_amd import camera, synthetic
-    st = synthetic.Stream(synthetic.BASE_SEED + 5 + 1000)
-    dirs = synthetic._sphere_dirs(st, n_poses)
-    return [camera.pinhole(width, height, 70.0, camera.look_at(5.0 * d)) for d in dirs]
-
-
 def bench_config5(args):
     """Config 5, render only: 6M SH3 gaussians with config-2 distributions
     (generated on the GPU), 4946x3286, 100 poses on a radius-5 sphere; render
@@ -281,7 +249,7 @@ def bench_config5(args):
     params = synthetic.device_cloud(6_000_000, 3, synthetic.BASE_SEED + 5)
     g = device.DeviceGaussians.from_tensors(params, 3)
     del params
-    cams = config5_cameras()
+    cams = synthetic.config5_cameras()
     setups = [camera.prepare_cam(c) for c in cams]
     out = torch.empty((setups[0].height, setups[0].width, 3), dtype=torch.float32, device="cuda")
     for i in range(3):
@@ -404,8 +372,8 @@ def main():
     degree = 3
     t = time.perf_counter()
     params = device_params = synthetic.device_cloud(args.n, degree, synthetic.BASE_SEED + 3)
-    cams = config3_cameras()
-    targets = make_targets(params, cams, degree, bg)
+    cams = synthetic.config3_cameras()
+    targets = synthetic.device_targets(params, cams, degree, bg, synthetic.BASE_SEED + 3)
     torch.cuda.synchronize()
     log(f"setup: {args.n} gaussians, {len(cams)} cameras, targets ready in {time.perf_counter() - t:.1f}s")
 

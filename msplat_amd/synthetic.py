@@ -210,3 +210,46 @@ def device_cloud(n: int, degree: int, seed: int):
     f_dc = device_randn(3 * n, k(4), 0.0, 0.3).view(n, 3)
     f_rest = device_randn(nb * 3 * n, k(5), 0.0, 0.05).view(n, nb, 3)
     return [means, scales, quats.contiguous(), f_dc, f_rest, opac]
+
+
+# Poses and targets of the benchmark workloads whose gaussians are generated
+# on the GPU (device_cloud).  Each pose set has a stream of its own, so it
+# does not depend on how the gaussians were drawn.
+
+def config2_cameras(n_cams: int = 1, width: int = 1297, height: int = 840) -> List[Camera]:
+    """Config-2 poses: uniform directions on a radius-5 sphere, FOV 70."""
+    st = Stream(BASE_SEED + 2 + 1000)
+    dirs = _sphere_dirs(st, n_cams)
+    return [pinhole(width, height, 70.0, look_at(5.0 * d)) for d in dirs]
+
+
+def config3_cameras(n_cams: int = 32, width: int = 1297, height: int = 840) -> List[Camera]:
+    """Config-3 poses: 32 cameras at radius U[4,6] in uniform directions, FOV 70."""
+    st = Stream(BASE_SEED + 3 + 1000)
+    dirs = _sphere_dirs(st, n_cams)
+    radii = 4.0 + 2.0 * st.uniform(n_cams)
+    return [pinhole(width, height, 70.0, look_at(r * d)) for r, d in zip(radii, dirs)]
+
+
+def config5_cameras(n_poses: int = 100, width: int = 4946, height: int = 3286) -> List[Camera]:
+    """Config-5 poses: uniform directions on a radius-5 sphere, FOV 70."""
+    st = Stream(BASE_SEED + 5 + 1000)
+    dirs = _sphere_dirs(st, n_poses)
+    return [pinhole(width, height, 70.0, look_at(5.0 * d)) for d in dirs]
+
+
+def device_targets(params, cams, degree: int, background, seed: int):
+    """Targets of configs 2/3 on the GPU: a render of the cloud (six device
+    tensors) with means jittered by N(0, 0.02), plus N(0, 0.01) pixel noise
+    (not clamped), one (H, W, 3) device tensor per camera."""
+    from . import camera, device
+    jit = list(params)
+    jit[0] = params[0] + device_randn(params[0].numel(), seed * 7 + 11, 0.0, 0.02).view_as(params[0])
+    g = device.DeviceGaussians.from_tensors(jit, degree)
+    out = []
+    for i, c in enumerate(cams):
+        img = device.render(g, camera.prepare_cam(c), degree, background).clone()
+        img += device_randn(img.numel(), seed * 13 + i, 0.0, 0.01).view_as(img)
+        out.append(img)
+    del g
+    return out

@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 
 import orc
-from helpers import BG, LRS, assert_bits_equal, grad_close, small_scene, target_for
+import parity
+from helpers import BG, LRS, assert_bits_equal, small_scene, target_for
 from msplat_amd import camera, synthetic
 
 pytestmark = pytest.mark.gpu
@@ -28,35 +29,8 @@ def dev():
 
 
 def _render_and_compare(dev, scene, dtu=None, cam_idx=0):
-    deg = scene.sh_degree
-    dtu = deg if dtu is None else dtu
-    su = camera.prepare_cam(scene.cameras[cam_idx])
-    g = dev.DeviceGaussians.from_arrays(scene.params(), deg)
-    img = dev.render(g, su, dtu, BG).cpu().numpy()
-    cam = orc.camera(su, deg, dtu, BG)
-    p = orc.project(cam, scene.means, scene.scales, scene.quats, scene.f_dc, scene.f_rest)
-    n = scene.n
-    radii = dev.intermediate("radii", np.int32)
-    assert_bits_equal(radii, p["radii"], "radii")
-    assert_bits_equal(dev.intermediate("num_tiles_hit", np.int32), p["num_tiles_hit"], "num_tiles_hit")
-    vis = p["radii"] > 0
-    assert vis.sum() > 0
-    assert_bits_equal(dev.intermediate("xys").reshape(n, 2)[vis], p["xys"][vis], "xys")
-    assert_bits_equal(dev.intermediate("depths")[vis], p["depths"][vis], "depths")
-    assert_bits_equal(dev.intermediate("aabb").reshape(n, 2)[vis], p["aabb"][vis], "aabb")
-    assert_bits_equal(dev.intermediate("conics").reshape(n, 3)[vis], p["conics"][vis], "conics")
-    assert_bits_equal(dev.intermediate("colors").reshape(n, 3)[vis], p["colors"][vis], "colors")
-    counts, tile_bins, ids = orc.bin_sort(cam, p)
-    assert_bits_equal(dev.intermediate("tile_bins", np.int32).reshape(-1, 2), tile_bins, "tile_bins")
-    assert_bits_equal(dev.intermediate("gaussian_ids", np.int32), ids, "gaussian_ids")
-    r = orc.rasterize(cam, p, scene.opacities, tile_bins, ids)
-    H, W = su.height, su.width
-    assert_bits_equal(dev.intermediate("final_Ts").reshape(H, W), r["final_Ts"], "final_Ts")
-    assert_bits_equal(dev.intermediate("final_index", np.int32).reshape(H, W), r["final_index"], "final_index")
-    assert_bits_equal(img, r["out_img"], "out_img")
-    work = dev.raster_work()
-    assert [work[k] for k in dev.RASTER_WORK_KEYS[:3]] == orc.raster_counts()[:3], (work, orc.raster_counts())
-    return dev.meta(), counts
+    return parity.render_and_compare(dev, scene.params(), scene.sh_degree, scene.cameras[cam_idx], dtu=dtu,
+                                     label=scene.name)
 
 
 def test_render_config1(dev):
@@ -109,51 +83,10 @@ def test_render_empty_and_culled(dev):
 
 
 def _train_compare(dev, scene, steps=1, dtu=None, check_grads=True):
-    deg = scene.sh_degree
-    dtu = deg if dtu is None else dtu
     su = camera.prepare_cam(scene.cameras[0])
-    H, W = su.height, su.width
-    gt = target_for(scene, (H, W))
-    torch = pytest.importorskip("torch")
-    g = dev.DeviceGaussians.from_arrays(scene.params(), deg, capacity=scene.n)
-    gt_d = dev.to_dev(gt)
-    n = scene.n
-    grads = {k: torch.zeros((n, d), dtype=torch.float32, device="cuda") for k, d in
-             (("v_mean3d", 3), ("v_scale", 3), ("v_quat", 4))}
-    # oracle state
-    params = [np.ascontiguousarray(a, np.float32).copy() for a in scene.params()]
-    m = [np.zeros_like(a) for a in params]
-    v = [np.zeros_like(a) for a in params]
-    vis, gnorm, max2d = (np.zeros(n, np.float32) for _ in range(3))
-    cam = orc.camera(su, deg, dtu, BG)
-    for step in range(1, steps + 1):
-        loss_g = dev.train_step(g, su, dtu, BG, gt_d, 0.2, LRS, step, grads_out=grads)
-        want = ("out_img", "radii", "v_xy", "v_conic", "v_rgb", "v_opacity", "v_mean3d", "v_scale", "v_quat",
-                "v_rendered")
-        loss_o, o = orc.train_step(cam, params, m, v, orc.adam_hparams(LRS, step), gt, 0.2, vis, gnorm, max2d,
-                                   want=want)
-        assert abs(loss_g - loss_o) <= 1e-5 * abs(loss_o), (loss_g, loss_o)
-        if step == 1:
-            work = dev.raster_work()
-            assert [work[k] for k in dev.RASTER_WORK_KEYS] == orc.raster_counts(), (work, orc.raster_counts())
-            assert_bits_equal(dev.intermediate("out_img").reshape(H, W, 3), o["out_img"], "out_img")
-            assert_bits_equal(dev.intermediate("v_rendered").reshape(H, W, 3), o["v_rendered"], "v_rendered")
-            assert_bits_equal(dev.intermediate("radii", np.int32), o["radii"], "radii")
-        if check_grads and step == 1:
-            for k, d in (("v_xy", 2), ("v_conic", 3), ("v_rgb", 3), ("v_opacity", 1)):
-                grad_close(dev.intermediate(k).reshape(n, d) if d > 1 else dev.intermediate(k),
-                           o[k], what=k)
-            for k in ("v_mean3d", "v_scale", "v_quat"):
-                grad_close(grads[k].cpu().numpy(), o[k], what=k)
-    gp = g.numpy()
-    names = ("means", "scales", "quats", "f_dc", "f_rest", "opacities")
-    for i in range(6):
-        grad_close(gp[i], params[i], rtol=1e-3, floor=1e-6, what=f"param {names[i]}")
-        grad_close(g.m[i][:n].cpu().numpy(), m[i], what=f"exp_avg {names[i]}")
-        grad_close(g.v[i][:n].cpu().numpy(), v[i], rtol=2e-3, what=f"exp_avg_sq {names[i]}")
-    grad_close(g.vis[:n].cpu().numpy(), vis, rtol=0, floor=0, what="vis_counts")
-    grad_close(g.gnorm[:n].cpu().numpy(), gnorm, what="xys_grad_norm")
-    grad_close(g.max2d[:n].cpu().numpy(), max2d, rtol=0, floor=0, what="max_2d_size")
+    gt = target_for(scene, (su.height, su.width))
+    return parity.train_compare(dev, scene.params(), scene.sh_degree, scene.cameras[0], gt, steps=steps, dtu=dtu,
+                                check_grads=check_grads, label=scene.name)
 
 
 def test_train_step_small(dev):
@@ -167,6 +100,33 @@ def test_train_step_chunked(dev):
 
 def test_train_step_monolithic(dev):
     _train_compare(dev, small_scene(n=12000, width=336, height=208, seed_off=82))
+
+
+def test_render_partial_edge_tiles(dev):
+    """167x93: W % 16, W % 32, H % 16 and H % 32 all nonzero, so the last tile
+    column and row are partial (pixels outside the image in every wave of
+    them, and quadrants with no pixel at all)."""
+    _render_and_compare(dev, small_scene(n=5000, width=167, height=93, seed_off=90))
+
+
+def test_train_step_partial_edge_tiles(dev):
+    """Train step at 167x93: partial raster tiles in the forward and backward,
+    and SSIM windows cut by the right and bottom image edges (rows and
+    columns past the image contribute zero statistics, D14)."""
+    _train_compare(dev, small_scene(n=5000, width=167, height=93, seed_off=91))
+
+
+def test_train_step_partial_edge_tiles_chunked(dev):
+    """Partial edge tiles in chunk mode (fewer than 400 tiles) with
+    multi-chunk tiles: prefix / suffix backward at the image border."""
+    _train_compare(dev, small_scene(n=30000, width=101, height=75, seed_off=92, spread=0.6))
+
+
+def test_render_benchmark_resolution_small_cloud(dev):
+    """The benchmark image size 1297x840 (82 x 53 tiles, partial last column
+    and row) at 20k gaussians."""
+    sc = small_scene(n=20000, width=1297, height=840, seed_off=93)
+    _render_and_compare(dev, sc)
 
 
 def test_raster_counters_match_work(dev):
