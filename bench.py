@@ -28,6 +28,15 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
+# The CPU baseline's OpenMP threads stay on the cores they start on (read by
+# the OpenMP runtime when it loads, so set before torch or the oracle loads).
+os.environ.setdefault("OMP_PROC_BIND", "close")
+# CPUs this process may use, read before an OpenMP runtime binds the main
+# thread to one of them.
+try:
+    USABLE_CPUS = len(os.sched_getaffinity(0))
+except AttributeError:
+    USABLE_CPUS = os.cpu_count()
 
 METRIC = "train iters/sec + render FPS, 1.5M Gaussians SH3 @1297×840, 1×MI355X"
 HBM_PEAK = 8.0e12
@@ -48,9 +57,16 @@ FP32_PEAK = 157.3e12
 FWD_PAIR_FLOPS = 11 + 3 + 9
 BWD_PAIR_FLOPS = 11 + 3 + 64
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "raster_bwd_config3_traffic.json")
-# Stage names in the order of the library's stage-timing bits.
-STAGES = ["proj_sh_fwd", "depth_sort", "tile_lists", "rast_fwd", "loss_fwd_bwd", "rast_bwd",
-          "sh_rest_adam", "proj_sh_bwd_adam"]
+# Stage names in the order of the library's stage-timing bits: the
+# reference profiler's train stages (msplat_metal.mm:30-34), ".part" where a
+# stage runs as two kernels, and densify.
+STAGES = ["proj_sh_fwd", "prefix_sort_pack.depth_sort", "prefix_sort_pack.tile_lists", "rast_fwd",
+          "loss_fwd_bwd", "rast_bwd", "proj_sh_bwd_adam.sh_rest", "proj_sh_bwd_adam.dense", "densify"]
+# The reference's eight train stages; blit_zero runs inside proj_sh_fwd here
+# (the projection zeroes the gradient accumulators) and grad_stats inside
+# proj_sh_bwd_adam.dense.
+REFERENCE_STAGES = ["blit_zero", "proj_sh_fwd", "prefix_sort_pack", "rast_fwd", "loss_fwd_bwd", "rast_bwd",
+                    "proj_sh_bwd_adam", "grad_stats"]
 
 
 def log(*a):
@@ -69,26 +85,49 @@ def stage_times(lib):
     return {names[i].decode(): (ms[i], cnt[i]) for i in range(n.value)}, calls.value
 
 
-def cpu_baseline(params_dev, cams, targets, degree, bg, n_steps):
+def cpu_baseline(state, cams, targets, degree, bg, n_steps, first_step):
     """The CPU oracle (oracle/liboracle.so, OpenMP) on a bounded sample of the
-    same workload: n_steps full train steps at the full 1.5M / 1297x840 size."""
+    same workload: n_steps full train steps at the full size, from the
+    trainer's state after the timed steps (parameters and Adam moments, host
+    copies), with the cameras and Adam step numbers that come next.  Returns
+    the rate, the thread count, the seconds and the mean wall milliseconds per
+    step of each reference train stage (the oracle's rast_bwd recomputes each
+    pixel's forward before its backward)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import ctypes
     import orc
     from msplat_amd import camera
-    params = [p.detach().cpu().numpy().astype(np.float32).copy() for p in params_dev]
-    m = [np.zeros_like(a) for a in params]
-    v = [np.zeros_like(a) for a in params]
+    params, m, v = state
     n = params[0].shape[0]
     z = [np.zeros(n, np.float32) for _ in range(3)]
     lrs = [0.00016, 0.005, 0.001, 0.0025, 0.000125, 0.05]
+    orc.lib().orc_stage_times((ctypes.c_double * 8)(), None)
     t0 = time.perf_counter()
     for s in range(n_steps):
-        su = camera.prepare_cam(cams[s % len(cams)])
+        ci = (first_step - 1 + s) % len(cams)
+        su = camera.prepare_cam(cams[ci])
         cam = orc.camera(su, degree, degree, bg)
-        gt = targets[s % len(cams)].cpu().numpy()
-        orc.train_step(cam, params, m, v, orc.adam_hparams(lrs, s + 1), gt, 0.2, *z)
+        gt = targets[ci].cpu().numpy()
+        orc.train_step(cam, params, m, v, orc.adam_hparams(lrs, first_step + s), gt, 0.2, *z)
     dt = time.perf_counter() - t0
-    return n_steps / dt, int(orc.lib().orc_num_threads()), dt
+    ms = (ctypes.c_double * 8)()
+    steps = ctypes.c_int64(0)
+    orc.lib().orc_stage_times(ms, ctypes.byref(steps))
+    stage_ms = {name: ms[i] / max(steps.value, 1) for i, name in enumerate(REFERENCE_STAGES)}
+    return n_steps / dt, int(orc.lib().orc_num_threads()), dt, stage_ms
+
+
+def trainer_state(tr, degree):
+    """Host copies of a trainer's parameters and Adam moments in the oracle's
+    layouts (f_rest [N, K-1, 3], opacities [N, 1])."""
+    nb = (degree + 1) ** 2 - 1
+    out = []
+    for which in range(3):
+        gs = [tr.group(g, which) for g in range(6)]
+        gs[4] = gs[4].reshape(gs[4].shape[0], nb, 3)
+        gs[5] = gs[5].reshape(-1, 1)
+        out.append([np.ascontiguousarray(a, np.float32) for a in gs])
+    return out
 
 
 def rocprof_summary(d: str, first: int, count: int, command: str) -> str:
@@ -166,6 +205,33 @@ def traffic_summary(dirs: list, copy_mib: int, last: int, commands: str,
 
 def _stage_line(stages):
     return {k: ms / c for k, (ms, c) in stages.items() if c}
+
+
+def _reference_stages(parts: dict) -> dict:
+    """Per-call milliseconds under the reference's stage names: the parts of a
+    stage summed; the fused blit_zero and grad_stats are 0."""
+    out = {}
+    for name in REFERENCE_STAGES:
+        tot = sum(v for k, v in parts.items() if k == name or k.startswith(name + "."))
+        if tot or name in ("blit_zero", "grad_stats"):
+            out[name] = tot
+    return out
+
+
+def cpu_description() -> dict:
+    """Host CPU model, logical CPUs usable by this process and the OpenMP
+    thread binding, for the CPU baseline."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "cpus_usable": USABLE_CPUS, "binding": os.environ.get("OMP_PROC_BIND", "unset"),
+            "places": os.environ.get("OMP_PLACES", "unset")}
 
 
 def proj_bytes(n_vis, n_cul):
@@ -308,6 +374,9 @@ def main():
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--frames", type=int, default=200)
+    ap.add_argument("--preroll", type=int, default=200,
+                    help="untimed train steps before --warmup: through the opacity reset (step 100) "
+                         "and the first densification (step 200) of the refinement policy")
     ap.add_argument("--train-only", action="store_true",
                     help="stop after the timed train steps (counter runs: the timed steps are then "
                          "the last dispatches of every train kernel)")
@@ -340,7 +409,8 @@ def main():
         print(json.dumps(res[kernels[0]] if len(kernels) == 1 else res, indent=1))
         return
     if args.rocprof_summary:
-        print(rocprof_summary(args.rocprof_summary, args.warmup, args.steps, args.rocprof_command), end="")
+        print(rocprof_summary(args.rocprof_summary, args.preroll + args.warmup, args.steps,
+                              args.rocprof_command), end="")
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -371,7 +441,7 @@ def main():
     bg = np.array([0.6130, 0.0101, 0.3984], np.float32)
     degree = 3
     t = time.perf_counter()
-    params = device_params = synthetic.device_cloud(args.n, degree, synthetic.BASE_SEED + 3)
+    params = synthetic.device_cloud(args.n, degree, synthetic.BASE_SEED + 3)
     cams = synthetic.config3_cameras()
     targets = synthetic.device_targets(params, cams, degree, bg, synthetic.BASE_SEED + 3)
     torch.cuda.synchronize()
@@ -380,31 +450,58 @@ def main():
     cfg = TrainingConfig(iterations=30000, sh_degree=degree, sh_degree_interval=0, num_downscales=0,
                          warmup_length=0, cull_alpha_thresh=0.005, shuffle_cameras=False)
     tr = GaussianTrainer(params, cams, targets, cfg)
+    _abi = device._abi
+    # Pre-roll (untimed): through the opacity reset at step refine_every and
+    # the first densification at 2 refine_every, so that the timed steps see
+    # the post-reset cloud whatever --steps is.  Densification calls are
+    # bracketed by HIP events from here on, so their cost is known even when
+    # the timed window holds none.
+    _abi.check(lib.msplat_hip_set_stage_timing_mask(1 << STAGES.index("densify")))
+    _abi.check(lib.msplat_hip_enable_stage_timing(1))
+    for _ in range(args.preroll):
+        tr.step()
+    device.sync()
+    pre, _ = stage_times(lib)
+    device.drain_raster_counters()
+    pre_dens = pre["densify"]
+    log(f"pre-roll: {args.preroll} steps, {pre_dens[1]} densification(s), gaussians {args.n} -> "
+        f"{tr.splat_count()}")
     for _ in range(args.warmup):
         tr.step()
     device.sync()
-    _abi = device._abi
     # The timed steps bracket only the raster backward (the roofline kernel)
-    # with HIP events: every event leaves the GPU idle for a few microseconds.
-    _abi.check(lib.msplat_hip_set_stage_timing_mask(1 << STAGES.index("rast_bwd")))
+    # and densification calls with HIP events: every event leaves the GPU idle
+    # for a few microseconds.
+    _abi.check(lib.msplat_hip_set_stage_timing_mask((1 << STAGES.index("rast_bwd")) |
+                                                    (1 << STAGES.index("densify"))))
     _abi.check(lib.msplat_hip_enable_stage_timing(1))
     n_start = tr.splat_count()
+    first_step = args.preroll + args.warmup + 1
     device.sync()
     t0 = time.perf_counter()
-    counts = []
     for _ in range(args.steps):
-        st = tr.step()
-        counts.append(st.splat_count)
+        tr.step()
     device.sync()
     t1 = time.perf_counter()
     timed, _ = stage_times(lib)
     train_pairs = device.drain_raster_counters()
-    train_s = t1 - t0
-    its = args.steps / train_s
-    log(f"train: {args.steps} steps in {train_s:.3f}s = {its:.1f} it/s; gaussians {n_start} -> {tr.splat_count()}")
+    window_s = t1 - t0
+    win_dens_ms, win_dens_n = timed["densify"]
+    dens_n = pre_dens[1] + win_dens_n
+    densify_ms = (pre_dens[0] + win_dens_ms) / dens_n if dens_n else 0.0
+    # steady-state cost of a step: the timed steps without the densification
+    # calls that fell inside them, plus one densification per refine_every steps
+    step_ms_no_densify = (1e3 * window_s - win_dens_ms) / args.steps
+    ms_per_step = step_ms_no_densify + densify_ms / cfg.refine_every
+    its = 1e3 / ms_per_step
+    cpu_state = None if args.no_cpu or args.cpu_steps <= 0 else trainer_state(tr, degree)
+    log(f"train: steps {first_step}..{first_step + args.steps - 1} in {window_s:.3f}s "
+        f"({args.steps / window_s:.1f} it/s wall, {win_dens_n} densification(s) inside); "
+        f"{step_ms_no_densify:.3f} ms/step + densify {densify_ms:.2f} ms / {cfg.refine_every} "
+        f"= {ms_per_step:.3f} ms/step = {its:.1f} it/s; gaussians {n_start} -> {tr.splat_count()}")
     if args.train_only:
         print(json.dumps({"metric": METRIC, "value": its, "unit": "it/s", "steps": args.steps,
-                          "warmup": args.warmup, "train_only": True}), flush=True)
+                          "warmup": args.warmup, "preroll": args.preroll, "train_only": True}), flush=True)
         return
     # Per-stage breakdown: further steps with every stage bracketed.
     _abi.check(lib.msplat_hip_set_stage_timing_mask(0xFFFFFFFF))
@@ -414,11 +511,13 @@ def main():
     device.sync()
     stages, _ = stage_times(lib)
     device.drain_raster_counters()
-    step_ms = sum(ms / c for ms, c in stages.values() if c)
+    parts = _stage_line(stages)
+    parts.pop("densify", None)
+    ref_stages = _reference_stages(parts)
+    step_ms = sum(parts.values())
     log(f"stage breakdown over {args.stage_steps} more steps (sum {step_ms:.3f} ms/step):")
-    for k, (ms, c) in stages.items():
-        if c:
-            log(f"  {k:18s} {ms / c:8.3f} ms/call  ({c} calls, {100 * ms / c / step_ms:5.1f}% of stage sum)")
+    for k, v in parts.items():
+        log(f"  {k:30s} {v:8.3f} ms/call  ({100 * v / step_ms:5.1f}% of stage sum)")
 
     # render FPS over the 32 camera poses (render_from_pose into a device buffer)
     out = torch.empty((cams[0].height, cams[0].width, 3), dtype=torch.float32, device="cuda")
@@ -445,9 +544,9 @@ def main():
     rstages, _ = stage_times(lib)
     device.drain_raster_counters()
     _abi.check(lib.msplat_hip_enable_stage_timing(0))
-    for k, (ms, c) in rstages.items():
-        if c:
-            log(f"  {k:18s} {ms / c:8.3f} ms/call")
+    rparts = _stage_line(rstages)
+    for k, v in rparts.items():
+        log(f"  {k:30s} {v:8.3f} ms/call")
 
     # Roofline of the dominant kernel (raster backward): algorithmic flops from
     # the GPU pair counters over exactly the timed launches, divided by those
@@ -478,7 +577,7 @@ def main():
 
     # HBM-bound stages: algorithmic bytes per launch (visible / culled
     # gaussians counted separately, from the last step's radii) over the
-    # stages' HIP-event times in the timed train steps.
+    # stages' HIP-event times.
     radii = device.intermediate("radii", np.int32)
     n_all = int(radii.size)
     n_vis = int((radii > 0).sum())
@@ -488,38 +587,50 @@ def main():
         "proj_sh_fwd": proj_bytes(n_vis, n_cul),
         # f_rest, its two moments read and written (1080 B), direction 16 B,
         # v_rgb 12 B, radii 4 B (culled: radii only)
-        "sh_rest_adam": n_vis * (1080 + 16 + 12 + 4) + n_cul * 4,
+        "proj_sh_bwd_adam.sh_rest": n_vis * (1080 + 16 + 12 + 4) + n_cul * 4,
         # dense Adam on means / scales / quats / opacity (11 floats x p, m, v
         # read + written = 264 B), f_dc Adam for visible (72 B), record 48 B,
         # gradient accumulator 36 B, radii 4 B, three statistics r + w 24 B
-        "proj_sh_bwd_adam": n_vis * (264 + 72 + 48 + 36 + 4 + 24) + n_cul * (264 + 4),
+        "proj_sh_bwd_adam.dense": n_vis * (264 + 72 + 48 + 36 + 4 + 24) + n_cul * (264 + 4),
         # read render + target, write the loss gradient image: 36 B per pixel
         "loss_fwd_bwd": 36 * px,
     }
     hbm = {}
     for k, b in algo_bytes.items():
-        ms = stages[k][0] / max(stages[k][1], 1)
+        ms = parts[k]
         hbm[k] = {"ms": ms, "bytes": b, "GBps": b / (ms * 1e-3) / 1e9, "frac": b / (ms * 1e-3) / HBM_PEAK}
-        log(f"  {k:18s} {b / 1e6:8.1f} MB algorithmic in {ms:.3f} ms = {hbm[k]['GBps']:7.0f} GB/s "
+        log(f"  {k:30s} {b / 1e6:8.1f} MB algorithmic in {ms:.3f} ms = {hbm[k]['GBps']:7.0f} GB/s "
             f"({100 * hbm[k]['frac']:.1f}% of HBM peak)")
 
     cpu = None
     if not args.no_cpu and args.cpu_steps > 0:
-        rate, cores, dt = cpu_baseline(device_params, cams, targets, degree, bg, args.cpu_steps)
+        nxt = first_step + args.steps
+        rate, cores, dt, cpu_stage_ms = cpu_baseline(cpu_state, cams, targets, degree, bg, args.cpu_steps, nxt)
         cpu = {"value": rate, "unit": "it/s", "cores": cores, "kind": "port",
-               "sample": f"{args.cpu_steps} full train steps of the same 1.5M SH3 1297x840 workload "
-                         f"(initial parameters, cameras 0..{args.cpu_steps - 1}), {dt:.1f}s"}
-        log(f"cpu baseline: {rate:.4f} it/s on {cores} threads")
+               "sample": f"{args.cpu_steps} full train steps of the same workload from the trainer's state "
+                         f"after the timed steps ({cpu_state[0][0].shape[0]} gaussians, steps {nxt}.."
+                         f"{nxt + args.cpu_steps - 1}), {dt:.1f}s",
+               **cpu_description(), "stage_ms": cpu_stage_ms,
+               "gpu_speedup_per_stage": {k: cpu_stage_ms[k] / ref_stages[k] for k in cpu_stage_ms
+                                         if ref_stages.get(k)}}
+        log(f"cpu baseline: {rate:.4f} it/s on {cores} threads ({cpu['cpu_model']}, "
+            f"OMP_PROC_BIND={cpu['binding']})")
 
     res = {
         "metric": METRIC, "value": its, "unit": "it/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": 1e3 * train_s / args.steps, "higher_is_better": True,
+        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "config3: 1.5M SH3 gaussians, 1297x840, 32 cameras cycled, densify every 100 steps",
+        "config": {"workload": "config3: 1.5M SH3 gaussians, 1297x840, 32 cameras cycled, densify every 100 "
+                               "steps; timed after the opacity reset and the first densification",
+                   "preroll_steps": args.preroll, "timed_steps": [first_step, first_step + args.steps - 1],
                    "gaussians_start": n_start, "gaussians_end": tr.splat_count(), "render_frames": args.frames},
+        "window_wall_it_s": args.steps / window_s,
+        "step_ms_without_densify": step_ms_no_densify,
+        "densify_ms": densify_ms, "densifies_measured": dens_n, "densifies_in_window": win_dens_n,
         "render_fps": fps,
-        "stage_ms": {k: ms / c for k, (ms, c) in stages.items() if c},
-        "render_stage_ms": {k: ms / c for k, (ms, c) in rstages.items() if c},
+        "stage_ms": ref_stages,
+        "stage_parts_ms": parts,
+        "render_stage_ms": _reference_stages(rparts),
         "rast_fwd_render_tflops": fwd_flops / fwd_ms / 1e9,
         "hbm_stages": hbm,
         "visible_gaussians": n_vis,

@@ -223,11 +223,18 @@ int msplat_hip_image_metrics_noalloc(const float* img, const float* gt, int32_t 
 int msplat_hip_knn_mean_dist(const float* xyz, int64_t n, float* mean_dist);
 
 /* Per-stage GPU timing (msplat_enable_gpu_timing / msplat_drain_stage_times,
- * bindings.h:28-33).  When enabled every stage of every render / train call is
- * bracketed by HIP events on the context stream (no extra synchronisation).
- * drain waits for the stream, then returns for each stage i the summed
- * milliseconds ms[i] and the number of timed instances counts[i] since the
- * last drain (or enable), its name, and the number of calls timed. */
+ * bindings.h:28-33).  When enabled every stage of every render / train /
+ * densify call is bracketed by HIP events on the context stream (no extra
+ * synchronisation).  drain waits for the stream, then returns for each stage
+ * i the summed milliseconds ms[i] and the number of timed instances
+ * counts[i] since the last drain (or enable), its name, and the number of
+ * calls timed.  Stage names are the reference profiler's
+ * (msplat_metal.mm:30-34), with ".part" where a stage runs as two kernels:
+ * proj_sh_fwd, prefix_sort_pack.depth_sort, prefix_sort_pack.tile_lists,
+ * rast_fwd, loss_fwd_bwd, rast_bwd, proj_sh_bwd_adam.sh_rest,
+ * proj_sh_bwd_adam.dense, and densify (one msplat_hip_densify call).  The
+ * reference's blit_zero is part of proj_sh_fwd here and its grad_stats part
+ * of proj_sh_bwd_adam.dense. */
 int msplat_hip_enable_stage_timing(int enable);
 /* Bracket only the stages whose bit (1 << stage index, in the order drain
  * names them) is set; the default is every stage.  Each event leaves the GPU

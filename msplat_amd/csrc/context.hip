@@ -42,13 +42,24 @@ using namespace msp;
 constexpr int kMaxDevices = 64;
 double* g_scratch_dev[kMaxDevices] = {};
 
-// Stage names (as msplat_metal.mm:30-34 where they coincide).
-constexpr int kNumStages = 8;
+// Stage names: the reference profiler's train stages (msplat_metal.mm:30-34),
+// "stage.part" where this build runs a stage as two kernels.  The
+// reference's blit_zero (zeroing the gradient buffers) is fused into
+// proj_sh_fwd (the projection zeroes each gaussian's accumulators) and its
+// grad_stats into proj_sh_bwd_adam.dense.  densify brackets a densification
+// call (msplat_densify, which the reference does not profile).
+constexpr int kNumStages = 9;
 constexpr int kMaxMarks = 12;
-const char* kStageNames[kNumStages] = {"proj_sh_fwd", "depth_sort", "tile_lists", "rast_fwd",
-                                       "loss_fwd_bwd", "rast_bwd", "sh_rest_adam",
-                                       "proj_sh_bwd_adam"};
-enum Stage { S_PROJ, S_DEPTH, S_TILES, S_RFWD, S_LOSS, S_RBWD, S_SHADAM, S_PBWD, S_END };
+const char* kStageNames[kNumStages] = {"proj_sh_fwd",
+                                       "prefix_sort_pack.depth_sort",
+                                       "prefix_sort_pack.tile_lists",
+                                       "rast_fwd",
+                                       "loss_fwd_bwd",
+                                       "rast_bwd",
+                                       "proj_sh_bwd_adam.sh_rest",
+                                       "proj_sh_bwd_adam.dense",
+                                       "densify"};
+enum Stage { S_PROJ, S_DEPTH, S_TILES, S_RFWD, S_LOSS, S_RBWD, S_SHADAM, S_PBWD, S_DENSIFY, S_END };
 
 struct Buf {
     void* p = nullptr;
@@ -103,7 +114,7 @@ struct Ctx {
     float* loss_h = nullptr;
     int* count_h = nullptr;
     // densify scratch
-    Buf d_split, d_dup, d_sp, d_dp, d_keep, d_kp, d_tot, d_scratch, d_rnd;
+    Buf d_split, d_dup, d_sp, d_dp, d_keep, d_kp, d_tot, d_scratch, d_rnd, d_src;
 
     const uint32_t* sorted_ids = nullptr;   // tile-sorted gaussian ids (tval or tval2)
     Meta meta{};
@@ -179,7 +190,7 @@ void free_all(Ctx* c) {
                    &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
                    &c->count_d, &c->work_d, &c->isect_d, &c->eval_part, &c->eval_out, &c->knn_k, &c->knn_v, &c->knn_k2, &c->knn_v2,
                    &c->knn_tmp, &c->knn_s, &c->knn_e, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
-                   &c->d_tot, &c->d_scratch, &c->d_rnd};
+                   &c->d_tot, &c->d_scratch, &c->d_rnd, &c->d_src};
     for (Buf* b : bufs)
         if (b->p) { (void)hipFree(b->p); b->p = nullptr; b->bytes = 0; }
     if (c->meta_h) (void)hipHostFree(c->meta_h);
@@ -896,8 +907,9 @@ int msplat_hip_densify(const MsplatDensifyArgs* a, int32_t* new_count) {
     ENSURE(c->d_keep, (size_t)worst * 4);
     ENSURE(c->d_kp, (size_t)worst * 4);
     ENSURE(c->d_tot, (size_t)scan_block_count(worst) * 4 + 64);
-    ENSURE(c->d_scratch, (size_t)worst * std::max(4, a->fr_stride) * 4);
     ENSURE(c->count_d, 16);
+    stage_begin(c);
+    stage_mark(c, S_DENSIFY);
     const float* rnd = a->random_samples;
     if (!rnd) {
         ENSURE(c->d_rnd, (size_t)2 * N * 3 * 4);
@@ -919,11 +931,28 @@ int msplat_hip_densify(const MsplatDensifyArgs* a, int32_t* new_count) {
     launch_densify(c->stream, hp, a->xys_grad_norm, a->vis_counts, a->max_2d_size, a->bufs,
                    a->adam_exp_avg_buf, a->adam_exp_avg_sq_buf, rnd, P<int>(c->d_split),
                    P<int>(c->d_dup), P<int>(c->d_sp), P<int>(c->d_dp), P<int>(c->d_keep),
-                   P<int>(c->d_kp), P<int>(c->d_tot), P<float>(c->d_scratch), P<int>(c->count_d));
+                   P<int>(c->d_kp), P<int>(c->d_tot), P<int>(c->count_d));
     HIP_TRY(hipGetLastError());
-    HIP_TRY(hipMemcpyAsync(c->count_h, c->count_d.p, 4, hipMemcpyDeviceToHost, c->stream));
+    // rows after appending and rows kept size the compaction exactly
+    HIP_TRY(hipMemcpyAsync(c->count_h, c->count_d.p, 8, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
-    *new_count = c->count_h[0];
+    const int rows = c->count_h[0], kept = c->count_h[1];
+    if (rows < 0 || rows > worst || kept < 0 || kept > rows)
+        return fail(MSPLAT_ERR_HIP, "densify counts out of range: %d rows, %d kept (N = %d)", rows,
+                    kept, N);
+    ENSURE(c->d_src, (size_t)std::max(kept, 1) * 4);
+    ENSURE(c->d_scratch, (size_t)densify_workspace_floats(kept, a->fr_stride) * 4);
+    launch_densify_compact(c->stream, rows, kept, a->fr_stride, a->bufs, a->adam_exp_avg_buf,
+                           a->adam_exp_avg_sq_buf, P<int>(c->d_keep), P<int>(c->d_kp),
+                           P<int>(c->d_src), P<float>(c->d_scratch));
+    HIP_TRY(hipGetLastError());
+    stage_mark(c, S_END);
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (c->timing) {   // the previous call and this one have completed
+        stage_fold(c, c->cur ^ 1);
+        stage_fold(c, c->cur);
+    }
+    *new_count = kept;
     return MSPLAT_OK;
 }
 

@@ -8,6 +8,13 @@
 // compact_copy_back (.metal:3698-3729) and the two-level block scan
 // (.metal:2368-2439).  The scans here are three-pass (block totals, scan of
 // the totals, block scans with offsets) over 1024-element blocks.
+//
+// Compaction: the reference scatters and copies back each of the 18 buffers
+// in its own pair of passes over the 3N-row worst case.  Here the host reads
+// the kept count after the keep scan, then one kernel gathers every kept row
+// of all 18 buffers, in order, into a packed workspace and one kernel copies
+// the packed rows back (float4 stores): three launches sized by the rows that
+// exist.  The order is the same stable keep-prefix order.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -148,29 +155,80 @@ __global__ __launch_bounds__(256) void k_cull(DensifyHP hp, int worst, const int
     keep[i] = cull ? 0 : 1;
 }
 
-__global__ __launch_bounds__(256) void k_compact_scatter(const float* __restrict__ src,
-                                                         float* __restrict__ dst,
-                                                         const int* __restrict__ kp,
-                                                         const int* __restrict__ keep, int64_t n,
-                                                         int stride) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t elem = t / stride, sub = t - elem * stride;
-    if (elem >= n || keep[elem] == 0) return;
-    dst[(int64_t)(kp[elem] - 1) * stride + sub] = src[t];
+// Appended rows end at N + 2 nSplits + nDups; count_out = {that, kept rows}.
+__global__ void k_read_counts(int N, const int* sp, const int* dp, const int* kp, int64_t last,
+                              int* out) {
+    out[0] = N + 2 * sp[N - 1] + dp[N - 1];
+    out[1] = kp[last];
 }
 
-__global__ __launch_bounds__(256) void k_copy_back(const float* __restrict__ src,
-                                                   float* __restrict__ dst,
-                                                   const int* __restrict__ kp, int64_t last,
-                                                   int64_t n, int stride) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= n * stride) return;
-    const int64_t cnt = kp[last];
-    if (t / stride >= cnt) return;
-    dst[t] = src[t];
+// src_of[r] = the r-th kept row (rows i < n with keep[i], in order).
+__global__ __launch_bounds__(256) void k_keep_sources(const int* __restrict__ keep,
+                                                      const int* __restrict__ kp, int n,
+                                                      int* __restrict__ src_of) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n && keep[i]) src_of[kp[i] - 1] = i;
 }
 
-__global__ void k_read_count(const int* kp, int64_t last, int* out) { out[0] = kp[last]; }
+// Workspace layout of the 18 buffers (parameters, first moments, second
+// moments; six groups each): buffer k holds cnt rows of stride st[k] floats
+// at float offset off[k] (a multiple of 4).
+struct Packed18 {
+    const float* src[18];
+    float* dst[18];
+    int st[18];
+    int64_t off[18];
+    int64_t f4_end[18];   // cumulative float4 count of the copy-back, buffers 0..k
+    int vec[18];          // the buffer is 16-byte aligned (float4 stores)
+};
+
+// Gather: workgroup b takes output rows [256 b, 256 b + 256) of every buffer,
+// reading each row from its source row (rows of one workgroup come mostly
+// from consecutive sources, so reads coalesce like the writes).
+__global__ __launch_bounds__(256) void k_gather_rows(Packed18 P, const int* __restrict__ src_of,
+                                                     int cnt, float* __restrict__ ws) {
+    __shared__ int s_src[256];
+    const int r0 = blockIdx.x * 256, tid = threadIdx.x;
+    const int nr = min(256, cnt - r0);
+    if (tid < nr) s_src[tid] = src_of[r0 + tid];
+    __syncthreads();
+    for (int k = 0; k < 18; ++k) {
+        const int st = P.st[k];
+        if (st == 0) continue;
+        const float* __restrict__ src = P.src[k];
+        float* __restrict__ dst = ws + P.off[k] + (int64_t)r0 * st;
+        // element e = lr * st + sub, advanced by 256 per step without dividing
+        const int q = 256 / st, rem = 256 - q * st;
+        int lr = tid / st, sub = tid - lr * st;
+        for (int e = tid; e < nr * st; e += 256) {
+            dst[e] = src[(int64_t)s_src[lr] * st + sub];
+            lr += q;
+            sub += rem;
+            if (sub >= st) { sub -= st; ++lr; }
+        }
+    }
+}
+
+// Copy-back of the packed rows: one thread per float4 of the 18 buffers'
+// kept rows; the workspace regions are 16-byte aligned, a buffer's last
+// float4 may be partial, and a buffer that is not 16-byte aligned is copied
+// by scalar stores.
+__global__ __launch_bounds__(256) void k_copy_back_rows(Packed18 P, int cnt,
+                                                        const float* __restrict__ ws) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= P.f4_end[17]) return;
+    int k = 0;
+    while (t >= P.f4_end[k]) ++k;
+    const int64_t i = t - (k ? P.f4_end[k - 1] : 0);
+    const int64_t nf = (int64_t)cnt * P.st[k];
+    const float* s = ws + P.off[k];
+    float* d = P.dst[k];
+    if (4 * i + 4 <= nf && P.vec[k]) {
+        reinterpret_cast<float4*>(d)[i] = reinterpret_cast<const float4*>(s)[i];
+    } else {
+        for (int64_t e = 4 * i; e < nf; ++e) d[e] = s[e];
+    }
+}
 
 // Opacity reset of afterTrain (model.cpp:280-287): logits above hi become hi.
 __global__ __launch_bounds__(256) void k_clamp_max(float* __restrict__ p, int64_t n, float hi) {
@@ -195,7 +253,7 @@ void launch_clamp_max(hipStream_t s, float* p, int64_t n, float hi) {
 void launch_densify(hipStream_t s, const DensifyHP& hp, const float* gnorm, const float* vis,
                     const float* max2d, float* const bufs[6], float* const m[6],
                     float* const v[6], const float* rnd, int* split, int* dup, int* sp, int* dp,
-                    int* keep, int* kp, int* tot, float* scratch, int* count_out) {
+                    int* keep, int* kp, int* tot, int* counts_out) {
     const int N = hp.N;
     const int64_t worst = 3 * (int64_t)N;
     Bufs18 B;
@@ -212,19 +270,41 @@ void launch_densify(hipStream_t s, const DensifyHP& hp, const float* gnorm, cons
                        (const int*)sp, (const int*)dp, (const int*)split, (const float*)bufs[5],
                        (const float*)bufs[1], max2d, keep);
     launch_scan_i32(s, keep, kp, worst, tot);
-    const int strides[6] = {3, 3, 4, 3, hp.fr, 1};
-    for (int set = 0; set < 3; ++set)
-        for (int gi = 0; gi < 6; ++gi) {
-            float* buf = set == 0 ? bufs[gi] : set == 1 ? m[gi] : v[gi];
-            const int st = strides[gi];
-            if (st == 0) continue;
-            hipLaunchKernelGGL(k_compact_scatter, dim3(blocks_for(worst * st)), dim3(256), 0, s,
-                               (const float*)buf, scratch, (const int*)kp, (const int*)keep, worst,
-                               st);
-            hipLaunchKernelGGL(k_copy_back, dim3(blocks_for(worst * st)), dim3(256), 0, s,
-                               (const float*)scratch, buf, (const int*)kp, worst - 1, worst, st);
-        }
-    hipLaunchKernelGGL(k_read_count, dim3(1), dim3(1), 0, s, (const int*)kp, worst - 1, count_out);
+    hipLaunchKernelGGL(k_read_counts, dim3(1), dim3(1), 0, s, N, (const int*)sp, (const int*)dp,
+                       (const int*)kp, worst - 1, counts_out);
+}
+
+int64_t densify_workspace_floats(int cnt, int fr) {
+    const int64_t rows = ((int64_t)cnt + 3) & ~(int64_t)3;
+    return rows * 3 * (3 + 3 + 4 + 3 + fr + 1);
+}
+
+void launch_densify_compact(hipStream_t s, int rows, int cnt, int fr, float* const bufs[6],
+                            float* const m[6], float* const v[6], const int* keep,
+                            const int* kp, int* src_of, float* ws) {
+    if (cnt <= 0) return;
+    const int strides[6] = {3, 3, 4, 3, fr, 1};
+    const int64_t cap = ((int64_t)cnt + 3) & ~(int64_t)3;
+    Packed18 P;
+    int64_t off = 0, f4 = 0;
+    for (int k = 0; k < 18; ++k) {
+        const int g = k % 6, set = k / 6;
+        float* b = set == 0 ? bufs[g] : set == 1 ? m[g] : v[g];
+        P.src[k] = b;
+        P.dst[k] = b;
+        P.st[k] = strides[g];
+        P.off[k] = off;
+        P.vec[k] = (reinterpret_cast<uintptr_t>(b) & 15) == 0;
+        off += cap * strides[g];
+        f4 += ((int64_t)cnt * strides[g] + 3) / 4;
+        P.f4_end[k] = f4;
+    }
+    hipLaunchKernelGGL(k_keep_sources, dim3(blocks_for(rows)), dim3(256), 0, s, keep, kp, rows,
+                       src_of);
+    hipLaunchKernelGGL(k_gather_rows, dim3(blocks_for(cnt)), dim3(256), 0, s, P,
+                       (const int*)src_of, cnt, ws);
+    hipLaunchKernelGGL(k_copy_back_rows, dim3(blocks_for(f4)), dim3(256), 0, s, P, cnt,
+                       (const float*)ws);
 }
 
 }  // namespace msp

@@ -171,11 +171,18 @@ struct DensifyHP {
 };
 void launch_randn(hipStream_t s, float* dst, int64_t n, uint64_t seed);
 void launch_clamp_max(hipStream_t s, float* p, int64_t n, float hi);
+// Classify, split / duplicate append, cull flags and keep scan; writes
+// counts_out[0] = rows after appending, counts_out[1] = rows kept.
 void launch_densify(hipStream_t s, const DensifyHP& hp, const float* gnorm, const float* vis,
                     const float* max2d, float* const bufs[6], float* const m[6],
                     float* const v[6], const float* rnd, int* split, int* dup, int* sp,
-                    int* dp, int* keep, int* kp, int* block_tot, float* scratch,
-                    int* count_out);
+                    int* dp, int* keep, int* kp, int* block_tot, int* counts_out);
+// Stable compaction of the cnt kept rows (of `rows` rows) of all 18 buffers
+// through a workspace of densify_workspace_floats(cnt, fr) floats.
+int64_t densify_workspace_floats(int cnt, int fr);
+void launch_densify_compact(hipStream_t s, int rows, int cnt, int fr, float* const bufs[6],
+                            float* const m[6], float* const v[6], const int* keep,
+                            const int* kp, int* src_of, float* ws);
 
 // Evaluation images: RGBA8 display conversion and PSNR / L1 / SSIM.
 struct EvalWindow {

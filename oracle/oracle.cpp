@@ -38,6 +38,7 @@
 #include "oracle.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -541,9 +542,31 @@ inline void raster_pixel_bwd(const Entry* ent, int s, int bin_final, float px, f
 }  // namespace
 
 // ======================================================================
+// Per-stage wall time of orc_train_step, under the reference profiler's
+// train stage names (msplat_metal.mm:30-34): blit_zero, proj_sh_fwd,
+// prefix_sort_pack, rast_fwd, loss_fwd_bwd, rast_bwd, proj_sh_bwd_adam,
+// grad_stats (blit_zero stays 0: the buffers are zeroed as they are made).
+double g_stage_ms[8] = {};
+int64_t g_stage_steps = 0;
+struct StageClock {
+    std::chrono::steady_clock::time_point t = std::chrono::steady_clock::now();
+    void lap(int stage) {
+        const auto now = std::chrono::steady_clock::now();
+        g_stage_ms[stage] += std::chrono::duration<double, std::milli>(now - t).count();
+        t = now;
+    }
+    ~StageClock() { ++g_stage_steps; }
+};
+
 extern "C" {
 
 uint32_t orc_version(void) { return 1; }
+
+void orc_stage_times(double ms[8], int64_t* steps) {
+    for (int i = 0; i < 8; ++i) { ms[i] = g_stage_ms[i]; g_stage_ms[i] = 0.0; }
+    if (steps) *steps = g_stage_steps;
+    g_stage_steps = 0;
+}
 
 int32_t orc_num_threads(void) {
 #ifdef _OPENMP
@@ -1002,31 +1025,37 @@ float orc_train_step(const OrcCamera* cam, int32_t N, int32_t rest_bases,
     const int W = cam->width, H = cam->height, T = tiles_x(cam) * tiles_y(cam);
     const size_t P = (size_t)H * W;
     const int rp = rest_bases * 3;
+    StageClock clk;
     std::vector<float> xys(2 * (size_t)N, 0.f), depths(N, 0.f), conics(3 * (size_t)N, 0.f),
         colors(3 * (size_t)N, 0.f), aabb(2 * (size_t)N, 0.f);
     std::vector<int32_t> radii(N), nth(N);
     orc_project_forward(cam, N, params[0], params[1], params[2], params[3], params[4], xys.data(),
                         depths.data(), radii.data(), conics.data(), nth.data(), colors.data(),
                         aabb.data());
+    clk.lap(1);   // proj_sh_fwd
     int64_t cap = 0;
     for (int32_t g = 0; g < N; ++g) cap += nth[g];
     std::vector<int32_t> tile_bins(2 * (size_t)T), ids((size_t)std::max<int64_t>(cap, 1));
     if (orc_bin_sort(cam, N, xys.data(), depths.data(), radii.data(), aabb.data(), cap, nullptr,
                      tile_bins.data(), ids.data()) < 0)
         return std::numeric_limits<float>::quiet_NaN();
+    clk.lap(2);   // prefix_sort_pack
     std::vector<float> Ts(P), img(P * 3), v_rendered(P * 3);
     std::vector<int32_t> fidx(P);
     // Forward first (image needed by the loss), backward after the loss.
     orc_rasterize(cam, N, xys.data(), conics.data(), colors.data(), params[5], tile_bins.data(),
                   ids.data(), Ts.data(), fidx.data(), img.data(), nullptr, nullptr, nullptr,
                   nullptr, nullptr);
+    clk.lap(3);   // rast_fwd
     const float inv_n = 1.0f / (float)(H * W * 3);
     const double loss_sum = orc_ssim_loss(H, W, img.data(), gt, ssim_weight, inv_n,
                                           v_rendered.data(), nullptr, nullptr);
+    clk.lap(4);   // loss_fwd_bwd
     std::vector<float> v_xy(2 * (size_t)N), v_conic(3 * (size_t)N), v_rgb(3 * (size_t)N), v_op(N);
     orc_rasterize(cam, N, xys.data(), conics.data(), colors.data(), params[5], tile_bins.data(),
                   ids.data(), Ts.data(), fidx.data(), img.data(), v_rendered.data(), v_xy.data(),
                   v_conic.data(), v_rgb.data(), v_op.data());
+    clk.lap(5);   // rast_bwd (the backward call recomputes each pixel's forward)
     std::vector<float> v_mean(3 * (size_t)N), v_scale(3 * (size_t)N), v_quat(4 * (size_t)N);
     orc_project_backward(cam, N, params[0], params[1], params[2], radii.data(), conics.data(),
                          v_xy.data(), v_conic.data(), v_mean.data(), v_scale.data(), v_quat.data());
@@ -1058,8 +1087,10 @@ float orc_train_step(const OrcCamera* cam, int32_t N, int32_t rest_bases,
     for (int gi : {0, 1, 2, 5})
         orc_adam(numel[gi], params[gi], grads[gi], m[gi], v[gi], ad->step_size[gi], ad->beta1,
                  ad->beta2, ad->bc2_sqrt[gi], ad->eps);
+    clk.lap(6);   // proj_sh_bwd_adam
     orc_grad_stats(N, radii.data(), v_xy.data(), vis, gnorm, max2d,
                    1.0f / (float)std::max(H, W));
+    clk.lap(7);   // grad_stats
     if (out) {
         if (out->out_img) std::memcpy(out->out_img, img.data(), P * 3 * sizeof(float));
         if (out->radii) std::memcpy(out->radii, radii.data(), (size_t)N * 4);

@@ -50,6 +50,12 @@ typedef struct OrcAdam {
 
 uint32_t orc_version(void);
 int32_t orc_num_threads(void);
+/* Summed wall milliseconds per train stage of the orc_train_step calls since
+ * the last call (blit_zero, proj_sh_fwd, prefix_sort_pack, rast_fwd,
+ * loss_fwd_bwd, rast_bwd, proj_sh_bwd_adam, grad_stats; the names of the
+ * reference profiler, msplat_metal.mm:30-34) and the number of steps; resets
+ * the sums. */
+void orc_stage_times(double ms[8], int64_t* steps);
 
 /* ---- scalar building blocks (exported for the closed-form tests) ---- */
 float orc_expf(float x);

@@ -193,8 +193,36 @@ def test_stage_timing_mask(dev):
             assert np.allclose(x, y, rtol=1e-4, atol=1e-6)
 
 
-STAGE_NAMES = ["proj_sh_fwd", "depth_sort", "tile_lists", "rast_fwd", "loss_fwd_bwd", "rast_bwd",
-               "sh_rest_adam", "proj_sh_bwd_adam"]
+# the eight stages of a train step, in the order of their timing-mask bits
+# (bit 8, densify, brackets densification calls)
+STAGE_NAMES = ["proj_sh_fwd", "prefix_sort_pack.depth_sort", "prefix_sort_pack.tile_lists", "rast_fwd",
+               "loss_fwd_bwd", "rast_bwd", "proj_sh_bwd_adam.sh_rest", "proj_sh_bwd_adam.dense"]
+
+
+def test_densify_stage_timing(dev):
+    """A densification call is bracketed as the "densify" stage (timing bit
+    8), one timed instance per call, and brackets nothing else."""
+    torch = pytest.importorskip("torch")
+    sc = small_scene(n=3000, seed_off=87)
+    n = sc.n
+    g = dev.DeviceGaussians.from_arrays(sc.params(), 3, capacity=3 * n)
+    g.vis[:n].fill_(1.0)
+    g.gnorm[:n].fill_(1e-3)
+    lib = dev.init()
+    try:
+        dev._abi.check(lib.msplat_hip_set_stage_timing_mask(1 << 8))
+        dev._abi.check(lib.msplat_hip_enable_stage_timing(1))
+        nn = dev.densify(g, grad_thresh=2e-4, size_thresh=0.01, screen_thresh=0.05, check_screen=1,
+                         cull_alpha=0.005, cull_scale=0.5, cull_screen=0.15, check_huge=0, half_max_dim=80.0,
+                         seed=5)
+        st = _drain_stages(dev)
+    finally:
+        dev._abi.check(lib.msplat_hip_set_stage_timing_mask(0xFFFFFFFF))
+        dev._abi.check(lib.msplat_hip_enable_stage_timing(0))
+    assert nn > n
+    assert st["densify"][1] == 1 and st["densify"][0] > 0, st
+    assert all(c == 0 for k, (ms, c) in st.items() if k != "densify"), st
+    torch.cuda.synchronize()
 
 
 def test_train_three_steps(dev):

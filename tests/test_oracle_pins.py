@@ -819,3 +819,30 @@ def test_knn_mean_dist_against_kdtree():
         want = d[:, 1:].mean(axis=1)
         assert np.allclose(got, want, rtol=2e-6, atol=1e-7)
         assert not np.allclose(d[:, :3].mean(axis=1), want, rtol=2e-6, atol=1e-7)
+
+
+def test_train_step_stage_times():
+    """orc_stage_times: one train step's reference-named stages add up to
+    about its wall time, and the sums reset."""
+    import time
+    sc = small_scene(n=800, width=64, height=48, seed_off=250)
+    su = camera.prepare_cam(sc.cameras[0])
+    cam = orc.camera(su, 3, 3, BG)
+    gt = np.zeros((su.height, su.width, 3), F32)
+    params = [np.ascontiguousarray(a, F32).copy() for a in sc.params()]
+    m = [np.zeros_like(a) for a in params]
+    v = [np.zeros_like(a) for a in params]
+    z = [np.zeros(sc.n, F32) for _ in range(3)]
+    ms = (ctypes.c_double * 8)()
+    steps = ctypes.c_int64(0)
+    orc.lib().orc_stage_times(ms, ctypes.byref(steps))
+    t0 = time.perf_counter()
+    orc.train_step(cam, params, m, v, orc.adam_hparams([1e-3] * 6, 1), gt, 0.2, *z)
+    wall = 1e3 * (time.perf_counter() - t0)
+    orc.lib().orc_stage_times(ms, ctypes.byref(steps))
+    assert steps.value == 1
+    tot = sum(ms)
+    assert all(x >= 0 for x in ms) and ms[1] > 0 and ms[3] > 0 and ms[5] > 0
+    assert 0.5 * wall <= tot <= wall, (tot, wall)
+    orc.lib().orc_stage_times(ms, ctypes.byref(steps))
+    assert steps.value == 0 and sum(ms) == 0.0
