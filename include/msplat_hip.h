@@ -245,6 +245,13 @@ int msplat_hip_set_stage_timing_mask(uint32_t mask);
 int msplat_hip_drain_stage_times(double* ms, int64_t* counts, const char** names, int max_stages,
                                  int* n_stages, int64_t* n_calls);
 
+/* The bracketed GPU milliseconds of each timed call since the last drain (or
+ * enable), in call order: the sum of its stages' intervals, all stages with
+ * the default mask (msplat_drain_gpu_times, bindings.h:29-30, which the
+ * reference fills per command buffer).  Waits for the stream; fills up to
+ * max_calls values (the context keeps the latest 65536) and clears them. */
+int msplat_hip_drain_call_times(double* ms, int max_calls, int* n_calls);
+
 /* While stage timing is enabled the rasteriser also counts, on the GPU,
  * counts[0] (pixel, entry) pairs composited by the forward, counts[1] pairs
  * that carry a gradient in the backward, and counts[2] / counts[3] the

@@ -1,20 +1,22 @@
 /*
- * msplat_trainer.h — C API of the host-side trainer (libmsplat_hip.so).
+ * msplat_trainer.h — the host-side trainer's C API beyond the reference's
+ * (libmsplat_hip.so).
  *
- * Mirrors the trainer part of the reference's C API
- * (core/include/msplat_c_api.h:16-118: MsplatConfig, MsplatStats,
- * MsplatPixelBuffer, msplat_trainer_step / render / render_pose /
- * render_pose_to_buffer / splat_count / iteration / destroy) and of
- * GaussianTrainer (python/bindings.cpp:101-280).  The reference builds a
- * trainer from a Dataset (COLMAP / Nerfstudio loading, out of scope here);
- * this one is built from gaussian parameter arrays, cameras and target
- * images, host or device resident.  Everything runs through the C ABI of
- * msplat_hip.h; call msplat_hip_init first.
+ * include/msplat_c_api.h holds the reference's C API with its exact
+ * prototypes (core/include/msplat_c_api.h: MsplatConfig, MsplatStats,
+ * MsplatEvalMetrics, MsplatPixelBuffer, the dataset and trainer calls); this
+ * header adds what the MI355X build offers next to it: a trainer built from
+ * gaussian arrays, cameras and target images already in memory (host or
+ * device), evaluation on caller-supplied images, render into a device buffer,
+ * the lower-level COLMAP reader, PLY resume and scene-file writers, the
+ * camera set-up, an image-decoder hook and error messages.
  */
 #ifndef MSPLAT_TRAINER_H
 #define MSPLAT_TRAINER_H
 
 #include <stdint.h>
+
+#include "msplat_c_api.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -81,100 +83,42 @@ typedef struct MsplatCamSetup {
  * device work).  Returns 0 or a negative code. */
 int32_t msplat_prepare_cam(const MsplatTrainerCamera* cam, int32_t downscale, MsplatCamSetup* out);
 
-/* MsplatStats (msplat_c_api.h:58-62). */
-typedef struct MsplatStats {
-    int32_t iteration;
-    int32_t splatCount;
-    float msPerStep;
-} MsplatStats;
-
-/* MsplatPixelBuffer (msplat_c_api.h:74-78): RGB float32 HWC, caller free()s. */
-typedef struct MsplatPixelBuffer {
-    float* data;
-    int32_t width;
-    int32_t height;
-} MsplatPixelBuffer;
-
-typedef void* MsplatTrainer;
-
-/* Builds a trainer.  params[6] = means[N,3], scales[N,3] (log), quats[N,4]
+/* Builds a trainer from arrays (the reference builds one from a dataset,
+ * msplat_trainer_create in msplat_c_api.h).  params[6] = means[N,3], scales[N,3] (log), quats[N,4]
  * (w,x,y,z), f_dc[N,3], f_rest[N,(shDegree+1)^2-1,3], opacities[N] (logits);
  * targets[i] is the full-resolution [H,W,3] image of cameras[i] (images for
  * downscaled steps are box-filtered from it once, on the host).
  * on_device: 1 if params and targets are device pointers.  Returns NULL on
  * error (message in msplat_trainer_last_error). */
-MsplatTrainer msplat_trainer_create(const MsplatTrainerConfig* config, int64_t n,
-                                    const float* const params[6], int32_t n_cameras,
-                                    const MsplatTrainerCamera* cameras,
-                                    const float* const* targets, int32_t on_device);
-void msplat_trainer_destroy(MsplatTrainer t);
+MsplatTrainer msplat_trainer_create_from_arrays(const MsplatTrainerConfig* config, int64_t n,
+                                                const float* const params[6], int32_t n_cameras,
+                                                const MsplatTrainerCamera* cameras,
+                                                const float* const* targets, int32_t on_device);
+/* Message of the latest failed call of this API or of msplat_c_api.h ("" if
+ * the latest call succeeded). */
 const char* msplat_trainer_last_error(void);
-
-/* One training iteration (GaussianTrainer::step, bindings.cpp:144-167):
- * fullIteration, schedulersStep, afterTrain, commit.  msPerStep is host
- * time of the enqueue (the reference measures the same span). */
-MsplatStats msplat_trainer_step(MsplatTrainer t);
 
 /* Loss of the most recent step known to have completed (wait = 0) or of
  * the latest step (wait = 1). */
 float msplat_trainer_last_loss(MsplatTrainer t, int32_t wait);
 
-/* Render camera cameraIndex at the current step's resolution (host copy). */
-MsplatPixelBuffer msplat_trainer_render(MsplatTrainer t, int32_t cameraIndex);
-
-/* Render an arbitrary pose with the intrinsics of refCameraIndex
- * (render_from_pose, bindings.cpp:236-259; msplat_c_api.h:101). */
-MsplatPixelBuffer msplat_trainer_render_pose(MsplatTrainer t, const float camToWorld[16],
-                                             int32_t refCameraIndex);
-
-/* Same into a caller-provided RGBA8 host buffer (msplat_c_api.h:106-108):
- * call with outRGBA = NULL to get the size.  Each channel is clamped to
- * [0, 1], times 255, truncated (msplat_api.mm:230-238); the conversion runs
- * on the GPU and 4 bytes per pixel are copied.  Returns 0 or a negative
- * code. */
-int32_t msplat_trainer_render_pose_to_buffer(MsplatTrainer t, const float camToWorld[16],
-                                             int32_t refCameraIndex, uint8_t* outRGBA,
-                                             int32_t* outWidth, int32_t* outHeight);
-
-/* Same, rendered straight into a caller-provided device buffer of H*W*3
- * floats (no copy, no synchronisation; outDevice NULL: size only): the
- * display-loop form of renderFromPoseToBuffer. */
+/* msplat_trainer_render_pose rendered straight into a caller-provided
+ * device buffer of H*W*3 floats (no copy, no synchronisation; outDevice
+ * NULL: size only): the display-loop form of renderFromPoseToBuffer. */
 int32_t msplat_trainer_render_pose_device(MsplatTrainer t, const float camToWorld[16],
                                           int32_t refCameraIndex, float* outDevice,
                                           int32_t* outWidth, int32_t* outHeight);
 
-/* MsplatEvalMetrics (msplat_c_api.h:64-70). */
-typedef struct MsplatEvalMetrics {
-    float psnr;
-    float ssim;
-    float l1;
-    int32_t numTest;
-    int32_t numGaussians;
-} MsplatEvalMetrics;
-
-/* Evaluation on held-out cameras (msplat_trainer_evaluate, msplat_c_api.h:99;
- * Trainer::evaluate, msplat_api.mm:138-166): each camera is rendered at the
- * final iteration's resolution, its full-resolution target is box-filtered
- * to that size, and PSNR / SSIM (11 taps, sigma 1.5) / L1 are averaged over
- * the cameras (msplat_hip_image_metrics).  The reference's test cameras come
- * from its dataset; here they are passed in (images on the device when
- * on_device != 0).  numTest = 0 on error. */
-MsplatEvalMetrics msplat_trainer_evaluate(MsplatTrainer t, int32_t n_test,
-                                          const MsplatTrainerCamera* cameras,
-                                          const float* const* images, int32_t on_device);
-
-/* Scene files (msplat_c_api.h:109-110; Trainer::exportPly / exportSplat,
- * msplat_api.mm:240-246; layouts of save_gaussians.cpp).  0 or a negative
- * code (message in msplat_trainer_last_error). */
-int32_t msplat_trainer_export_ply(MsplatTrainer t, const char* path);
-int32_t msplat_trainer_export_splat(MsplatTrainer t, const char* path);
-
-/* Checkpoints in the reference's .msplat byte format (msplat_c_api.h:111-112;
- * Model::saveCheckpoint / loadCheckpoint, model.cpp:361-488).  load returns
- * the saved step (>= 0; training continues after it, with the camera order
- * reshuffled as Trainer::loadCheckpoint does) or a negative code. */
-int32_t msplat_trainer_save_checkpoint(MsplatTrainer t, const char* path);
-int32_t msplat_trainer_load_checkpoint(MsplatTrainer t, const char* path);
+/* Evaluation on caller-supplied cameras and full-resolution images (images
+ * on the device when on_device != 0), as msplat_trainer_evaluate does for a
+ * dataset's test cameras (Trainer::evaluate, msplat_api.mm:138-166): each
+ * camera is rendered at the final iteration's resolution, its image is
+ * box-filtered to that size, and PSNR / SSIM (11 taps, sigma 1.5) / L1 are
+ * averaged over the cameras (msplat_hip_image_metrics).  numTest = 0 on
+ * error. */
+MsplatEvalMetrics msplat_trainer_evaluate_images(MsplatTrainer t, int32_t n_test,
+                                                 const MsplatTrainerCamera* cameras,
+                                                 const float* const* images, int32_t on_device);
 
 /* Resume from an exported PLY (the CLI's --resume, cli/msplat.cpp:132;
  * Model::loadPly, model.cpp:319-330): replaces the gaussians, restarts the
@@ -190,7 +134,7 @@ int32_t msplat_trainer_set_crs(MsplatTrainer t, float scale, const float transla
 
 /* Host-memory scene files (no GPU call): the writers and the reader behind
  * the trainer's exports, for parameter arrays already in host memory
- * (params[6] as for msplat_trainer_create; opacities [n]).  read: call with
+ * (params[6] as for msplat_trainer_create_from_arrays; opacities [n]).  read: call with
  * params == NULL for *n and *rest_bases, then with six buffers of those
  * sizes.  0 or a negative code (message in msplat_trainer_last_error). */
 int32_t msplat_scene_write_ply(const char* path, int64_t n, int32_t rest_bases,
@@ -203,23 +147,21 @@ int32_t msplat_scene_read_ply(const char* path, float crs_scale, const float crs
                               int32_t keep_crs, int64_t* n, int32_t* rest_bases, int32_t* step,
                               float* const params[6]);
 
-/* A COLMAP dataset (msplat_dataset_create, msplat_c_api.h:84-89; loadColmap,
- * load_colmap.cpp:121-164): cameras.bin / images.bin / points3D.bin (or
- * points3D.ply) under path or path/sparse/0, cameras sorted by image name,
- * OpenGL camera-to-world poses, then autoScaleAndCenter
- * (input_data.cpp:79-125).  image_dir NULL: path/images if present, else
- * path.  Images are not decoded: each camera carries its image path and the
- * caller supplies pixels to msplat_trainer_create.  NULL on error. */
-typedef void* MsplatDataset;
-MsplatDataset msplat_dataset_create(const char* path, const char* image_dir);
-void msplat_dataset_destroy(MsplatDataset ds);
+/* A COLMAP reconstruction without its images (the reader under
+ * msplat_dataset_create; loadColmap, load_colmap.cpp:121-164):
+ * cameras.bin / images.bin / points3D.bin (or points3D.ply) under path or
+ * path/sparse/0, cameras sorted by image name, OpenGL camera-to-world poses,
+ * then autoScaleAndCenter (input_data.cpp:79-125).  image_dir NULL:
+ * path/images if present, else path.  Each camera carries its image path; the
+ * caller decodes and supplies pixels to msplat_trainer_create_from_arrays.
+ * Every camera counts as a training camera.  Released with
+ * msplat_dataset_destroy.  NULL on error. */
+MsplatDataset msplat_dataset_open_colmap(const char* path, const char* image_dir);
 int32_t msplat_dataset_num_cameras(MsplatDataset ds);
 /* Camera i: intrinsics and pose (cam), distortion k1 k2 p1 p2 (nullable),
  * image path (nullable; valid while ds lives). */
 int32_t msplat_dataset_camera(MsplatDataset ds, int32_t i, MsplatTrainerCamera* cam,
                               float distortion[4], const char** image_path);
-/* msplat_dataset_camera_pose (msplat_c_api.h:115). */
-int32_t msplat_dataset_camera_pose(MsplatDataset ds, int32_t i, float camToWorld[16]);
 int64_t msplat_dataset_num_points(MsplatDataset ds);
 /* Normalised points [n,3] and colours [n,3] (either nullable). */
 int32_t msplat_dataset_points(MsplatDataset ds, float* xyz, uint8_t* rgb);
@@ -230,14 +172,29 @@ int32_t msplat_dataset_normalisation(MsplatDataset ds, float* scale, float trans
  * run on the GPU (msplat_hip_knn_mean_dist). */
 int32_t msplat_dataset_init_gaussians(MsplatDataset ds, int32_t sh_degree, float* const params[6]);
 
-int32_t msplat_trainer_splat_count(MsplatTrainer t);
-int32_t msplat_trainer_iteration(MsplatTrainer t);
-
 /* Device pointer and row count of parameter group g (0..5) or of its Adam
  * moments (which = 0 params, 1 exp_avg, 2 exp_avg_sq); the first
  * splat_count rows are active.  Valid until the next step. */
 int32_t msplat_trainer_group(MsplatTrainer t, int32_t g, int32_t which, float** devPtr,
                              int64_t* rows, int64_t* rowFloats);
+
+/* Image decoding for msplat_dataset_create: a function that decodes the
+ * file at path into a malloc'ed float32 RGB HWC buffer in [0, 1] (*rgb, which
+ * the library free()s) of *width x *height pixels and returns 0, or returns
+ * nonzero if it cannot.  PNG files are decoded by the library itself; other
+ * formats (e.g. the JPEG files of most COLMAP datasets) need a registered
+ * decoder.  NULL removes it. */
+typedef int (*MsplatImageDecoder)(const char* path, float** rgb, int* width, int* height);
+void msplat_set_image_decoder(MsplatImageDecoder decoder);
+
+/* An image file decoded as msplat_dataset_create decodes it (the registered
+ * decoder, else the built-in PNG decoder: colour types grey, RGB, palette,
+ * grey + alpha and RGBA at 1-16 bits, not interlaced; alpha dropped, 16-bit
+ * samples by their high byte, each channel byte / 255 as imreadRGB,
+ * image_io.cpp:12-50): a malloc'ed float32 RGB HWC buffer in *rgb that the
+ * caller free()s.  Host only.  0 or a negative code (message in
+ * msplat_trainer_last_error). */
+int32_t msplat_image_read(const char* path, float** rgb, int32_t* width, int32_t* height);
 
 #ifdef __cplusplus
 }

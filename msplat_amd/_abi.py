@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
+from ctypes import POINTER, c_bool, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmsplat_hip.so")
@@ -102,6 +102,34 @@ class TrainerConfig(ctypes.Structure):
     ]
 
 
+class Config(ctypes.Structure):
+    """MsplatConfig (include/msplat_c_api.h, the reference's layout)."""
+
+    _fields_ = [
+        ("iterations", c_int), ("shDegree", c_int), ("shDegreeInterval", c_int),
+        ("ssimWeight", c_float), ("numDownscales", c_int), ("resolutionSchedule", c_int),
+        ("refineEvery", c_int), ("warmupLength", c_int), ("resetAlphaEvery", c_int),
+        ("densifyGradThresh", c_float), ("densifySizeThresh", c_float), ("stopScreenSizeAt", c_int),
+        ("splitScreenSize", c_float), ("keepCrs", c_bool), ("downscaleFactor", c_float),
+        ("bgColor", c_float * 3),
+    ]
+
+
+def default_config() -> Config:
+    """msplat_default_config() (a static inline function of the header)."""
+    c = Config()
+    c.iterations, c.shDegree, c.shDegreeInterval, c.ssimWeight = 30000, 3, 1000, 0.2
+    c.numDownscales, c.resolutionSchedule, c.refineEvery, c.warmupLength = 2, 3000, 100, 500
+    c.resetAlphaEvery, c.densifyGradThresh, c.densifySizeThresh = 30, 0.0002, 0.01
+    c.stopScreenSizeAt, c.splitScreenSize, c.keepCrs, c.downscaleFactor = 4000, 0.05, False, 1.0
+    c.bgColor[:] = [0.6130, 0.0101, 0.3984]
+    return c
+
+
+# int (*)(const char* path, float** rgb, int* width, int* height)
+ImageDecoder = ctypes.CFUNCTYPE(c_int, c_char_p, POINTER(POINTER(c_float)), POINTER(c_int), POINTER(c_int))
+
+
 class TrainerCamera(ctypes.Structure):
     """MsplatTrainerCamera (include/msplat_trainer.h)."""
 
@@ -118,13 +146,13 @@ class CamSetupC(ctypes.Structure):
 
 
 class Stats(ctypes.Structure):
-    """MsplatStats (include/msplat_trainer.h)."""
+    """MsplatStats (include/msplat_c_api.h)."""
 
     _fields_ = [("iteration", c_int32), ("splatCount", c_int32), ("msPerStep", c_float)]
 
 
 class PixelBuffer(ctypes.Structure):
-    """MsplatPixelBuffer (include/msplat_trainer.h)."""
+    """MsplatPixelBuffer (include/msplat_c_api.h)."""
 
     _fields_ = [("data", POINTER(c_float)), ("width", c_int32), ("height", c_int32)]
 
@@ -136,14 +164,14 @@ class ImageMetrics(ctypes.Structure):
 
 
 class EvalMetrics(ctypes.Structure):
-    """MsplatEvalMetrics (include/msplat_trainer.h)."""
+    """MsplatEvalMetrics (include/msplat_c_api.h)."""
 
     _fields_ = [("psnr", c_float), ("ssim", c_float), ("l1", c_float), ("numTest", c_int32),
                 ("numGaussians", c_int32)]
 
 
-# (name, restype, argtypes) for every symbol declared in include/msplat_hip.h
-# and include/msplat_trainer.h
+# (name, restype, argtypes) for every symbol declared in include/msplat_hip.h,
+# include/msplat_c_api.h and include/msplat_trainer.h
 SIGNATURES = [
     ("msplat_hip_init", c_int, [c_int]),
     ("msplat_hip_shutdown", c_int, []),
@@ -170,6 +198,7 @@ SIGNATURES = [
      [POINTER(c_double), POINTER(c_int64), POINTER(c_char_p), c_int, POINTER(c_int), POINTER(c_int64)]),
     ("msplat_hip_copy_intermediate", c_int, [c_char_p, c_void_p, POINTER(c_size_t)]),
     ("msplat_hip_raster_work", c_int, [POINTER(c_int64)]),
+    ("msplat_hip_drain_call_times", c_int, [POINTER(c_double), c_int, POINTER(c_int)]),
     ("msplat_hip_drain_raster_counters", c_int, [POINTER(c_int64)]),
     ("msplat_hip_image_to_rgba8", c_int, [c_void_p, c_int64, c_void_p]),
     ("msplat_hip_knn_mean_dist", c_int, [c_void_p, c_int64, c_void_p]),
@@ -181,26 +210,40 @@ SIGNATURES = [
      [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, POINTER(ImageMetrics)]),
     ("msplat_hip_image_metrics_noalloc", c_int,
      [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, POINTER(ImageMetrics)]),
-    # include/msplat_trainer.h
-    ("msplat_trainer_create", c_void_p,
-     [POINTER(TrainerConfig), c_int64, c_void_p * 6, c_int32, POINTER(TrainerCamera), POINTER(c_void_p), c_int32]),
+    # include/msplat_c_api.h (the reference's C API)
+    ("msplat_dataset_create", c_void_p, [c_char_p, c_float, c_bool, c_int]),
+    ("msplat_dataset_destroy", None, [c_void_p]),
+    ("msplat_dataset_num_train", c_int, [c_void_p]),
+    ("msplat_dataset_num_test", c_int, [c_void_p]),
+    ("msplat_trainer_create", c_void_p, [c_void_p, Config]),
     ("msplat_trainer_destroy", None, [c_void_p]),
-    ("msplat_trainer_last_error", c_char_p, []),
     ("msplat_trainer_step", Stats, [c_void_p]),
+    ("msplat_trainer_train", None, [c_void_p]),
+    ("msplat_trainer_evaluate", EvalMetrics, [c_void_p]),
+    ("msplat_trainer_render", PixelBuffer, [c_void_p, c_int, c_bool]),
+    ("msplat_trainer_render_pose", PixelBuffer, [c_void_p, POINTER(c_float), c_int]),
+    ("msplat_trainer_render_pose_to_buffer", None,
+     [c_void_p, POINTER(c_float), c_int, c_void_p, POINTER(c_int), POINTER(c_int)]),
+    ("msplat_trainer_export_ply", None, [c_void_p, c_char_p]),
+    ("msplat_trainer_export_splat", None, [c_void_p, c_char_p]),
+    ("msplat_trainer_save_checkpoint", None, [c_void_p, c_char_p]),
+    ("msplat_trainer_load_checkpoint", c_int, [c_void_p, c_char_p]),
+    ("msplat_trainer_splat_count", c_int, [c_void_p]),
+    ("msplat_trainer_iteration", c_int, [c_void_p]),
+    ("msplat_dataset_camera_pose", None, [c_void_p, c_int, POINTER(c_float)]),
+    ("msplat_set_metallib_path", None, [c_char_p]),
+    ("msplat_sync", None, []),
+    ("msplat_cleanup", None, []),
+    # include/msplat_trainer.h
+    ("msplat_trainer_create_from_arrays", c_void_p,
+     [POINTER(TrainerConfig), c_int64, c_void_p * 6, c_int32, POINTER(TrainerCamera), POINTER(c_void_p), c_int32]),
+    ("msplat_trainer_last_error", c_char_p, []),
     ("msplat_trainer_last_loss", c_float, [c_void_p, c_int32]),
-    ("msplat_trainer_render", PixelBuffer, [c_void_p, c_int32]),
-    ("msplat_trainer_render_pose", PixelBuffer, [c_void_p, POINTER(c_float), c_int32]),
-    ("msplat_trainer_render_pose_to_buffer", c_int32,
-     [c_void_p, POINTER(c_float), c_int32, c_void_p, POINTER(c_int32), POINTER(c_int32)]),
     ("msplat_trainer_render_pose_device", c_int32,
      [c_void_p, POINTER(c_float), c_int32, c_void_p, POINTER(c_int32), POINTER(c_int32)]),
     ("msplat_prepare_cam", c_int32, [POINTER(TrainerCamera), c_int32, POINTER(CamSetupC)]),
-    ("msplat_trainer_evaluate", EvalMetrics,
+    ("msplat_trainer_evaluate_images", EvalMetrics,
      [c_void_p, c_int32, POINTER(TrainerCamera), POINTER(c_void_p), c_int32]),
-    ("msplat_trainer_export_ply", c_int32, [c_void_p, c_char_p]),
-    ("msplat_trainer_export_splat", c_int32, [c_void_p, c_char_p]),
-    ("msplat_trainer_save_checkpoint", c_int32, [c_void_p, c_char_p]),
-    ("msplat_trainer_load_checkpoint", c_int32, [c_void_p, c_char_p]),
     ("msplat_trainer_load_ply", c_int32, [c_void_p, c_char_p]),
     ("msplat_trainer_set_crs", c_int32, [c_void_p, c_float, POINTER(c_float), c_int32]),
     ("msplat_scene_write_ply", c_int32,
@@ -210,20 +253,18 @@ SIGNATURES = [
     ("msplat_scene_read_ply", c_int32,
      [c_char_p, c_float, POINTER(c_float), c_int32, POINTER(c_int64), POINTER(c_int32),
       POINTER(c_int32), POINTER(c_void_p)]),
-    ("msplat_dataset_create", c_void_p, [c_char_p, c_char_p]),
-    ("msplat_dataset_destroy", None, [c_void_p]),
+    ("msplat_dataset_open_colmap", c_void_p, [c_char_p, c_char_p]),
     ("msplat_dataset_num_cameras", c_int32, [c_void_p]),
     ("msplat_dataset_camera", c_int32,
      [c_void_p, c_int32, POINTER(TrainerCamera), POINTER(c_float), POINTER(c_char_p)]),
-    ("msplat_dataset_camera_pose", c_int32, [c_void_p, c_int32, POINTER(c_float)]),
     ("msplat_dataset_num_points", c_int64, [c_void_p]),
     ("msplat_dataset_points", c_int32, [c_void_p, c_void_p, c_void_p]),
     ("msplat_dataset_normalisation", c_int32, [c_void_p, POINTER(c_float), POINTER(c_float)]),
     ("msplat_dataset_init_gaussians", c_int32, [c_void_p, c_int32, c_void_p * 6]),
-    ("msplat_trainer_splat_count", c_int32, [c_void_p]),
-    ("msplat_trainer_iteration", c_int32, [c_void_p]),
     ("msplat_trainer_group", c_int32,
      [c_void_p, c_int32, c_int32, POINTER(c_void_p), POINTER(c_int64), POINTER(c_int64)]),
+    ("msplat_set_image_decoder", None, [ImageDecoder]),
+    ("msplat_image_read", c_int32, [c_char_p, POINTER(POINTER(c_float)), POINTER(c_int32), POINTER(c_int32)]),
 ]
 
 _lib = None

@@ -85,6 +85,7 @@ struct Ctx {
     double stage_sum[kNumStages] = {};
     int64_t stage_cnt[kNumStages] = {};
     int64_t calls = 0;
+    std::vector<double> call_ms;   // bracketed milliseconds of each timed call since the last drain
     hipEvent_t ev_total = nullptr;   // recorded after the intersection total's copy to the host
 
     // per gaussian
@@ -263,6 +264,7 @@ void stage_mark(Ctx* c, int st) {
 // Fold the finished intervals of the other event set into the sums.
 void stage_fold(Ctx* c, int set) {
     const int n = c->n_marks[set];
+    double call = 0.0;
     for (int i = 0; i + 1 < n; ++i) {
         float t = 0.f;
         if (hipEventElapsedTime(&t, c->ev[set][i], c->ev[set][i + 1]) == hipSuccess) {
@@ -270,10 +272,14 @@ void stage_fold(Ctx* c, int set) {
             if (st >= 0 && st < kNumStages) {
                 c->stage_sum[st] += t;
                 c->stage_cnt[st] += 1;
+                call += t;
             }
         }
     }
-    if (n > 1) c->calls += 1;
+    if (n > 1) {
+        c->calls += 1;
+        if (c->call_ms.size() < (1u << 16)) c->call_ms.push_back(call);
+    }
     c->n_marks[set] = 0;
 }
 
@@ -968,6 +974,7 @@ int msplat_hip_enable_stage_timing(int enable) {
     c->n_marks[0] = c->n_marks[1] = 0;
     for (int i = 0; i < kNumStages; ++i) { c->stage_sum[i] = 0.0; c->stage_cnt[i] = 0; }
     c->calls = 0;
+    c->call_ms.clear();
     return MSPLAT_OK;
 }
 
@@ -996,6 +1003,20 @@ int msplat_hip_drain_stage_times(double* ms, int64_t* counts, const char** names
     if (n_stages) *n_stages = n;
     if (n_calls) *n_calls = c->calls;
     c->calls = 0;
+    return MSPLAT_OK;
+}
+
+int msplat_hip_drain_call_times(double* ms, int max_calls, int* n_calls) {
+    Ctx* c = g_ctx;
+    if (!c) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!n_calls || (max_calls > 0 && !ms)) return fail(MSPLAT_ERR_ARG, "null argument");
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    stage_fold(c, c->cur);
+    stage_fold(c, c->cur ^ 1);
+    const int n = (int)std::min<size_t>((size_t)std::max(max_calls, 0), c->call_ms.size());
+    for (int i = 0; i < n; ++i) ms[i] = c->call_ms[i];
+    *n_calls = n;
+    c->call_ms.clear();
     return MSPLAT_OK;
 }
 

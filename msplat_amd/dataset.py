@@ -27,7 +27,7 @@ class Dataset:
         self.eval_mode = bool(eval_mode)
         self.test_every = int(test_every)
         self._lib = _abi.load()
-        self._h = self._lib.msplat_dataset_create(str(path).encode(),
+        self._h = self._lib.msplat_dataset_open_colmap(str(path).encode(),
                                                   str(image_dir).encode() if image_dir else None)
         if not self._h:
             raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())

@@ -2,6 +2,8 @@
 #include "bindings.hpp"
 
 #include <cstring>
+#include <stdexcept>
+#include <string>
 
 namespace msplat {
 
@@ -46,6 +48,17 @@ void cleanup_msplat() {
     g_out_img.reset();
     g_radii.reset();
     msplat_hip_shutdown();
+}
+
+void cleanup_msplat_metal() { cleanup_msplat(); }
+
+void* msplat_device() { return msplat_hip_get_stream(); }
+
+void msplat_drain_gpu_times(std::vector<double>& out) {
+    std::vector<double> ms(1 << 16);
+    int n = 0;
+    check(msplat_hip_drain_call_times(ms.data(), (int)ms.size(), &n), "drain gpu times");
+    out.insert(out.end(), ms.begin(), ms.begin() + n);
 }
 
 MTensor gpu_zeros(std::vector<int64_t> shape, DType dtype) { return MTensor::zeros(std::move(shape), dtype); }
@@ -148,6 +161,78 @@ std::tuple<MTensor, float> msplat_train_step(
     float loss = 0.f;
     check(msplat_hip_last_loss(&loss, 0), "msplat_train_step");
     return {g_radii.view(num_points), loss};
+}
+
+namespace {
+// A camera matrix or colour held in a device tensor, read back to the host.
+template <int K>
+void host_floats(const MTensor& t, float (&dst)[K], const char* what) {
+    if (!t.defined() || t.numel() < K) throw std::runtime_error(std::string(what) + ": too few elements");
+    t.copy_to_host(dst, sizeof(dst));
+}
+}  // namespace
+
+MTensor msplat_render(int num_points, MTensor& means3d, MTensor& scales, float glob_scale,
+                      MTensor& quats, MTensor& viewmat, MTensor& projmat, float fx, float fy,
+                      float cx, float cy, unsigned img_height, unsigned img_width,
+                      const std::tuple<int, int, int> tile_bounds, float clip_thresh,
+                      unsigned degree, unsigned degrees_to_use, float cam_pos[3],
+                      MTensor& features_dc, MTensor& features_rest, MTensor& opacities,
+                      MTensor& background) {
+    float vm[16], pm[16], bg[3];
+    host_floats(viewmat, vm, "viewmat");
+    host_floats(projmat, pm, "projmat");
+    host_floats(background, bg, "background");
+    return msplat_render(num_points, means3d, scales, glob_scale, quats, vm, pm, fx, fy, cx, cy,
+                         img_height, img_width, tile_bounds, clip_thresh, degree, degrees_to_use,
+                         cam_pos, features_dc, features_rest, opacities, bg);
+}
+
+std::tuple<MTensor, float> msplat_train_step(
+    int num_points, MTensor& means3d, MTensor& scales, float glob_scale, MTensor& quats,
+    MTensor& viewmat, MTensor& projmat, float fx, float fy, float cx, float cy,
+    unsigned img_height, unsigned img_width, const std::tuple<int, int, int> tile_bounds,
+    float clip_thresh, unsigned degree, unsigned degrees_to_use, float cam_pos[3],
+    MTensor& features_dc, MTensor& features_rest, MTensor& opacities, MTensor& background,
+    MTensor& gt, MTensor& window2d, float ssim_weight, float loss_inv_n, int features_rest_bases,
+    int num_adam_groups, MTensor adam_params[], MTensor adam_exp_avg[],
+    MTensor adam_exp_avg_sq[], float adam_step_sizes[], float adam_bc2_sqrts[],
+    float adam_beta1, float adam_beta2, float adam_eps, MTensor& vis_counts,
+    MTensor& xys_grad_norm, MTensor& max_2d_size, float inv_max_dim) {
+    (void)window2d;
+    float vm[16], pm[16], bg[3];
+    host_floats(viewmat, vm, "viewmat");
+    host_floats(projmat, pm, "projmat");
+    host_floats(background, bg, "background");
+    return msplat_train_step(num_points, means3d, scales, glob_scale, quats, vm, pm, fx, fy, cx, cy,
+                             img_height, img_width, tile_bounds, clip_thresh, degree, degrees_to_use,
+                             cam_pos, features_dc, features_rest, opacities, bg, gt, ssim_weight,
+                             loss_inv_n, features_rest_bases, num_adam_groups, adam_params,
+                             adam_exp_avg, adam_exp_avg_sq, adam_step_sizes, adam_bc2_sqrts,
+                             adam_beta1, adam_beta2, adam_eps, vis_counts, xys_grad_norm,
+                             max_2d_size, inv_max_dim);
+}
+
+int msplat_densify(int N, int buf_capacity, float grad_thresh, float size_thresh,
+                   float screen_thresh, int check_screen, float cull_alpha_thresh,
+                   float cull_scale_thresh, float cull_screen_size, int check_huge,
+                   MTensor& xys_grad_norm, MTensor& vis_counts, MTensor& max_2d_size,
+                   float half_max_dim, MTensor& means_buf, MTensor& scales_buf,
+                   MTensor& quats_buf, MTensor& featuresDc_buf, MTensor& featuresRest_buf,
+                   MTensor& opacities_buf, int fr_stride, MTensor adam_exp_avg_buf[],
+                   MTensor adam_exp_avg_sq_buf[], MTensor& split_flag, MTensor& dup_flag,
+                   MTensor& split_prefix, MTensor& dup_prefix, MTensor& keep_flag,
+                   MTensor& keep_prefix, MTensor& block_totals, MTensor& compact_scratch,
+                   MTensor& random_samples) {
+    (void)split_flag; (void)dup_flag; (void)split_prefix; (void)dup_prefix;
+    (void)keep_flag; (void)keep_prefix; (void)block_totals; (void)compact_scratch;
+    if (!random_samples.defined()) throw std::runtime_error("msplat_densify: random_samples is required");
+    return msplat_densify(N, buf_capacity, grad_thresh, size_thresh, screen_thresh, check_screen,
+                          cull_alpha_thresh, cull_scale_thresh, cull_screen_size, check_huge,
+                          xys_grad_norm, vis_counts, max_2d_size, half_max_dim, means_buf,
+                          scales_buf, quats_buf, featuresDc_buf, featuresRest_buf, opacities_buf,
+                          fr_stride, adam_exp_avg_buf, adam_exp_avg_sq_buf, random_samples,
+                          (uint64_t)0);
 }
 
 int msplat_densify(int N, int buf_capacity, float grad_thresh, float size_thresh,

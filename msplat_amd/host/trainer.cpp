@@ -1,5 +1,6 @@
-// trainer.cpp — GaussianTrainer (python/bindings.cpp:101-280) and the C API
-// of include/msplat_trainer.h.
+// trainer.cpp — GaussianTrainer (python/bindings.cpp:101-280; Trainer,
+// msplat_api.mm:54-278), the reference's C API of include/msplat_c_api.h
+// (msplat_api.mm:280-390) and the additions of include/msplat_trainer.h.
 #include "../../include/msplat_trainer.h"
 
 #include <algorithm>
@@ -16,6 +17,7 @@
 
 #include "dataset.hpp"
 #include "model.hpp"
+#include "png_decode.hpp"
 
 namespace msplat {
 
@@ -112,17 +114,40 @@ public:
     MsplatEvalMetrics evaluate(int n, const MsplatTrainerCamera* cams, const float* const* images,
                                bool on_device) {
         if (n <= 0 || !cams || !images) throw std::runtime_error("no test cameras");
-        const int ds = model->getDownscaleFactor(cfg.iterations);
-        double sp = 0.0, ss = 0.0, sl = 0.0;
+        std::vector<Camera> cs(n);
+        std::vector<MTensor> gts(n);
         for (int i = 0; i < n; ++i) {
-            Camera cam;
+            Camera& cam = cs[i];
             cam.width = cams[i].width; cam.height = cams[i].height;
             cam.fx = cams[i].fx; cam.fy = cams[i].fy; cam.cx = cams[i].cx; cam.cy = cams[i].cy;
             std::memcpy(cam.camToWorld, cams[i].camToWorld, sizeof(cam.camToWorld));
             if (!images[i]) throw std::runtime_error("missing test image");
-            MTensor gt = gpu_empty({cam.height, cam.width, 3}, DType::Float32);
-            if (on_device) gt.copy_from_device(images[i], gt.nbytes());
-            else gt.copy_from_host(images[i], gt.nbytes());
+            gts[i] = gpu_empty({cam.height, cam.width, 3}, DType::Float32);
+            if (on_device) gts[i].copy_from_device(images[i], gts[i].nbytes());
+            else gts[i].copy_from_host(images[i], gts[i].nbytes());
+        }
+        return evaluate_cameras(cs, gts);
+    }
+
+    // The held-out cameras of the dataset the trainer was built from.
+    void set_test(std::vector<Camera> cams, std::vector<MTensor> images) {
+        test_cameras = std::move(cams);
+        test_images = std::move(images);
+    }
+
+    // Trainer::evaluate over the held-out cameras; all zero without any.
+    MsplatEvalMetrics evaluate_test() {
+        if (test_cameras.empty()) return MsplatEvalMetrics{0.f, 0.f, 0.f, 0, 0};
+        return evaluate_cameras(test_cameras, test_images);
+    }
+
+    MsplatEvalMetrics evaluate_cameras(std::vector<Camera> cams, const std::vector<MTensor>& images) {
+        const int n = (int)cams.size();
+        const int ds = model->getDownscaleFactor(cfg.iterations);
+        double sp = 0.0, ss = 0.0, sl = 0.0;
+        for (int i = 0; i < n; ++i) {
+            Camera& cam = cams[i];
+            MTensor gt = images[i];
             if (ds > 1) gt = downscaled(gt, cam.width, cam.height, ds);
             const int h2 = (int)gt.size(0), w2 = (int)gt.size(1);
             MTensor img = model->render(cam, cfg.iterations);
@@ -159,10 +184,15 @@ public:
         model->renderTo(cam, current_step, dst, w, h);
     }
 
-    MTensor render_camera(int i) {
-        if (i < 0 || i >= (int)cameras.size()) throw std::runtime_error("camera index out of range");
-        return model->render(cameras[i], current_step);
+    // Trainer::render (msplat_api.mm:168-186): a training or held-out camera
+    // at the current step's resolution; an empty tensor when out of range.
+    MTensor render_camera(int i, bool use_test) {
+        std::vector<Camera>& cs = use_test ? test_cameras : cameras;
+        if (i < 0 || i >= (int)cs.size()) return MTensor();
+        return model->render(cs[i], current_step);
     }
+
+    int num_cameras() const { return (int)cameras.size(); }
 
     MsplatTrainerConfig cfg;
     std::unique_ptr<Model> model;
@@ -188,6 +218,8 @@ private:
     }
 
     std::vector<Camera> cameras;
+    std::vector<Camera> test_cameras;
+    std::vector<MTensor> test_images;
     std::vector<std::map<int, MTensor>> gpu_images;
     std::vector<size_t> cam_indices;
     size_t cam_iter_pos = 0;
@@ -200,8 +232,11 @@ using msplat::GaussianTrainer;
 
 namespace {
 
+// Clears the last error, runs f and turns an exception into on_error with
+// its message kept for msplat_trainer_last_error.
 template <typename F>
 auto guarded(F&& f, decltype(f()) on_error) -> decltype(f()) {
+    msplat::g_err.clear();
     try {
         return f();
     } catch (const std::exception& e) {
@@ -210,29 +245,211 @@ auto guarded(F&& f, decltype(f()) on_error) -> decltype(f()) {
     }
 }
 
+// Runs f for a call without a result (the reference's void functions).
+template <typename F>
+void guarded_void(F&& f) {
+    msplat::g_err.clear();
+    try {
+        f();
+    } catch (const std::exception& e) {
+        msplat::g_err = e.what();
+    }
+}
+
 GaussianTrainer* T(MsplatTrainer t) { return static_cast<GaussianTrainer*>(t); }
 
 MsplatPixelBuffer to_host(const msplat::MTensor& img) {
     MsplatPixelBuffer b{nullptr, 0, 0};
-    b.height = (int32_t)img.size(0);
-    b.width = (int32_t)img.size(1);
+    if (img.dim() == 0) return b;
+    b.height = (int)img.size(0);
+    b.width = (int)img.size(1);
     b.data = static_cast<float*>(std::malloc(img.nbytes()));
     if (!b.data) throw std::runtime_error("out of host memory");
     img.copy_to_host(b.data, img.nbytes());
     return b;
 }
 
+// A dataset handle: the COLMAP reconstruction and, when built by
+// msplat_dataset_create, each camera's prepared image on the GPU and the
+// train / test split (Dataset::Impl, msplat_api.mm:20-46).
+struct CDataset {
+    msplat::Dataset data;
+    bool with_images = false;
+    std::vector<msplat::Camera> train_cams, test_cams;
+    std::vector<msplat::MTensor> train_imgs, test_imgs;
+};
+
+CDataset* D(MsplatDataset ds) { return static_cast<CDataset*>(ds); }
+
+MsplatImageDecoder g_decoder = nullptr;
+
+// The device context, created on first use on GPU 0 (as the reference
+// creates its Metal context on first use).
+void ensure_device() {
+    if (msplat_hip_init(0) == MSPLAT_OK) return;
+    if (std::strstr(msplat_hip_last_error(), "already initialised")) return;   // on another GPU
+    throw std::runtime_error(std::string("device initialisation failed: ") + msplat_hip_last_error());
+}
+
+// imreadRGB (image_io.cpp:12-50): a registered decoder, else the PNG decoder.
+msplat::DecodedImage read_image(const std::string& path) {
+    if (g_decoder) {
+        float* rgb = nullptr;
+        int w = 0, h = 0;
+        if (g_decoder(path.c_str(), &rgb, &w, &h) != 0 || !rgb || w <= 0 || h <= 0) {
+            std::free(rgb);
+            throw std::runtime_error("the registered image decoder failed on " + path);
+        }
+        msplat::DecodedImage img;
+        img.width = w;
+        img.height = h;
+        img.rgb.assign(rgb, rgb + (size_t)w * h * 3);
+        std::free(rgb);
+        return img;
+    }
+    if (!msplat::is_png_file(path))
+        throw std::runtime_error(path + ": not a PNG file; register a decoder for this format "
+                                        "with msplat_set_image_decoder");
+    return msplat::decode_png(path);
+}
+
+// Camera::loadImage (input_data.cpp:17-52) on the GPU: intrinsics rescaled
+// when the file's size differs from the camera's, the optional load-time
+// downscale by an area resize, then the undistortion of a distorted camera
+// (crop to the valid rectangle); fp32 intrinsics arithmetic as there.
+msplat::MTensor load_camera_image(const msplat::DatasetCamera& dc, float downscale, msplat::Camera& cam) {
+    using msplat::MTensor;
+    const msplat::DecodedImage raw = read_image(dc.filePath);
+    MTensor img = msplat::gpu_empty({raw.height, raw.width, 3}, msplat::DType::Float32);
+    img.copy_from_host(raw.rgb.data(), img.nbytes());
+    float fx = dc.fx, fy = dc.fy, cx = dc.cx, cy = dc.cy;
+    int width = dc.width, height = dc.height;
+    if (width > 0 && height > 0 && (raw.width != width || raw.height != height)) {
+        const float sx = (float)raw.width / (float)width, sy = (float)raw.height / (float)height;
+        fx *= sx; fy *= sy; cx *= sx; cy *= sy;
+        width = raw.width;
+        height = raw.height;
+    } else if (width == 0 || height == 0) {
+        width = raw.width;
+        height = raw.height;
+    }
+    if (downscale > 1.0f) {
+        const int nw = (int)(width / downscale), nh = (int)(height / downscale);
+        if (nw <= 0 || nh <= 0) throw std::runtime_error("downscale factor too large for " + dc.filePath);
+        MTensor small = msplat::gpu_empty({nh, nw, 3}, msplat::DType::Float32);
+        msplat::check(msplat_hip_resize_area(img.data<float>(), width, height, small.data<float>(), nw, nh),
+                      "resize");
+        img = small;
+        const float sc = 1.0f / downscale;
+        fx *= sc; fy *= sc; cx *= sc; cy *= sc;
+        width = nw;
+        height = nh;
+    }
+    if (dc.k1 != 0.f || dc.k2 != 0.f || dc.p1 != 0.f || dc.p2 != 0.f) {
+        const float intr[4] = {fx, fy, cx, cy};
+        const float dist[5] = {dc.k1, dc.k2, dc.p1, dc.p2, 0.f};
+        int32_t roi[4];
+        msplat::check(msplat_undistort_roi(width, height, intr, dist, roi), "undistortion rectangle");
+        MTensor out = msplat::gpu_empty({roi[3], roi[2], 3}, msplat::DType::Float32);
+        msplat::check(msplat_hip_undistort(img.data<float>(), width, height, intr, dist, roi,
+                                           out.data<float>()),
+                      "undistort");
+        img = out;
+        cx -= (float)roi[0];
+        cy -= (float)roi[1];
+        width = roi[2];
+        height = roi[3];
+    }
+    cam.width = width;
+    cam.height = height;
+    cam.fx = fx; cam.fy = fy; cam.cx = cx; cam.cy = cy;
+    std::memcpy(cam.camToWorld, dc.camToWorld, sizeof(cam.camToWorld));
+    cam.cached = false;
+    return img;
+}
+
+MsplatTrainerCamera c_camera(const msplat::Camera& k) {
+    MsplatTrainerCamera c;
+    c.width = k.width; c.height = k.height;
+    c.fx = k.fx; c.fy = k.fy; c.cx = k.cx; c.cy = k.cy;
+    std::memcpy(c.camToWorld, k.camToWorld, sizeof(c.camToWorld));
+    return c;
+}
+
+const msplat::DatasetCamera& dcam(MsplatDataset ds, int32_t i) {
+    if (!ds || i < 0 || i >= (int32_t)D(ds)->data.cameras.size())
+        throw std::runtime_error("camera index out of range");
+    return D(ds)->data.cameras[i];
+}
+
 }  // namespace
 
 extern "C" {
 
-MsplatTrainer msplat_trainer_create(const MsplatTrainerConfig* config, int64_t n,
-                                    const float* const params[6], int32_t n_cameras,
-                                    const MsplatTrainerCamera* cameras,
-                                    const float* const* targets, int32_t on_device) {
+MsplatTrainer msplat_trainer_create_from_arrays(const MsplatTrainerConfig* config, int64_t n,
+                                                const float* const params[6], int32_t n_cameras,
+                                                const MsplatTrainerCamera* cameras,
+                                                const float* const* targets, int32_t on_device) {
     return guarded([&]() -> MsplatTrainer {
         if (!config || !params || !cameras || !targets) throw std::runtime_error("null argument");
         return new GaussianTrainer(*config, n, params, n_cameras, cameras, targets, on_device != 0);
+    }, nullptr);
+}
+
+// msplat_trainer_create (msplat_c_api.h:94; msplat_api.mm:322-327 and
+// Trainer::Trainer, msplat_api.mm:76-98): gaussians from the point cloud, the
+// training cameras and their images, the held-out ones kept for evaluation.
+MsplatTrainer msplat_trainer_create(MsplatDataset ds, MsplatConfig config) {
+    return guarded([&]() -> MsplatTrainer {
+        if (!ds) throw std::runtime_error("null dataset");
+        CDataset* d = D(ds);
+        if (!d->with_images)
+            throw std::runtime_error("the dataset has no images (open it with msplat_dataset_create)");
+        if (d->train_cams.empty()) throw std::runtime_error("the dataset has no training cameras");
+        ensure_device();
+        MsplatTrainerConfig c = msplat_trainer_default_config();
+        c.iterations = config.iterations;
+        c.shDegree = config.shDegree;
+        c.shDegreeInterval = config.shDegreeInterval;
+        c.ssimWeight = config.ssimWeight;
+        c.numDownscales = config.numDownscales;
+        c.resolutionSchedule = config.resolutionSchedule;
+        c.refineEvery = config.refineEvery;
+        c.warmupLength = config.warmupLength;
+        c.resetAlphaEvery = config.resetAlphaEvery;
+        c.densifyGradThresh = config.densifyGradThresh;
+        c.densifySizeThresh = config.densifySizeThresh;
+        c.stopScreenSizeAt = config.stopScreenSizeAt;
+        c.splitScreenSize = config.splitScreenSize;
+        for (int k = 0; k < 3; ++k) c.bgColor[k] = config.bgColor[k];
+        // The initial gaussians go to the device first: the trainer takes
+        // parameters and images from the same memory space, and the images
+        // are already on the device.
+        msplat::HostGaussians g = msplat::init_gaussians(d->data.xyz, d->data.rgb, config.shDegree);
+        const std::vector<float>* host[6] = {&g.means, &g.scales, &g.quats,
+                                             &g.f_dc, &g.f_rest, &g.opacities};
+        msplat::MTensor dev[6];
+        const float* params[6];
+        for (int k = 0; k < 6; ++k) {
+            dev[k] = msplat::gpu_empty({(int64_t)std::max<size_t>(host[k]->size(), 1)},
+                                       msplat::DType::Float32);
+            if (!host[k]->empty()) dev[k].copy_from_host(host[k]->data(), host[k]->size() * sizeof(float));
+            params[k] = dev[k].data<float>();
+        }
+        std::vector<MsplatTrainerCamera> cams;
+        std::vector<const float*> imgs;
+        for (size_t i = 0; i < d->train_cams.size(); ++i) {
+            cams.push_back(c_camera(d->train_cams[i]));
+            imgs.push_back(d->train_imgs[i].data<float>());
+        }
+        std::unique_ptr<GaussianTrainer> tr(new GaussianTrainer(
+            c, g.n, params, (int)cams.size(), cams.data(), imgs.data(), true));
+        tr->set_test(d->test_cams, d->test_imgs);
+        msplat::Crs& crs = tr->model->crs;
+        crs.scale = d->data.scale;
+        for (int k = 0; k < 3; ++k) crs.translation[k] = d->data.translation[k];
+        crs.keep = config.keepCrs;
+        return tr.release();
     }, nullptr);
 }
 
@@ -246,6 +463,14 @@ MsplatStats msplat_trainer_step(MsplatTrainer t) {
     return guarded([&]() { return T(t)->step(); }, bad);
 }
 
+// Trainer::train (msplat_api.mm:130-136).
+void msplat_trainer_train(MsplatTrainer t) {
+    if (!t) return;
+    guarded_void([&]() {
+        while (T(t)->current_step < T(t)->cfg.iterations) T(t)->step();
+    });
+}
+
 float msplat_trainer_last_loss(MsplatTrainer t, int32_t wait) {
     if (!t) return NAN;
     float v = NAN;
@@ -253,35 +478,41 @@ float msplat_trainer_last_loss(MsplatTrainer t, int32_t wait) {
     return v;
 }
 
-MsplatPixelBuffer msplat_trainer_render(MsplatTrainer t, int32_t cameraIndex) {
+MsplatPixelBuffer msplat_trainer_render(MsplatTrainer t, int cameraIndex, bool useTest) {
     MsplatPixelBuffer empty{nullptr, 0, 0};
     if (!t) return empty;
-    return guarded([&]() { return to_host(T(t)->render_camera(cameraIndex)); }, empty);
+    return guarded([&]() { return to_host(T(t)->render_camera(cameraIndex, useTest)); }, empty);
 }
 
 MsplatPixelBuffer msplat_trainer_render_pose(MsplatTrainer t, const float camToWorld[16],
-                                             int32_t refCameraIndex) {
+                                             int refCameraIndex) {
     MsplatPixelBuffer empty{nullptr, 0, 0};
     if (!t || !camToWorld) return empty;
+    if (refCameraIndex < 0 || refCameraIndex >= T(t)->num_cameras()) return empty;
     return guarded([&]() { return to_host(T(t)->render_pose(camToWorld, refCameraIndex)); }, empty);
 }
 
-int32_t msplat_trainer_render_pose_to_buffer(MsplatTrainer t, const float camToWorld[16],
-                                             int32_t refCameraIndex, uint8_t* outRGBA,
-                                             int32_t* outWidth, int32_t* outHeight) {
-    if (!t || !camToWorld) return MSPLAT_ERR_ARG;
-    return guarded([&]() -> int32_t {
+// Trainer::renderFromPoseToBuffer (msplat_api.mm:207-238): the RGBA8
+// conversion runs on the GPU and 4 bytes per pixel are copied.
+void msplat_trainer_render_pose_to_buffer(MsplatTrainer t, const float camToWorld[16],
+                                          int refCameraIndex, uint8_t* outRGBA, int* outWidth,
+                                          int* outHeight) {
+    if (!t || !camToWorld || refCameraIndex < 0 || refCameraIndex >= T(t)->num_cameras()) {
+        if (outWidth) *outWidth = 0;
+        if (outHeight) *outHeight = 0;
+        return;
+    }
+    guarded_void([&]() {
         msplat::MTensor img = T(t)->render_pose(camToWorld, refCameraIndex);
         const int h = (int)img.size(0), w = (int)img.size(1);
         if (outWidth) *outWidth = w;
         if (outHeight) *outHeight = h;
-        if (!outRGBA) return MSPLAT_OK;
+        if (!outRGBA) return;
         const int64_t n = (int64_t)w * h;
         msplat::MTensor rgba = msplat::gpu_empty({n}, msplat::DType::Int32);   // 4 bytes per pixel
         msplat::check(msplat_hip_image_to_rgba8(img.data<float>(), n, rgba.data<uint8_t>()), "rgba8");
         rgba.copy_to_host(outRGBA, (size_t)n * 4);
-        return MSPLAT_OK;
-    }, (int32_t)MSPLAT_ERR_ARG);
+    });
 }
 
 int32_t msplat_trainer_render_pose_device(MsplatTrainer t, const float camToWorld[16],
@@ -316,41 +547,38 @@ int32_t msplat_prepare_cam(const MsplatTrainerCamera* cam, int32_t downscale, Ms
     return MSPLAT_OK;
 }
 
-MsplatEvalMetrics msplat_trainer_evaluate(MsplatTrainer t, int32_t n_test,
-                                          const MsplatTrainerCamera* cameras,
-                                          const float* const* images, int32_t on_device) {
+MsplatEvalMetrics msplat_trainer_evaluate_images(MsplatTrainer t, int32_t n_test,
+                                                 const MsplatTrainerCamera* cameras,
+                                                 const float* const* images, int32_t on_device) {
     MsplatEvalMetrics bad{0.f, 0.f, 0.f, 0, 0};
     if (!t) return bad;
     return guarded([&]() { return T(t)->evaluate(n_test, cameras, images, on_device != 0); }, bad);
 }
 
-int32_t msplat_trainer_export_ply(MsplatTrainer t, const char* path) {
-    if (!t || !path) return MSPLAT_ERR_ARG;
-    return guarded([&]() -> int32_t {
-        T(t)->model->savePly(path, T(t)->current_step);
-        return MSPLAT_OK;
-    }, (int32_t)MSPLAT_ERR_ARG);
+MsplatEvalMetrics msplat_trainer_evaluate(MsplatTrainer t) {
+    MsplatEvalMetrics bad{0.f, 0.f, 0.f, 0, 0};
+    if (!t) return bad;
+    return guarded([&]() { return T(t)->evaluate_test(); }, bad);
 }
 
-int32_t msplat_trainer_export_splat(MsplatTrainer t, const char* path) {
-    if (!t || !path) return MSPLAT_ERR_ARG;
-    return guarded([&]() -> int32_t {
-        T(t)->model->saveSplat(path);
-        return MSPLAT_OK;
-    }, (int32_t)MSPLAT_ERR_ARG);
+void msplat_trainer_export_ply(MsplatTrainer t, const char* path) {
+    if (!t || !path) return;
+    guarded_void([&]() { T(t)->model->savePly(path, T(t)->current_step); });
 }
 
-int32_t msplat_trainer_save_checkpoint(MsplatTrainer t, const char* path) {
-    if (!t || !path) return MSPLAT_ERR_ARG;
-    return guarded([&]() -> int32_t {
-        T(t)->model->saveCheckpoint(path, T(t)->current_step);
-        return MSPLAT_OK;
-    }, (int32_t)MSPLAT_ERR_ARG);
+void msplat_trainer_export_splat(MsplatTrainer t, const char* path) {
+    if (!t || !path) return;
+    guarded_void([&]() { T(t)->model->saveSplat(path); });
 }
 
-int32_t msplat_trainer_load_checkpoint(MsplatTrainer t, const char* path) {
+void msplat_trainer_save_checkpoint(MsplatTrainer t, const char* path) {
+    if (!t || !path) return;
+    guarded_void([&]() { T(t)->model->saveCheckpoint(path, T(t)->current_step); });
+}
+
+int msplat_trainer_load_checkpoint(MsplatTrainer t, const char* path) {
     if (!t || !path) return MSPLAT_ERR_ARG;
-    return guarded([&]() -> int32_t { return T(t)->load_checkpoint(path); }, (int32_t)MSPLAT_ERR_ARG);
+    return guarded([&]() -> int { return T(t)->load_checkpoint(path); }, (int)MSPLAT_ERR_ARG);
 }
 
 int32_t msplat_trainer_load_ply(MsplatTrainer t, const char* path) {
@@ -439,26 +667,60 @@ int32_t msplat_scene_read_ply(const char* path, float crs_scale, const float crs
     }, (int32_t)MSPLAT_ERR_ARG);
 }
 
-MsplatDataset msplat_dataset_create(const char* path, const char* image_dir) {
+MsplatDataset msplat_dataset_open_colmap(const char* path, const char* image_dir) {
     if (!path) return nullptr;
     return guarded([&]() -> MsplatDataset {
-        return new msplat::Dataset(msplat::load_colmap(path, image_dir ? image_dir : ""));
+        std::unique_ptr<CDataset> d(new CDataset);
+        d->data = msplat::load_colmap(path, image_dir ? image_dir : "");
+        for (const msplat::DatasetCamera& dc : d->data.cameras) {
+            msplat::Camera k;
+            k.width = dc.width; k.height = dc.height;
+            k.fx = dc.fx; k.fy = dc.fy; k.cx = dc.cx; k.cy = dc.cy;
+            std::memcpy(k.camToWorld, dc.camToWorld, sizeof(k.camToWorld));
+            d->train_cams.push_back(k);
+        }
+        return d.release();
     }, nullptr);
 }
 
-void msplat_dataset_destroy(MsplatDataset ds) { delete static_cast<msplat::Dataset*>(ds); }
-
-namespace {
-msplat::Dataset* D(MsplatDataset ds) { return static_cast<msplat::Dataset*>(ds); }
-const msplat::DatasetCamera& dcam(MsplatDataset ds, int32_t i) {
-    if (!ds || i < 0 || i >= (int32_t)D(ds)->cameras.size())
-        throw std::runtime_error("camera index out of range");
-    return D(ds)->cameras[i];
+// msplat_dataset_create (msplat_c_api.h:84-85; Dataset::Dataset,
+// msplat_api.mm:27-46): the COLMAP reconstruction, every camera's image
+// prepared on the GPU, then the split (InputData::splitTrainTest,
+// input_data.cpp:152-161: cameras 0, testEvery, 2 testEvery, ... are held out).
+MsplatDataset msplat_dataset_create(const char* path, float downscaleFactor, bool evalMode,
+                                    int testEvery) {
+    if (!path) return nullptr;
+    return guarded([&]() -> MsplatDataset {
+        if (evalMode && testEvery <= 0) throw std::runtime_error("testEvery must be positive");
+        std::unique_ptr<CDataset> d(new CDataset);
+        d->data = msplat::load_colmap(path, "");
+        ensure_device();
+        d->with_images = true;
+        for (size_t i = 0; i < d->data.cameras.size(); ++i) {
+            msplat::Camera k;
+            msplat::MTensor img = load_camera_image(d->data.cameras[i], downscaleFactor, k);
+            const bool test = evalMode && (int)(i % (size_t)testEvery) == 0;
+            (test ? d->test_cams : d->train_cams).push_back(k);
+            (test ? d->test_imgs : d->train_imgs).push_back(img);
+        }
+        return d.release();
+    }, nullptr);
 }
-}  // namespace
+
+void msplat_dataset_destroy(MsplatDataset ds) { delete D(ds); }
+
+int msplat_dataset_num_train(MsplatDataset ds) { return ds ? (int)D(ds)->train_cams.size() : -1; }
+
+int msplat_dataset_num_test(MsplatDataset ds) { return ds ? (int)D(ds)->test_cams.size() : -1; }
+
+// Dataset::cameraPose (msplat_api.mm:50-53): training camera cameraIndex.
+void msplat_dataset_camera_pose(MsplatDataset ds, int cameraIndex, float camToWorld[16]) {
+    if (!ds || !camToWorld || cameraIndex < 0 || cameraIndex >= (int)D(ds)->train_cams.size()) return;
+    std::memcpy(camToWorld, D(ds)->train_cams[cameraIndex].camToWorld, 16 * sizeof(float));
+}
 
 int32_t msplat_dataset_num_cameras(MsplatDataset ds) {
-    return ds ? (int32_t)D(ds)->cameras.size() : -1;
+    return ds ? (int32_t)D(ds)->data.cameras.size() : -1;
 }
 
 int32_t msplat_dataset_camera(MsplatDataset ds, int32_t i, MsplatTrainerCamera* cam,
@@ -478,37 +740,29 @@ int32_t msplat_dataset_camera(MsplatDataset ds, int32_t i, MsplatTrainerCamera* 
     }, (int32_t)MSPLAT_ERR_ARG);
 }
 
-int32_t msplat_dataset_camera_pose(MsplatDataset ds, int32_t i, float camToWorld[16]) {
-    if (!camToWorld) return MSPLAT_ERR_ARG;
-    return guarded([&]() -> int32_t {
-        std::memcpy(camToWorld, dcam(ds, i).camToWorld, 16 * sizeof(float));
-        return MSPLAT_OK;
-    }, (int32_t)MSPLAT_ERR_ARG);
-}
-
 int64_t msplat_dataset_num_points(MsplatDataset ds) {
-    return ds ? (int64_t)(D(ds)->xyz.size() / 3) : -1;
+    return ds ? (int64_t)(D(ds)->data.xyz.size() / 3) : -1;
 }
 
 int32_t msplat_dataset_points(MsplatDataset ds, float* xyz, uint8_t* rgb) {
     if (!ds) return MSPLAT_ERR_ARG;
-    if (xyz) std::memcpy(xyz, D(ds)->xyz.data(), D(ds)->xyz.size() * sizeof(float));
-    if (rgb) std::memcpy(rgb, D(ds)->rgb.data(), D(ds)->rgb.size());
+    if (xyz) std::memcpy(xyz, D(ds)->data.xyz.data(), D(ds)->data.xyz.size() * sizeof(float));
+    if (rgb) std::memcpy(rgb, D(ds)->data.rgb.data(), D(ds)->data.rgb.size());
     return MSPLAT_OK;
 }
 
 int32_t msplat_dataset_normalisation(MsplatDataset ds, float* scale, float translation[3]) {
     if (!ds) return MSPLAT_ERR_ARG;
-    if (scale) *scale = D(ds)->scale;
+    if (scale) *scale = D(ds)->data.scale;
     if (translation)
-        for (int k = 0; k < 3; ++k) translation[k] = D(ds)->translation[k];
+        for (int k = 0; k < 3; ++k) translation[k] = D(ds)->data.translation[k];
     return MSPLAT_OK;
 }
 
 int32_t msplat_dataset_init_gaussians(MsplatDataset ds, int32_t sh_degree, float* const params[6]) {
     if (!ds || !params) return MSPLAT_ERR_ARG;
     return guarded([&]() -> int32_t {
-        msplat::HostGaussians g = msplat::init_gaussians(D(ds)->xyz, D(ds)->rgb, sh_degree);
+        msplat::HostGaussians g = msplat::init_gaussians(D(ds)->data.xyz, D(ds)->data.rgb, sh_degree);
         const std::vector<float>* src[6] = {&g.means, &g.scales, &g.quats,
                                             &g.f_dc, &g.f_rest, &g.opacities};
         for (int k = 0; k < 6; ++k) {
@@ -519,9 +773,9 @@ int32_t msplat_dataset_init_gaussians(MsplatDataset ds, int32_t sh_degree, float
     }, (int32_t)MSPLAT_ERR_ARG);
 }
 
-int32_t msplat_trainer_splat_count(MsplatTrainer t) { return t ? (int32_t)T(t)->model->numActive() : -1; }
+int msplat_trainer_splat_count(MsplatTrainer t) { return t ? (int)T(t)->model->numActive() : -1; }
 
-int32_t msplat_trainer_iteration(MsplatTrainer t) { return t ? T(t)->current_step : -1; }
+int msplat_trainer_iteration(MsplatTrainer t) { return t ? T(t)->current_step : -1; }
 
 int32_t msplat_trainer_group(MsplatTrainer t, int32_t g, int32_t which, float** devPtr,
                              int64_t* rows, int64_t* rowFloats) {
@@ -534,5 +788,28 @@ int32_t msplat_trainer_group(MsplatTrainer t, int32_t g, int32_t which, float** 
         return MSPLAT_OK;
     }, (int32_t)MSPLAT_ERR_ARG);
 }
+
+void msplat_set_image_decoder(MsplatImageDecoder decoder) { g_decoder = decoder; }
+
+int32_t msplat_image_read(const char* path, float** rgb, int32_t* width, int32_t* height) {
+    if (!path || !rgb || !width || !height) return MSPLAT_ERR_ARG;
+    return guarded([&]() -> int32_t {
+        const msplat::DecodedImage img = read_image(path);
+        float* out = static_cast<float*>(std::malloc(img.rgb.size() * sizeof(float)));
+        if (!out) throw std::runtime_error("out of host memory");
+        std::memcpy(out, img.rgb.data(), img.rgb.size() * sizeof(float));
+        *rgb = out;
+        *width = img.width;
+        *height = img.height;
+        return MSPLAT_OK;
+    }, (int32_t)MSPLAT_ERR_ARG);
+}
+
+// Lifecycle (msplat_c_api.h:119-121; msplat_api.mm:275-278, 388-389).
+void msplat_set_metallib_path(const char* path) { (void)path; }
+
+void msplat_sync(void) { (void)msplat_hip_sync(); }
+
+void msplat_cleanup(void) { (void)msplat_hip_shutdown(); }
 
 }  // extern "C"

@@ -135,8 +135,9 @@ class GaussianTrainer:
                 raise ValueError(f"target shape {tuple(t.shape)} does not match camera {cam.height}x{cam.width}")
         cams = (_abi.TrainerCamera * len(self.cameras))(*[_c_camera(c) for c in self.cameras])
         cfg_c = self.config.to_c()
-        self._h = lib.msplat_trainer_create(ctypes.byref(cfg_c), n, pp, len(self.cameras), cams,
-                                            ctypes.cast(tp, ctypes.POINTER(ctypes.c_void_p)), int(on_dev))
+        self._h = lib.msplat_trainer_create_from_arrays(ctypes.byref(cfg_c), n, pp, len(self.cameras), cams,
+                                                        ctypes.cast(tp, ctypes.POINTER(ctypes.c_void_p)),
+                                                        int(on_dev))
         if not self._h:
             raise _abi.MsplatError(lib.msplat_trainer_last_error().decode())
         if on_dev:
@@ -185,7 +186,9 @@ class GaussianTrainer:
             ctypes.CDLL(None).free(ctypes.cast(buf.data, ctypes.c_void_p))
 
     def render(self, camera_index: int) -> np.ndarray:
-        return self._to_numpy(self._lib.msplat_trainer_render(self._h, camera_index))
+        if not 0 <= camera_index < len(self.cameras):
+            raise IndexError("camera index out of range")
+        return self._to_numpy(self._lib.msplat_trainer_render(self._h, camera_index, False))
 
     def render_from_pose(self, cam_to_world, ref_cam_idx: int = 0) -> np.ndarray:
         """Render a pose with the intrinsics of camera ref_cam_idx -> (H, W, 3) numpy."""
@@ -205,18 +208,25 @@ class GaussianTrainer:
 
     def render_from_pose_rgba8(self, cam_to_world, ref_cam_idx: int = 0) -> np.ndarray:
         """renderFromPoseToBuffer: (H, W, 4) uint8 display image (converted on the GPU)."""
+        if not 0 <= ref_cam_idx < len(self.cameras):
+            raise IndexError("ref_cam_idx out of range")
         _, p = _pose(cam_to_world)
-        w, h = ctypes.c_int32(0), ctypes.c_int32(0)
-        rc = self._lib.msplat_trainer_render_pose_to_buffer(self._h, p, ref_cam_idx, None,
-                                                            ctypes.byref(w), ctypes.byref(h))
-        if rc != 0:
-            raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())
+        w, h = ctypes.c_int(0), ctypes.c_int(0)
+        self._lib.msplat_trainer_render_pose_to_buffer(self._h, p, ref_cam_idx, None, ctypes.byref(w),
+                                                       ctypes.byref(h))
+        self._raise_on_error()
         out = np.empty((h.value, w.value, 4), np.uint8)
-        rc = self._lib.msplat_trainer_render_pose_to_buffer(self._h, p, ref_cam_idx, out.ctypes.data,
-                                                            ctypes.byref(w), ctypes.byref(h))
-        if rc != 0:
-            raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())
+        self._lib.msplat_trainer_render_pose_to_buffer(self._h, p, ref_cam_idx, out.ctypes.data,
+                                                       ctypes.byref(w), ctypes.byref(h))
+        self._raise_on_error()
         return out
+
+    def _raise_on_error(self) -> None:
+        """Raise the message of the latest failed call (the reference's void
+        calls report failures only through msplat_trainer_last_error)."""
+        msg = self._lib.msplat_trainer_last_error()
+        if msg:
+            raise _abi.MsplatError(msg.decode())
 
     def evaluate(self, cameras: Optional[List[Camera]] = None, images=None) -> dict:
         """Metrics on held-out cameras (GaussianTrainer.evaluate, python/bindings.cpp:180-205):
@@ -239,8 +249,8 @@ class GaussianTrainer:
                 raise ValueError("test image shape does not match its camera")
         cams = (_abi.TrainerCamera * len(cameras))(*[_c_camera(c) for c in cameras])
         ptrs = (ctypes.c_void_p * len(ims))(*[im.ctypes.data for im in ims])
-        m = self._lib.msplat_trainer_evaluate(self._h, len(cameras), cams,
-                                              ctypes.cast(ptrs, ctypes.POINTER(ctypes.c_void_p)), 0)
+        m = self._lib.msplat_trainer_evaluate_images(self._h, len(cameras), cams,
+                                                     ctypes.cast(ptrs, ctypes.POINTER(ctypes.c_void_p)), 0)
         if m.numTest == 0:
             raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())
         return {"psnr": m.psnr, "ssim": m.ssim, "l1": m.l1, "num_test": m.numTest,
@@ -252,14 +262,18 @@ class GaussianTrainer:
             raise _abi.MsplatError(self._lib.msplat_trainer_last_error().decode())
         return int(rc)
 
+    def _void_path_call(self, fn, path: str) -> None:
+        fn(self._h, str(path).encode())
+        self._raise_on_error()
+
     def export_ply(self, path: str) -> None:
-        self._path_call(self._lib.msplat_trainer_export_ply, path)
+        self._void_path_call(self._lib.msplat_trainer_export_ply, path)
 
     def export_splat(self, path: str) -> None:
-        self._path_call(self._lib.msplat_trainer_export_splat, path)
+        self._void_path_call(self._lib.msplat_trainer_export_splat, path)
 
     def save_checkpoint(self, path: str) -> None:
-        self._path_call(self._lib.msplat_trainer_save_checkpoint, path)
+        self._void_path_call(self._lib.msplat_trainer_save_checkpoint, path)
 
     def load_checkpoint(self, path: str) -> int:
         """Restore a checkpoint; returns its step (training continues after it)."""

@@ -21,15 +21,19 @@ from msplat_amd import _abi
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "msplat_hip.h")
 TRAINER_HEADER = os.path.join(ROOT, "include", "msplat_trainer.h")
+C_API_HEADER = os.path.join(ROOT, "include", "msplat_c_api.h")
+HEADERS = (HEADER, C_API_HEADER, TRAINER_HEADER)
+# every exported function starts with one of these
+EXPORT_RE = r"msplat_(?:hip_|trainer_|scene_|dataset_|undistort_|prepare_cam|image_|sync|cleanup|set_)\w*"
 
 
 def _declared():
-    """Functions declared in both headers (static inline helpers excluded)."""
+    """Functions declared in the three headers (static inline helpers excluded)."""
     names = set()
-    for h in (HEADER, TRAINER_HEADER):
+    for h in HEADERS:
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
         text = re.sub(r"static inline[^{]*\{.*?\n\}", "", text, flags=re.S)
-        names |= set(re.findall(r"\b(msplat_(?:hip_|trainer_|scene_|dataset_|undistort_|prepare_cam)\w*)\s*\(", text))
+        names |= set(re.findall(r"\b(" + EXPORT_RE + r")\s*\(", text))
     return sorted(names)
 
 
@@ -46,11 +50,11 @@ def test_library_exports_every_declared_symbol():
     nm = shutil.which("nm")
     if nm:
         out = subprocess.check_output([nm, "-D", "--defined-only", _abi.LIB_PATH], text=True)
-        exported = set(re.findall(r"\bT (msplat_(?:hip_|trainer_|scene_|dataset_|undistort_|prepare_cam)\w*)", out))
+        exported = set(re.findall(r"\bT (" + EXPORT_RE + ")", out))
         assert set(_declared()) <= exported
 
 
-STRUCTS = {"MsplatRenderArgs": _abi.RenderArgs, "MsplatTrainArgs": _abi.TrainArgs,
+STRUCTS = {"MsplatConfig": _abi.Config, "MsplatRenderArgs": _abi.RenderArgs, "MsplatTrainArgs": _abi.TrainArgs,
            "MsplatDensifyArgs": _abi.DensifyArgs, "MsplatTrainerConfig": _abi.TrainerConfig,
            "MsplatTrainerCamera": _abi.TrainerCamera, "MsplatStats": _abi.Stats,
            "MsplatCamSetup": _abi.CamSetupC,
@@ -63,7 +67,7 @@ def test_struct_layouts_match_header(tmp_path):
     if not cc:
         pytest.skip("no host C compiler")
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"',
-             f'#include "{TRAINER_HEADER}"', "int main(void) {"]
+             f'#include "{C_API_HEADER}"', f'#include "{TRAINER_HEADER}"', "int main(void) {"]
     for cname, py in STRUCTS.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in py._fields_:

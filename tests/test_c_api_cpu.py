@@ -1,0 +1,218 @@
+"""The reference-shaped C API (include/msplat_c_api.h) and the image reader,
+without a GPU.
+
+* Every function of the reference's core/include/msplat_c_api.h is declared
+  in include/msplat_c_api.h with the same return type, name and parameter
+  list, and the four structs have the same fields and layouts (sizes and
+  offsets printed by the host C compiler from each header).  These two tests
+  read the reference tree and are skipped where it is absent.
+* msplat_image_read (the dataset's image decoder) equals Pillow's RGB
+  decoding for PNG files of every colour type it writes; 16-bit grey takes
+  the high byte.
+* Calls that fail before any device work give the reference's empty results
+  and a message.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from msplat_amd import _abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+OURS = os.path.join(ROOT, "include", "msplat_c_api.h")
+REF = "/root/reference/core/include/msplat_c_api.h"
+
+
+def _strip(text):
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return re.sub(r"static inline[^{]*\{.*?\n\}", "", text, flags=re.S)
+
+
+def _norm(s):
+    s = re.sub(r"\s+", " ", s).strip()
+    return re.sub(r"\s*([*,()\[\]])\s*", r"\1", s)
+
+
+def _prototypes(path):
+    text = _strip(open(path).read())
+    out = {}
+    for ret, name, params in re.findall(r"([\w\s\*]+?)\b(msplat_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.S):
+        ret = ret.strip().split("\n")[-1]
+        out[name] = (_norm(ret), _norm(params))
+    return out
+
+
+def _structs(path):
+    text = _strip(open(path).read())
+    return {name: [_norm(f) for f in body.split(";") if f.strip()]
+            for body, name in re.findall(r"typedef struct\s*\{(.*?)\}\s*(\w+)\s*;", text, flags=re.S)}
+
+
+def _ref_or_skip():
+    if not os.path.exists(REF):
+        pytest.skip("reference tree absent")
+
+
+def test_c_api_prototypes_match_reference():
+    _ref_or_skip()
+    ref, ours = _prototypes(REF), _prototypes(OURS)
+    assert len(ref) == 22, sorted(ref)
+    for name, sig in ref.items():
+        assert name in ours, f"{name} missing from include/msplat_c_api.h"
+        assert ours[name] == sig, (name, ours[name], sig)
+    assert set(ours) == set(ref)
+    # the other header declares none of these names with another signature
+    trainer = _prototypes(os.path.join(ROOT, "include", "msplat_trainer.h"))
+    assert not set(trainer) & set(ref), set(trainer) & set(ref)
+
+
+def test_c_api_types_match_reference(tmp_path):
+    _ref_or_skip()
+    ref, ours = _structs(REF), _structs(OURS)
+    for name in ("MsplatConfig", "MsplatStats", "MsplatEvalMetrics", "MsplatPixelBuffer"):
+        assert ours[name] == ref[name], name
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        pytest.skip("no host C compiler")
+    fields = {n: [re.split(r"[\s\*]+", f.split("[")[0])[-1] for f in ref[n]] for n in
+              ("MsplatConfig", "MsplatStats", "MsplatEvalMetrics", "MsplatPixelBuffer")}
+
+    def layout(header):
+        lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{header}"', "int main(void) {"]
+        for n, fs in fields.items():
+            lines.append(f'printf("{n} %zu\\n", sizeof({n}));')
+            lines += [f'printf("{n}.{f} %zu\\n", offsetof({n}, {f}));' for f in fs]
+        lines.append("MsplatConfig c = msplat_default_config();")
+        lines.append('printf("default %d %d %g %d %g %d %g\\n", c.iterations, c.shDegreeInterval, '
+                     'c.ssimWeight, c.warmupLength, c.densifyGradThresh, (int)c.keepCrs, c.bgColor[1]);')
+        lines += ["return 0;", "}"]
+        src = tmp_path / f"l{abs(hash(header))}.c"
+        src.write_text("\n".join(lines))
+        exe = str(src)[:-2]
+        subprocess.check_call([cc, "-std=c99", "-o", exe, str(src)])
+        return subprocess.check_output([exe], text=True)
+
+    assert layout(OURS) == layout(REF)
+
+
+def _lib():
+    if not os.path.exists(_abi.LIB_PATH):
+        pytest.skip("libmsplat_hip.so not built")
+    return _abi.load()
+
+
+def _read(lib, path):
+    rgb = ctypes.POINTER(ctypes.c_float)()
+    w, h = ctypes.c_int32(0), ctypes.c_int32(0)
+    rc = lib.msplat_image_read(str(path).encode(), ctypes.byref(rgb), ctypes.byref(w), ctypes.byref(h))
+    if rc != 0:
+        return None, lib.msplat_trainer_last_error().decode()
+    try:
+        return np.ctypeslib.as_array(rgb, shape=(h.value, w.value, 3)).copy(), ""
+    finally:
+        ctypes.CDLL(None).free(ctypes.cast(rgb, ctypes.c_void_p))
+
+
+@pytest.mark.parametrize("mode", ["RGB", "RGBA", "L", "LA", "P", "1"])
+def test_png_decoder_matches_pillow(mode, tmp_path):
+    Image = pytest.importorskip("PIL.Image")
+    lib = _lib()
+    rng = np.random.default_rng(31)
+    h, w = 37, 53   # odd sizes: rows of sub-byte pixels end mid-byte
+    rgb = rng.integers(0, 256, (h, w, 3), dtype=np.uint8)
+    im = Image.fromarray(rgb, "RGB")
+    im = im.convert(mode) if mode != "P" else im.quantize(colors=61)
+    if mode in ("RGBA", "LA"):
+        alpha = Image.fromarray(rng.integers(0, 256, (h, w), dtype=np.uint8), "L")
+        im.putalpha(alpha)
+    path = tmp_path / f"img_{mode}.png"
+    im.save(path, format="PNG")
+    with Image.open(path) as f:
+        want = np.asarray(f.convert("RGB"), dtype=np.uint8).astype(np.float32) / np.float32(255.0)
+    got, err = _read(lib, path)
+    assert got is not None, err
+    assert got.shape == want.shape
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+
+
+def test_png_decoder_16_bit_grey_and_errors(tmp_path):
+    Image = pytest.importorskip("PIL.Image")
+    lib = _lib()
+    rng = np.random.default_rng(32)
+    v = rng.integers(0, 65536, (19, 23), dtype=np.uint16)
+    path = tmp_path / "g16.png"
+    Image.fromarray(v.astype(np.int32), "I").convert("I;16").save(path, format="PNG")
+    with Image.open(path) as f:
+        raw = np.asarray(f, dtype=np.uint16)
+    got, err = _read(lib, path)
+    assert got is not None, err
+    want = ((raw >> 8).astype(np.float32) / np.float32(255.0))[..., None].repeat(3, axis=2)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    # a truncated file, a non-image file, a missing file
+    data = open(path, "rb").read()
+    (tmp_path / "cut.png").write_bytes(data[: len(data) // 2])
+    (tmp_path / "text.png").write_bytes(b"not an image at all")
+    for p, msg in ((tmp_path / "cut.png", "PNG"), (tmp_path / "text.png", "not a PNG"),
+                   (tmp_path / "none.png", "")):
+        got, err = _read(lib, p)
+        assert got is None and msg in err, (p, err)
+
+
+def test_c_api_calls_that_fail_before_device_work(tmp_path):
+    """Failures give the reference's empty results (NULL handles, -1
+    counts, zero-sized buffers) with a message, and touch no device."""
+    lib = _lib()
+    assert not lib.msplat_dataset_create(str(tmp_path / "missing").encode(), 1.0, False, 8)
+    assert lib.msplat_trainer_last_error()
+    assert lib.msplat_dataset_num_train(None) == -1 and lib.msplat_dataset_num_test(None) == -1
+    assert not lib.msplat_trainer_create(None, _abi.default_config())
+    assert b"null dataset" in lib.msplat_trainer_last_error()
+    buf = lib.msplat_trainer_render(None, 0, False)
+    assert not buf.data and buf.width == 0 and buf.height == 0
+    pose = (ctypes.c_float * 16)(*np.eye(4, dtype=np.float32).reshape(16))
+    w, h = ctypes.c_int(7), ctypes.c_int(7)
+    lib.msplat_trainer_render_pose_to_buffer(None, pose, 0, None, ctypes.byref(w), ctypes.byref(h))
+    assert w.value == 0 and h.value == 0
+    lib.msplat_set_metallib_path(b"/nonexistent/default.metallib")
+    lib.msplat_dataset_camera_pose(None, 0, pose)
+    assert list(pose) == list(np.eye(4, dtype=np.float32).reshape(16))
+
+
+REF_BINDINGS = "/root/reference/core/metal/bindings.h"
+
+
+def test_bindings_shim_has_every_reference_prototype(tmp_path):
+    """Each function of the reference's core/metal/bindings.h exists in
+    msplat_amd/host/bindings.hpp with the same type: the C++ compiler takes a
+    pointer of the reference's exact type to it (an overload that differs in
+    any parameter or the return type does not convert)."""
+    if not os.path.exists(REF_BINDINGS):
+        pytest.skip("reference tree absent")
+    cxx = shutil.which("g++")
+    if not cxx:
+        pytest.skip("no host C++ compiler")
+    text = open(REF_BINDINGS).read()
+    text = re.sub(r"#ifdef __OBJC__.*?#else(.*?)#endif", r"\1", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    text = re.sub(r"#[^\n]*", "", text)
+    protos = re.findall(r"([\w:<>,\s\*&]+?[\s\*&])(\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.S)
+    names = [n for _, n, _ in protos]
+    assert len(protos) >= 12 and "msplat_densify" in names and "msplat_train_step" in names, names
+    lines = ['#include "bindings.hpp"', "using namespace msplat;"]
+    for k, (ret, name, params) in enumerate(protos):
+        ret = " ".join(ret.split())
+        lines.append(f"static {ret} (*p{k})({' '.join(params.split())}) = &msplat::{name};")
+    lines.append("int main() { return 0; }")
+    src = tmp_path / "shim.cpp"
+    src.write_text("\n".join(lines))
+    host = os.path.join(ROOT, "msplat_amd", "host")
+    subprocess.check_call([cxx, "-std=c++17", "-fsyntax-only", "-I", host, "-I", os.path.join(ROOT, "include"),
+                           str(src)])
