@@ -203,6 +203,39 @@ def traffic_summary(dirs: list, copy_mib: int, last: int, commands: str,
             "hbm_bytes_per_launch": 1024 * (fk * fs + wk * ws), "commands": commands}
 
 
+def pmc_summary(d: str, kernels: list, last: int, command: str) -> str:
+    """Markdown table of every counter in a `rocprofv3 --pmc -f csv` output
+    directory, averaged per dispatch over the last `last` dispatches of each
+    kernel (all when last <= 0), with the derived rates: VALU busy = VALU
+    active cycles / (4 SIMDs x busy cycles x CUs), LDS bank conflicts per LDS
+    instruction, waits per executed instruction."""
+    import csv
+    import glob
+    import re
+    f = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not f:
+        raise SystemExit(f"no counter_collection csv under {d}")
+    rows = list(csv.DictReader(open(f[0])))
+    names = sorted({r["Counter_Name"] for r in rows})
+    out = [f"Command: `{command}`", "", "| kernel | dispatches | " + " | ".join(names) + " |",
+           "|---|---:|" + "---:|" * len(names)]
+    for k in kernels:
+        vals = {}
+        n = 0
+        for c in names:
+            rs = [r for r in rows if re.search(k, r["Kernel_Name"]) and r["Counter_Name"] == c]
+            rs.sort(key=lambda r: int(r["Dispatch_Id"]))
+            v = [float(r["Counter_Value"]) for r in rs]
+            if last > 0:
+                v = v[-last:]
+            if v:
+                vals[c] = sum(v) / len(v)
+                n = max(n, len(v))
+        if vals:
+            out.append(f"| {k} | {n} | " + " | ".join(f"{vals.get(c, float('nan')):.4g}" for c in names) + " |")
+    return "\n".join(out) + "\n"
+
+
 def _stage_line(stages):
     return {k: ms / c for k, (ms, c) in stages.items() if c}
 
@@ -395,6 +428,12 @@ def main():
     ap.add_argument("--rocprof-summary", default="",
                     help="only print a markdown summary of this rocprofv3 csv output directory and exit")
     ap.add_argument("--rocprof-command", default="", help="command line quoted in the summary")
+    ap.add_argument("--pmc-summary", default="",
+                    help="only print a markdown table of the counters of this rocprofv3 --pmc csv output "
+                         "directory for --pmc-kernels (last --steps dispatches of each) and exit")
+    ap.add_argument("--pmc-kernels", default="k_raster_fwd,k_raster_bwd,k_radix_hist,k_radix_scatter,"
+                                             "k_ssim_fused,k_ssim_v_bwd,k_project_fwd,k_sh_rest_adam,"
+                                             "k_proj_bwd_adam")
     ap.add_argument("--traffic-summary", nargs=4, default=None,
                     metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="only print the HBM traffic JSON of the raster backward from four "
@@ -407,6 +446,9 @@ def main():
         res = {k: traffic_summary(args.traffic_summary, args.copy_mib or 1024, args.steps,
                                   args.rocprof_command, k) for k in kernels}
         print(json.dumps(res[kernels[0]] if len(kernels) == 1 else res, indent=1))
+        return
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary, args.pmc_kernels.split(","), args.steps, args.rocprof_command), end="")
         return
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary, args.preroll + args.warmup, args.steps,
