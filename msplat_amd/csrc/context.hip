@@ -436,12 +436,18 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     float* img = dst_img ? dst_img : P<float>(c->out_img);
     stage_mark(c, S_RFWD);
     ChunkBufs cb = chunks(c);
-    launch_raster_fwd(c->stream, p, max_items, P<Meta>(c->meta_d), it, P<int>(c->tile_bins), pk,
-                      P<float>(c->final_T), P<int>(c->final_idx), img, cb,
-                      work_counters(c));
-    launch_raster_merge(c->stream, p, P<Meta>(c->meta_d), P<int>(c->l_chunked), it,
-                        P<float>(c->final_T), P<int>(c->final_idx), img, cb,
-                        training);
+    if (training) {
+        // every chunk's state is kept: the backward's suffix sums run over
+        // all chunks of a tile
+        launch_raster_fwd(c->stream, p, max_items, P<Meta>(c->meta_d), it, P<int>(c->tile_bins),
+                          pk, P<float>(c->final_T), P<int>(c->final_idx), img, cb,
+                          work_counters(c));
+        launch_raster_merge(c->stream, p, P<Meta>(c->meta_d), P<int>(c->l_chunked), it,
+                            P<float>(c->final_T), P<int>(c->final_idx), img, cb, true);
+    } else {
+        launch_render_tiles(c->stream, p, it, P<int>(c->tile_bins), pk, P<float>(c->final_T),
+                            P<int>(c->final_idx), img, work_counters(c));
+    }
     HIP_TRY(hipGetLastError());
     c->meta_valid = false;
     return MSPLAT_OK;

@@ -130,6 +130,11 @@ inline int64_t items_bound(int64_t T, int64_t I) { return T + I / 512 + I / 2048
 void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Entries pk, float* final_T, int* final_idx,
                        float* out_img, ChunkBufs cb, unsigned long long* work);
+// Render-only forward, one workgroup per tile (chunked tiles rasterised chunk
+// by chunk up to the merge cutoff); writes the final image, T and index.
+void launch_render_tiles(hipStream_t s, const CamParams& p, Items it, const int* tile_bins,
+                         Entries pk, float* final_T, int* final_idx, float* out_img,
+                         unsigned long long* work);
 void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
                          Items it, float* final_T, int* final_idx, float* out_img, ChunkBufs cb,
                          bool with_suffix);

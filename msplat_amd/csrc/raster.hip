@@ -146,35 +146,17 @@ __device__ __forceinline__ float wave_sum8_lds(const float* v, int lane, float* 
     return u;
 }
 
-__global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float bg0, float bg1,
-                                                    float bg2, const Meta* __restrict__ meta,
-                                                    Items it,
-                                                    const int* __restrict__ tile_bins, Entries pk,
-                                                    float* __restrict__ final_T,
-                                                    int* __restrict__ final_idx,
-                                                    float* __restrict__ out_img, ChunkBufs cb,
-                                                    unsigned long long* __restrict__ work) {
-    __shared__ float4 s_geo[256];    // x, y, conic a, b
-    __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
-    __shared__ float4 s_aux[256];    // clamped b, mask (bits); 16-byte stride shares the address
-    const int item = blockIdx.x;
-    if (item >= meta->n_items) return;
-    int t, K, cs, ce;
-    item_range(it, tile_bins, item, t, K, cs, ce);
-    const Px px = pixel_of(t, tbx, W, H);
-    float fx = (float)px.j, fy = (float)px.i;
-    // opaque to the compiler, so that the loop keeps the converted
-    // coordinates instead of converting the integers again every step
-    asm volatile("" : "+v"(fx), "+v"(fy));
+// Forward of the entries [cs, ce) at this lane's pixel, from the state
+// (T, C, last) passed in: entries are staged 256 at a time through LDS and
+// each wave walks the entries of its quadrant in order.  live: the lanes
+// whose pixel still composites (wave-uniform mask).  Every thread of the
+// workgroup calls this with the same range (it holds workgroup barriers).
+__device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float fx, float fy,
+                                          int tx0, int ty0, const Entries& pk, float4* s_geo,
+                                          float4* s_col, float4* s_aux, float& T, float& C0,
+                                          float& C1, float& C2, int& last, unsigned& ncl,
+                                          unsigned& nwit) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int tx0 = (t % tbx) * BLOCK, ty0 = (t / tbx) * BLOCK;
-
-    float T = 1.f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
-    int last = cs - 1;
-    unsigned ncl = 0;       // pairs composited by this lane
-    unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
-    // lanes whose pixel is still compositing (wave-uniform lane mask)
-    uint64_t live = wave_ballot(px.inside);
     for (int b = cs; b < ce; b += 256) {
         if (__syncthreads_and(live == 0)) break;
         const int idx = b + tid;
@@ -237,13 +219,47 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
             if (live == 0) break;
         }
     }
-    if (work) {
-        unsigned long long* ws = work_slot(work);
-        unsigned ncomp = ncl;
-        for (int off = 32; off >= 1; off >>= 1) ncomp += __shfl_xor(ncomp, off, 64);
-        if (lane == 0 && ncomp) atomicAdd(ws, (unsigned long long)ncomp);
-        if (lane == 0 && nwit) atomicAdd(ws + 2, (unsigned long long)nwit);
-    }
+}
+
+__device__ __forceinline__ void add_work(unsigned long long* work, unsigned ncl, unsigned nwit) {
+    if (!work) return;
+    unsigned long long* ws = work_slot(work);
+    unsigned ncomp = ncl;
+    for (int off = 32; off >= 1; off >>= 1) ncomp += __shfl_xor(ncomp, off, 64);
+    const int lane = threadIdx.x & 63;
+    if (lane == 0 && ncomp) atomicAdd(ws, (unsigned long long)ncomp);
+    if (lane == 0 && nwit) atomicAdd(ws + 2, (unsigned long long)nwit);
+}
+
+__global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float bg0, float bg1,
+                                                    float bg2, const Meta* __restrict__ meta,
+                                                    Items it,
+                                                    const int* __restrict__ tile_bins, Entries pk,
+                                                    float* __restrict__ final_T,
+                                                    int* __restrict__ final_idx,
+                                                    float* __restrict__ out_img, ChunkBufs cb,
+                                                    unsigned long long* __restrict__ work) {
+    __shared__ float4 s_geo[256];    // x, y, conic a, b
+    __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
+    __shared__ float4 s_aux[256];    // clamped b, mask (bits); 16-byte stride shares the address
+    const int item = blockIdx.x;
+    if (item >= meta->n_items) return;
+    int t, K, cs, ce;
+    item_range(it, tile_bins, item, t, K, cs, ce);
+    const Px px = pixel_of(t, tbx, W, H);
+    float fx = (float)px.j, fy = (float)px.i;
+    // opaque to the compiler, so that the loop keeps the converted
+    // coordinates instead of converting the integers again every step
+    asm volatile("" : "+v"(fx), "+v"(fy));
+    const int tx0 = (t % tbx) * BLOCK, ty0 = (t / tbx) * BLOCK;
+
+    float T = 1.f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
+    int last = cs - 1;
+    unsigned ncl = 0;       // pairs composited by this lane
+    unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
+    fwd_range(cs, ce, wave_ballot(px.inside), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, T, C0, C1,
+              C2, last, ncl, nwit);
+    add_work(work, ncl, nwit);
     if (!px.inside) return;
     if (K == 1) {
         const size_t pix = (size_t)px.i * W + px.j;
@@ -260,6 +276,70 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
         cb.cC[3 * o + 2] = C2;
         cb.cidx[o] = last;
     }
+}
+
+// Render-only forward, one workgroup per tile.  A tile rasterised in one
+// piece is the forward above.  A chunked tile's chunks are rasterised in
+// order, each from T = 1 as rasterize_forward_chunked_kernel does
+// (.metal:2633-2741), and folded into the pixel's running state as the merge
+// does (.metal:2746-2799): colour += chunk colour * T_running, T_running *=
+// chunk T, final index = the chunk's last contributor, until T_running <=
+// 1e-4.  A pixel past that cutoff takes no part in later chunks, and the
+// workgroup stops once every pixel is past it: the chunks behind the cutoff,
+// which only the backward's suffix sums read, are not rasterised.  The
+// results are those of the chunk items plus the merge, bit for bit.
+__global__ __launch_bounds__(256) void k_render_tiles(int W, int H, int tbx, float bg0,
+                                                      float bg1, float bg2, Items it,
+                                                      const int* __restrict__ tile_bins,
+                                                      Entries pk, float* __restrict__ final_T,
+                                                      int* __restrict__ final_idx,
+                                                      float* __restrict__ out_img,
+                                                      unsigned long long* __restrict__ work) {
+    __shared__ float4 s_geo[256];
+    __shared__ float4 s_col[256];
+    __shared__ float4 s_aux[256];
+    const int t = blockIdx.x;
+    const int K = it.tile_K[t];
+    const int s = tile_bins[2 * t], e = tile_bins[2 * t + 1];
+    const Px px = pixel_of(t, tbx, W, H);
+    float fx = (float)px.j, fy = (float)px.i;
+    asm volatile("" : "+v"(fx), "+v"(fy));
+    const int tx0 = (t % tbx) * BLOCK, ty0 = (t / tbx) * BLOCK;
+    unsigned ncl = 0, nwit = 0;
+    float Tr = 1.f, R0 = 0.f, R1 = 0.f, R2 = 0.f;
+    int li;
+    if (K == 1) {
+        li = s - 1;
+        fwd_range(s, e, wave_ballot(px.inside), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, Tr, R0,
+                  R1, R2, li, ncl, nwit);
+    } else {
+        li = -1;
+        bool done = !px.inside;
+        for (int k = 0; k < K; ++k) {
+            if (__syncthreads_and(done)) break;
+            const int cs = s + k * CHUNK, ce = min(cs + CHUNK, e);
+            float T = 1.f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
+            int last = cs - 1;
+            fwd_range(cs, ce, wave_ballot(!done), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, T,
+                      C0, C1, C2, last, ncl, nwit);
+            if (!done) {
+                R0 = fmaf(C0, Tr, R0);
+                R1 = fmaf(C1, Tr, R1);
+                R2 = fmaf(C2, Tr, R2);
+                Tr *= T;
+                if (last >= 0) li = last;
+                if (Tr <= 1e-4f) done = true;
+            }
+        }
+    }
+    add_work(work, ncl, nwit);
+    if (!px.inside) return;
+    const size_t pix = (size_t)px.i * W + px.j;
+    final_T[pix] = Tr;
+    final_idx[pix] = li;
+    out_img[3 * pix + 0] = clamp01(fmaf(bg0, Tr, R0));
+    out_img[3 * pix + 1] = clamp01(fmaf(bg1, Tr, R1));
+    out_img[3 * pix + 2] = clamp01(fmaf(bg2, Tr, R2));
 }
 
 __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, float bg0,
@@ -605,6 +685,16 @@ void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, con
     hipLaunchKernelGGL(k_raster_fwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
                        p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx,
                        out_img, cb, work);
+}
+
+void launch_render_tiles(hipStream_t s, const CamParams& p, Items it, const int* tile_bins,
+                         Entries pk, float* final_T, int* final_idx, float* out_img,
+                         unsigned long long* work) {
+    const int T = p.tbx * p.tby;
+    if (T <= 0) return;
+    hipLaunchKernelGGL(k_render_tiles, dim3((unsigned)T), dim3(256), 0, s, p.W, p.H, p.tbx,
+                       p.bg[0], p.bg[1], p.bg[2], it, tile_bins, pk, final_T, final_idx, out_img,
+                       work);
 }
 
 void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
