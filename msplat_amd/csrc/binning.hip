@@ -23,8 +23,6 @@ namespace msp {
 
 namespace {
 
-constexpr int SCAN_T = 1024;
-
 // Emission of the (tile id, gaussian id) pairs of 64 depth-consecutive
 // gaussians by one wave, with coalesced stores.  Gaussians with fewer than
 // EMIT_BIG pairs are written together: their pairs are numbered 0..S-1 in
@@ -103,89 +101,156 @@ __global__ __launch_bounds__(256) void k_emit(int N, int tbx, int tby, GaussOut 
     }
 }
 
+// Run edges of the sorted tile keys: tstart[t] / tend[t] = first / one past
+// the last position of key t.  Four keys per thread with one 16-byte load
+// (tkey is 256-byte aligned); the neighbours across a thread's four come from
+// single loads of the same or the adjacent line.
 __global__ __launch_bounds__(256) void k_tile_edges(int64_t I, const uint32_t* __restrict__ tkey,
                                                     int* __restrict__ tstart,
                                                     int* __restrict__ tend) {
-    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= I) return;
-    const uint32_t t = tkey[p];
-    if (p == 0 || tkey[p - 1] != t) tstart[t] = (int)p;
-    if (p == I - 1 || tkey[p + 1] != t) tend[t] = (int)(p + 1);
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t p0 = 4 * q;
+    if (p0 >= I) return;
+    uint32_t k[6];      // k[1..4]: this thread's keys, k[0] / k[5]: the neighbours
+    if (p0 + 4 <= I) {
+        const uint4 v = reinterpret_cast<const uint4*>(tkey)[q];
+        k[1] = v.x; k[2] = v.y; k[3] = v.z; k[4] = v.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) k[1 + j] = p0 + j < I ? tkey[p0 + j] : 0xFFFFFFFFu;
+    }
+    k[0] = p0 > 0 ? tkey[p0 - 1] : 0xFFFFFFFFu;
+    k[5] = p0 + 4 < I ? tkey[p0 + 4] : 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = 1; j <= 4; ++j) {
+        const int64_t p = p0 + j - 1;
+        if (p >= I) break;
+        const uint32_t t = k[j];
+        if (p == 0 || k[j - 1] != t) tstart[t] = (int)p;
+        if (p == I - 1 || k[j + 1] != t) tend[t] = (int)(p + 1);
+    }
 }
 
-__global__ __launch_bounds__(SCAN_T) void k_tile_scan(int T, int* __restrict__ tstart,
-                                                      int* __restrict__ tend,
-                                                      unsigned long long* __restrict__ isect,
-                                                      int* __restrict__ tile_bins, Items it,
-                                                      TileLists tl, Meta* __restrict__ meta) {
-    __shared__ long long s_c[SCAN_T];
-    __shared__ int s_i[SCAN_T];
-    __shared__ int s_max[SCAN_T];
-    __shared__ int s_nch;
-    const int tid = threadIdx.x;
-    const int per = (T + SCAN_T - 1) / SCAN_T;
-    const int b = min(tid * per, T), e = min(b + per, T);
-    long long cs = 0;
-    int is = 0, mx = 0;
-    for (int t = b; t < e; ++t) {
-        const int n = tend[t] - tstart[t];
-        cs += n;
-        is += tile_chunks(n, T);
-        mx = max(mx, n);
+// Tile scan over TS_BLOCK tiles per workgroup in two kernels.  k_tile_counts:
+// each block's tile count total, chunk-item total and largest count.
+// k_tile_offsets: each block adds the totals of the blocks before it, scans
+// its own tiles and writes tile_bins, the chunk counts and first items, the
+// work items (tile, chunk) and the list of chunked tiles; the last block
+// writes the summary.
+constexpr int TS_T = 256, TS_PER = 4, TS_BLOCK = TS_T * TS_PER;
+
+template <bool MAX>
+__device__ __forceinline__ int block_combine(int v, int* sh) {
+    for (int off = 32; off >= 1; off >>= 1) {
+        const int o = __shfl_xor(v, off, 64);
+        v = MAX ? max(v, o) : v + o;
     }
-    s_c[tid] = cs;
-    s_i[tid] = is;
-    s_max[tid] = mx;
-    if (tid == 0) s_nch = 0;
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
     __syncthreads();
-    for (int off = 1; off < SCAN_T; off <<= 1) {
-        long long c = 0;
-        int i = 0;
-        if (tid >= off) { c = s_c[tid - off]; i = s_i[tid - off]; }
-        const int m = s_max[tid ^ off];
+    int r = sh[0];
+#pragma unroll
+    for (int k = 1; k < TS_T / 64; ++k) r = MAX ? max(r, sh[k]) : r + sh[k];
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(TS_T) void k_tile_counts(int T, const int* __restrict__ tstart,
+                                                      const int* __restrict__ tend,
+                                                      int* __restrict__ tot,
+                                                      Meta* __restrict__ meta) {
+    __shared__ int sh[TS_T / 64];
+    const int b = blockIdx.x;
+    int sn = 0, sk = 0, mx = 0;
+#pragma unroll
+    for (int k = 0; k < TS_PER; ++k) {
+        const int t = b * TS_BLOCK + k * TS_T + (int)threadIdx.x;
+        if (t < T) {
+            const int n = tend[t] - tstart[t];
+            sn += n;
+            sk += tile_chunks(n, T);
+            mx = max(mx, n);
+        }
+    }
+    sn = block_combine<false>(sn, sh);
+    sk = block_combine<false>(sk, sh);
+    mx = block_combine<true>(mx, sh);
+    if (threadIdx.x == 0) {
+        tot[3 * b] = sn;
+        tot[3 * b + 1] = sk;
+        tot[3 * b + 2] = mx;
+        if (b == 0) meta->n_chunked_tiles = 0;
+    }
+}
+
+__global__ __launch_bounds__(TS_T) void k_tile_offsets(int T, int nb, int* __restrict__ tstart,
+                                                       int* __restrict__ tend,
+                                                       const int* __restrict__ tot,
+                                                       unsigned long long* __restrict__ isect,
+                                                       int* __restrict__ tile_bins, Items it,
+                                                       TileLists tl, Meta* __restrict__ meta) {
+    __shared__ int sh[TS_T / 64];
+    __shared__ int s_n[TS_T], s_k[TS_T];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    int pn = 0, pk = 0;
+    for (int i = tid; i < b; i += TS_T) {
+        pn += tot[3 * i];
+        pk += tot[3 * i + 1];
+    }
+    pn = block_combine<false>(pn, sh);
+    pk = block_combine<false>(pk, sh);
+    // this thread's TS_PER consecutive tiles
+    const int t0 = b * TS_BLOCK + TS_PER * tid;
+    int n[TS_PER], K[TS_PER], sn = 0, sk = 0;
+#pragma unroll
+    for (int k = 0; k < TS_PER; ++k) {
+        const int t = t0 + k;
+        n[k] = t < T ? tend[t] - tstart[t] : 0;
+        K[k] = t < T ? tile_chunks(n[k], T) : 0;
+        sn += n[k];
+        sk += K[k];
+    }
+    s_n[tid] = sn;
+    s_k[tid] = sk;
+    __syncthreads();
+    for (int off = 1; off < TS_T; off <<= 1) {
+        const int a = tid >= off ? s_n[tid - off] : 0;
+        const int c = tid >= off ? s_k[tid - off] : 0;
         __syncthreads();
-        s_c[tid] += c;
-        s_i[tid] += i;
-        s_max[tid] = max(s_max[tid], m);
+        s_n[tid] += a;
+        s_k[tid] += c;
         __syncthreads();
     }
-    long long off = s_c[tid] - cs;
-    int ioff = s_i[tid] - is;
-    for (int t = b; t < e; ++t) {
-        const int n = tend[t] - tstart[t];
+    int off = pn + s_n[tid] - sn, ioff = pk + s_k[tid] - sk;
+#pragma unroll
+    for (int k = 0; k < TS_PER; ++k) {
+        const int t = t0 + k;
+        if (t >= T) break;
         // cleared for the next frame's run edges (they write present tiles only)
         tstart[t] = 0;
         tend[t] = 0;
-        tile_bins[2 * t] = (int)off;
-        off += n;
-        tile_bins[2 * t + 1] = (int)off;
-        const int K = tile_chunks(n, T);
-        it.tile_K[t] = K;
+        tile_bins[2 * t] = off;
+        off += n[k];
+        tile_bins[2 * t + 1] = off;
+        it.tile_K[t] = K[k];
         it.tile_item0[t] = ioff;
-        ioff += K;
-        if (K > 1) tl.chunked[atomicAdd(&s_nch, 1)] = t;
+        for (int j = 0; j < K[k]; ++j) {
+            it.tile[ioff + j] = t;
+            it.k[ioff + j] = j;
+        }
+        ioff += K[k];
+        if (K[k] > 1) tl.chunked[atomicAdd(&meta->n_chunked_tiles, 1)] = t;
     }
     // the projection's intersection counters, copied to the host earlier
     // on the stream, cleared for the next frame
-    if (tid < ISECT_SLOTS) isect[(size_t)tid * ISECT_STRIDE] = 0ull;
-    __syncthreads();
-    if (tid == SCAN_T - 1) {
-        meta->total_isect = s_c[SCAN_T - 1];
-        meta->max_count = s_max[0];
-        meta->n_items = s_i[SCAN_T - 1];
-        meta->n_chunked_tiles = s_nch;
+    if (b == 0 && tid < ISECT_SLOTS) isect[(size_t)tid * ISECT_STRIDE] = 0ull;
+    if (b == nb - 1 && tid == 0) {
+        int mx = 0;
+        for (int i = 0; i < nb; ++i) mx = max(mx, tot[3 * i + 2]);
+        meta->total_isect = (int64_t)pn + s_n[TS_T - 1];
+        meta->max_count = mx;
+        meta->n_items = pk + s_k[TS_T - 1];
         meta->n_large = 0;
         meta->n_huge = 0;
-    }
-}
-
-__global__ __launch_bounds__(256) void k_build_items(int T, Items it) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= T) return;
-    const int K = it.tile_K[t], i0 = it.tile_item0[t];
-    for (int k = 0; k < K; ++k) {
-        it.tile[i0 + k] = t;
-        it.k[i0 + k] = k;
     }
 }
 
@@ -195,8 +260,8 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 void launch_run_edges(hipStream_t s, int64_t n, const uint32_t* sorted_keys, int* start, int* end) {
     if (n > 0)
-        hipLaunchKernelGGL(k_tile_edges, dim3(blocks_for(n)), dim3(256), 0, s, n, sorted_keys, start,
-                           end);
+        hipLaunchKernelGGL(k_tile_edges, dim3(blocks_for((n + 3) / 4)), dim3(256), 0, s, n,
+                           sorted_keys, start, end);
 }
 
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
@@ -213,8 +278,9 @@ void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, ui
 const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go,
                                   const uint32_t* order, const int* eoff, const int* hits,
                                   uint32_t* tkey, uint32_t* tval, uint32_t* tkey2, uint32_t* tval2,
-                                  int* radix_temp, int* tstart, int* tend, int* tile_bins, Items it,
-                                  TileLists tl, Meta* meta, unsigned long long* isect) {
+                                  int* radix_temp, int* tstart, int* tend, int* tscan,
+                                  int* tile_bins, Items it, TileLists tl, Meta* meta,
+                                  unsigned long long* isect) {
     const int T = p.tbx * p.tby;
     const uint32_t* sorted_ids = tval;
     // tstart / tend arrive zeroed: fresh buffers are, and every tile scan
@@ -227,11 +293,14 @@ const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, 
         const bool flip = launch_radix_sort(s, tkey, tval, tkey2, tval2, I, bits, radix_temp);
         const uint32_t* sk = flip ? tkey2 : tkey;
         sorted_ids = flip ? tval2 : tval;
-        hipLaunchKernelGGL(k_tile_edges, dim3(blocks_for(I)), dim3(256), 0, s, I, sk, tstart, tend);
+        hipLaunchKernelGGL(k_tile_edges, dim3(blocks_for((I + 3) / 4)), dim3(256), 0, s, I, sk,
+                           tstart, tend);
     }
-    hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(SCAN_T), 0, s, T, tstart, tend, isect,
-                       tile_bins, it, tl, meta);
-    hipLaunchKernelGGL(k_build_items, dim3(blocks_for(T)), dim3(256), 0, s, T, it);
+    const int nb = (T + TS_BLOCK - 1) / TS_BLOCK;
+    hipLaunchKernelGGL(k_tile_counts, dim3(nb), dim3(TS_T), 0, s, T, (const int*)tstart,
+                       (const int*)tend, tscan, meta);
+    hipLaunchKernelGGL(k_tile_offsets, dim3(nb), dim3(TS_T), 0, s, T, nb, tstart, tend,
+                       (const int*)tscan, isect, tile_bins, it, tl, meta);
     return sorted_ids;
 }
 

@@ -92,7 +92,7 @@ struct Ctx {
     Buf rec, radii, tiles_hit, gacc;
     Buf dkey, dval, dkey2, dval2, hits, eoff, dtemp, stemp;
     // per tile
-    Buf tstart, tend, tile_bins, tile_K, tile_item0, l_chunked;
+    Buf tstart, tend, tscan, tile_bins, tile_K, tile_item0, l_chunked;
     // per intersection
     Buf tkey, tval, tkey2, tval2, ttemp;
     // per item
@@ -184,7 +184,7 @@ T* P(Buf& b) { return reinterpret_cast<T*>(b.p); }
 void free_all(Ctx* c) {
     Buf* bufs[] = {&c->rec, &c->radii, &c->tiles_hit,
                    &c->gacc, &c->dkey, &c->dval, &c->dkey2, &c->dval2, &c->hits, &c->eoff,
-                   &c->dtemp, &c->stemp, &c->tstart, &c->tend, &c->tile_bins, &c->tile_K,
+                   &c->dtemp, &c->stemp, &c->tstart, &c->tend, &c->tscan, &c->tile_bins, &c->tile_K,
                    &c->tile_item0, &c->l_chunked, &c->tkey, &c->tval, &c->tkey2, &c->tval2,
                    &c->ttemp, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
@@ -358,6 +358,7 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     ENSURE(c->stemp, ((size_t)scan_block_count(N) + 8) * 4);
     ENSURE(c->tstart, (size_t)T * 4);
     ENSURE(c->tend, (size_t)T * 4);
+    ENSURE(c->tscan, (size_t)tile_scan_ints(T) * 4);
     ENSURE(c->tile_bins, (size_t)T * 8);
     ENSURE(c->tile_K, (size_t)T * 4);
     ENSURE(c->tile_item0, (size_t)T * 4);
@@ -429,6 +430,7 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
                                       P<int>(c->hits), P<uint32_t>(c->tkey), P<uint32_t>(c->tval),
                                       P<uint32_t>(c->tkey2), P<uint32_t>(c->tval2),
                                       P<int>(c->ttemp), P<int>(c->tstart), P<int>(c->tend),
+                                      P<int>(c->tscan),
                                       P<int>(c->tile_bins), it, tl, P<Meta>(c->meta_d),
                                       P<unsigned long long>(c->isect_d));
     c->isect_dirty = false;   // the tile scan clears the counters

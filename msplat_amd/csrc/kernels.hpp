@@ -110,8 +110,11 @@ void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, ui
 const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go,
                                   const uint32_t* order, const int* eoff, const int* hits,
                                   uint32_t* tkey, uint32_t* tval, uint32_t* tkey2, uint32_t* tval2,
-                                  int* radix_temp, int* tstart, int* tend, int* tile_bins, Items it,
-                                  TileLists tl, Meta* meta, unsigned long long* isect);
+                                  int* radix_temp, int* tstart, int* tend, int* tscan,
+                                  int* tile_bins, Items it, TileLists tl, Meta* meta,
+                                  unsigned long long* isect);
+// Ints of the tile scan's scratch (tscan) for T tiles.
+inline int64_t tile_scan_ints(int64_t T) { return 3 * ((T + 1023) / 1024) + 8; }
 
 // Raster pair counters: WORK_SLOTS sets of four u64 counters, each set in
 // its own 128-byte line (WORK_SLOT_U64 apart); totals are the sums over sets.
@@ -211,6 +214,8 @@ void launch_knn_cells(hipStream_t s, int64_t n, const float* xyz, const KnnGrid&
 void launch_knn_search(hipStream_t s, int64_t n, const float* xyz, const KnnGrid& g,
                        const uint32_t* order, const int* cstart, const int* cend,
                        float* mean_dist);
+// Run edges of sorted keys (sorted_keys 16-byte aligned): start[k] / end[k] =
+// first / one past the last position of key k; keys absent keep their value.
 void launch_run_edges(hipStream_t s, int64_t n, const uint32_t* sorted_keys, int* start, int* end);
 
 // Target images: area resize and Brown-Conrady undistortion (image.hip).
