@@ -333,7 +333,9 @@ def bench_config4(args):
                        "intersections": m["total_isect"], "largest_tile": m["max_count"],
                        "chunked_tiles": m["n_chunked_tiles"], "raster_items": m["n_items"]},
             "stage_ms": _stage_line(stages),
-            "bwd_grad_pairs_per_step": pairs[1] / n_staged}
+            "bwd_grad_pairs_per_step": pairs[1] / n_staged,
+            "raster_per_step": {"fwd_composited": pairs[0] / n_staged, "bwd_with_grad": pairs[1] / n_staged,
+                                "fwd_wave_steps": pairs[2] / n_staged, "bwd_wave_steps": pairs[3] / n_staged}}
 
 
 def bench_config5(args):

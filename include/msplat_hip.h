@@ -264,8 +264,11 @@ int msplat_hip_drain_raster_counters(int64_t counts[4]);
 /* Copy a named intermediate of the last render / train step to host memory.
  * Names: xys, depths, radii, conics, colors, aabb, num_tiles_hit,
  * tile_bins, gaussian_ids, final_Ts, final_index, out_img, v_rendered,
- * v_xy, v_conic, v_rgb, v_opacity, meta.  *nbytes is set to the size; pass
- * dst == NULL to query it. */
+ * v_xy, v_conic, v_rgb, v_opacity, meta, tile_done (after a train step, for
+ * each tile of more than 16 depth chunks: 1 if every pixel's running
+ * transmittance was exactly 0 after its first 16 chunks, so that its later
+ * chunks were not rasterised).  *nbytes is set to the size; pass dst == NULL
+ * to query it. */
 int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes);
 
 /* Algorithmic rasteriser work of the last render / train step, counted on the

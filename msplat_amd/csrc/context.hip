@@ -92,7 +92,7 @@ struct Ctx {
     Buf rec, radii, tiles_hit, gacc;
     Buf dkey, dval, dkey2, dval2, hits, eoff, dtemp, stemp;
     // per tile
-    Buf tstart, tend, tscan, tile_bins, tile_K, tile_item0, l_chunked;
+    Buf tstart, tend, tscan, tile_bins, tile_K, tile_item0, l_chunked, tile_done;
     // per intersection
     Buf tkey, tval, tkey2, tval2, ttemp;
     // per item
@@ -184,7 +184,7 @@ T* P(Buf& b) { return reinterpret_cast<T*>(b.p); }
 void free_all(Ctx* c) {
     Buf* bufs[] = {&c->rec, &c->radii, &c->tiles_hit,
                    &c->gacc, &c->dkey, &c->dval, &c->dkey2, &c->dval2, &c->hits, &c->eoff,
-                   &c->dtemp, &c->stemp, &c->tstart, &c->tend, &c->tscan, &c->tile_bins, &c->tile_K,
+                   &c->dtemp, &c->stemp, &c->tstart, &c->tend, &c->tscan, &c->tile_done, &c->tile_bins, &c->tile_K,
                    &c->tile_item0, &c->l_chunked, &c->tkey, &c->tval, &c->tkey2, &c->tval2,
                    &c->ttemp, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
@@ -363,6 +363,7 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     ENSURE(c->tile_K, (size_t)T * 4);
     ENSURE(c->tile_item0, (size_t)T * 4);
     ENSURE(c->l_chunked, (size_t)T * 4);
+    ENSURE(c->tile_done, (size_t)T * 4);
     ENSURE(c->final_T, Px * 4);
     ENSURE(c->final_idx, Px * 4);
     ENSURE(c->out_img, Px * 12);
@@ -443,9 +444,10 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
         // all chunks of a tile
         launch_raster_fwd(c->stream, p, max_items, P<Meta>(c->meta_d), it, P<int>(c->tile_bins),
                           pk, P<float>(c->final_T), P<int>(c->final_idx), img, cb,
-                          work_counters(c));
+                          work_counters(c), P<int>(c->l_chunked), P<int>(c->tile_done));
         launch_raster_merge(c->stream, p, P<Meta>(c->meta_d), P<int>(c->l_chunked), it,
-                            P<float>(c->final_T), P<int>(c->final_idx), img, cb, true);
+                            P<float>(c->final_T), P<int>(c->final_idx), img, cb, true,
+                            P<int>(c->tile_done));
     } else {
         launch_render_tiles(c->stream, p, it, P<int>(c->tile_bins), pk, P<float>(c->final_T),
                             P<int>(c->final_idx), img, work_counters(c));
@@ -1087,6 +1089,7 @@ int msplat_hip_copy_intermediate(const char* name, void* dst, size_t* nbytes) {
         {"final_Ts", &c->final_T, Px * 4},
         {"final_index", &c->final_idx, Px * 4}, {"out_img", &c->out_img, Px * 12},
         {"v_rendered", &c->v_rendered, Px * 12}, {"gacc", &c->gacc, N * 36},
+        {"tile_done", &c->tile_done, T * 4},
     };
     for (const D& d : direct) {
         if (n != d.name) continue;

@@ -130,9 +130,16 @@ inline int64_t items_bound(int64_t T, int64_t I) { return T + I / 512 + I / 2048
 // counter 0 and its wave-wide entry steps to counter 2, the backward its
 // pairs that carry a gradient to counter 1 and its wave-wide entry steps to
 // counter 3.
+// Training forward: every work item's chunk state (chunked tiles) or final
+// pixels (tiles in one piece).  A chunked tile with more than FWD_P chunks
+// whose running transmittance is exactly 0 at every pixel after its first
+// FWD_P chunks is marked in done[tile] (T ints) and its later chunks, which
+// change no output, are not computed; chunked is the tile scan's list.
+constexpr int FWD_P = 16;
 void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Entries pk, float* final_T, int* final_idx,
-                       float* out_img, ChunkBufs cb, unsigned long long* work);
+                       float* out_img, ChunkBufs cb, unsigned long long* work, const int* chunked,
+                       int* done);
 // Render-only forward, one workgroup per tile (chunked tiles rasterised chunk
 // by chunk up to the merge cutoff); writes the final image, T and index.
 void launch_render_tiles(hipStream_t s, const CamParams& p, Items it, const int* tile_bins,
@@ -140,7 +147,7 @@ void launch_render_tiles(hipStream_t s, const CamParams& p, Items it, const int*
                          unsigned long long* work);
 void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
                          Items it, float* final_T, int* final_idx, float* out_img, ChunkBufs cb,
-                         bool with_suffix);
+                         bool with_suffix, const int* done);
 void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Entries pk, const float* final_T,
                        const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc,

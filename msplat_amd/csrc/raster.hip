@@ -238,12 +238,17 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
                                                     float* __restrict__ final_T,
                                                     int* __restrict__ final_idx,
                                                     float* __restrict__ out_img, ChunkBufs cb,
-                                                    unsigned long long* __restrict__ work) {
+                                                    unsigned long long* __restrict__ work,
+                                                    int kmin, int kmax,
+                                                    const int* __restrict__ done) {
     __shared__ float4 s_geo[256];    // x, y, conic a, b
     __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
     __shared__ float4 s_aux[256];    // clamped b, mask (bits); 16-byte stride shares the address
     const int item = blockIdx.x;
     if (item >= meta->n_items) return;
+    // this launch's chunks: kmin <= k < kmax, of tiles not marked done
+    const int kk = it.k[item];
+    if (kk < kmin || kk >= kmax || (done && done[it.tile[item]])) return;
     int t, K, cs, ce;
     item_range(it, tile_bins, item, t, K, cs, ce);
     const Px px = pixel_of(t, tbx, W, H);
@@ -342,6 +347,41 @@ __global__ __launch_bounds__(256) void k_render_tiles(int W, int H, int tbx, flo
     out_img[3 * pix + 2] = clamp01(fmaf(bg2, Tr, R2));
 }
 
+// Training forward of the chunked tiles in two launches: chunks k < P first;
+// then, for a tile with more than P chunks, chunk k >= P only if some pixel
+// of the tile still has a nonzero running transmittance after the first P
+// (pT_P = T_0 T_1 ... T_{P-1}, multiplied in chunk order as the merge does).
+// Where every pixel's pT_P is exactly 0, every later chunk j has pT_j = 0:
+// its colour enters the suffix sums as pT_j * C_j = 0, it lies past every
+// pixel's merge cutoff (T_running = pT <= 1e-4 before it), so the merge
+// gives it index -1 and the backward skips it.  Its state would change no
+// output bit, so it is not computed; the merge reads only the first P chunks
+// of such a tile.  k_chunk_done marks those tiles.
+__global__ __launch_bounds__(256) void k_chunk_done(int W, int H, int tbx,
+                                                    const Meta* __restrict__ meta,
+                                                    const int* __restrict__ chunked, Items it,
+                                                    ChunkBufs cb, int P, int* __restrict__ done) {
+    __shared__ int s_any;
+    if ((int)blockIdx.x >= meta->n_chunked_tiles) return;
+    const int t = chunked[blockIdx.x];
+    const int K = it.tile_K[t], i0 = it.tile_item0[t];
+    if (K <= P) {
+        if (threadIdx.x == 0) done[t] = 0;
+        return;
+    }
+    if (threadIdx.x == 0) s_any = 0;
+    __syncthreads();
+    const int lp = threadIdx.x, lx = lp & 15, ly = lp >> 4;
+    const int j = (t % tbx) * BLOCK + lx, i = (t / tbx) * BLOCK + ly;
+    if (i < H && j < W) {
+        float pT = 1.f;
+        for (int k = 0; k < P; ++k) pT *= cb.cT[(size_t)(i0 + k) * TILE_PIX + lp];
+        if (pT != 0.f) s_any = 1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) done[t] = s_any ? 0 : 1;
+}
+
 __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, float bg0,
                                                       float bg1, float bg2,
                                                       const Meta* __restrict__ meta,
@@ -349,10 +389,14 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
                                                       float* __restrict__ final_T,
                                                       int* __restrict__ final_idx,
                                                       float* __restrict__ out_img, ChunkBufs cb,
-                                                      int with_suffix) {
+                                                      int with_suffix, const int* __restrict__ done,
+                                                      int P) {
     if ((int)blockIdx.x >= meta->n_chunked_tiles) return;
     const int t = chunked[blockIdx.x];
     const int K = it.tile_K[t], i0 = it.tile_item0[t];
+    // chunks with state: all K, or the first P of a tile whose later chunks
+    // were not computed (they carry pT = 0 and change no output)
+    const int Kc = (done && done[t]) ? min(K, P) : K;
     const int lp = threadIdx.x, lx = lp & 15, ly = lp >> 4;
     const int j = (t % tbx) * BLOCK + lx, i = (t / tbx) * BLOCK + ly;
     if (i >= H || j >= W) return;
@@ -363,13 +407,13 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
     // (every k < K is a valid chunk), so a tile with hundreds of chunks
     // costs one memory round trip per MG chunks instead of two per chunk.
     constexpr int MG = 8;
-    bool done = false;
-    for (int k0 = 0; k0 < K && !done; k0 += MG) {
+    bool stop = false;
+    for (int k0 = 0; k0 < Kc && !stop; k0 += MG) {
         int cf[MG];
         float cT[MG], c0[MG], c1[MG], c2[MG];
 #pragma unroll
         for (int u = 0; u < MG; ++u) {
-            const int k = min(k0 + u, K - 1);
+            const int k = min(k0 + u, Kc - 1);
             const size_t o = (size_t)(i0 + k) * TILE_PIX + lp;
             cf[u] = cb.cidx[o];
             cT[u] = cb.cT[o];
@@ -380,8 +424,8 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
 #pragma unroll
         for (int u = 0; u < MG; ++u) {
             const int k = k0 + u;
-            if (k >= K || (cf[u] < 0 && k > 0)) {
-                done = true;
+            if (k >= Kc || (cf[u] < 0 && k > 0)) {
+                stop = true;
                 break;
             }
             R0 = fmaf(c0[u], Tr, R0);
@@ -391,7 +435,7 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
             if (cf[u] >= 0) li = cf[u];
             if (Tr <= 1e-4f) {
                 cutoff = k + 1;
-                done = true;
+                stop = true;
                 break;
             }
         }
@@ -405,22 +449,23 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
     out_img[3 * pix + 2] = clamp01(fmaf(bg2, Tr, R2));
     if (!with_suffix) return;
     // prefix products of T and suffix sums of the chunk colours, each over
-    // all K chunks, with the loads of MG chunks issued ahead of their stores
+    // all chunks with state (the rest add pT * C = 0), with the loads of MG
+    // chunks issued ahead of their stores
     float pT = 1.f;
-    for (int k0 = 0; k0 < K; k0 += MG) {
+    for (int k0 = 0; k0 < Kc; k0 += MG) {
         float t[MG];
 #pragma unroll
         for (int u = 0; u < MG; ++u)
-            t[u] = cb.cT[(size_t)(i0 + min(k0 + u, K - 1)) * TILE_PIX + lp];
+            t[u] = cb.cT[(size_t)(i0 + min(k0 + u, Kc - 1)) * TILE_PIX + lp];
 #pragma unroll
         for (int u = 0; u < MG; ++u) {
-            if (k0 + u >= K) break;
+            if (k0 + u >= Kc) break;
             cb.pT[(size_t)(i0 + k0 + u) * TILE_PIX + lp] = pT;
             pT *= t[u];
         }
     }
     float a0 = 0.f, a1 = 0.f, a2 = 0.f;
-    for (int k1 = K - 1; k1 >= 0; k1 -= MG) {
+    for (int k1 = Kc - 1; k1 >= 0; k1 -= MG) {
         float pp[MG], q0[MG], q1[MG], q2[MG];
 #pragma unroll
         for (int u = 0; u < MG; ++u) {
@@ -680,11 +725,20 @@ void launch_raster_work(hipStream_t s, const CamParams& p, int64_t max_items, co
 
 void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Entries pk, float* final_T, int* final_idx,
-                       float* out_img, ChunkBufs cb, unsigned long long* work) {
+                       float* out_img, ChunkBufs cb, unsigned long long* work, const int* chunked,
+                       int* done) {
     if (max_items <= 0) return;
+    // chunks 0 .. FWD_P - 1 of every tile, then the tiles' later chunks that
+    // k_chunk_done does not mark as past an all-zero running transmittance
     hipLaunchKernelGGL(k_raster_fwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
                        p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx,
-                       out_img, cb, work);
+                       out_img, cb, work, 0, FWD_P, (const int*)nullptr);
+    const int T = p.tbx * p.tby;
+    hipLaunchKernelGGL(k_chunk_done, dim3((unsigned)T), dim3(256), 0, s, p.W, p.H, p.tbx, meta,
+                       chunked, it, cb, FWD_P, done);
+    hipLaunchKernelGGL(k_raster_fwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
+                       p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx,
+                       out_img, cb, work, FWD_P, 1 << 30, (const int*)done);
 }
 
 void launch_render_tiles(hipStream_t s, const CamParams& p, Items it, const int* tile_bins,
@@ -699,11 +753,11 @@ void launch_render_tiles(hipStream_t s, const CamParams& p, Items it, const int*
 
 void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
                          Items it, float* final_T, int* final_idx, float* out_img, ChunkBufs cb,
-                         bool with_suffix) {
+                         bool with_suffix, const int* done) {
     const int T = p.tbx * p.tby;
     hipLaunchKernelGGL(k_raster_merge, dim3(T), dim3(256), 0, s, p.W, p.H, p.tbx, p.bg[0], p.bg[1],
                        p.bg[2], meta, chunked, it, final_T, final_idx, out_img, cb,
-                       with_suffix ? 1 : 0);
+                       with_suffix ? 1 : 0, done, FWD_P);
 }
 
 void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,

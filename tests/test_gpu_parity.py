@@ -98,6 +98,25 @@ def test_train_step_chunked(dev):
     _train_compare(dev, small_scene(n=30000, width=96, height=64, seed_off=81, spread=0.6))
 
 
+def test_train_step_deep_chunks_past_zero_transmittance(dev):
+    """Tiles of more than 16 depth chunks (20k gaussians of scale about 1 in a
+    64x64 image: 16 tiles of 18k-20k entries, all chunked).  Twelve tiles
+    reach a running transmittance of exactly 0 at every pixel within their
+    first 16 chunks, so their later chunks are not rasterised; the four
+    corner tiles do not, and theirs are.  Image, T, final index, gradients
+    and the Adam step still equal the oracle's, which rasterises every
+    chunk."""
+    sc = small_scene(n=20000, width=64, height=64, seed_off=86, spread=0.2)
+    sc.scales = sc.scales + np.float32(4.5)      # log scales N(0, 0.5^2)
+    _train_compare(dev, sc)
+    tb = dev.intermediate("tile_bins", np.int32).reshape(-1, 2)
+    counts = tb[:, 1] - tb[:, 0]
+    assert (counts > 16 * 512).all(), counts
+    done = dev.intermediate("tile_done", np.int32)[: counts.size]
+    # both launches of the chunked forward ran: skipped and computed tails
+    assert set(np.nonzero(done == 0)[0]) == {0, 3, 12, 15}, done
+
+
 def test_train_step_monolithic(dev):
     _train_compare(dev, small_scene(n=12000, width=336, height=208, seed_off=82))
 
