@@ -205,10 +205,8 @@ def traffic_summary(dirs: list, copy_mib: int, last: int, commands: str,
 
 def pmc_summary(d: str, kernels: list, last: int, command: str) -> str:
     """Markdown table of every counter in a `rocprofv3 --pmc -f csv` output
-    directory, averaged per dispatch over the last `last` dispatches of each
-    kernel (all when last <= 0), with the derived rates: VALU busy = VALU
-    active cycles / (4 SIMDs x busy cycles x CUs), LDS bank conflicts per LDS
-    instruction, waits per executed instruction."""
+    directory for each kernel whose name matches one of `kernels`, averaged
+    per dispatch over its last `last` dispatches (all when last <= 0)."""
     import csv
     import glob
     import re

@@ -134,9 +134,9 @@ __global__ __launch_bounds__(256) void k_tile_edges(int64_t I, const uint32_t* _
 // Tile scan over TS_BLOCK tiles per workgroup in two kernels.  k_tile_counts:
 // each block's tile count total, chunk-item total and largest count.
 // k_tile_offsets: each block adds the totals of the blocks before it, scans
-// its own tiles and writes tile_bins, the chunk counts and first items, the
-// work items (tile, chunk) and the list of chunked tiles; the last block
-// writes the summary.
+// its own tiles and writes tile_bins, the chunk counts and first items and
+// the list of chunked tiles; the last block writes the summary.  Then
+// k_build_items writes the work items (tile, chunk), one thread per item.
 constexpr int TS_T = 256, TS_PER = 4, TS_BLOCK = TS_T * TS_PER;
 
 template <bool MAX>
@@ -233,10 +233,6 @@ __global__ __launch_bounds__(TS_T) void k_tile_offsets(int T, int nb, int* __res
         tile_bins[2 * t + 1] = off;
         it.tile_K[t] = K[k];
         it.tile_item0[t] = ioff;
-        for (int j = 0; j < K[k]; ++j) {
-            it.tile[ioff + j] = t;
-            it.k[ioff + j] = j;
-        }
         ioff += K[k];
         if (K[k] > 1) tl.chunked[atomicAdd(&meta->n_chunked_tiles, 1)] = t;
     }
@@ -252,6 +248,21 @@ __global__ __launch_bounds__(TS_T) void k_tile_offsets(int T, int nb, int* __res
         meta->n_large = 0;
         meta->n_huge = 0;
     }
+}
+
+// Work item i: the tile t with tile_item0[t] <= i < tile_item0[t + 1] (every
+// tile has at least one item, so the first items ascend), found by binary
+// search, and its chunk i - tile_item0[t].
+__global__ __launch_bounds__(256) void k_build_items(int T, const Meta* __restrict__ meta, Items it) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= meta->n_items) return;
+    int lo = 0, hi = T - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (it.tile_item0[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    it.tile[i] = lo;
+    it.k[i] = i - it.tile_item0[lo];
 }
 
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -301,6 +312,8 @@ const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, 
                        (const int*)tend, tscan, meta);
     hipLaunchKernelGGL(k_tile_offsets, dim3(nb), dim3(TS_T), 0, s, T, nb, tstart, tend,
                        (const int*)tscan, isect, tile_bins, it, tl, meta);
+    hipLaunchKernelGGL(k_build_items, dim3(blocks_for(items_bound(T, I))), dim3(256), 0, s, T,
+                       (const Meta*)meta, it);
     return sorted_ids;
 }
 
