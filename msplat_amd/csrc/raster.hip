@@ -231,24 +231,14 @@ __device__ __forceinline__ void add_work(unsigned long long* work, unsigned ncl,
     if (lane == 0 && nwit) atomicAdd(ws + 2, (unsigned long long)nwit);
 }
 
-__global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float bg0, float bg1,
-                                                    float bg2, const Meta* __restrict__ meta,
-                                                    Items it,
-                                                    const int* __restrict__ tile_bins, Entries pk,
-                                                    float* __restrict__ final_T,
-                                                    int* __restrict__ final_idx,
-                                                    float* __restrict__ out_img, ChunkBufs cb,
-                                                    unsigned long long* __restrict__ work,
-                                                    int kmin, int kmax,
-                                                    const int* __restrict__ done) {
-    __shared__ float4 s_geo[256];    // x, y, conic a, b
-    __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
-    __shared__ float4 s_aux[256];    // clamped b, mask (bits); 16-byte stride shares the address
-    const int item = blockIdx.x;
-    if (item >= meta->n_items) return;
-    // this launch's chunks: kmin <= k < kmax, of tiles not marked done
-    const int kk = it.k[item];
-    if (kk < kmin || kk >= kmax || (done && done[it.tile[item]])) return;
+// One work item of the training forward: its chunk's state (chunked tile)
+// or the tile's final pixels (tile in one piece).
+__device__ __forceinline__ void fwd_item(int item, int W, int H, int tbx, float bg0, float bg1,
+                                         float bg2, const Items& it, const int* tile_bins,
+                                         const Entries& pk, float* final_T, int* final_idx,
+                                         float* out_img, const ChunkBufs& cb,
+                                         unsigned long long* work, float4* s_geo, float4* s_col,
+                                         float4* s_aux) {
     int t, K, cs, ce;
     item_range(it, tile_bins, item, t, K, cs, ce);
     const Px px = pixel_of(t, tbx, W, H);
@@ -280,6 +270,45 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
         cb.cC[3 * o + 1] = C1;
         cb.cC[3 * o + 2] = C2;
         cb.cidx[o] = last;
+    }
+}
+
+// Chunks 0 .. kmax - 1 of every tile, one item per workgroup.
+__global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float bg0, float bg1,
+                                                    float bg2, const Meta* __restrict__ meta,
+                                                    Items it,
+                                                    const int* __restrict__ tile_bins, Entries pk,
+                                                    float* __restrict__ final_T,
+                                                    int* __restrict__ final_idx,
+                                                    float* __restrict__ out_img, ChunkBufs cb,
+                                                    unsigned long long* __restrict__ work,
+                                                    int kmax) {
+    __shared__ float4 s_geo[256];    // x, y, conic a, b
+    __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
+    __shared__ float4 s_aux[256];    // clamped b, mask (bits); 16-byte stride shares the address
+    const int item = blockIdx.x;
+    if (item >= meta->n_items || it.k[item] >= kmax) return;
+    fwd_item(item, W, H, tbx, bg0, bg1, bg2, it, tile_bins, pk, final_T, final_idx, out_img, cb,
+             work, s_geo, s_col, s_aux);
+}
+
+// Chunks kmin and later of the tiles not marked done, the workgroups striding
+// over the items (few items qualify, so a small grid visits them all).
+__global__ __launch_bounds__(256) void k_raster_fwd_tail(int W, int H, int tbx,
+                                                         const Meta* __restrict__ meta, Items it,
+                                                         const int* __restrict__ tile_bins,
+                                                         Entries pk, ChunkBufs cb,
+                                                         unsigned long long* __restrict__ work,
+                                                         int kmin, const int* __restrict__ done) {
+    __shared__ float4 s_geo[256];
+    __shared__ float4 s_col[256];
+    __shared__ float4 s_aux[256];
+    const int n = meta->n_items;
+    for (int item = blockIdx.x; item < n; item += gridDim.x) {
+        if (it.k[item] < kmin || done[it.tile[item]]) continue;
+        // chunked tiles only (k >= kmin > 0): no final pixels are written
+        fwd_item(item, W, H, tbx, 0.f, 0.f, 0.f, it, tile_bins, pk, nullptr, nullptr, nullptr, cb,
+                 work, s_geo, s_col, s_aux);
     }
 }
 
@@ -362,24 +391,27 @@ __global__ __launch_bounds__(256) void k_chunk_done(int W, int H, int tbx,
                                                     const int* __restrict__ chunked, Items it,
                                                     ChunkBufs cb, int P, int* __restrict__ done) {
     __shared__ int s_any;
-    if ((int)blockIdx.x >= meta->n_chunked_tiles) return;
-    const int t = chunked[blockIdx.x];
-    const int K = it.tile_K[t], i0 = it.tile_item0[t];
-    if (K <= P) {
-        if (threadIdx.x == 0) done[t] = 0;
-        return;
+    const int nch = meta->n_chunked_tiles;
+    for (int b = blockIdx.x; b < nch; b += gridDim.x) {
+        const int t = chunked[b];
+        const int K = it.tile_K[t], i0 = it.tile_item0[t];
+        if (K <= P) {
+            if (threadIdx.x == 0) done[t] = 0;
+            continue;
+        }
+        __syncthreads();     // the previous tile's s_any has been read
+        if (threadIdx.x == 0) s_any = 0;
+        __syncthreads();
+        const int lp = threadIdx.x, lx = lp & 15, ly = lp >> 4;
+        const int j = (t % tbx) * BLOCK + lx, i = (t / tbx) * BLOCK + ly;
+        if (i < H && j < W) {
+            float pT = 1.f;
+            for (int k = 0; k < P; ++k) pT *= cb.cT[(size_t)(i0 + k) * TILE_PIX + lp];
+            if (pT != 0.f) s_any = 1;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) done[t] = s_any ? 0 : 1;
     }
-    if (threadIdx.x == 0) s_any = 0;
-    __syncthreads();
-    const int lp = threadIdx.x, lx = lp & 15, ly = lp >> 4;
-    const int j = (t % tbx) * BLOCK + lx, i = (t / tbx) * BLOCK + ly;
-    if (i < H && j < W) {
-        float pT = 1.f;
-        for (int k = 0; k < P; ++k) pT *= cb.cT[(size_t)(i0 + k) * TILE_PIX + lp];
-        if (pT != 0.f) s_any = 1;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) done[t] = s_any ? 0 : 1;
 }
 
 __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, float bg0,
@@ -732,13 +764,13 @@ void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, con
     // k_chunk_done does not mark as past an all-zero running transmittance
     hipLaunchKernelGGL(k_raster_fwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
                        p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx,
-                       out_img, cb, work, 0, FWD_P, (const int*)nullptr);
+                       out_img, cb, work, FWD_P);
     const int T = p.tbx * p.tby;
-    hipLaunchKernelGGL(k_chunk_done, dim3((unsigned)T), dim3(256), 0, s, p.W, p.H, p.tbx, meta,
-                       chunked, it, cb, FWD_P, done);
-    hipLaunchKernelGGL(k_raster_fwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
-                       p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx,
-                       out_img, cb, work, FWD_P, 1 << 30, (const int*)done);
+    hipLaunchKernelGGL(k_chunk_done, dim3((unsigned)std::min(T, 256)), dim3(256), 0, s, p.W, p.H,
+                       p.tbx, meta, chunked, it, cb, FWD_P, done);
+    hipLaunchKernelGGL(k_raster_fwd_tail, dim3((unsigned)std::min<int64_t>(max_items, 1024)),
+                       dim3(256), 0, s, p.W, p.H, p.tbx, meta, it, tile_bins, pk, cb, work, FWD_P,
+                       (const int*)done);
 }
 
 void launch_render_tiles(hipStream_t s, const CamParams& p, Items it, const int* tile_bins,
