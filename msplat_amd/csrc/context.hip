@@ -89,12 +89,16 @@ struct Ctx {
     hipEvent_t ev_total = nullptr;   // recorded after the intersection total's copy to the host
 
     // per gaussian
-    Buf rec, radii, tiles_hit, gacc;
-    Buf dkey, dval, dkey2, dval2, hits, eoff, dtemp, stemp;
+    Buf rec, radii, tiles_hit, rect, gacc;
+    Buf dkey, dval, dkey2, dval2, rect_sorted, hits, eoff, dtemp, stemp;
     // per tile
-    Buf tstart, tend, tscan, tile_bins, tile_K, tile_item0, l_chunked, tile_done;
-    // per intersection
-    Buf tkey, tval, tkey2, tval2, ttemp;
+    Buf tcount, tscan, tile_bins, tile_K, tile_item0, l_chunked, tile_done;
+    // per super-tile, per super-tile reference, per pair block
+    Buf st_r0, st_r1, st_p0, st_p1, st_re, bstart;
+    Buf rkey, rval, rkey2, rval2, rtemp, npairs, poff, pscan;
+    Buf blk, blk_wend, phist;
+    // per intersection: the tile-sorted gaussian ids
+    Buf tval;
     // per item
     Buf it_tile, it_k, c_T, c_C, c_idx, c_pT, c_aC;
     // per pixel
@@ -117,7 +121,7 @@ struct Ctx {
     // densify scratch
     Buf d_split, d_dup, d_sp, d_dp, d_keep, d_kp, d_tot, d_scratch, d_rnd, d_src;
 
-    const uint32_t* sorted_ids = nullptr;   // tile-sorted gaussian ids (tval or tval2)
+    const uint32_t* sorted_ids = nullptr;   // tile-sorted gaussian ids (tval)
     Meta meta{};
     bool meta_valid = false;
     // Loss of the most recent train step known to have completed (NaN before
@@ -182,11 +186,13 @@ template <typename T>
 T* P(Buf& b) { return reinterpret_cast<T*>(b.p); }
 
 void free_all(Ctx* c) {
-    Buf* bufs[] = {&c->rec, &c->radii, &c->tiles_hit,
+    Buf* bufs[] = {&c->rec, &c->radii, &c->tiles_hit, &c->rect, &c->rect_sorted,
                    &c->gacc, &c->dkey, &c->dval, &c->dkey2, &c->dval2, &c->hits, &c->eoff,
-                   &c->dtemp, &c->stemp, &c->tstart, &c->tend, &c->tscan, &c->tile_done, &c->tile_bins, &c->tile_K,
-                   &c->tile_item0, &c->l_chunked, &c->tkey, &c->tval, &c->tkey2, &c->tval2,
-                   &c->ttemp, &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
+                   &c->dtemp, &c->stemp, &c->tcount, &c->tscan, &c->tile_done, &c->tile_bins, &c->tile_K,
+                   &c->tile_item0, &c->l_chunked, &c->st_r0, &c->st_r1, &c->st_p0, &c->st_p1,
+                   &c->st_re, &c->bstart, &c->rkey, &c->rval, &c->rkey2, &c->rval2, &c->rtemp,
+                   &c->npairs, &c->poff, &c->pscan, &c->blk, &c->blk_wend, &c->phist, &c->tval,
+                   &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
                    &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
                    &c->count_d, &c->work_d, &c->isect_d, &c->eval_part, &c->eval_out, &c->knn_k, &c->knn_v, &c->knn_k2, &c->knn_v2,
@@ -210,6 +216,7 @@ GaussOut gauss_out(Ctx* c) {
     go.rec = P<float4>(c->rec);
     go.radii = P<int>(c->radii);
     go.tiles_hit = P<int>(c->tiles_hit);
+    go.rect = P<uint2>(c->rect);
     return go;
 }
 
@@ -347,6 +354,8 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     ENSURE(c->rec, Nn * 64);
     ENSURE(c->radii, Nn * 4);
     ENSURE(c->tiles_hit, Nn * 4);
+    ENSURE(c->rect, Nn * 8);
+    ENSURE(c->rect_sorted, Nn * 8);
     ENSURE(c->gacc, Nn * 36);
     ENSURE(c->dkey, Nn * 4);
     ENSURE(c->dval, Nn * 4);
@@ -356,9 +365,18 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     ENSURE(c->eoff, Nn * 4);
     ENSURE(c->dtemp, (size_t)radix_temp_ints(N) * 4);
     ENSURE(c->stemp, ((size_t)scan_block_count(N) + 8) * 4);
-    ENSURE(c->tstart, (size_t)T * 4);
-    ENSURE(c->tend, (size_t)T * 4);
+    ENSURE(c->tcount, (size_t)T * 4);
     ENSURE(c->tscan, (size_t)tile_scan_ints(T) * 4);
+    const int nst = super_tiles(p.tbx, p.tby);
+    if (nst > 65536 || p.tbx > 65535 || p.tby > 65535)
+        return fail(MSPLAT_ERR_ARG, "%dx%d tiles exceed the binning's limits (65535 per side, "
+                    "65536 super-tiles of %dx%d)", p.tbx, p.tby, SUPER, SUPER);
+    ENSURE(c->st_r0, (size_t)nst * 4);
+    ENSURE(c->st_r1, (size_t)nst * 4);
+    ENSURE(c->st_p0, (size_t)nst * 4);
+    ENSURE(c->st_p1, (size_t)nst * 4);
+    ENSURE(c->st_re, (size_t)nst * 4);
+    ENSURE(c->bstart, ((size_t)nst + 1) * 4);
     ENSURE(c->tile_bins, (size_t)T * 8);
     ENSURE(c->tile_K, (size_t)T * 4);
     ENSURE(c->tile_item0, (size_t)T * 4);
@@ -392,25 +410,37 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     uint32_t* order = nullptr;
     launch_depth_order(c->stream, N, P<uint32_t>(c->dkey), P<uint32_t>(c->dval),
                        P<uint32_t>(c->dkey2), P<uint32_t>(c->dval2), P<int>(c->dtemp),
-                       P<int>(c->tiles_hit), P<int>(c->hits), P<int>(c->eoff), P<int>(c->stemp),
-                       &order);
+                       P<uint2>(c->rect), P<uint2>(c->rect_sorted), P<int>(c->hits),
+                       P<int>(c->eoff), P<int>(c->stemp), &order);
     HIP_TRY(hipEventSynchronize(c->ev_total));
     if (c->timing) stage_fold(c, c->cur ^ 1);   // the previous call has completed
     if (c->loss_pending) {                       // so has its loss copy
         c->last_loss = c->loss_h[1] * c->loss_scale;
         c->loss_pending = false;
     }
-    int64_t I64 = 0;
-    for (int k = 0; k < ISECT_SLOTS; ++k) I64 += (int64_t)c->isect_h[(size_t)k * ISECT_STRIDE];
+    int64_t I64 = 0, R64 = 0;
+    for (int k = 0; k < ISECT_SLOTS; ++k) {
+        I64 += (int64_t)c->isect_h[(size_t)k * ISECT_STRIDE];
+        R64 += (int64_t)c->isect_h[(size_t)k * ISECT_STRIDE + 1];
+    }
     if (I64 > (int64_t)0x7FFFFFFF - 4096)
         return fail(MSPLAT_ERR_ARG, "%lld tile intersections exceed the 32-bit index range",
                     (long long)I64);
     const size_t I = (size_t)std::max<int64_t>(I64, 1);
-    ENSURE(c->tkey, I * 4);
+    const size_t R = (size_t)std::max<int64_t>(R64, 1);
+    const size_t NB = (size_t)pair_blocks_bound(I64, nst);
     ENSURE(c->tval, I * 4);
-    ENSURE(c->tkey2, I * 4);
-    ENSURE(c->tval2, I * 4);
-    ENSURE(c->ttemp, (size_t)radix_temp_ints((int64_t)I) * 4);
+    ENSURE(c->rkey, R * 4);
+    ENSURE(c->rval, R * 4);
+    ENSURE(c->rkey2, R * 4);
+    ENSURE(c->rval2, R * 4);
+    ENSURE(c->rtemp, (size_t)radix_temp_ints((int64_t)R) * 4);
+    ENSURE(c->npairs, R * 4);
+    ENSURE(c->poff, R * 4);
+    ENSURE(c->pscan, ((size_t)scan_block_count((int64_t)R) + 8) * 4);
+    ENSURE(c->blk, NB * 16);
+    ENSURE(c->blk_wend, NB * 4);
+    ENSURE(c->phist, NB * SUPER * SUPER * 4);
     const int64_t max_items = items_bound(T, I64);
     ENSURE(c->it_tile, (size_t)max_items * 4);
     ENSURE(c->it_k, (size_t)max_items * 4);
@@ -423,17 +453,32 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
         ENSURE(c->c_aC, S * 12);
     }
     c->max_items = max_items;
-    go = gauss_out(c);
     stage_mark(c, S_TILES);
     TileLists tl{P<int>(c->l_chunked), nullptr, nullptr};
     Items it = items(c);
-    c->sorted_ids = launch_tile_lists(c->stream, p, I64, go, order, P<int>(c->eoff),
-                                      P<int>(c->hits), P<uint32_t>(c->tkey), P<uint32_t>(c->tval),
-                                      P<uint32_t>(c->tkey2), P<uint32_t>(c->tval2),
-                                      P<int>(c->ttemp), P<int>(c->tstart), P<int>(c->tend),
-                                      P<int>(c->tscan),
-                                      P<int>(c->tile_bins), it, tl, P<Meta>(c->meta_d),
-                                      P<unsigned long long>(c->isect_d));
+    RefBufs rb;
+    rb.key = P<uint32_t>(c->rkey);
+    rb.val = P<uint32_t>(c->rval);
+    rb.key2 = P<uint32_t>(c->rkey2);
+    rb.val2 = P<uint32_t>(c->rval2);
+    rb.radix_temp = P<int>(c->rtemp);
+    rb.npairs = P<int>(c->npairs);
+    rb.poff = P<int>(c->poff);
+    rb.scan_temp = P<int>(c->pscan);
+    rb.st_r0 = P<int>(c->st_r0);
+    rb.st_r1 = P<int>(c->st_r1);
+    rb.st_p0 = P<int>(c->st_p0);
+    rb.st_p1 = P<int>(c->st_p1);
+    rb.st_re = P<int>(c->st_re);
+    rb.bstart = P<int>(c->bstart);
+    rb.blk = P<int4>(c->blk);
+    rb.blk_wend = P<int>(c->blk_wend);
+    rb.hist = P<int>(c->phist);
+    rb.tcount = P<int>(c->tcount);
+    launch_tile_lists(c->stream, p, I64, R64, order, P<int>(c->eoff), P<uint2>(c->rect_sorted), rb,
+                      P<uint32_t>(c->tval), P<int>(c->tscan), P<int>(c->tile_bins), it, tl,
+                      P<Meta>(c->meta_d), P<unsigned long long>(c->isect_d));
+    c->sorted_ids = P<uint32_t>(c->tval);
     c->isect_dirty = false;   // the tile scan clears the counters
     Entries pk = packed(c);
     float* img = dst_img ? dst_img : P<float>(c->out_img);

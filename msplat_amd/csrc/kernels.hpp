@@ -34,6 +34,7 @@ struct GaussOut {
     float4* rec;
     int* radii;
     int* tiles_hit;
+    uint2* rect;         // tile rectangle: (x0 | y0 << 16, x1 | y1 << 16), 0 when culled
 };
 
 // Tile-sorted entries: ids[i] is the gaussian of entry i; the rasteriser
@@ -79,8 +80,10 @@ struct ChunkBufs {
     float* aC;           // x3
 };
 
-// Intersection-total counters of the projection: ISECT_SLOTS u64 counters
-// ISECT_STRIDE u64 apart (one 128-byte line each); the total is their sum.
+// Intersection-total counters of the projection: ISECT_SLOTS u64 counter
+// pairs ISECT_STRIDE u64 apart (one 128-byte line each); the first of a pair
+// counts (gaussian, tile) pairs, the second (gaussian, super-tile)
+// references; the totals are the sums over the slots.
 constexpr int ISECT_SLOTS = 64;
 constexpr int ISECT_STRIDE = 16;
 void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
@@ -99,20 +102,57 @@ int64_t radix_temp_ints(int64_t n);
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
                        int64_t n, int bits, int* temp);
 
-// Binning (binning.hip).  The projection adds the intersection total to
-// meta->total_isect (needed on the host before launch_tile_lists);
-// launch_depth_order orders the gaussians by depth and scans their tile
-// counts in that order.
+// Super-tiles: SUPER x SUPER tiles of the tile grid.  A gaussian's tile
+// rectangle is cut into one reference per super-tile it overlaps; the
+// references are sorted by super-tile and each super-tile's (tile, gaussian)
+// pairs are enumerated from them in blocks of PAIR_BLOCK pairs.
+constexpr int SUPER = 16;
+constexpr int PAIR_BLOCK = 4096;
+inline int super_tiles(int tbx, int tby) {
+    return ((tbx + SUPER - 1) / SUPER) * ((tby + SUPER - 1) / SUPER);
+}
+// Super-tiles overlapped by the non-empty tile rectangle [x0, x1) x [y0, y1).
+__host__ __device__ inline int super_span(int x0, int y0, int x1, int y1) {
+    return ((x1 - 1) / SUPER - x0 / SUPER + 1) * ((y1 - 1) / SUPER - y0 / SUPER + 1);
+}
+
+// Binning (binning.hip).  The projection adds the intersection and
+// reference totals to the counters above (needed on the host before
+// launch_tile_lists); launch_depth_order orders the gaussians by depth,
+// gathers their tile rectangles in that order (rect_sorted) and scans their
+// super-tile counts (rcount) into reference offsets (roff).
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
-                        uint32_t* dval2, int* radix_temp, const int* tiles_hit, int* hits_sorted,
-                        int* eoff, int* scan_temp, uint32_t** order_out);
-// Returns the buffer (tval or tval2) that holds the tile-sorted gaussian ids.
-const uint32_t* launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, GaussOut go,
-                                  const uint32_t* order, const int* eoff, const int* hits,
-                                  uint32_t* tkey, uint32_t* tval, uint32_t* tkey2, uint32_t* tval2,
-                                  int* radix_temp, int* tstart, int* tend, int* tscan,
-                                  int* tile_bins, Items it, TileLists tl, Meta* meta,
-                                  unsigned long long* isect);
+                        uint32_t* dval2, int* radix_temp, const uint2* rect, uint2* rect_sorted,
+                        int* rcount, int* roff, int* scan_temp, uint32_t** order_out);
+// Upper bound of the pair blocks for I pairs over S super-tiles.
+inline int64_t pair_blocks_bound(int64_t I, int64_t S) { return I / PAIR_BLOCK + S + 1; }
+
+// Scratch of launch_tile_lists for R references, S super-tiles, NB =
+// pair_blocks_bound(I, S) pair blocks and T tiles.
+struct RefBufs {
+    uint32_t *key, *val, *key2, *val2;   // R each: references, ping-pong
+    int* radix_temp;                     // radix_temp_ints(R)
+    int* npairs;                         // R
+    int* poff;                           // R: first pair of each reference
+    int* scan_temp;                      // scan_block_count(R) + 8
+    int* st_r0;                          // S: reference range of each super-tile;
+    int* st_r1;                          //    S; both zero between calls
+    int* st_p0;                          // S: pair range of each super-tile
+    int* st_p1;                          // S
+    int* st_re;                          // S: end of its reference range
+    int* bstart;                         // S + 1: first pair block of each super-tile
+    int4* blk;                           // NB: (super-tile, reference holding the first
+                                         //     pair, first pair, pairs) of each pair block
+    int* blk_wend;                       // NB: end of the block's reference window
+    int* hist;                           // NB * 256: pairs per local tile and block
+    int* tcount;                         // T: pairs per tile
+};
+// Writes the tile-sorted gaussian ids (I of them) to ids, tile_bins, the
+// work items and the summary in meta.
+void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
+                       const uint32_t* order, const int* roff, const uint2* rect_sorted, RefBufs rb,
+                       uint32_t* ids, int* tscan, int* tile_bins, Items it, TileLists tl,
+                       Meta* meta, unsigned long long* isect);
 // Ints of the tile scan's scratch (tscan) for T tiles.
 inline int64_t tile_scan_ints(int64_t T) { return 3 * ((T + 1023) / 1024) + 8; }
 

@@ -1,6 +1,7 @@
 // project.hip — projection + SH colour of every gaussian (one thread each),
-// fused with the depth-key output for the binning, the intersection total
-// the host reads, and the zeroing of the raster gradient accumulators.
+// fused with the depth-key output for the binning, the intersection and
+// super-tile reference totals the host reads, and the zeroing of the raster
+// gradient accumulators.
 //
 // Follows project_and_sh_forward_kernel (.metal:1695-1787) and its helpers
 // quat_to_rotmat (.metal:111-131), scale_rot_to_cov3d (.metal:175-188),
@@ -87,6 +88,7 @@ constexpr int PROJ_T = 128;   // gaussians per workgroup
 // projection that does not need its SH coefficients).
 struct Geo {
     int area;   // tiles hit; 0 when culled
+    int nref;   // super-tiles overlapped
     float px, py, ca, cb, cc, ex, ey, z;
 };
 
@@ -180,20 +182,27 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     const int area = ge.area;
     if (area > 0)
         project_col(p, g, pw, dc, ol, s_rest + (size_t)p.rest_per * threadIdx.x, ge, go, dkey);
-    // Intersection total for the host: one atomic per workgroup, on one of
-    // ISECT_SLOTS counters so that workgroups do not queue on one address.
-    int v = area;
+    // Intersection and reference totals for the host: one atomic each per
+    // workgroup, on one of ISECT_SLOTS counter pairs so that workgroups do
+    // not queue on one address.
+    int v = area, vr = ge.nref;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    __shared__ int s_tot[PROJ_T / 64];
-    if ((threadIdx.x & 63) == 0) s_tot[threadIdx.x >> 6] = v;
+    for (int off = 32; off >= 1; off >>= 1) {
+        v += __shfl_xor(v, off, 64);
+        vr += __shfl_xor(vr, off, 64);
+    }
+    __shared__ int s_tot[2][PROJ_T / 64];
+    if ((threadIdx.x & 63) == 0) {
+        s_tot[0][threadIdx.x >> 6] = v;
+        s_tot[1][threadIdx.x >> 6] = vr;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 2) {
         long long t = 0;
 #pragma unroll
-        for (int k = 0; k < PROJ_T / 64; ++k) t += s_tot[k];
+        for (int k = 0; k < PROJ_T / 64; ++k) t += s_tot[threadIdx.x][k];
         if (t)
-            atomicAdd(total_isect + (size_t)(blockIdx.x % ISECT_SLOTS) * ISECT_STRIDE,
+            atomicAdd(total_isect + (size_t)(blockIdx.x % ISECT_SLOTS) * ISECT_STRIDE + threadIdx.x,
                       (unsigned long long)t);
     }
 }
@@ -206,6 +215,7 @@ __device__ __forceinline__ Geo project_geo(const CamParams& p, int g, V3 pw, con
     Geo r{};
     go.radii[g] = 0;
     go.tiles_hit[g] = 0;
+    go.rect[g] = make_uint2(0u, 0u);
     dkey[g] = 0xFFFFFFFFu;
     dval[g] = (uint32_t)g;
 
@@ -263,8 +273,10 @@ __device__ __forceinline__ Geo project_geo(const CamParams& p, int g, V3 pw, con
     if (area <= 0) return r;
 
     go.tiles_hit[g] = area;
+    go.rect[g] = make_uint2((uint32_t)x0 | (uint32_t)y0 << 16, (uint32_t)x1 | (uint32_t)y1 << 16);
     go.radii[g] = f2i(radius);
     r.area = area;
+    r.nref = super_span(x0, y0, x1, y1);   // one binning reference per super-tile
     r.px = px; r.py = py; r.ca = ca; r.cb = cb; r.cc = cc; r.ex = ex; r.ey = ey; r.z = pv.z;
     return r;
 }
