@@ -14,19 +14,19 @@
 //   4. one reference (super-tile, rectangle part, gaussian id) per
 //      overlapped super-tile, in depth order
 //   5. stable radix sort of the references by super-tile
-//   6. each super-tile's (tile, gaussian) pairs, enumerated reference by
-//      reference in blocks of PAIR_BLOCK: per-block pair counts of its 256
-//      tiles, their scan over the super-tile's blocks and the tile scan ->
-//      tile_bins and chunk work items; then each block ranks its pairs by
-//      tile (stable), reorders them in LDS and writes the gaussian ids
-//      straight to their tile ranges.
-// Only the references (about one per visible gaussian) go through the
-// radix sort and memory; the pairs exist in LDS only, and the one write of
-// each pair is its final one.
+//   6. each super-tile's references cut into segments of SEG_REFS: the
+//      segment's pair count of each of the super-tile's 256 tiles (2-D
+//      difference array of the rectangles), their scan over the super-tile's
+//      segments and the tile scan -> tile_bins and chunk work items; then
+//      one wave per tile row of the segment's super-tile writes the gaussian
+//      ids of the references covering the row straight to their tiles'
+//      ranges, ranked per tile by ballots.
+// Only the references (about one per visible gaussian) go through the radix
+// sort and memory; each (tile, gaussian) entry is written once, in place.
 // The rasteriser gathers each entry's projection record by id, in place of
 // the reference's packed per-entry copies (.metal:2128-2137).
-// Equal depths keep ascending id order because both sorts and the block
-// ranking are stable and the first sort starts from id order.  Tiles have no
+// Equal depths keep ascending id order because both sorts and the per-tile
+// ranking keep their input order and the first sort starts from id order.  Tiles have no
 // size limit (the reference drops entries beyond 2048 per tile).
 #include "common.hpp"
 #include "kernels.hpp"
@@ -42,10 +42,6 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 // inside it, 24-27 / 28-31 the part's width / height minus one.  The radix
 // sort orders by the super-tile bits and carries the rest.
 constexpr uint32_t ST_MASK = 0xFFFFu;
-
-__device__ __forceinline__ int ref_pairs(uint32_t k) {
-    return (int)(((k >> 24) & 15u) + 1u) * (int)(((k >> 28) & 15u) + 1u);
-}
 
 // Tile rectangles gathered into depth order, and each one's super-tile
 // count (0 for culled gaussians, whose rectangle is empty and whose depth
@@ -92,17 +88,13 @@ __global__ __launch_bounds__(256) void k_emit_refs(int N, int sbx, const uint32_
     }
 }
 
-// Pairs of each sorted reference, and the reference range [st_r0, st_r1)
-// of each super-tile present.
-__global__ __launch_bounds__(256) void k_ref_pairs(int R, const uint32_t* __restrict__ rkey,
-                                                   int* __restrict__ npairs,
+// Reference range [st_r0, st_r1) of each super-tile present.
+__global__ __launch_bounds__(256) void k_ref_edges(int R, const uint32_t* __restrict__ rkey,
                                                    int* __restrict__ st_r0,
                                                    int* __restrict__ st_r1) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= R) return;
-    const uint32_t k = rkey[i];
-    const uint32_t st = k & ST_MASK;
-    npairs[i] = ref_pairs(k);
+    const uint32_t st = rkey[i] & ST_MASK;
     if (i == 0 || (rkey[i - 1] & ST_MASK) != st) st_r0[st] = i;
     if (i == R - 1 || (rkey[i + 1] & ST_MASK) != st) st_r1[st] = i + 1;
 }
@@ -130,217 +122,119 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* sh, int& total) 
     return wofs + x - v;
 }
 
-// Pair blocks of the super-tiles (one workgroup): super-tile s holds the
-// pairs [st_p0, st_p1) of the global reference-order enumeration and
-// ceil((st_p1 - st_p0) / PAIR_BLOCK) blocks from bstart[s] on; bstart[S] is
-// the block count.  The reference ranges are moved to st_re and cleared for
-// the next call (k_ref_pairs writes those of present super-tiles only).
-__global__ __launch_bounds__(1024) void k_block_table(int S, int* __restrict__ st_r0,
-                                                      int* __restrict__ st_r1,
-                                                      const int* __restrict__ poff,
-                                                      const int* __restrict__ npairs,
-                                                      int* __restrict__ st_p0,
-                                                      int* __restrict__ st_p1,
-                                                      int* __restrict__ st_re,
-                                                      int* __restrict__ bstart) {
+// Segments of the super-tiles (one workgroup): super-tile s's references
+// are cut into ceil(n / SEG_REFS) segments of SEG_REFS consecutive ones,
+// numbered from sstart[s] on (sstart[S] = the segment count).  The
+// reference ranges move to st_rs / st_re and are cleared for the next call
+// (k_ref_edges writes those of present super-tiles only).
+__global__ __launch_bounds__(1024) void k_seg_table(int S, int* __restrict__ st_r0,
+                                                    int* __restrict__ st_r1,
+                                                    int* __restrict__ st_rs,
+                                                    int* __restrict__ st_re,
+                                                    int* __restrict__ sstart) {
     __shared__ int sh[16];
     const int per = (S + 1023) / 1024;
     const int b = min((int)threadIdx.x * per, S), e = min(b + per, S);
     int sum = 0;
-    for (int s = b; s < e; ++s) {
-        const int r0 = st_r0[s], r1 = st_r1[s];
-        int p0 = 0, p1 = 0;
-        if (r1 > r0) {
-            p0 = poff[r0];
-            p1 = poff[r1 - 1] + npairs[r1 - 1];
-        }
-        st_p0[s] = p0;
-        st_p1[s] = p1;
-        st_re[s] = r1;
-        st_r0[s] = 0;
-        st_r1[s] = 0;
-        sum += (p1 - p0 + PAIR_BLOCK - 1) / PAIR_BLOCK;
-    }
+    for (int s = b; s < e; ++s) sum += (st_r1[s] - st_r0[s] + SEG_REFS - 1) / SEG_REFS;
     int total;
     int run = block_exclusive_scan<1024>(sum, sh, total);
     for (int s = b; s < e; ++s) {
-        bstart[s] = run;
-        run += (st_p1[s] - st_p0[s] + PAIR_BLOCK - 1) / PAIR_BLOCK;
+        const int r0 = st_r0[s], r1 = st_r1[s];
+        sstart[s] = run;
+        run += (r1 - r0 + SEG_REFS - 1) / SEG_REFS;
+        st_rs[s] = r0;
+        st_re[s] = r1;
+        st_r0[s] = 0;
+        st_r1[s] = 0;
     }
-    if (threadIdx.x == 0) bstart[S] = total;
+    if (threadIdx.x == 0) sstart[S] = total;
 }
 
-// Pair block records: block bb of super-tile s starts in the reference i
-// whose pairs contain pair bb * PAIR_BLOCK of the super-tile (a reference
-// has at most 256 pairs, so at most one block starts in it); that thread
-// writes the block's (super-tile, first reference, first pair, pair count),
-// the window end of the block before it (the window runs through the
-// reference holding the next block's first pair) and, for the super-tile's
-// last block, its window end (the super-tile's last reference).
-__global__ __launch_bounds__(256) void k_block_refs(int R, const uint32_t* __restrict__ rkey,
-                                                    const int* __restrict__ poff,
-                                                    const int* __restrict__ npairs,
-                                                    const int* __restrict__ st_p0,
-                                                    const int* __restrict__ st_p1,
-                                                    const int* __restrict__ st_re,
-                                                    const int* __restrict__ bstart,
-                                                    int4* __restrict__ blk,
-                                                    int* __restrict__ blk_wend) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= R) return;
-    const int s = (int)(rkey[i] & ST_MASK);
-    const int a = poff[i] - st_p0[s];
-    const int bb = (a + PAIR_BLOCK - 1) / PAIR_BLOCK;
-    if (bb * PAIR_BLOCK < a + npairs[i]) {
-        const int j = bstart[s] + bb;
-        const int p0 = st_p0[s] + bb * PAIR_BLOCK;
-        blk[j] = make_int4(s, i, p0, min(PAIR_BLOCK, st_p1[s] - p0));
-        if (bb > 0) blk_wend[j - 1] = i + 1;
-        if (j == bstart[s + 1] - 1) blk_wend[j] = st_re[s];
+// Record of each segment (one thread each): its super-tile s (the last
+// with sstart[s] <= j, by binary search) and its reference range.
+__global__ __launch_bounds__(256) void k_seg_records(int S, int nbound,
+                                                     const int* __restrict__ sstart,
+                                                     const int* __restrict__ st_rs,
+                                                     const int* __restrict__ st_re,
+                                                     int4* __restrict__ seg) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= nbound || j >= sstart[S]) return;
+    int lo = 0, hi = S - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (sstart[mid] <= j) lo = mid; else hi = mid - 1;
     }
+    const int r0 = st_rs[lo] + (j - sstart[lo]) * SEG_REFS;
+    seg[j] = make_int4(lo, r0, min(r0 + SEG_REFS, st_re[lo]), 0);
 }
 
-// Pair block set-up shared by the count and scatter kernels.
-constexpr int PT = 1024;                  // threads per pair block
-constexpr int PW = PT / 64;               // waves
-constexpr int PK = PAIR_BLOCK / PT;       // pairs per thread
-constexpr int WP = PAIR_BLOCK / PW;       // consecutive pairs per wave
-static_assert(PK == 4, "the owner scan reads one int4 per thread");
-
-struct PairArgs {
-    int S;
-    const uint32_t* rkey;
-    const uint32_t* rval;
-    const int* poff;
-    const int* bstart;
-    const int4* blk;
-    const int* blk_wend;
-};
-
-// LDS of a pair block: the window of references whose pairs meet the block
-// (key, first pair relative to the block, gaussian id) and the owner of
-// each pair (its reference's index in the window).
-struct __align__(16) PairLds {
-    int own[PAIR_BLOCK];
-    uint32_t rk[PAIR_BLOCK];
-    int ro[PAIR_BLOCK];
-    uint32_t rv[PAIR_BLOCK];
-    int sh[PW];
-};
-
-// Loads block j's window into LDS and finds each pair's owner.  Returns the
-// block's pair count (workgroup-uniform), or -1 past the last block; s is
-// the block's super-tile.  Ends with a barrier.
-template <bool VAL>
-__device__ __forceinline__ int pair_block_load(int j, const PairArgs& a, PairLds& L, int& s) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    // one round trip for the block count and the block's record (in bounds
-    // for every block of the grid; used only below the count)
-    const int nblocks = a.bstart[a.S];
-    const int4 b = a.blk[j];
-    const int wend = a.blk_wend[j];
-    if (j >= nblocks) return -1;
-    s = b.x;
-    const int rf = b.y, p0 = b.z, n = b.w;
-    // references rf .. wend - 1 meet the block (the last one may start
-    // exactly at its end); at most PAIR_BLOCK of them start before it
-    const int nwin = min(wend - rf, PAIR_BLOCK);
-    reinterpret_cast<int4*>(L.own)[tid] = make_int4(0, 0, 0, 0);
-    int mark[PK];
-#pragma unroll
-    for (int k = 0; k < PK; ++k) {
-        const int i = tid + k * PT;
-        mark[k] = -1;
-        if (i < nwin) {
-            const int r = rf + i;
-            const int o = a.poff[r] - p0;
-            if (o < n) {
-                L.rk[i] = a.rkey[r];
-                L.ro[i] = o;
-                if (VAL) L.rv[i] = a.rval[r];
-                if (i > 0) mark[k] = o;   // reference rf owns pair 0 (the clear value)
-            }
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < PK; ++k)
-        if (mark[k] >= 0) L.own[mark[k]] = tid + k * PT;
-    __syncthreads();
-    // owner of pair q = the last reference starting at or before q: an
-    // inclusive max scan (marks ascend with q), four pairs per thread
-    int4 o4 = reinterpret_cast<int4*>(L.own)[tid];
-    o4.y = max(o4.y, o4.x);
-    o4.z = max(o4.z, o4.y);
-    o4.w = max(o4.w, o4.z);
-    int x = o4.w;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(x, off, 64);
-        if (lane >= off) x = max(x, y);
-    }
-    if (lane == 63) L.sh[w] = x;
-    int pre = __shfl_up(x, 1, 64);
-    if (lane == 0) pre = 0;
-    __syncthreads();
-    for (int k = 0; k < w; ++k) pre = max(pre, L.sh[k]);
-    o4.x = max(o4.x, pre);
-    o4.y = max(o4.y, pre);
-    o4.z = max(o4.z, pre);
-    o4.w = max(o4.w, pre);
-    reinterpret_cast<int4*>(L.own)[tid] = o4;
-    __syncthreads();
-    return n;
+// Rectangle part of a reference key in local tile coordinates [x0, x1) x [y0, y1).
+__device__ __forceinline__ void ref_rect(uint32_t k, int& x0, int& y0, int& x1, int& y1) {
+    x0 = (int)((k >> 16) & 15u);
+    y0 = (int)((k >> 20) & 15u);
+    x1 = x0 + (int)((k >> 24) & 15u) + 1;
+    y1 = y0 + (int)((k >> 28) & 15u) + 1;
 }
 
-// Local tile (ly * SUPER + lx) of pair q of the block and its window index.
-__device__ __forceinline__ int pair_tile(const PairLds& L, int q, int& i) {
-    i = L.own[q];
-    const uint32_t k = L.rk[i];
-    const int loc = q - L.ro[i];   // pair index within the reference, row-major
-    const int w = (int)((k >> 24) & 15u) + 1;
-    // loc / w for loc < 256, w <= 16: (loc + 0.5) / w stays >= 1/32 away
-    // from an integer, far beyond the rounding of the float product
-    const int row = (int)(((float)loc + 0.5f) * (1.f / (float)w));
-    const int col = loc - row * w;
-    return ((int)((k >> 20) & 15u) + row) * SUPER + (int)((k >> 16) & 15u) + col;
-}
-
-// Pairs per local tile of each block -> hist[j * 256 + local tile].
-__global__ __launch_bounds__(PT) void k_pair_hist(PairArgs a, int* __restrict__ hist) {
-    __shared__ PairLds L;
-    __shared__ int s_h[SUPER * SUPER];
+// Pairs per local tile of each segment -> hist[j * 256 + ly * 16 + lx]:
+// the references' rectangles are added to a 17 x 17 difference array (four
+// LDS atomics each) whose 2-D prefix sums are the counts.
+constexpr int DW = SUPER + 1;
+__global__ __launch_bounds__(256) void k_seg_count(int S, const int* __restrict__ sstart,
+                                                   const int4* __restrict__ seg,
+                                                   const uint32_t* __restrict__ rkey,
+                                                   int* __restrict__ hist) {
+    __shared__ int diff[DW * DW];
     const int j = blockIdx.x, tid = threadIdx.x;
-    if (tid < SUPER * SUPER) s_h[tid] = 0;
-    int s;
-    const int n = pair_block_load<false>(j, a, L, s);
-    if (n < 0) return;
-#pragma unroll
-    for (int k = 0; k < PK; ++k) {
-        const int q = tid + k * PT;
-        if (q < n) {
-            int i;
-            atomicAdd(&s_h[pair_tile(L, q, i)], 1);
+    // in bounds for every workgroup of the grid; used only below the count
+    const int nseg = sstart[S];
+    const int4 sg = seg[j];
+    if (j >= nseg) return;
+    for (int i = tid; i < DW * DW; i += 256) diff[i] = 0;
+    __syncthreads();
+    for (int r = sg.y + tid; r < sg.z; r += 256) {
+        int x0, y0, x1, y1;
+        ref_rect(rkey[r], x0, y0, x1, y1);
+        atomicAdd(&diff[y0 * DW + x0], 1);
+        atomicAdd(&diff[y0 * DW + x1], -1);
+        atomicAdd(&diff[y1 * DW + x0], -1);
+        atomicAdd(&diff[y1 * DW + x1], 1);
+    }
+    __syncthreads();
+    if (tid < SUPER) {   // prefix along x of row tid
+        int run = 0;
+        for (int x = 0; x < SUPER; ++x) {
+            run += diff[tid * DW + x];
+            diff[tid * DW + x] = run;
         }
     }
     __syncthreads();
-    if (tid < SUPER * SUPER) hist[(size_t)j * (SUPER * SUPER) + tid] = s_h[tid];
+    if (tid < SUPER) {   // prefix along y of column tid
+        int run = 0;
+        for (int y = 0; y < SUPER; ++y) {
+            run += diff[y * DW + tid];
+            diff[y * DW + tid] = run;
+        }
+    }
+    __syncthreads();
+    hist[(size_t)j * (SUPER * SUPER) + tid] = diff[(tid / SUPER) * DW + tid % SUPER];
 }
 
 // Per super-tile (one workgroup; thread d + 256 g handles local tile d in
-// the g-th quarter of the super-tile's blocks): each block's count of a tile
-// becomes the tile's pairs in the super-tile's earlier blocks, and the tile's
-// total goes to tcount (every tile of the grid lies in exactly one
-// super-tile, so tcount is rewritten whole).  Two passes over the counts:
-// quarter totals, then offsets.
-constexpr int PO_T = 4 * SUPER * SUPER;
-__global__ __launch_bounds__(PO_T) void k_pair_offsets(int tbx, int tby, int sbx,
-                                                       const int* __restrict__ bstart,
-                                                       int* __restrict__ hist,
-                                                       int* __restrict__ tcount) {
+// the g-th quarter of the super-tile's segments): each segment's count of a
+// tile becomes the tile's pairs in the super-tile's earlier segments, and
+// the tile's total goes to tcount (every tile of the grid lies in exactly
+// one super-tile, so tcount is rewritten whole).  Two passes over the
+// counts: quarter totals, then offsets.
+constexpr int SO_T = 4 * SUPER * SUPER;
+__global__ __launch_bounds__(SO_T) void k_seg_offsets(int tbx, int tby, int sbx,
+                                                      const int* __restrict__ sstart,
+                                                      int* __restrict__ hist,
+                                                      int* __restrict__ tcount) {
     __shared__ int part[4][SUPER * SUPER];
     const int s = blockIdx.x, d = threadIdx.x % (SUPER * SUPER), g = threadIdx.x / (SUPER * SUPER);
-    const int b0 = bstart[s], b1 = bstart[s + 1];
+    const int b0 = sstart[s], b1 = sstart[s + 1];
     const int per = (b1 - b0 + 3) / 4;
     const int q0 = min(b0 + g * per, b1), q1 = min(q0 + per, b1);
     int sum = 0;
@@ -366,100 +260,95 @@ __global__ __launch_bounds__(PO_T) void k_pair_offsets(int tbx, int tby, int sbx
     }
     if (g == 0) {
         const int tx = (s % sbx) * SUPER + (d % SUPER), ty = (s / sbx) * SUPER + d / SUPER;
-        if (tx < tbx && ty < tby) tcount[ty * tbx + tx] = part[0][d] + part[1][d] + part[2][d] + part[3][d];
+        if (tx < tbx && ty < tby)
+            tcount[ty * tbx + tx] = part[0][d] + part[1][d] + part[2][d] + part[3][d];
     }
 }
 
-// Pairs of each block ranked stably by local tile (each wave ranks its WP
-// consecutive pairs in 64-pair rounds by ballot-matching the tile bits,
-// keeping per-tile running counts; wave counts combine in wave order),
-// reordered by tile in LDS and written to their tiles' ranges: tile start
-// (tile_bins) + the tile's pairs in earlier blocks (hist) + rank.
-// Consecutive blocks fill neighbouring parts of the same tiles' ranges: the
-// grid is a multiple of 8 and workgroup b takes block (b % 8) * (grid / 8)
-// + b / 8, so that the hardware's round-robin of workgroups over the 8 XCDs
-// hands each XCD a contiguous run of blocks and their partial lines meet in
-// one L2.  Blocks at or past nbound do not exist.
-__global__ __launch_bounds__(PT) void k_pair_scatter(PairArgs a, int nbound, int tbx, int tby,
-                                                     int sbx, const int* __restrict__ hist,
-                                                     const int* __restrict__ tile_bins,
-                                                     uint32_t* __restrict__ ids) {
-    __shared__ PairLds L;
-    __shared__ uint16_t wcnt[PW][SUPER * SUPER];
-    __shared__ int dstart[SUPER * SUPER];
-    __shared__ int gofs[SUPER * SUPER];
-    __shared__ int scan_sh[PW];
-    const int j = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
-    if (j >= nbound) return;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    for (int i = tid; i < PW * SUPER * SUPER; i += PT) (&wcnt[0][0])[i] = 0;
-    int s;
-    const int n = pair_block_load<true>(j, a, L, s);
-    if (n < 0) return;
-    // start of each local tile's range for this block, loaded now so that
-    // the loads overlap the ranking
-    int my_gofs = 0;
-    if (tid < SUPER * SUPER) {
-        const int tx = (s % sbx) * SUPER + (tid % SUPER), ty = (s / sbx) * SUPER + tid / SUPER;
+// Ids of up to 64 references of one tile row (lane < cnt holds reference
+// k / gaussian g), written to their tiles: for each column x of the row, the
+// lanes covering tile x write to its next free slots base[x].. in lane
+// order, so each store instruction writes consecutive slots of one tile.
+__device__ __forceinline__ void write_row_refs(bool ok, uint32_t k, uint32_t g, int* base,
+                                               uint32_t* __restrict__ ids) {
+    int x0, y0, x1, y1;
+    ref_rect(k, x0, y0, x1, y1);
+    const uint32_t cols = ok ? ((1u << x1) - 1u) & ~((1u << x0) - 1u) : 0u;
+#pragma unroll
+    for (int x = 0; x < SUPER; ++x) {
+        const bool on = (cols >> x) & 1u;
+        const uint64_t b = wave_ballot(on);
+        if (b == 0) continue;
+        // covering lanes below this one
+        const int below = (int)__builtin_amdgcn_mbcnt_hi(
+            (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        if (on) ids[base[x] + below] = g;
+        base[x] += __popcll(b);
+    }
+}
+
+// Gaussian ids of each segment written to their tiles' ranges.  The
+// segment's references are staged in LDS; wave ly of the workgroup owns
+// local tile row ly: it walks them in order, 64 per round, appends the ones
+// whose rectangle covers its row to a ring of reference indices, and writes
+// each full group of 64 (and the rest at the end) with write_row_refs.  A
+// tile's next free slot starts at the tile's start + its pairs in earlier
+// segments; the 16 of the row are wave-uniform (scalar registers).  Entries
+// keep reference (depth) order per tile.
+__global__ __launch_bounds__(1024) void k_seg_write(int S, const int* __restrict__ sstart,
+                                                    const int4* __restrict__ seg,
+                                                    const uint32_t* __restrict__ rkey,
+                                                    const uint32_t* __restrict__ rval,
+                                                    const int* __restrict__ hist,
+                                                    const int* __restrict__ tile_bins, int tbx,
+                                                    int tby, int sbx, uint32_t* __restrict__ ids) {
+    __shared__ uint32_t s_k[SEG_REFS], s_g[SEG_REFS];
+    __shared__ uint16_t s_q[SUPER][128];   // per row: ring of covering reference indices
+    const int j = blockIdx.x, lane = threadIdx.x & 63, ly = threadIdx.x >> 6;
+    const int nseg = sstart[S];
+    const int4 sg = seg[j];
+    if (j >= nseg) return;
+    const int s = sg.x;
+    const int n = sg.z - sg.y;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        s_k[i] = rkey[sg.y + i];
+        s_g[i] = rval[sg.y + i];
+    }
+    const int ty = (s / sbx) * SUPER + ly;
+    int myb = 0;
+    if (lane < SUPER) {
+        const int tx = (s % sbx) * SUPER + lane;
         if (tx < tbx && ty < tby)
-            my_gofs = tile_bins[2 * (ty * tbx + tx)] + hist[(size_t)j * (SUPER * SUPER) + tid];
+            myb = tile_bins[2 * (ty * tbx + tx)] + hist[(size_t)j * (SUPER * SUPER) + ly * SUPER + lane];
     }
-    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int dig[PK], rank[PK];
-    uint32_t val[PK];
+    int base[SUPER];
 #pragma unroll
-    for (int k = 0; k < PK; ++k) {
-        const int q = w * WP + k * 64 + lane;
-        const bool ok = q < n;
-        int d = SUPER * SUPER, i = 0;
-        if (ok) d = pair_tile(L, q, i);
-        val[k] = ok ? L.rv[i] : 0u;
-        dig[k] = d;
-        uint64_t peers = wave_ballot(ok);
-        if (!ok) peers = ~peers;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const uint64_t bb = wave_ballot((d >> b) & 1);
-            peers &= ((d >> b) & 1) ? bb : ~bb;
+    for (int x = 0; x < SUPER; ++x) base[x] = __builtin_amdgcn_readlane(myb, x);
+    __syncthreads();
+    int head = 0, tail = 0;   // wave-uniform ring positions (tail - head <= 127)
+    for (int r0 = 0; r0 < n; r0 += 64) {
+        const int r = r0 + lane;
+        const uint32_t k = r < n ? s_k[r] : 0u;
+        const int y0 = (int)((k >> 20) & 15u), y1 = y0 + (int)((k >> 28) & 15u) + 1;
+        const bool cov = r < n && y0 <= ly && ly < y1;
+        const uint64_t b = wave_ballot(cov);
+        const int below = (int)__builtin_amdgcn_mbcnt_hi(
+            (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        if (cov) s_q[ly][(tail + below) & 127] = (uint16_t)r;
+        tail += __popcll(b);
+        if (tail - head >= 64) {
+            __builtin_amdgcn_wave_barrier();
+            const int i = s_q[ly][(head + lane) & 127];
+            write_row_refs(true, s_k[i], s_g[i], base, ids);
+            head += 64;
+            __builtin_amdgcn_wave_barrier();
         }
-        const int before = __popcll(peers & lt);
-        const int dd = ok ? d : 0;
-        const int base_cnt = ok ? (int)wcnt[w][dd] : 0;
-        rank[k] = base_cnt + before;
-        // the lowest lane of each tile group advances that tile's count
-        if (ok && before == 0) wcnt[w][dd] = (uint16_t)(base_cnt + __popcll(peers));
     }
-    __syncthreads();
-    // per local tile (threads 0..255): wave offsets in wave order, the
-    // block's count and its start in the reordered block
-    int cnt = 0;
-    if (tid < SUPER * SUPER) {
-#pragma unroll
-        for (int ww = 0; ww < PW; ++ww) {
-            const int c = wcnt[ww][tid];
-            wcnt[ww][tid] = (uint16_t)cnt;
-            cnt += c;
-        }
-        gofs[tid] = my_gofs;
-    }
-    int total;
-    const int start = block_exclusive_scan<PT>(cnt, scan_sh, total);
-    if (tid < SUPER * SUPER) dstart[tid] = start;
-    __syncthreads();
-    // reorder by tile: ids into L.own, tiles into L.ro (the window is no
-    // longer read)
-#pragma unroll
-    for (int k = 0; k < PK; ++k) {
-        const int d = dig[k];
-        if (d >= SUPER * SUPER) continue;
-        const int p = dstart[d] + (int)wcnt[w][d] + rank[k];
-        L.own[p] = (int)val[k];
-        L.ro[p] = d;
-    }
-    __syncthreads();
-    for (int p = tid; p < n; p += PT) {
-        const int d = L.ro[p];
-        ids[gofs[d] + (p - dstart[d])] = (uint32_t)L.own[p];
+    if (tail > head) {
+        __builtin_amdgcn_wave_barrier();
+        const bool ok = head + lane < tail;
+        const int i = ok ? s_q[ly][(head + lane) & 127] : 0;
+        write_row_refs(ok, s_k[i], s_g[i], base, ids);
     }
 }
 
@@ -662,25 +551,22 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
             rk = rb.key2;
             rv = rb.val2;
         }
-        hipLaunchKernelGGL(k_ref_pairs, dim3(blocks_for(R)), dim3(256), 0, s, (int)R, rk,
-                           rb.npairs, rb.st_r0, rb.st_r1);
-        launch_exclusive_scan_i32(s, rb.npairs, rb.poff, R, rb.scan_temp);
+        hipLaunchKernelGGL(k_ref_edges, dim3(blocks_for(R)), dim3(256), 0, s, (int)R, rk,
+                           rb.st_r0, rb.st_r1);
     }
-    // with no references every super-tile is empty: zero blocks, zero counts
-    hipLaunchKernelGGL(k_block_table, dim3(1), dim3(1024), 0, s, S, rb.st_r0, rb.st_r1,
-                       (const int*)rb.poff, (const int*)rb.npairs, rb.st_p0, rb.st_p1, rb.st_re,
-                       rb.bstart);
-    const int64_t NB = pair_blocks_bound(I, S);
-    PairArgs pa{S, rk, rv, rb.poff, rb.bstart, rb.blk, rb.blk_wend};
+    // with no references every super-tile is empty: no segments, zero counts
+    hipLaunchKernelGGL(k_seg_table, dim3(1), dim3(1024), 0, s, S, rb.st_r0, rb.st_r1, rb.st_rs,
+                       rb.st_re, rb.sstart);
+    const int64_t NS = segments_bound(R, S);
     if (R > 0) {
-        hipLaunchKernelGGL(k_block_refs, dim3(blocks_for(R)), dim3(256), 0, s, (int)R, rk,
-                           (const int*)rb.poff, (const int*)rb.npairs, (const int*)rb.st_p0,
-                           (const int*)rb.st_p1, (const int*)rb.st_re, (const int*)rb.bstart,
-                           rb.blk, rb.blk_wend);
-        hipLaunchKernelGGL(k_pair_hist, dim3((unsigned)NB), dim3(PT), 0, s, pa, rb.hist);
+        hipLaunchKernelGGL(k_seg_records, dim3(blocks_for(NS)), dim3(256), 0, s, S, (int)NS,
+                           (const int*)rb.sstart, (const int*)rb.st_rs, (const int*)rb.st_re,
+                           rb.seg);
+        hipLaunchKernelGGL(k_seg_count, dim3((unsigned)NS), dim3(256), 0, s, S,
+                           (const int*)rb.sstart, (const int4*)rb.seg, rk, rb.hist);
     }
-    hipLaunchKernelGGL(k_pair_offsets, dim3(S), dim3(PO_T), 0, s, p.tbx, p.tby, sbx,
-                       (const int*)rb.bstart, rb.hist, rb.tcount);
+    hipLaunchKernelGGL(k_seg_offsets, dim3(S), dim3(SO_T), 0, s, p.tbx, p.tby, sbx,
+                       (const int*)rb.sstart, rb.hist, rb.tcount);
     const int nb = (T + TS_BLOCK - 1) / TS_BLOCK;
     hipLaunchKernelGGL(k_tile_counts, dim3(nb), dim3(TS_T), 0, s, T, (const int*)rb.tcount, tscan,
                        meta);
@@ -689,9 +575,9 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
     hipLaunchKernelGGL(k_build_items, dim3(blocks_for(items_bound(T, I))), dim3(256), 0, s, T,
                        (const Meta*)meta, it);
     if (R > 0)
-        hipLaunchKernelGGL(k_pair_scatter, dim3((unsigned)((NB + 7) / 8 * 8)), dim3(PT), 0, s, pa,
-                           (int)NB, p.tbx, p.tby, sbx, (const int*)rb.hist,
-                           (const int*)tile_bins, ids);
+        hipLaunchKernelGGL(k_seg_write, dim3((unsigned)NS), dim3(1024), 0, s, S,
+                           (const int*)rb.sstart, (const int4*)rb.seg, rk, rv,
+                           (const int*)rb.hist, (const int*)tile_bins, p.tbx, p.tby, sbx, ids);
 }
 
 }  // namespace msp

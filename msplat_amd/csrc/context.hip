@@ -94,9 +94,9 @@ struct Ctx {
     // per tile
     Buf tcount, tscan, tile_bins, tile_K, tile_item0, l_chunked, tile_done;
     // per super-tile, per super-tile reference, per pair block
-    Buf st_r0, st_r1, st_p0, st_p1, st_re, bstart;
-    Buf rkey, rval, rkey2, rval2, rtemp, npairs, poff, pscan;
-    Buf blk, blk_wend, phist;
+    Buf st_r0, st_r1, st_rs, st_re, sstart;
+    Buf rkey, rval, rkey2, rval2, rtemp;
+    Buf seg, phist;
     // per intersection: the tile-sorted gaussian ids
     Buf tval;
     // per item
@@ -189,9 +189,9 @@ void free_all(Ctx* c) {
     Buf* bufs[] = {&c->rec, &c->radii, &c->tiles_hit, &c->rect, &c->rect_sorted,
                    &c->gacc, &c->dkey, &c->dval, &c->dkey2, &c->dval2, &c->hits, &c->eoff,
                    &c->dtemp, &c->stemp, &c->tcount, &c->tscan, &c->tile_done, &c->tile_bins, &c->tile_K,
-                   &c->tile_item0, &c->l_chunked, &c->st_r0, &c->st_r1, &c->st_p0, &c->st_p1,
-                   &c->st_re, &c->bstart, &c->rkey, &c->rval, &c->rkey2, &c->rval2, &c->rtemp,
-                   &c->npairs, &c->poff, &c->pscan, &c->blk, &c->blk_wend, &c->phist, &c->tval,
+                   &c->tile_item0, &c->l_chunked, &c->st_r0, &c->st_r1, &c->st_rs, &c->st_re, &c->sstart,
+                   &c->rkey, &c->rval, &c->rkey2, &c->rval2, &c->rtemp, &c->seg, &c->phist,
+                   &c->tval,
                    &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
                    &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
@@ -373,10 +373,9 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
                     "65536 super-tiles of %dx%d)", p.tbx, p.tby, SUPER, SUPER);
     ENSURE(c->st_r0, (size_t)nst * 4);
     ENSURE(c->st_r1, (size_t)nst * 4);
-    ENSURE(c->st_p0, (size_t)nst * 4);
-    ENSURE(c->st_p1, (size_t)nst * 4);
+    ENSURE(c->st_rs, (size_t)nst * 4);
     ENSURE(c->st_re, (size_t)nst * 4);
-    ENSURE(c->bstart, ((size_t)nst + 1) * 4);
+    ENSURE(c->sstart, ((size_t)nst + 1) * 4);
     ENSURE(c->tile_bins, (size_t)T * 8);
     ENSURE(c->tile_K, (size_t)T * 4);
     ENSURE(c->tile_item0, (size_t)T * 4);
@@ -428,19 +427,15 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
                     (long long)I64);
     const size_t I = (size_t)std::max<int64_t>(I64, 1);
     const size_t R = (size_t)std::max<int64_t>(R64, 1);
-    const size_t NB = (size_t)pair_blocks_bound(I64, nst);
+    const size_t NS = (size_t)segments_bound(R64, nst);
     ENSURE(c->tval, I * 4);
     ENSURE(c->rkey, R * 4);
     ENSURE(c->rval, R * 4);
     ENSURE(c->rkey2, R * 4);
     ENSURE(c->rval2, R * 4);
     ENSURE(c->rtemp, (size_t)radix_temp_ints((int64_t)R) * 4);
-    ENSURE(c->npairs, R * 4);
-    ENSURE(c->poff, R * 4);
-    ENSURE(c->pscan, ((size_t)scan_block_count((int64_t)R) + 8) * 4);
-    ENSURE(c->blk, NB * 16);
-    ENSURE(c->blk_wend, NB * 4);
-    ENSURE(c->phist, NB * SUPER * SUPER * 4);
+    ENSURE(c->seg, NS * 16);
+    ENSURE(c->phist, NS * SUPER * SUPER * 4);
     const int64_t max_items = items_bound(T, I64);
     ENSURE(c->it_tile, (size_t)max_items * 4);
     ENSURE(c->it_k, (size_t)max_items * 4);
@@ -462,17 +457,12 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     rb.key2 = P<uint32_t>(c->rkey2);
     rb.val2 = P<uint32_t>(c->rval2);
     rb.radix_temp = P<int>(c->rtemp);
-    rb.npairs = P<int>(c->npairs);
-    rb.poff = P<int>(c->poff);
-    rb.scan_temp = P<int>(c->pscan);
     rb.st_r0 = P<int>(c->st_r0);
     rb.st_r1 = P<int>(c->st_r1);
-    rb.st_p0 = P<int>(c->st_p0);
-    rb.st_p1 = P<int>(c->st_p1);
+    rb.st_rs = P<int>(c->st_rs);
     rb.st_re = P<int>(c->st_re);
-    rb.bstart = P<int>(c->bstart);
-    rb.blk = P<int4>(c->blk);
-    rb.blk_wend = P<int>(c->blk_wend);
+    rb.sstart = P<int>(c->sstart);
+    rb.seg = P<int4>(c->seg);
     rb.hist = P<int>(c->phist);
     rb.tcount = P<int>(c->tcount);
     launch_tile_lists(c->stream, p, I64, R64, order, P<int>(c->eoff), P<uint2>(c->rect_sorted), rb,

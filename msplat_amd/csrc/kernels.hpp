@@ -104,13 +104,15 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
 
 // Super-tiles: SUPER x SUPER tiles of the tile grid.  A gaussian's tile
 // rectangle is cut into one reference per super-tile it overlaps; the
-// references are sorted by super-tile and each super-tile's (tile, gaussian)
-// pairs are enumerated from them in blocks of PAIR_BLOCK pairs.
+// references are sorted by super-tile and each super-tile's references are
+// processed in segments of SEG_REFS.
 constexpr int SUPER = 16;
-constexpr int PAIR_BLOCK = 4096;
+constexpr int SEG_REFS = 2048;
 inline int super_tiles(int tbx, int tby) {
     return ((tbx + SUPER - 1) / SUPER) * ((tby + SUPER - 1) / SUPER);
 }
+// Upper bound of the segments of R references over S super-tiles.
+inline int64_t segments_bound(int64_t R, int64_t S) { return R / SEG_REFS + S + 1; }
 // Super-tiles overlapped by the non-empty tile rectangle [x0, x1) x [y0, y1).
 __host__ __device__ inline int super_span(int x0, int y0, int x1, int y1) {
     return ((x1 - 1) / SUPER - x0 / SUPER + 1) * ((y1 - 1) / SUPER - y0 / SUPER + 1);
@@ -124,27 +126,19 @@ __host__ __device__ inline int super_span(int x0, int y0, int x1, int y1) {
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
                         uint32_t* dval2, int* radix_temp, const uint2* rect, uint2* rect_sorted,
                         int* rcount, int* roff, int* scan_temp, uint32_t** order_out);
-// Upper bound of the pair blocks for I pairs over S super-tiles.
-inline int64_t pair_blocks_bound(int64_t I, int64_t S) { return I / PAIR_BLOCK + S + 1; }
 
-// Scratch of launch_tile_lists for R references, S super-tiles, NB =
-// pair_blocks_bound(I, S) pair blocks and T tiles.
+// Scratch of launch_tile_lists for R references, S super-tiles, NS =
+// segments_bound(R, S) segments and T tiles.
 struct RefBufs {
     uint32_t *key, *val, *key2, *val2;   // R each: references, ping-pong
     int* radix_temp;                     // radix_temp_ints(R)
-    int* npairs;                         // R
-    int* poff;                           // R: first pair of each reference
-    int* scan_temp;                      // scan_block_count(R) + 8
     int* st_r0;                          // S: reference range of each super-tile;
     int* st_r1;                          //    S; both zero between calls
-    int* st_p0;                          // S: pair range of each super-tile
-    int* st_p1;                          // S
-    int* st_re;                          // S: end of its reference range
-    int* bstart;                         // S + 1: first pair block of each super-tile
-    int4* blk;                           // NB: (super-tile, reference holding the first
-                                         //     pair, first pair, pairs) of each pair block
-    int* blk_wend;                       // NB: end of the block's reference window
-    int* hist;                           // NB * 256: pairs per local tile and block
+    int* st_rs;                          // S: copies of the reference ranges
+    int* st_re;                          // S
+    int* sstart;                         // S + 1: first segment of each super-tile
+    int4* seg;                           // NS: (super-tile, first reference, end reference)
+    int* hist;                           // NS * 256: pairs per local tile and segment
     int* tcount;                         // T: pairs per tile
 };
 // Writes the tile-sorted gaussian ids (I of them) to ids, tile_bins, the
