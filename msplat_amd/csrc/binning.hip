@@ -221,47 +221,52 @@ __global__ __launch_bounds__(256) void k_seg_count(int S, const int* __restrict_
     hist[(size_t)j * (SUPER * SUPER) + tid] = diff[(tid / SUPER) * DW + tid % SUPER];
 }
 
-// Per super-tile (one workgroup; thread d + 256 g handles local tile d in
-// the g-th quarter of the super-tile's segments): each segment's count of a
-// tile becomes the tile's pairs in the super-tile's earlier segments, and
-// the tile's total goes to tcount (every tile of the grid lies in exactly
-// one super-tile, so tcount is rewritten whole).  Two passes over the
-// counts: quarter totals, then offsets.
-constexpr int SO_T = 4 * SUPER * SUPER;
+// Per super-tile s and quarter q of its 256 tiles (workgroup (s, q); thread
+// d + 64 g handles local tile 64 q + d in the g-th of 16 groups of the
+// super-tile's segments): each segment's count of a tile becomes the tile's
+// pairs in the super-tile's earlier segments, and the tile's total goes to
+// tcount (every tile of the grid lies in exactly one super-tile, so tcount
+// is rewritten whole).  Two passes over the counts: group totals, then
+// offsets.
+constexpr int SO_G = 16, SO_D = 64, SO_T = SO_G * SO_D;
 __global__ __launch_bounds__(SO_T) void k_seg_offsets(int tbx, int tby, int sbx,
                                                       const int* __restrict__ sstart,
                                                       int* __restrict__ hist,
                                                       int* __restrict__ tcount) {
-    __shared__ int part[4][SUPER * SUPER];
-    const int s = blockIdx.x, d = threadIdx.x % (SUPER * SUPER), g = threadIdx.x / (SUPER * SUPER);
+    __shared__ int part[SO_G][SO_D];
+    const int s = blockIdx.x, tile = blockIdx.y * SO_D + threadIdx.x % SO_D;
+    const int d = threadIdx.x % SO_D, g = threadIdx.x / SO_D;
     const int b0 = sstart[s], b1 = sstart[s + 1];
-    const int per = (b1 - b0 + 3) / 4;
+    const int per = (b1 - b0 + SO_G - 1) / SO_G;
     const int q0 = min(b0 + g * per, b1), q1 = min(q0 + per, b1);
     int sum = 0;
-    for (int j = q0; j < q1; j += 8) {
+    for (int j = q0; j < q1; j += 4) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            sum += j + u < q1 ? hist[(size_t)(j + u) * (SUPER * SUPER) + d] : 0;
+        for (int u = 0; u < 4; ++u)
+            sum += j + u < q1 ? hist[(size_t)(j + u) * (SUPER * SUPER) + tile] : 0;
     }
     part[g][d] = sum;
     __syncthreads();
-    int run = 0;
-    for (int k = 0; k < g; ++k) run += part[k][d];
-    for (int j = q0; j < q1; j += 8) {
-        int c[8];
+    int run = 0, total = 0;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            c[u] = j + u < q1 ? hist[(size_t)(j + u) * (SUPER * SUPER) + d] : 0;
+    for (int k = 0; k < SO_G; ++k) {
+        if (k < g) run += part[k][d];
+        total += part[k][d];
+    }
+    for (int j = q0; j < q1; j += 4) {
+        int c[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            if (j + u < q1) hist[(size_t)(j + u) * (SUPER * SUPER) + d] = run;
+        for (int u = 0; u < 4; ++u)
+            c[u] = j + u < q1 ? hist[(size_t)(j + u) * (SUPER * SUPER) + tile] : 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (j + u < q1) hist[(size_t)(j + u) * (SUPER * SUPER) + tile] = run;
             run += c[u];
         }
     }
     if (g == 0) {
-        const int tx = (s % sbx) * SUPER + (d % SUPER), ty = (s / sbx) * SUPER + d / SUPER;
-        if (tx < tbx && ty < tby)
-            tcount[ty * tbx + tx] = part[0][d] + part[1][d] + part[2][d] + part[3][d];
+        const int tx = (s % sbx) * SUPER + (tile % SUPER), ty = (s / sbx) * SUPER + tile / SUPER;
+        if (tx < tbx && ty < tby) tcount[ty * tbx + tx] = total;
     }
 }
 
@@ -565,7 +570,8 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
         hipLaunchKernelGGL(k_seg_count, dim3((unsigned)NS), dim3(256), 0, s, S,
                            (const int*)rb.sstart, (const int4*)rb.seg, rk, rb.hist);
     }
-    hipLaunchKernelGGL(k_seg_offsets, dim3(S), dim3(SO_T), 0, s, p.tbx, p.tby, sbx,
+    hipLaunchKernelGGL(k_seg_offsets, dim3(S, SUPER * SUPER / SO_D), dim3(SO_T), 0, s, p.tbx,
+                       p.tby, sbx,
                        (const int*)rb.sstart, rb.hist, rb.tcount);
     const int nb = (T + TS_BLOCK - 1) / TS_BLOCK;
     hipLaunchKernelGGL(k_tile_counts, dim3(nb), dim3(TS_T), 0, s, T, (const int*)rb.tcount, tscan,

@@ -107,7 +107,7 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
 // references are sorted by super-tile and each super-tile's references are
 // processed in segments of SEG_REFS.
 constexpr int SUPER = 16;
-constexpr int SEG_REFS = 2048;
+constexpr int SEG_REFS = 1024;
 inline int super_tiles(int tbx, int tby) {
     return ((tbx + SUPER - 1) / SUPER) * ((tby + SUPER - 1) / SUPER);
 }
