@@ -389,7 +389,8 @@ __global__ __launch_bounds__(256) void k_render_tiles(int W, int H, int tbx, flo
 __global__ __launch_bounds__(256) void k_chunk_done(int W, int H, int tbx,
                                                     const Meta* __restrict__ meta,
                                                     const int* __restrict__ chunked, Items it,
-                                                    ChunkBufs cb, int P, int* __restrict__ done) {
+                                                    ChunkBufs cb, int* __restrict__ done) {
+    constexpr int P = FWD_P;
     __shared__ int s_any;
     const int nch = meta->n_chunked_tiles;
     for (int b = blockIdx.x; b < nch; b += gridDim.x) {
@@ -405,8 +406,13 @@ __global__ __launch_bounds__(256) void k_chunk_done(int W, int H, int tbx,
         const int lp = threadIdx.x, lx = lp & 15, ly = lp >> 4;
         const int j = (t % tbx) * BLOCK + lx, i = (t / tbx) * BLOCK + ly;
         if (i < H && j < W) {
+            // all P loads in flight, then the product in chunk order
+            float c[P];
+#pragma unroll
+            for (int k = 0; k < P; ++k) c[k] = cb.cT[(size_t)(i0 + k) * TILE_PIX + lp];
             float pT = 1.f;
-            for (int k = 0; k < P; ++k) pT *= cb.cT[(size_t)(i0 + k) * TILE_PIX + lp];
+#pragma unroll
+            for (int k = 0; k < P; ++k) pT *= c[k];
             if (pT != 0.f) s_any = 1;
         }
         __syncthreads();
@@ -767,7 +773,7 @@ void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, con
                        out_img, cb, work, FWD_P);
     const int T = p.tbx * p.tby;
     hipLaunchKernelGGL(k_chunk_done, dim3((unsigned)std::min(T, 256)), dim3(256), 0, s, p.W, p.H,
-                       p.tbx, meta, chunked, it, cb, FWD_P, done);
+                       p.tbx, meta, chunked, it, cb, done);
     hipLaunchKernelGGL(k_raster_fwd_tail, dim3((unsigned)std::min<int64_t>(max_items, 1024)),
                        dim3(256), 0, s, p.W, p.H, p.tbx, meta, it, tile_bins, pk, cb, work, FWD_P,
                        (const int*)done);

@@ -221,11 +221,14 @@ __global__ __launch_bounds__(256) void k_ssim_v_bwd(int W, int H, const float* _
     }
 }
 
-__global__ __launch_bounds__(256) void k_loss_final(int nparts, const float* __restrict__ part,
-                                                    float w_ssim, float* __restrict__ out) {
-    __shared__ double s[3][256];
+// Final fold of the workgroup partials in a fixed order (float64): thread t
+// adds parts t, t + 1024, ... in order, then a tree over the 1024 threads.
+constexpr int LF_T = 1024;
+__global__ __launch_bounds__(LF_T) void k_loss_final(int nparts, const float* __restrict__ part,
+                                                     float w_ssim, float* __restrict__ out) {
+    __shared__ double s[3][LF_T];
     double a = 0.0, b = 0.0, n = 0.0;
-    for (int i = threadIdx.x; i < nparts; i += 256) {
+    for (int i = threadIdx.x; i < nparts; i += LF_T) {
         a += part[3 * i];
         b += part[3 * i + 1];
         n += part[3 * i + 2];
@@ -234,7 +237,7 @@ __global__ __launch_bounds__(256) void k_loss_final(int nparts, const float* __r
     s[1][threadIdx.x] = b;
     s[2][threadIdx.x] = n;
     __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
+    for (int off = LF_T / 2; off > 0; off >>= 1) {
         if ((int)threadIdx.x < off)
             for (int k = 0; k < 3; ++k) s[k][threadIdx.x] += s[k][threadIdx.x + off];
         __syncthreads();
@@ -254,8 +257,8 @@ void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt,
     const dim3 grid((W + VX - 1) / VX, (H + VY - 1) / VY);
     hipLaunchKernelGGL(k_ssim_v_bwd, grid, dim3(256), 0, s, W, H, img, gt, dbuf, w, inv_n,
                        v_rendered);
-    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(256), 0, s, (int)(fgrid.x * fgrid.y), loss_part,
-                       w, loss_out);
+    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(LF_T), 0, s, (int)(fgrid.x * fgrid.y),
+                       loss_part, w, loss_out);
 }
 
 }  // namespace msp
