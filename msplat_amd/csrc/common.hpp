@@ -15,7 +15,11 @@ namespace msp {
 constexpr int BLOCK = 16;              // tile edge (msplat.hpp:4-5)
 constexpr int TILE_PIX = BLOCK * BLOCK;
 constexpr int CHUNK = 512;             // depth chunk (.metal:2616)
-constexpr int MONO_MAX = 2048;         // largest tile rasterised in one piece (.metal:2021)
+// Largest tile rasterised in one piece outside chunk mode: the reference's
+// monolithic kernel keeps at most 2048 entries per tile (.metal:2021) and
+// drops the rest; tiles of up to 8192 are rasterised in one piece here,
+// uncapped, and larger ones in 512-entry chunks.
+constexpr int MONO_MAX = 8192;
 constexpr int CHUNK_MODE_TILES = 400;  // below this many tiles every tile is chunked (.mm:876)
 
 // SH constants (.metal:14-39).

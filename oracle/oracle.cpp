@@ -52,7 +52,12 @@ namespace {
 
 constexpr int BLOCK = 16;          // msplat.hpp:4-5
 constexpr int CHUNK = 512;         // .metal:2616
-constexpr int MONO_MAX = 2048;     // MAX_TILE_ELEMS, .metal:2021
+// Largest tile rasterised in one piece outside chunk mode.  The reference's
+// monolithic kernel bins at most MAX_TILE_ELEMS = 2048 entries per tile
+// (.metal:2021) and drops the rest; here tiles of up to 8192 entries are
+// rasterised in one piece, uncapped (the reference's monolithic result
+// wherever it keeps every entry), and larger ones in 512-entry chunks.
+constexpr int MONO_MAX = 8192;
 constexpr int CHUNK_MODE_TILES = 400;  // .mm:876
 
 // SH constants (.metal:14-39).

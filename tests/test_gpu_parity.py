@@ -50,9 +50,10 @@ def test_render_sh_degrees(dev):
 
 
 def test_render_monolithic_tiles(dev):
-    """>= 400 tiles: the monolithic kernel (reference selector, .mm:876)."""
+    """>= 400 tiles: the monolithic kernel (reference selector, .mm:876),
+    uncapped up to 8192 entries per tile."""
     meta, counts = _render_and_compare(dev, small_scene(n=20000, width=400, height=272, seed_off=70))
-    assert meta["n_chunked_tiles"] == int((counts > 2048).sum())
+    assert meta["n_chunked_tiles"] == int((counts > 8192).sum())
 
 
 def test_render_heavy_chunked_tiles(dev):
@@ -119,6 +120,19 @@ def test_train_step_deep_chunks_past_zero_transmittance(dev):
 
 def test_train_step_monolithic(dev):
     _train_compare(dev, small_scene(n=12000, width=336, height=208, seed_off=82))
+
+
+def test_train_step_large_tiles_monolithic_and_chunked(dev):
+    """>= 400 tiles (336x320, 420 tiles): tiles of 2049..8192 entries are
+    rasterised in one piece, uncapped (the reference's monolithic kernel
+    keeps at most 2048), and the tiles above 8192 in 512-entry chunks, in
+    one train step."""
+    _train_compare(dev, small_scene(n=80000, width=336, height=320, seed_off=91, spread=0.5))
+    tb = dev.intermediate("tile_bins", np.int32).reshape(-1, 2)
+    counts = tb[:, 1] - tb[:, 0]
+    assert ((counts > 2048) & (counts <= 8192)).sum() > 10, counts.max()
+    assert (counts > 8192).sum() > 0, counts.max()
+    assert dev.meta()["n_chunked_tiles"] == int((counts > 8192).sum())
 
 
 def test_render_partial_edge_tiles(dev):

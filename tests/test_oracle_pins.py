@@ -383,11 +383,11 @@ def test_bin_sort_brute_force():
 
 def test_tile_chunks_rule():
     """Chunk counts: one chunk per 512 entries below 400 tiles; above, one
-    piece unless a tile exceeds 2048 entries; never truncated."""
+    piece unless a tile exceeds 8192 entries; never truncated."""
     f = orc.lib().orc_tile_chunks
-    for n in (0, 1, 511, 512, 513, 2048, 2049, 20000):
+    for n in (0, 1, 511, 512, 513, 2048, 2049, 8192, 8193, 20000):
         assert f(n, 256) == max(1, -(-n // 512))
-        assert f(n, 4000) == (1 if n <= 2048 else -(-n // 512))
+        assert f(n, 4000) == (1 if n <= 8192 else -(-n // 512))
 
 
 # --------------------------------------------------- raster forward ----------
