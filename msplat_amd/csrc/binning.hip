@@ -410,11 +410,23 @@ __device__ __forceinline__ int block_combine(int v, int* sh) {
     return r;
 }
 
+// Size class of a tile of n entries in K work items: floor(log2) of the
+// entries of one item (0 for an empty tile).  The raster kernels take items
+// and tiles in descending class, so the longest ones start first.
+__device__ __forceinline__ int size_class(int n, int K) {
+    const int w = K == 1 ? n : min(n, CHUNK);
+    return w > 0 ? 31 - __clz(w) : 0;
+}
+
 __global__ __launch_bounds__(TS_T) void k_tile_counts(int T, const int* __restrict__ tcount,
                                                       int* __restrict__ tot,
-                                                      Meta* __restrict__ meta) {
+                                                      Meta* __restrict__ meta,
+                                                      int* __restrict__ cls) {
     __shared__ int sh[TS_T / 64];
     const int b = blockIdx.x;
+    // the class counters, read by this frame's item build, cleared before
+    // the tile offsets add to them
+    if (b == 0 && threadIdx.x < 128) cls[threadIdx.x] = 0;
     int sn = 0, sk = 0, mx = 0;
 #pragma unroll
     for (int k = 0; k < TS_PER; ++k) {
@@ -445,7 +457,9 @@ __global__ __launch_bounds__(TS_T) void k_tile_offsets(int T, int nb,
                                                        TileLists tl, Meta* __restrict__ meta) {
     __shared__ int sh[TS_T / 64];
     __shared__ int s_n[TS_T], s_k[TS_T];
+    __shared__ int s_cls[64];       // this block's items / tiles per size class
     const int b = blockIdx.x, tid = threadIdx.x;
+    if (tid < 64) s_cls[tid] = 0;
     int pn = 0, pk = 0;
     for (int i = tid; i < b; i += TS_T) {
         pn += tot[3 * i];
@@ -487,6 +501,14 @@ __global__ __launch_bounds__(TS_T) void k_tile_offsets(int T, int nb,
         it.tile_item0[t] = ioff;
         ioff += K[k];
         if (K[k] > 1) tl.chunked[atomicAdd(&meta->n_chunked_tiles, 1)] = t;
+        const int c = size_class(n[k], K[k]);
+        atomicAdd(&s_cls[c], K[k]);
+        atomicAdd(&s_cls[32 + c], 1);
+    }
+    __syncthreads();
+    if (tid < 32) {
+        if (s_cls[tid]) atomicAdd(&it.cls[tid], s_cls[tid]);
+        if (s_cls[32 + tid]) atomicAdd(&it.cls[64 + tid], s_cls[32 + tid]);
     }
     // the projection's intersection and reference counters, copied to the
     // host earlier on the stream, cleared for the next frame
@@ -502,19 +524,67 @@ __global__ __launch_bounds__(TS_T) void k_tile_offsets(int T, int nb,
     }
 }
 
+// Slot of this lane's element in descending size-class order: base[c] is
+// the first slot of class c (the elements of higher classes before it) and
+// fill[c] the class's running fill; the lanes of a wave with the same class
+// take consecutive slots with one atomic.
+__device__ __forceinline__ int class_slot(bool ok, int c, const int* base, int* fill) {
+    const int lane = threadIdx.x & 63;
+    uint64_t peers = wave_ballot(ok);
+#pragma unroll
+    for (int bit = 0; bit < 5; ++bit) {
+        const uint64_t bb = wave_ballot((c >> bit) & 1);
+        peers &= ((c >> bit) & 1) ? bb : ~bb;
+    }
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const int before = __popcll(peers & lt);
+    int first = 0;
+    if (ok && before == 0) first = atomicAdd(&fill[c], __popcll(peers));
+    // the group's first slot from its lowest lane
+    first = __shfl(first, __builtin_ctzll(peers | (1ull << 63)), 64);
+    return base[c] + first + before;
+}
+
 // Work item i: the tile t with tile_item0[t] <= i < tile_item0[t + 1] (every
 // tile has at least one item, so the first items ascend), found by binary
-// search, and its chunk i - tile_item0[t].
-__global__ __launch_bounds__(256) void k_build_items(int T, const Meta* __restrict__ meta, Items it) {
+// search, and its chunk i - tile_item0[t].  Each item, and each tile (thread
+// i < T), also takes its slot in the launch orders, heaviest class first.
+__global__ __launch_bounds__(256) void k_build_items(int T, const Meta* __restrict__ meta,
+                                                     const int* __restrict__ tile_bins, Items it) {
+    __shared__ int s_base[2][32];
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= meta->n_items) return;
-    int lo = 0, hi = T - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (it.tile_item0[mid] <= i) lo = mid; else hi = mid - 1;
+    if (threadIdx.x < 64) {
+        // first slot of each class: the elements of all higher classes
+        const int k = threadIdx.x >> 5, c = threadIdx.x & 31;
+        int sum = 0;
+        for (int d = 31; d > c; --d) sum += it.cls[64 * k + d];
+        s_base[k][c] = sum;
     }
-    it.tile[i] = lo;
-    it.k[i] = i - it.tile_item0[lo];
+    __syncthreads();
+    const int n_items = meta->n_items;
+    const bool item_ok = i < n_items;
+    int c = 0;
+    if (item_ok) {
+        int lo = 0, hi = T - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (it.tile_item0[mid] <= i) lo = mid; else hi = mid - 1;
+        }
+        it.tile[i] = lo;
+        it.k[i] = i - it.tile_item0[lo];
+        c = size_class(tile_bins[2 * lo + 1] - tile_bins[2 * lo], it.tile_K[lo]);
+    }
+    if (__syncthreads_or(item_ok)) {
+        const int slot = class_slot(item_ok, c, s_base[0], it.cls + 32);
+        if (item_ok) it.order[slot] = i;
+    }
+    const bool tile_ok = i < T;
+    int ct = 0;
+    if (tile_ok) ct = size_class(tile_bins[2 * i + 1] - tile_bins[2 * i], it.tile_K[i]);
+    if (__syncthreads_or(tile_ok)) {
+        const int slot = class_slot(tile_ok, ct, s_base[1], it.cls + 96);
+        if (tile_ok) it.tile_order[slot] = i;
+    }
 }
 
 }  // namespace
@@ -575,11 +645,11 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
                        (const int*)rb.sstart, rb.hist, rb.tcount);
     const int nb = (T + TS_BLOCK - 1) / TS_BLOCK;
     hipLaunchKernelGGL(k_tile_counts, dim3(nb), dim3(TS_T), 0, s, T, (const int*)rb.tcount, tscan,
-                       meta);
+                       meta, it.cls);
     hipLaunchKernelGGL(k_tile_offsets, dim3(nb), dim3(TS_T), 0, s, T, nb, (const int*)rb.tcount,
                        (const int*)tscan, isect, tile_bins, it, tl, meta);
-    hipLaunchKernelGGL(k_build_items, dim3(blocks_for(items_bound(T, I))), dim3(256), 0, s, T,
-                       (const Meta*)meta, it);
+    hipLaunchKernelGGL(k_build_items, dim3(blocks_for(std::max<int64_t>(items_bound(T, I), T))),
+                       dim3(256), 0, s, T, (const Meta*)meta, (const int*)tile_bins, it);
     if (R > 0)
         hipLaunchKernelGGL(k_seg_write, dim3((unsigned)NS), dim3(1024), 0, s, S,
                            (const int*)rb.sstart, (const int4*)rb.seg, rk, rv,

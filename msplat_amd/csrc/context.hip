@@ -100,7 +100,7 @@ struct Ctx {
     // per intersection: the tile-sorted gaussian ids
     Buf tval;
     // per item
-    Buf it_tile, it_k, c_T, c_C, c_idx, c_pT, c_aC;
+    Buf it_tile, it_k, it_order, tile_order, it_cls, c_T, c_C, c_idx, c_pT, c_aC;
     // per pixel
     Buf final_T, final_idx, out_img, dbuf, v_rendered, loss_part;
     // scalars
@@ -192,7 +192,7 @@ void free_all(Ctx* c) {
                    &c->tile_item0, &c->l_chunked, &c->st_r0, &c->st_r1, &c->st_rs, &c->st_re, &c->sstart,
                    &c->rkey, &c->rval, &c->rkey2, &c->rval2, &c->rtemp, &c->seg, &c->phist,
                    &c->tval,
-                   &c->it_tile, &c->it_k, &c->c_T, &c->c_C,
+                   &c->it_tile, &c->it_k, &c->it_order, &c->tile_order, &c->it_cls, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
                    &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
                    &c->count_d, &c->work_d, &c->isect_d, &c->eval_part, &c->eval_out, &c->knn_k, &c->knn_v, &c->knn_k2, &c->knn_v2,
@@ -226,6 +226,9 @@ Items items(Ctx* c) {
     it.k = P<int>(c->it_k);
     it.tile_K = P<int>(c->tile_K);
     it.tile_item0 = P<int>(c->tile_item0);
+    it.order = P<int>(c->it_order);
+    it.tile_order = P<int>(c->tile_order);
+    it.cls = P<int>(c->it_cls);
     return it;
 }
 
@@ -439,6 +442,9 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     const int64_t max_items = items_bound(T, I64);
     ENSURE(c->it_tile, (size_t)max_items * 4);
     ENSURE(c->it_k, (size_t)max_items * 4);
+    ENSURE(c->it_order, (size_t)max_items * 4);
+    ENSURE(c->tile_order, (size_t)T * 4);
+    ENSURE(c->it_cls, 4 * 32 * 4);
     const size_t S = (size_t)max_items * TILE_PIX;
     ENSURE(c->c_T, S * 4);
     ENSURE(c->c_C, S * 12);

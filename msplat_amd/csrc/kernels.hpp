@@ -50,6 +50,9 @@ struct Items {
     int* k;
     int* tile_K;         // chunks per tile
     int* tile_item0;     // first item of each tile
+    int* order;          // items, heaviest size class first (the raster launch order)
+    int* tile_order;     // tiles, heaviest size class first (the render launch order)
+    int* cls;            // 4 x 32 counters of the size classes (items, tiles; counts, fills)
 };
 
 // Host-visible summary written by the tile scan.

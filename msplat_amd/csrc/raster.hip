@@ -286,8 +286,10 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
     __shared__ float4 s_geo[256];    // x, y, conic a, b
     __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
     __shared__ float4 s_aux[256];    // clamped b, mask (bits); 16-byte stride shares the address
-    const int item = blockIdx.x;
-    if (item >= meta->n_items || it.k[item] >= kmax) return;
+    // items in launch order (heaviest size class first)
+    if ((int)blockIdx.x >= meta->n_items) return;
+    const int item = it.order[blockIdx.x];
+    if (it.k[item] >= kmax) return;
     fwd_item(item, W, H, tbx, bg0, bg1, bg2, it, tile_bins, pk, final_T, final_idx, out_img, cb,
              work, s_geo, s_col, s_aux);
 }
@@ -332,7 +334,7 @@ __global__ __launch_bounds__(256) void k_render_tiles(int W, int H, int tbx, flo
     __shared__ float4 s_geo[256];
     __shared__ float4 s_col[256];
     __shared__ float4 s_aux[256];
-    const int t = blockIdx.x;
+    const int t = it.tile_order[blockIdx.x];   // heaviest size class first
     const int K = it.tile_K[t];
     const int s = tile_bins[2 * t], e = tile_bins[2 * t + 1];
     const Px px = pixel_of(t, tbx, W, H);
@@ -543,8 +545,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
     // largest final index before the entry loop uses the area
     __shared__ float4 s_red4[4 * 8 * RED_ROW / 4];
     int& s_max = *reinterpret_cast<int*>(s_red4);
-    const int item = blockIdx.x;
-    if (item >= meta->n_items) return;
+    // items in launch order (heaviest size class first)
+    if ((int)blockIdx.x >= meta->n_items) return;
+    const int item = it.order[blockIdx.x];
     int t, K, cs, ce;
     item_range(it, tile_bins, item, t, K, cs, ce);
     const Px px = pixel_of(t, tbx, W, H);
