@@ -117,6 +117,8 @@ struct Ctx {
     Buf knn_k, knn_v, knn_k2, knn_v2, knn_tmp, knn_s, knn_e;
     Meta* meta_h = nullptr;
     float* loss_h = nullptr;
+    float* loss_hd = nullptr;   // loss_h as a device pointer: the loss kernel writes loss_h[1]
+    int* radii_dst = nullptr;   // the caller's radii_out of the current train step, or null
     int* count_h = nullptr;
     // densify scratch
     Buf d_split, d_dup, d_sp, d_dp, d_keep, d_kp, d_tot, d_scratch, d_rnd, d_src;
@@ -215,6 +217,7 @@ GaussOut gauss_out(Ctx* c) {
     GaussOut go;
     go.rec = P<float4>(c->rec);
     go.radii = P<int>(c->radii);
+    go.radii_out = c->radii_dst;
     go.tiles_hit = P<int>(c->tiles_hit);
     go.rect = P<uint2>(c->rect);
     return go;
@@ -349,13 +352,17 @@ CamParams cam_params(const MsplatRenderArgs* a) {
 
 // forward_pipeline (.mm:462-750): project -> depth order -> tile lists -> raster (+merge).
 // The image goes to dst_img, or to the context's own buffer when NULL.
-int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = nullptr) {
+int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = nullptr,
+            int32_t* radii_dst = nullptr) {
     const CamParams p = cam_params(a);
     const int N = p.N, T = p.tbx * p.tby;
     const size_t Px = (size_t)p.W * p.H;
     const size_t Nn = (size_t)std::max(N, 1);
     ENSURE(c->rec, Nn * 64);
     ENSURE(c->radii, Nn * 4);
+    // the projection also writes the radii into the caller's buffer when it
+    // gives one (no copy after the step)
+    c->radii_dst = radii_dst;
     ENSURE(c->tiles_hit, Nn * 4);
     ENSURE(c->rect, Nn * 8);
     ENSURE(c->rect_sorted, Nn * 8);
@@ -529,6 +536,7 @@ int msplat_hip_init(int device) {
     c->stream = c->own;
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->meta_h), sizeof(Meta)));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->loss_h), 16));
+    HIP_TRY(hipHostGetDevicePointer(reinterpret_cast<void**>(&c->loss_hd), c->loss_h, 0));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->count_h), 16));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->isect_h), ISECT_SLOTS * ISECT_STRIDE * 8));
     for (auto& row : c->ev)
@@ -644,7 +652,7 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
     if (!a->vis_counts || !a->xys_grad_norm || !a->max_2d_size)
         return fail(MSPLAT_ERR_ARG, "null grad-stat array");
     stage_begin(c);
-    r = forward(c, &a->r, true);
+    r = forward(c, &a->r, true, nullptr, radii_out);
     if (r != MSPLAT_OK) return r;
     const CamParams p = cam_params(&a->r);
     const size_t Px = (size_t)p.W * p.H;
@@ -654,9 +662,10 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
     ENSURE(c->loss_part, (size_t)sgrid.x * sgrid.y * 12);
     ENSURE(c->loss_d, 16);
     stage_mark(c, S_LOSS);
+    // the loss sum goes straight to pinned host memory (loss_h[1])
     launch_ssim(c->stream, p.H, p.W, P<float>(c->out_img), a->gt, a->ssim_weight, a->loss_inv_n,
                 P<float>(c->dbuf), P<float>(c->v_rendered), P<float>(c->loss_part),
-                P<float>(c->loss_d));
+                c->loss_hd + 1);
     stage_mark(c, S_RBWD);
     launch_raster_bwd(c->stream, p, c->max_items, P<Meta>(c->meta_d), items(c),
                       P<int>(c->tile_bins), packed(c),
@@ -681,19 +690,15 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
                         a->adam_exp_avg[4], a->adam_exp_avg_sq[4], hp);
     stage_mark(c, S_END);
     c->have_bwd = true;
-    if (radii_out && p.N > 0)
-        HIP_TRY(hipMemcpyAsync(radii_out, c->radii.p, (size_t)p.N * 4, hipMemcpyDeviceToDevice,
-                               c->stream));
     HIP_TRY(hipGetLastError());
     if (loss_out) {
-        HIP_TRY(hipMemcpyAsync(c->loss_h, c->loss_d.p, 4, hipMemcpyDeviceToHost, c->stream));
         HIP_TRY(hipStreamSynchronize(c->stream));
-        *loss_out = c->loss_h[0] / (float)(p.H * p.W);
+        *loss_out = c->loss_h[1] / (float)(p.H * p.W);
         c->last_loss = *loss_out;
         c->loss_pending = false;
     } else {
+        // read once a later wait on the stream has passed this step
         c->loss_scale = 1.f / (float)(p.H * p.W);
-        HIP_TRY(hipMemcpyAsync(c->loss_h + 1, c->loss_d.p, 4, hipMemcpyDeviceToHost, c->stream));
         c->loss_pending = true;
     }
     return MSPLAT_OK;

@@ -33,6 +33,7 @@ struct CamParams {
 struct GaussOut {
     float4* rec;
     int* radii;
+    int* radii_out;      // optional second copy of the radii (the caller's), or null
     int* tiles_hit;
     uint2* rect;         // tile rectangle: (x0 | y0 << 16, x1 | y1 << 16), 0 when culled
 };

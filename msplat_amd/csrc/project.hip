@@ -214,6 +214,7 @@ __device__ __forceinline__ Geo project_geo(const CamParams& p, int g, V3 pw, con
                                            uint32_t* __restrict__ dval) {
     Geo r{};
     go.radii[g] = 0;
+    if (go.radii_out) go.radii_out[g] = 0;
     go.tiles_hit[g] = 0;
     go.rect[g] = make_uint2(0u, 0u);
     dkey[g] = 0xFFFFFFFFu;
@@ -275,6 +276,7 @@ __device__ __forceinline__ Geo project_geo(const CamParams& p, int g, V3 pw, con
     go.tiles_hit[g] = area;
     go.rect[g] = make_uint2((uint32_t)x0 | (uint32_t)y0 << 16, (uint32_t)x1 | (uint32_t)y1 << 16);
     go.radii[g] = f2i(radius);
+    if (go.radii_out) go.radii_out[g] = f2i(radius);
     r.area = area;
     r.nref = super_span(x0, y0, x1, y1);   // one binning reference per super-tile
     r.px = px; r.py = py; r.ca = ca; r.cb = cb; r.cc = cc; r.ex = ex; r.ey = ey; r.z = pv.z;
