@@ -411,7 +411,7 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     GaussOut go = gauss_out(c);
     launch_project_fwd(c->stream, p, a->means3d, a->scales, a->quats, a->features_dc,
                        a->features_rest, a->opacities, go, P<uint32_t>(c->dkey),
-                       P<uint32_t>(c->dval), P<float>(c->gacc),
+                       P<uint32_t>(c->dval), training ? P<float>(c->gacc) : nullptr,
                        P<unsigned long long>(c->isect_d));
     stage_mark(c, S_DEPTH);
     HIP_TRY(hipMemcpyAsync(c->isect_h, c->isect_d.p, slots_bytes, hipMemcpyDeviceToHost, c->stream));

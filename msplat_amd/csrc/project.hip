@@ -126,8 +126,8 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
         ol = opac_logits[g];
     }
     // Zero this workgroup's raster gradient accumulators (PROJ_T * 9
-    // contiguous floats) with 16-byte stores.
-    {
+    // contiguous floats) with 16-byte stores; render-only calls pass none.
+    if (gacc) {
         const int64_t base = (int64_t)g0 * 9;
         const int cnt = (int)min((int64_t)PROJ_T * 9, (int64_t)p.N * 9 - base);
         float4* dst4 = reinterpret_cast<float4*>(gacc + base);
