@@ -1,5 +1,7 @@
 // radix.hip — device-wide scans and a stable LSD radix sort of (u32 key, u32
-// value) pairs, used by the binning to order intersections without atomics.
+// value) pairs, used by the binning to order the gaussians by depth and
+// their super-tile references by super-tile, and by the nearest-neighbour
+// search to order points by cell.
 //
 // Sort: digits of up to 8 bits, reduce-then-scan per pass over 4096-key
 // blocks (1024 threads x 4 keys):
