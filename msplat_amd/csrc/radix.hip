@@ -3,8 +3,8 @@
 // their super-tile references by super-tile, and by the nearest-neighbour
 // search to order points by cell.
 //
-// Sort: digits of up to 8 bits, reduce-then-scan per pass over 4096-key
-// blocks (1024 threads x 4 keys):
+// Sort: digits of up to 8 bits, reduce-then-scan per pass over 2048-key
+// blocks (512 threads x 4 keys):
 //   1. per-block digit histograms in LDS -> hist[digit][block], and the
 //      digit totals over all blocks (one global atomic per block and digit)
 //   2. one workgroup per digit scans its row of hist and adds the keys of
@@ -23,7 +23,7 @@ namespace msp {
 
 namespace {
 
-constexpr int RT = 1024;           // threads per sort block (16 waves)
+constexpr int RT = 512;            // threads per sort block (8 waves)
 constexpr int RW = RT / 64;        // waves per sort block
 constexpr int RK = 4;              // keys per thread
 constexpr int RB = RT * RK;        // keys per block
