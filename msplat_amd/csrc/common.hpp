@@ -82,6 +82,26 @@ __device__ __forceinline__ float exp_raster(float x) {
     return ldexpf(p, (int)k);
 }
 
+// exp_raster(-s), bit for bit, in a form without a negated operand: with
+// r' = -r = fma(k, ln2, s) the Horner steps run on u_j = (-1)^j p_j, since
+// fma(u_{j+1}, r', (-1)^j c_j) = (-1)^j fma(p_{j+1}, r, c_j) (round to
+// nearest is odd-symmetric; the p_j of |r| <= ln2/2 are far from 0, so no
+// signed zero arises).  Every step is then a two-VGPR multiply-add with a
+// literal (v_fmamk / v_fmaak), where the negated form needs a three-operand
+// fma with the constant in a scalar register.
+__device__ __forceinline__ float exp_neg_raster(float s) {
+    const float k = rintf(s * -0x1.715476p+0f);
+    const float r = fmaf(k, 0x1.62e430p-1f, s);
+    float u = 0x1.6ab980p-10f;
+    u = fmaf(u, r, -0x1.126d0cp-7f);
+    u = fmaf(u, r, 0x1.55589ap-5f);
+    u = fmaf(u, r, -0x1.55540ap-3f);
+    u = fmaf(u, r, 0x1.fffffap-2f);
+    u = fmaf(u, r, -1.0f);
+    u = fmaf(u, r, 1.0f);
+    return ldexpf(u, (int)k);
+}
+
 __device__ __forceinline__ float sigmoid(float o) { return 1.f / (1.f + exp_cw(-o)); }
 
 // float -> int with the operand clamped to [-2^30, 2^30] first: one defined
@@ -165,6 +185,26 @@ __device__ __forceinline__ float wave_sum_to_last(float v) {
         "s_nop 1"
         : "+v"(v));
     return v;
+}
+
+// The same sum with its total written into lane 63 of dst: the last masked
+// add goes to dst in row 3, bank 3 only (lanes 60..63: row_mask selects the
+// 16-lane row, bank_mask the group of four lanes within it), so lanes 60..62
+// of dst receive partial sums and every other lane keeps its dst value.
+// All lanes must be active.
+__device__ __forceinline__ float wave_sum_into_lane63(float v, float dst) {
+    v += dpp<0xB1>(v);                 // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);                 // quad_perm [2,3,0,1]
+    v += dpp<0x124>(v);                // row_ror:4
+    v += dpp<0x128>(v);                // row_ror:8  -> row sums
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %1, %1, %1 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %0, %1, %1 row_bcast:31 row_mask:0x8 bank_mask:0x8\n\t"
+        "s_nop 1"
+        : "+v"(dst), "+v"(v));
+    return dst;
 }
 
 __device__ __forceinline__ int wave_max_i(int v) {

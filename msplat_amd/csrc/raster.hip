@@ -143,6 +143,9 @@ __device__ __forceinline__ float wave_sum8_lds(const float* v, int lane, float* 
     u += dpp<0xB1>(u);     // quad_perm [1,0,3,2]
     u += dpp<0x4E>(u);     // quad_perm [2,3,0,1]
     u += dpp<0x141>(u);    // row_half_mirror: lane ^ 7 within each 8 lanes
+    // completed here, with every lane active, so that the move and the add
+    // stay one DPP add (sunk into a caller's lane-masked block they are two)
+    asm volatile("" : "+v"(u));
     return u;
 }
 
@@ -190,7 +193,7 @@ __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float f
                 const float cb = lds_f4(s_aux, qb).x;
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-                const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
+                const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma));
                 // hit: live && !(sigma < 0 || sigma >= 5.55) && !(alpha < 1/255)
                 const uint64_t hm = live & mask_uge(sigma, 0.f) & mask_ult(sigma, 5.55f) &
                                     mask_uge(alpha, 1.f / 255.f);
@@ -640,28 +643,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
                 const float4 x = lds_f4(s_aux, qb);
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-                const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
+                const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma));
                 // valid: qq >= qlo && !(sigma < 0 || sigma >= 5.55) && !(alpha < 1/255)
                 const uint64_t vmask = mask_ge_i(qq, qlo) & mask_uge(sigma, 0.f) &
                                        mask_ult(sigma, 5.55f) & mask_uge(alpha, 1.f / 255.f);
                 if (vmask == 0) continue;
-                // Branch-free per lane: lanes without a gradient compute the
-                // same terms and select zeros / their old state.
+                // Branch-free per lane: lanes without a gradient run the same
+                // steps with alpha = 0, which leaves their state as it is
+                // (1 / (1 - 0) = 1 exactly, so Tn = T; fac = 0, so E is
+                // unchanged) and makes every term they contribute zero.
                 const uint64_t gmask = vmask & mask_lt(alpha, 0.999f);
-                const bool grad = lane_of(gmask);
+                const float ag = lane_of(gmask) ? alpha : 0.f;
                 ngrad += (unsigned)__popcll(gmask);
                 const float r0 = c.z, r1 = c.w, r2 = x.x;   // max(raw + 0.5, 0)
-                // hardware reciprocal (1 ulp): the backward is compared with a tolerance
-                const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
+                // hardware reciprocal (1 ulp, exact at 1): the backward is
+                // compared with a tolerance
+                const float ra = __builtin_amdgcn_rcpf(1.f - ag);
                 const float Tn = T * ra;
-                const float fac = grad ? alpha * Tn : 0.f;
+                const float fac = ag * Tn;
                 // v_alpha = sum_k (r_k Tn - (B_k + T_final bg_k) ra) v_out_k
                 const float RV = fmaf(r2, vo2, fmaf(r1, vo1, r0 * vo0));
                 const float v_alpha = fmaf(Tn, RV, -ra * E);
                 E = fmaf(fac, RV, E);
-                T = grad ? Tn : T;
-                // v_sigma of the lanes with a gradient, zero elsewhere
-                const float vsg = grad ? -alpha * v_alpha : 0.f;
+                T = Tn;
+                // v_sigma: zero (signed) on the lanes without a gradient
+                const float vsg = -ag * v_alpha;
                 // v_xy = v_sigma (a dx + b dy, b dx + c dy) and v_conic =
                 // v_sigma / 2 (dx^2, dx dy, dy^2) are linear in the moments
                 // below with the gaussian's own conic, the same in every
@@ -677,14 +683,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
                 v[5] = fac * vo0;
                 v[6] = fac * vo1;
                 v[7] = fac * vo2;
-                const float u = wave_sum8_lds(v, lane, red);
-                // opacity (logit) term -v_sigma (1 - o), total in lane 63
-                const float s8 = wave_sum_to_last(vsg * x.y);
+                // opacity (logit) term -v_sigma (1 - o): its total goes to
+                // lane 63 of u (lanes 60..62 are no owners)
+                const float u = wave_sum_into_lane63(vsg * x.y, wave_sum8_lds(v, lane, red));
                 // v_rgb of a channel whose raw colour + 0.5 < 0 is dropped by
                 // its consumers (the mask is per gaussian, not per pixel)
                 float* ap = reinterpret_cast<float*>(reinterpret_cast<char*>(gacc) +
                                                      ((uint32_t)__float_as_int(x.z) + kofs));
-                if (own) atomicAdd(ap, lane == 63 ? s8 : u);
+                if (own) atomicAdd(ap, u);
             }
         }
     }
@@ -725,7 +731,7 @@ __global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
             const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
             if (sigma < 0.f || sigma >= 5.55f) continue;
             ++n[1];
-            const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
+            const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma));
             if (alpha < 1.f / 255.f) continue;
             const float nT = T * (1.f - alpha);
             if (nT <= 1e-4f) break;
@@ -743,7 +749,7 @@ __global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
             const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
             if (sigma < 0.f || sigma >= 5.55f) continue;
             ++n[4];
-            const float alpha = fminf(0.999f, c.y * exp_raster(-sigma));
+            const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma));
             if (alpha < 1.f / 255.f || !(alpha < 0.999f)) continue;
             ++n[5];
         }
