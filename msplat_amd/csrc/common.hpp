@@ -152,6 +152,15 @@ __device__ __forceinline__ uint64_t mask_ult(float a, float b) { return __builti
 __device__ __forceinline__ uint64_t mask_ge_i(int a, int b) { return __builtin_amdgcn_sicmp(a, b, 39); }
 __device__ __forceinline__ bool lane_of(uint64_t m) { return __builtin_amdgcn_inverse_ballot_w64(m); }
 
+// Index of the lowest set bit of a nonzero wave-uniform mask, cleared from the
+// mask: s_ff1 then s_bitset0, two scalar ALU instructions where m &= m - 1
+// takes a 64-bit decrement and an and.
+__device__ __forceinline__ int pop_low_bit(uint64_t& m) {
+    int bit;
+    asm volatile("s_ff1_i32_b64 %0, %1\n\ts_bitset0_b64 %1, %0" : "=&s"(bit), "+s"(m));
+    return bit;
+}
+
 // Sum over the 64 lanes; every lane gets the total.  All lanes must be active.
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp<0xB1>(v);    // quad_perm [1,0,3,2]

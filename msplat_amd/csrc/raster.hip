@@ -181,13 +181,14 @@ __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float f
             const int q = ch + lane;
             uint64_t m = wave_ballot(q < nb && ((__float_as_int(s_aux[q].y) >> w) & 1));
             nwit += __popcll(m);
+            // the chunk's byte offset in a VGPR: each entry's offset is then
+            // one vector shift-add from the bit index, shared by its LDS reads
+            int chb = ch * (int)sizeof(float4);
+            asm volatile("" : "+v"(chb));
             while (m) {
-                const int bit = __builtin_ctzll(m);
+                const int bit = pop_low_bit(m);
                 const int qq = ch + bit;
-                m &= ~(1ull << bit);
-                // the entry's byte offset in a VGPR once, for all its LDS reads
-                int qb = qq * (int)sizeof(float4);
-                asm volatile("" : "+v"(qb));
+                const int qb = chb + bit * (int)sizeof(float4);
                 const float4 g = lds_f4(s_geo, qb);
                 const float4 c = lds_f4(s_col, qb);
                 const float cb = lds_f4(s_aux, qb).x;
@@ -626,18 +627,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
         const int nb = min(256, top - cs + 1);
         const int q0 = max(0, top - wave_bf);
         const int qlo = top - bf;      // this pixel takes entries qq >= qlo (e_idx <= bf)
+        // in bytes of the LDS arrays, so that the step's index test compares
+        // two VGPRs; clamped to [0, 256] first, which keeps the test's outcome
+        // for every qq in [0, 256) (bf = -1 of a cut-off chunk makes qlo a
+        // global entry index, too large to scale)
+        const int qlob = min(max(qlo, 0), 256) * (int)sizeof(float4);
         for (int ch = (q0 / 64) * 64; ch < nb; ch += 64) {
             const int q = ch + lane;
             uint64_t m = wave_ballot(q >= q0 && q < nb &&
                                      ((__float_as_int(s_aux[q].w) >> w) & 1));
             nwit += __popcll(m);
+            // the chunk's byte offset in a VGPR: each entry's offset is then
+            // one vector shift-add from the bit index, shared by its LDS reads
+            int chb = ch * (int)sizeof(float4);
+            asm volatile("" : "+v"(chb));
             while (m) {
-                const int qq = ch + __builtin_ctzll(m);
-                m &= m - 1;
-                // the entry index in a VGPR once, so that every LDS read of
-                // this step uses it (instead of a copy from the SGPR each)
-                int qb = qq * (int)sizeof(float4);
-                asm volatile("" : "+v"(qb));
+                const int qb = chb + pop_low_bit(m) * (int)sizeof(float4);
                 const float4 g = lds_f4(s_geo, qb);
                 const float4 c = lds_f4(s_col, qb);
                 const float4 x = lds_f4(s_aux, qb);
@@ -645,7 +650,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
                 const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma));
                 // valid: qq >= qlo && !(sigma < 0 || sigma >= 5.55) && !(alpha < 1/255)
-                const uint64_t vmask = mask_ge_i(qq, qlo) & mask_uge(sigma, 0.f) &
+                const uint64_t vmask = mask_ge_i(qb, qlob) & mask_uge(sigma, 0.f) &
                                        mask_ult(sigma, 5.55f) & mask_uge(alpha, 1.f / 255.f);
                 if (vmask == 0) continue;
                 // Branch-free per lane: lanes without a gradient run the same
