@@ -9,8 +9,11 @@
 //   1. the projection wrote key = depth bits (0xFFFFFFFF if culled), value =
 //      id, and the number of super-tiles (SUPER x SUPER tiles) each
 //      gaussian's tile rectangle overlaps
-//   2. radix sort by depth                        (order of gaussians)
-//   3. super-tile counts gathered in that order by the scan -> offsets
+//   2. radix sort by depth                        (order of gaussians);
+//      its last pass also gathers each gaussian's tile rectangle into that
+//      order with its super-tile count (culled gaussians, whose key
+//      0xFFFFFFFF sorts them last, get an empty rectangle and 0)
+//   3. exclusive scan of the counts -> reference offsets
 //   4. one reference (super-tile, rectangle part, gaussian id) per
 //      overlapped super-tile, in depth order
 //   5. stable radix sort of the references by super-tile
@@ -42,23 +45,6 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 // inside it, 24-27 / 28-31 the part's width / height minus one.  The radix
 // sort orders by the super-tile bits and carries the rest.
 constexpr uint32_t ST_MASK = 0xFFFFu;
-
-// Tile rectangles gathered into depth order, and each one's super-tile
-// count (0 for culled gaussians, whose rectangle is empty and whose depth
-// key, 0xFFFFFFFF, sorts them last: their rectangles are not gathered).
-__global__ __launch_bounds__(256) void k_depth_rects(int N, const uint32_t* __restrict__ skey,
-                                                     const uint32_t* __restrict__ order,
-                                                     const uint2* __restrict__ rect,
-                                                     uint2* __restrict__ rs,
-                                                     int* __restrict__ cnt) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= N) return;
-    const uint2 rc = skey[i] != 0xFFFFFFFFu ? rect[order[i]] : make_uint2(0u, 0u);
-    rs[i] = rc;
-    const int x0 = (int)(rc.x & 0xFFFFu), y0 = (int)(rc.x >> 16);
-    const int x1 = (int)(rc.y & 0xFFFFu), y1 = (int)(rc.y >> 16);
-    cnt[i] = (x1 > x0 && y1 > y0) ? super_span(x0, y0, x1, y1) : 0;
-}
 
 // References of the gaussians in depth order: the thread of depth rank r
 // writes one per super-tile its tile rectangle overlaps (row by row), from
@@ -598,14 +584,14 @@ void launch_run_edges(hipStream_t s, int64_t n, const uint32_t* sorted_keys, int
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
                         uint32_t* dval2, int* radix_temp, const uint2* rect, uint2* rect_sorted,
                         int* rcount, int* roff, int* scan_temp, uint32_t** order_out) {
-    const bool flip = launch_radix_sort(s, dkey, dval, dkey2, dval2, N, 32, radix_temp);
+    // the sort's last pass gathers the rectangles into depth order and
+    // counts their super-tiles
+    const RectGather rg{rect, rect_sorted, rcount};
+    const bool flip = launch_radix_sort(s, dkey, dval, dkey2, dval2, N, 32, radix_temp, &rg);
     uint32_t* order = flip ? dval2 : dval;
     *order_out = order;
     if (N <= 0) return;
     // reference offsets: exclusive scan of the super-tile counts in depth order
-    hipLaunchKernelGGL(k_depth_rects, dim3(blocks_for(N)), dim3(256), 0, s, N,
-                       (const uint32_t*)(flip ? dkey2 : dkey), (const uint32_t*)order, rect,
-                       rect_sorted, rcount);
     launch_exclusive_scan_i32(s, rcount, roff, N, scan_temp);
 }
 

@@ -103,8 +103,16 @@ void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* blo
 void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot,
                                const uint32_t* gather = nullptr, int* gathered = nullptr);
 int64_t radix_temp_ints(int64_t n);
+// Optional epilogue of a sort's last pass, for the depth order: output
+// position i also gets rs[i] = rect[value] (zero for the culled key
+// 0xFFFFFFFF) and cnt[i] = the super-tile count of that rectangle.
+struct RectGather {
+    const uint2* rect;
+    uint2* rs;
+    int* cnt;
+};
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
-                       int64_t n, int bits, int* temp);
+                       int64_t n, int bits, int* temp, const RectGather* rg = nullptr);
 
 // Super-tiles: SUPER x SUPER tiles of the tile grid.  A gaussian's tile
 // rectangle is cut into one reference per super-tile it overlaps; the

@@ -211,13 +211,14 @@ __global__ __launch_bounds__(1024) void k_radix_offsets(int* __restrict__ hist, 
 // consecutive keys in 64-key rounds by ballot-matching the digit bits and
 // keeps per-digit running counts), reordered by digit in LDS, and written out
 // in digit runs so that neighbouring lanes store neighbouring addresses.
+template <bool RG>
 __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict__ kin,
                                                       const uint32_t* __restrict__ vin,
                                                       uint32_t* __restrict__ kout,
                                                       uint32_t* __restrict__ vout, int64_t n,
                                                       int shift, uint32_t mask, int nbits,
                                                       int nblocks, const int* __restrict__ offs,
-                                                      int* __restrict__ dtot) {
+                                                      int* __restrict__ dtot, RectGather rg) {
     // The pass's digit totals were last read by the offsets kernel: block 0
     // clears them for the next sort that uses this scratch.
     if (blockIdx.x == 0)
@@ -238,12 +239,14 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     uint32_t key[RK], val[RK];
     int dig[RK], rank[RK];
+    uint2 rc[RK];      // RG: the value's rectangle, gathered while the keys are ranked
 #pragma unroll
     for (int j = 0; j < RK; ++j) {
         const int64_t i = wbase + j * 64 + lane;
         const bool ok = i < n;
         key[j] = ok ? kin[i] : 0u;
         val[j] = ok ? vin[i] : 0u;
+        if (RG) rc[j] = ok && key[j] != 0xFFFFFFFFu ? rg.rect[val[j]] : make_uint2(0u, 0u);
         const int d = ok ? (int)((key[j] >> shift) & mask) : 256;
         dig[j] = d;
         uint64_t peers = wave_ballot(ok);
@@ -276,22 +279,53 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
     const int start = block_exclusive_scan<RT>(cnt, scan_sh);
     if (tid < 256) dstart[tid] = start;
     __syncthreads();
+    int lpos[RK];      // each key's place in the block's digit order
 #pragma unroll
     for (int j = 0; j < RK; ++j) {
         const int d = dig[j];
+        lpos[j] = -1;
         if (d > 255) continue;
         const int p = dstart[d] + wcnt[w][d] + rank[j];
+        lpos[j] = p;
         s_key[p] = key[j];
         s_val[p] = val[j];
     }
     __syncthreads();
     const int nvalid = (int)min((int64_t)RB, n - (int64_t)blockIdx.x * RB);
-    for (int p = tid; p < nvalid; p += RT) {
+    int64_t opos[RK];  // output position of block element tid + u RT
+#pragma unroll
+    for (int u = 0; u < RK; ++u) {
+        const int p = tid + u * RT;
+        opos[u] = -1;
+        if (p >= nvalid) continue;
         const uint32_t k = s_key[p];
         const int d = (int)((k >> shift) & mask);
         const int64_t pos = (int64_t)gofs[d] + (p - dstart[d]);
         kout[pos] = k;
         vout[pos] = s_val[p];
+        opos[u] = pos;
+    }
+    if (RG) {
+        // the rectangles take the keys' LDS places and go to the same
+        // output positions, with their super-tile counts
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < RK; ++j) {
+            if (lpos[j] < 0) continue;
+            s_key[lpos[j]] = rc[j].x;
+            s_val[lpos[j]] = rc[j].y;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < RK; ++u) {
+            if (opos[u] < 0) continue;
+            const int p = tid + u * RT;
+            const uint2 r = make_uint2(s_key[p], s_val[p]);
+            rg.rs[opos[u]] = r;
+            const int x0 = (int)(r.x & 0xFFFFu), y0 = (int)(r.x >> 16);
+            const int x1 = (int)(r.y & 0xFFFFu), y1 = (int)(r.y >> 16);
+            rg.cnt[opos[u]] = (x1 > x0 && y1 > y0) ? super_span(x0, y0, x1, y1) : 0;
+        }
     }
 }
 
@@ -342,9 +376,10 @@ int64_t radix_temp_ints(int64_t n) {
 // Sorts (k0, v0) by the bits [0, bits) of the keys; ping-pongs with (k1, v1).
 // The bits are split into ceil(bits / 8) passes of equal width (fewer digit
 // values give longer runs per digit and block).  Returns true when the result
-// ends up in (k1, v1).
+// ends up in (k1, v1).  With rg the last pass also writes each output
+// position's rectangle and super-tile count (RectGather).
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
-                       int64_t n, int bits, int* temp) {
+                       int64_t n, int bits, int* temp, const RectGather* rg) {
     if (n <= 0 || bits <= 0) return false;
     const int nb = (int)((n + RB - 1) / RB);
     const int passes = (bits + 7) / 8;
@@ -369,9 +404,14 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
                            mask, nb, hist, dt);
         hipLaunchKernelGGL(k_radix_offsets, dim3(mask + 1), dim3(1024), 0, s, hist, nb,
                            (const int*)dt);
-        hipLaunchKernelGGL(k_radix_scatter, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki,
-                           (const uint32_t*)vi, ko, vo, n, shift, mask, width, nb,
-                           (const int*)hist, dt);
+        if (rg && pass == passes - 1)
+            hipLaunchKernelGGL(k_radix_scatter<true>, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki,
+                               (const uint32_t*)vi, ko, vo, n, shift, mask, width, nb,
+                               (const int*)hist, dt, *rg);
+        else
+            hipLaunchKernelGGL(k_radix_scatter<false>, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki,
+                               (const uint32_t*)vi, ko, vo, n, shift, mask, width, nb,
+                               (const int*)hist, dt, RectGather{});
         flip = !flip;
         shift += width;
     }
