@@ -144,9 +144,7 @@ def rocprof_summary(d: str, first: int, count: int, command: str) -> str:
     if not stats or not trace:
         raise SystemExit(f"no kernel_stats / kernel_trace csv under {d}")
 
-    def short(name):
-        m = re.search(r"(k_\w+)", name)
-        return m.group(1) if m else name.split("(")[0][:60]
+    short = _kernel_name
 
     rows = sorted(csv.DictReader(open(stats[0])), key=lambda r: -float(r["TotalDurationNs"]))
     out = [f"Command: `{command}`", "",
@@ -165,17 +163,36 @@ def rocprof_summary(d: str, first: int, count: int, command: str) -> str:
     return "\n".join(out) + "\n"
 
 
+def _kernel_name(full: str) -> str:
+    """This library's kernel name in a profiler's kernel name, with its
+    template arguments (k_radix_scatter<true>); other names up to '('."""
+    import re
+    m = re.search(r"(k_\w+(?:<[^>(]*>)?)", full)
+    return m.group(1) if m else full.split("(")[0][:60]
+
+
+def _kernel_match(want: str, full: str) -> bool:
+    """A library kernel name (k_...) matches that kernel exactly, every
+    template instance when given without arguments; anything else is a
+    regular expression searched in the profiler's name."""
+    import re
+    if not want.startswith("k_"):
+        return re.search(want, full) is not None
+    name = _kernel_name(full)
+    return name == want or ("<" not in want and name.split("<")[0] == want)
+
+
 def _pmc_mean(d: str, kernel_re: str, counter: str, last: int) -> tuple:
-    """Mean of one counter over the dispatches of the kernels matching kernel_re
-    (the last `last` of them when last > 0) in a `rocprofv3 --pmc -f csv` directory."""
+    """Mean of one counter over the dispatches of the kernel kernel_re (as
+    _kernel_match reads it; the last `last` dispatches when last > 0) in a
+    `rocprofv3 --pmc -f csv` directory."""
     import csv
     import glob
-    import re
     f = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
     if not f:
         raise SystemExit(f"no counter_collection csv under {d}")
     rows = [r for r in csv.DictReader(open(f[0]))
-            if re.search(kernel_re, r["Kernel_Name"]) and r["Counter_Name"] == counter]
+            if _kernel_match(kernel_re, r["Kernel_Name"]) and r["Counter_Name"] == counter]
     rows.sort(key=lambda r: int(r["Dispatch_Id"]))
     v = [float(r["Counter_Value"]) for r in rows]
     if last > 0:
@@ -221,7 +238,7 @@ def pmc_summary(d: str, kernels: list, last: int, command: str) -> str:
         vals = {}
         n = 0
         for c in names:
-            rs = [r for r in rows if re.search(k, r["Kernel_Name"]) and r["Counter_Name"] == c]
+            rs = [r for r in rows if _kernel_match(k, r["Kernel_Name"]) and r["Counter_Name"] == c]
             rs.sort(key=lambda r: int(r["Dispatch_Id"]))
             v = [float(r["Counter_Value"]) for r in rs]
             if last > 0:
@@ -431,7 +448,8 @@ def main():
     ap.add_argument("--pmc-summary", default="",
                     help="only print a markdown table of the counters of this rocprofv3 --pmc csv output "
                          "directory for --pmc-kernels (last --steps dispatches of each) and exit")
-    ap.add_argument("--pmc-kernels", default="k_raster_fwd,k_raster_bwd,k_radix_hist,k_radix_scatter,"
+    ap.add_argument("--pmc-kernels", default="k_raster_fwd,k_raster_bwd,k_radix_hist,k_radix_scatter<false>,"
+                                             "k_radix_scatter<true>,k_seg_write,"
                                              "k_ssim_fused,k_ssim_v_bwd,k_project_fwd,k_sh_rest_adam,"
                                              "k_proj_bwd_adam")
     ap.add_argument("--traffic-summary", nargs=4, default=None,
