@@ -46,34 +46,6 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 // sort orders by the super-tile bits and carries the rest.
 constexpr uint32_t ST_MASK = 0xFFFFu;
 
-// References of the gaussians in depth order: the thread of depth rank r
-// writes one per super-tile its tile rectangle overlaps (row by row), from
-// roff[r] on.
-__global__ __launch_bounds__(256) void k_emit_refs(int N, int sbx, const uint32_t* __restrict__ order,
-                                                   const int* __restrict__ roff,
-                                                   const uint2* __restrict__ rs,
-                                                   uint32_t* __restrict__ rkey,
-                                                   uint32_t* __restrict__ rval) {
-    const int r = blockIdx.x * 256 + threadIdx.x;
-    if (r >= N) return;
-    const uint2 rc = rs[r];
-    const int x0 = (int)(rc.x & 0xFFFFu), y0 = (int)(rc.x >> 16);
-    const int x1 = (int)(rc.y & 0xFFFFu), y1 = (int)(rc.y >> 16);
-    if (x1 <= x0 || y1 <= y0) return;
-    const uint32_t g = order[r];
-    int o = roff[r];
-    for (int sy = y0 / SUPER; sy * SUPER < y1; ++sy) {
-        const int ly0 = max(y0 - sy * SUPER, 0), ly1 = min(y1 - sy * SUPER, SUPER);
-        for (int sx = x0 / SUPER; sx * SUPER < x1; ++sx) {
-            const int lx0 = max(x0 - sx * SUPER, 0), lx1 = min(x1 - sx * SUPER, SUPER);
-            rkey[o] = (uint32_t)(sy * sbx + sx) | (uint32_t)lx0 << 16 | (uint32_t)ly0 << 20 |
-                      (uint32_t)(lx1 - lx0 - 1) << 24 | (uint32_t)(ly1 - ly0 - 1) << 28;
-            rval[o] = g;
-            ++o;
-        }
-    }
-}
-
 // Reference range [st_r0, st_r1) of each super-tile present.
 __global__ __launch_bounds__(256) void k_ref_edges(int R, const uint32_t* __restrict__ rkey,
                                                    int* __restrict__ st_r0,
@@ -108,51 +80,67 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* sh, int& total) 
     return wofs + x - v;
 }
 
-// Segments of the super-tiles (one workgroup): super-tile s's references
-// are cut into ceil(n / SEG_REFS) segments of SEG_REFS consecutive ones,
-// numbered from sstart[s] on (sstart[S] = the segment count).  The
-// reference ranges move to st_rs / st_re and are cleared for the next call
-// (k_ref_edges writes those of present super-tiles only).
-__global__ __launch_bounds__(1024) void k_seg_table(int S, int* __restrict__ st_r0,
-                                                    int* __restrict__ st_r1,
-                                                    int* __restrict__ st_rs,
-                                                    int* __restrict__ st_re,
-                                                    int* __restrict__ sstart) {
-    __shared__ int sh[16];
-    const int per = (S + 1023) / 1024;
-    const int b = min((int)threadIdx.x * per, S), e = min(b + per, S);
-    int sum = 0;
-    for (int s = b; s < e; ++s) sum += (st_r1[s] - st_r0[s] + SEG_REFS - 1) / SEG_REFS;
-    int total;
-    int run = block_exclusive_scan<1024>(sum, sh, total);
-    for (int s = b; s < e; ++s) {
-        const int r0 = st_r0[s], r1 = st_r1[s];
-        sstart[s] = run;
-        run += (r1 - r0 + SEG_REFS - 1) / SEG_REFS;
-        st_rs[s] = r0;
-        st_re[s] = r1;
-        st_r0[s] = 0;
-        st_r1[s] = 0;
+// References of the gaussians in depth order: the thread of depth rank r
+// writes one per super-tile its tile rectangle overlaps (row by row), from
+// its first reference slot on.  The slots are the exclusive scan of the
+// super-tile counts, finished here: the 1024 ranks of a workgroup (one scan
+// block) scan their counts in the workgroup and add the totals of the scan
+// blocks before them (summed here, or already scanned when there are more
+// than SCAN_DIRECT_BLOCKS of them).
+constexpr int EMIT_T = SCAN_BLOCK;
+__global__ __launch_bounds__(EMIT_T) void k_emit_refs(int N, int sbx, const uint32_t* __restrict__ order,
+                                                      const int* __restrict__ rtot,
+                                                      const uint2* __restrict__ rs,
+                                                      uint32_t* __restrict__ rkey,
+                                                      uint32_t* __restrict__ rval) {
+    constexpr int NW = EMIT_T / 64;
+    __shared__ int sh_c[NW], sh_a[NW];
+    const int r = blockIdx.x * EMIT_T + threadIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int nb = (N + EMIT_T - 1) / EMIT_T;
+    // this thread's share of the earlier blocks' totals (none when they are
+    // already scanned) and its count; one pass scans the counts and sums the
+    // shares over the workgroup
+    int acc = 0;
+    if (nb <= SCAN_DIRECT_BLOCKS)
+        for (int b = threadIdx.x; b < (int)blockIdx.x; b += EMIT_T) acc += rtot[b];
+    // the rectangle and id are loaded before the scan, and the count is taken
+    // from the rectangle (as rcount holds it)
+    const uint2 rc = r < N ? rs[r] : make_uint2(0u, 0u);
+    const uint32_t g = r < N ? order[r] : 0u;
+    const int x0 = (int)(rc.x & 0xFFFFu), y0 = (int)(rc.x >> 16);
+    const int x1 = (int)(rc.y & 0xFFFFu), y1 = (int)(rc.y >> 16);
+    const int c = (x1 > x0 && y1 > y0) ? super_span(x0, y0, x1, y1) : 0;
+    int x = c;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+        acc += __shfl_xor(acc, off, 64);
     }
-    if (threadIdx.x == 0) sstart[S] = total;
-}
-
-// Record of each segment (one thread each): its super-tile s (the last
-// with sstart[s] <= j, by binary search) and its reference range.
-__global__ __launch_bounds__(256) void k_seg_records(int S, int nbound,
-                                                     const int* __restrict__ sstart,
-                                                     const int* __restrict__ st_rs,
-                                                     const int* __restrict__ st_re,
-                                                     int4* __restrict__ seg) {
-    const int j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= nbound || j >= sstart[S]) return;
-    int lo = 0, hi = S - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (sstart[mid] <= j) lo = mid; else hi = mid - 1;
+    if (lane == 63) {
+        sh_c[w] = x;
+        sh_a[w] = acc;
     }
-    const int r0 = st_rs[lo] + (j - sstart[lo]) * SEG_REFS;
-    seg[j] = make_int4(lo, r0, min(r0 + SEG_REFS, st_re[lo]), 0);
+    __syncthreads();
+    int o = nb > SCAN_DIRECT_BLOCKS ? rtot[blockIdx.x] : 0;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
+        if (k < w) o += sh_c[k];
+        o += sh_a[k];
+    }
+    o += x - c;
+    if (c == 0) return;   // culled, or an empty rectangle
+    for (int sy = y0 / SUPER; sy * SUPER < y1; ++sy) {
+        const int ly0 = max(y0 - sy * SUPER, 0), ly1 = min(y1 - sy * SUPER, SUPER);
+        for (int sx = x0 / SUPER; sx * SUPER < x1; ++sx) {
+            const int lx0 = max(x0 - sx * SUPER, 0), lx1 = min(x1 - sx * SUPER, SUPER);
+            rkey[o] = (uint32_t)(sy * sbx + sx) | (uint32_t)lx0 << 16 | (uint32_t)ly0 << 20 |
+                      (uint32_t)(lx1 - lx0 - 1) << 24 | (uint32_t)(ly1 - ly0 - 1) << 28;
+            rval[o] = g;
+            ++o;
+        }
+    }
 }
 
 // Rectangle part of a reference key in local tile coordinates [x0, x1) x [y0, y1).
@@ -163,20 +151,51 @@ __device__ __forceinline__ void ref_rect(uint32_t k, int& x0, int& y0, int& x1, 
     y1 = y0 + (int)((k >> 28) & 15u) + 1;
 }
 
-// Pairs per local tile of each segment -> hist[j * 256 + ly * 16 + lx]:
-// the references' rectangles are added to a 17 x 17 difference array (four
-// LDS atomics each) whose 2-D prefix sums are the counts.
+// Segments and their pair counts, one workgroup per segment (grid: the
+// segments_bound of the call).  Each workgroup first works out the segment
+// table itself from the super-tiles' reference ranges [st_r0, st_r1):
+// super-tile s's references are cut into ceil(n / SEG_REFS) segments of
+// SEG_REFS consecutive ones, numbered from sstart[s] on (sstart[S] = the
+// segment count; workgroup 0 writes sstart).  That is a scan over the S
+// super-tiles in every workgroup, a few values per thread at the image sizes
+// this serves.  Workgroup j then records its segment (super-tile, reference
+// range) in seg[j] and counts the pairs per local tile of its references ->
+// hist[j * 256 + ly * 16 + lx]: the rectangles are added to a 17 x 17
+// difference array (four LDS atomics each) whose 2-D prefix sums are the
+// counts.
 constexpr int DW = SUPER + 1;
-__global__ __launch_bounds__(256) void k_seg_count(int S, const int* __restrict__ sstart,
-                                                   const int4* __restrict__ seg,
+__global__ __launch_bounds__(256) void k_seg_count(int S, const int* __restrict__ st_r0,
+                                                   const int* __restrict__ st_r1,
+                                                   int* __restrict__ sstart,
+                                                   int4* __restrict__ seg,
                                                    const uint32_t* __restrict__ rkey,
                                                    int* __restrict__ hist) {
     __shared__ int diff[DW * DW];
+    __shared__ int sh[4];
+    __shared__ int4 s_rec;
     const int j = blockIdx.x, tid = threadIdx.x;
-    // in bounds for every workgroup of the grid; used only below the count
-    const int nseg = sstart[S];
-    const int4 sg = seg[j];
+    const int per = (S + 255) / 256;
+    const int b = min(tid * per, S), e = min(b + per, S);
+    int sum = 0;
+    for (int t = b; t < e; ++t) sum += (st_r1[t] - st_r0[t] + SEG_REFS - 1) / SEG_REFS;
+    if (tid == 0) s_rec = make_int4(0, 0, 0, 0);
+    int nseg;
+    int run = block_exclusive_scan<256>(sum, sh, nseg);
+    for (int t = b; t < e; ++t) {
+        const int r0 = st_r0[t], r1 = st_r1[t];
+        const int n = (r1 - r0 + SEG_REFS - 1) / SEG_REFS;
+        if (j == 0) sstart[t] = run;
+        if (j >= run && j < run + n) {
+            const int rs0 = r0 + (j - run) * SEG_REFS;
+            s_rec = make_int4(t, rs0, min(rs0 + SEG_REFS, r1), 0);
+        }
+        run += n;
+    }
+    if (j == 0 && tid == 0) sstart[S] = nseg;
+    __syncthreads();
     if (j >= nseg) return;
+    const int4 sg = s_rec;
+    if (tid == 0) seg[j] = sg;
     for (int i = tid; i < DW * DW; i += 256) diff[i] = 0;
     __syncthreads();
     for (int r = sg.y + tid; r < sg.z; r += 256) {
@@ -213,14 +232,22 @@ __global__ __launch_bounds__(256) void k_seg_count(int S, const int* __restrict_
 // pairs in the super-tile's earlier segments, and the tile's total goes to
 // tcount (every tile of the grid lies in exactly one super-tile, so tcount
 // is rewritten whole).  Two passes over the counts: group totals, then
-// offsets.
+// offsets.  Workgroup (s, 0) also clears super-tile s's reference range for
+// the next call (k_ref_edges writes those of present super-tiles only; every
+// k_seg_count workgroup has read them by now).
 constexpr int SO_G = 16, SO_D = 64, SO_T = SO_G * SO_D;
 __global__ __launch_bounds__(SO_T) void k_seg_offsets(int tbx, int tby, int sbx,
                                                       const int* __restrict__ sstart,
                                                       int* __restrict__ hist,
-                                                      int* __restrict__ tcount) {
+                                                      int* __restrict__ tcount,
+                                                      int* __restrict__ st_r0,
+                                                      int* __restrict__ st_r1) {
     __shared__ int part[SO_G][SO_D];
     const int s = blockIdx.x, tile = blockIdx.y * SO_D + threadIdx.x % SO_D;
+    if (blockIdx.y == 0 && threadIdx.x == 0) {
+        st_r0[s] = 0;
+        st_r1[s] = 0;
+    }
     const int d = threadIdx.x % SO_D, g = threadIdx.x / SO_D;
     const int b0 = sstart[s], b1 = sstart[s + 1];
     const int per = (b1 - b0 + SO_G - 1) / SO_G;
@@ -583,7 +610,7 @@ void launch_run_edges(hipStream_t s, int64_t n, const uint32_t* sorted_keys, int
 
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
                         uint32_t* dval2, int* radix_temp, const uint2* rect, uint2* rect_sorted,
-                        int* rcount, int* roff, int* scan_temp, uint32_t** order_out) {
+                        int* rcount, int* rtot, uint32_t** order_out) {
     // the sort's last pass gathers the rectangles into depth order and
     // counts their super-tiles
     const RectGather rg{rect, rect_sorted, rcount};
@@ -591,12 +618,14 @@ void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, ui
     uint32_t* order = flip ? dval2 : dval;
     *order_out = order;
     if (N <= 0) return;
-    // reference offsets: exclusive scan of the super-tile counts in depth order
-    launch_exclusive_scan_i32(s, rcount, roff, N, scan_temp);
+    // the block totals of the super-tile counts in depth order (the reference
+    // emission finishes their scan)
+    launch_block_totals(s, rcount, N, rtot);
 }
 
 void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
-                       const uint32_t* order, const int* roff, const uint2* rect_sorted, RefBufs rb,
+                       const uint32_t* order, const int* rtot,
+                       const uint2* rect_sorted, RefBufs rb,
                        uint32_t* ids, int* tscan, int* tile_bins, Items it, TileLists tl,
                        Meta* meta, unsigned long long* isect) {
     const int T = p.tbx * p.tby;
@@ -604,8 +633,8 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
     const uint32_t* rk = rb.key;
     const uint32_t* rv = rb.val;
     if (R > 0) {
-        hipLaunchKernelGGL(k_emit_refs, dim3(blocks_for(p.N)), dim3(256), 0, s, p.N, sbx, order,
-                           roff, rect_sorted, rb.key, rb.val);
+        hipLaunchKernelGGL(k_emit_refs, dim3((unsigned)((p.N + EMIT_T - 1) / EMIT_T)), dim3(EMIT_T), 0, s,
+                           p.N, sbx, order, rtot, rect_sorted, rb.key, rb.val);
         int bits = 0;
         while ((1 << bits) < S) ++bits;
         if (launch_radix_sort(s, rb.key, rb.val, rb.key2, rb.val2, R, bits, rb.radix_temp)) {
@@ -615,20 +644,14 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
         hipLaunchKernelGGL(k_ref_edges, dim3(blocks_for(R)), dim3(256), 0, s, (int)R, rk,
                            rb.st_r0, rb.st_r1);
     }
-    // with no references every super-tile is empty: no segments, zero counts
-    hipLaunchKernelGGL(k_seg_table, dim3(1), dim3(1024), 0, s, S, rb.st_r0, rb.st_r1, rb.st_rs,
-                       rb.st_re, rb.sstart);
+    // with no references every super-tile is empty: no segments (workgroup 0
+    // still writes the segment table), zero counts
     const int64_t NS = segments_bound(R, S);
-    if (R > 0) {
-        hipLaunchKernelGGL(k_seg_records, dim3(blocks_for(NS)), dim3(256), 0, s, S, (int)NS,
-                           (const int*)rb.sstart, (const int*)rb.st_rs, (const int*)rb.st_re,
-                           rb.seg);
-        hipLaunchKernelGGL(k_seg_count, dim3((unsigned)NS), dim3(256), 0, s, S,
-                           (const int*)rb.sstart, (const int4*)rb.seg, rk, rb.hist);
-    }
+    hipLaunchKernelGGL(k_seg_count, dim3((unsigned)NS), dim3(256), 0, s, S,
+                       (const int*)rb.st_r0, (const int*)rb.st_r1, rb.sstart, rb.seg, rk, rb.hist);
     hipLaunchKernelGGL(k_seg_offsets, dim3(S, SUPER * SUPER / SO_D), dim3(SO_T), 0, s, p.tbx,
                        p.tby, sbx,
-                       (const int*)rb.sstart, rb.hist, rb.tcount);
+                       (const int*)rb.sstart, rb.hist, rb.tcount, rb.st_r0, rb.st_r1);
     const int nb = (T + TS_BLOCK - 1) / TS_BLOCK;
     hipLaunchKernelGGL(k_tile_counts, dim3(nb), dim3(TS_T), 0, s, T, (const int*)rb.tcount, tscan,
                        meta, it.cls);

@@ -90,11 +90,11 @@ struct Ctx {
 
     // per gaussian
     Buf rec, radii, tiles_hit, rect, gacc;
-    Buf dkey, dval, dkey2, dval2, rect_sorted, hits, eoff, dtemp, stemp;
+    Buf dkey, dval, dkey2, dval2, rect_sorted, hits, dtemp, stemp;
     // per tile
     Buf tcount, tscan, tile_bins, tile_K, tile_item0, l_chunked, tile_done;
     // per super-tile, per super-tile reference, per pair block
-    Buf st_r0, st_r1, st_rs, st_re, sstart;
+    Buf st_r0, st_r1, sstart;
     Buf rkey, rval, rkey2, rval2, rtemp;
     Buf seg, phist;
     // per intersection: the tile-sorted gaussian ids
@@ -189,9 +189,9 @@ T* P(Buf& b) { return reinterpret_cast<T*>(b.p); }
 
 void free_all(Ctx* c) {
     Buf* bufs[] = {&c->rec, &c->radii, &c->tiles_hit, &c->rect, &c->rect_sorted,
-                   &c->gacc, &c->dkey, &c->dval, &c->dkey2, &c->dval2, &c->hits, &c->eoff,
+                   &c->gacc, &c->dkey, &c->dval, &c->dkey2, &c->dval2, &c->hits,
                    &c->dtemp, &c->stemp, &c->tcount, &c->tscan, &c->tile_done, &c->tile_bins, &c->tile_K,
-                   &c->tile_item0, &c->l_chunked, &c->st_r0, &c->st_r1, &c->st_rs, &c->st_re, &c->sstart,
+                   &c->tile_item0, &c->l_chunked, &c->st_r0, &c->st_r1, &c->sstart,
                    &c->rkey, &c->rval, &c->rkey2, &c->rval2, &c->rtemp, &c->seg, &c->phist,
                    &c->tval,
                    &c->it_tile, &c->it_k, &c->it_order, &c->tile_order, &c->it_cls, &c->c_T, &c->c_C,
@@ -372,7 +372,6 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     ENSURE(c->dkey2, Nn * 4);
     ENSURE(c->dval2, Nn * 4);
     ENSURE(c->hits, Nn * 4);
-    ENSURE(c->eoff, Nn * 4);
     ENSURE(c->dtemp, (size_t)radix_temp_ints(N) * 4);
     ENSURE(c->stemp, ((size_t)scan_block_count(N) + 8) * 4);
     ENSURE(c->tcount, (size_t)T * 4);
@@ -383,8 +382,6 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
                     "65536 super-tiles of %dx%d)", p.tbx, p.tby, SUPER, SUPER);
     ENSURE(c->st_r0, (size_t)nst * 4);
     ENSURE(c->st_r1, (size_t)nst * 4);
-    ENSURE(c->st_rs, (size_t)nst * 4);
-    ENSURE(c->st_re, (size_t)nst * 4);
     ENSURE(c->sstart, ((size_t)nst + 1) * 4);
     ENSURE(c->tile_bins, (size_t)T * 8);
     ENSURE(c->tile_K, (size_t)T * 4);
@@ -420,7 +417,7 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     launch_depth_order(c->stream, N, P<uint32_t>(c->dkey), P<uint32_t>(c->dval),
                        P<uint32_t>(c->dkey2), P<uint32_t>(c->dval2), P<int>(c->dtemp),
                        P<uint2>(c->rect), P<uint2>(c->rect_sorted), P<int>(c->hits),
-                       P<int>(c->eoff), P<int>(c->stemp), &order);
+                       P<int>(c->stemp), &order);
     HIP_TRY(hipEventSynchronize(c->ev_total));
     if (c->timing) stage_fold(c, c->cur ^ 1);   // the previous call has completed
     if (c->loss_pending) {                       // so has its loss copy
@@ -472,13 +469,12 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     rb.radix_temp = P<int>(c->rtemp);
     rb.st_r0 = P<int>(c->st_r0);
     rb.st_r1 = P<int>(c->st_r1);
-    rb.st_rs = P<int>(c->st_rs);
-    rb.st_re = P<int>(c->st_re);
     rb.sstart = P<int>(c->sstart);
     rb.seg = P<int4>(c->seg);
     rb.hist = P<int>(c->phist);
     rb.tcount = P<int>(c->tcount);
-    launch_tile_lists(c->stream, p, I64, R64, order, P<int>(c->eoff), P<uint2>(c->rect_sorted), rb,
+    launch_tile_lists(c->stream, p, I64, R64, order, P<int>(c->stemp),
+                      P<uint2>(c->rect_sorted), rb,
                       P<uint32_t>(c->tval), P<int>(c->tscan), P<int>(c->tile_bins), it, tl,
                       P<Meta>(c->meta_d), P<unsigned long long>(c->isect_d));
     c->sorted_ids = P<uint32_t>(c->tval);

@@ -98,7 +98,15 @@ void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
 
 // Scans and radix sort (radix.hip).  With `gather` the scanned values are
 // in[gather[i]], also stored to gathered[i] (n ints).
+constexpr int SCAN_BLOCK = 1024;   // elements per scan block
 int64_t scan_block_count(int64_t n);
+// Above this many 1024-element blocks a scan runs its block totals through a
+// one-workgroup scan; up to it, each block adds up the totals before it.
+constexpr int SCAN_DIRECT_BLOCKS = 2048;
+// The first half of a scan: the totals of the 1024-element blocks of in,
+// turned into exclusive block offsets when there are more than
+// SCAN_DIRECT_BLOCKS blocks (the consumer then reads tot[b] directly).
+void launch_block_totals(hipStream_t s, const int* in, int64_t n, int* tot);
 void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot);
 void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot,
                                const uint32_t* gather = nullptr, int* gathered = nullptr);
@@ -133,11 +141,13 @@ __host__ __device__ inline int super_span(int x0, int y0, int x1, int y1) {
 // Binning (binning.hip).  The projection adds the intersection and
 // reference totals to the counters above (needed on the host before
 // launch_tile_lists); launch_depth_order orders the gaussians by depth,
-// gathers their tile rectangles in that order (rect_sorted) and scans their
-// super-tile counts (rcount) into reference offsets (roff).
+// gathers their tile rectangles in that order (rect_sorted), with their
+// super-tile counts (rcount) and the counts' 1024-block totals (rtot, as
+// launch_block_totals leaves them), from which launch_tile_lists' reference
+// emission takes each gaussian's first reference slot.
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
                         uint32_t* dval2, int* radix_temp, const uint2* rect, uint2* rect_sorted,
-                        int* rcount, int* roff, int* scan_temp, uint32_t** order_out);
+                        int* rcount, int* rtot, uint32_t** order_out);
 
 // Scratch of launch_tile_lists for R references, S super-tiles, NS =
 // segments_bound(R, S) segments and T tiles.
@@ -146,8 +156,6 @@ struct RefBufs {
     int* radix_temp;                     // radix_temp_ints(R)
     int* st_r0;                          // S: reference range of each super-tile;
     int* st_r1;                          //    S; both zero between calls
-    int* st_rs;                          // S: copies of the reference ranges
-    int* st_re;                          // S
     int* sstart;                         // S + 1: first segment of each super-tile
     int4* seg;                           // NS: (super-tile, first reference, end reference)
     int* hist;                           // NS * 256: pairs per local tile and segment
@@ -156,7 +164,8 @@ struct RefBufs {
 // Writes the tile-sorted gaussian ids (I of them) to ids, tile_bins, the
 // work items and the summary in meta.
 void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
-                       const uint32_t* order, const int* roff, const uint2* rect_sorted, RefBufs rb,
+                       const uint32_t* order, const int* rtot,
+                       const uint2* rect_sorted, RefBufs rb,
                        uint32_t* ids, int* tscan, int* tile_bins, Items it, TileLists tl,
                        Meta* meta, unsigned long long* isect);
 // Ints of the tile scan's scratch (tscan) for T tiles.

@@ -28,7 +28,7 @@ constexpr int RW = RT / 64;        // waves per sort block
 constexpr int RK = 4;              // keys per thread
 constexpr int RB = RT * RK;        // keys per block
 constexpr int WK = RK * 64;        // keys per wave (RK rounds of 64)
-constexpr int SB = 1024;           // elements per scan block
+constexpr int SB = SCAN_BLOCK;     // elements per scan block
 constexpr int MAX_PASSES = 4;      // 32-bit keys in 8-bit digits
 constexpr int DCOPIES = 16;        // copies of the digit totals (block b adds to copy b % 16)
 
@@ -335,10 +335,6 @@ inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1)
 
 int64_t scan_block_count(int64_t n) { return (n + SB - 1) / SB; }
 
-// Up to this many blocks each scan block adds up the totals before it itself
-// (two kernels); beyond, a one-workgroup scan of the totals runs in between.
-constexpr int SCAN_DIRECT_BLOCKS = 2048;
-
 template <bool INCLUSIVE>
 void launch_scan(hipStream_t s, const int* in, int* out, int64_t n, int* tot,
                  const uint32_t* gather, int* gathered) {
@@ -357,6 +353,13 @@ void launch_scan(hipStream_t s, const int* in, int* out, int64_t n, int* tot,
         hipLaunchKernelGGL((k_block_scan<INCLUSIVE, false>), dim3(nb), dim3(256), 0, s, in, out, n,
                            (const int*)tot, gather);
     }
+}
+
+void launch_block_totals(hipStream_t s, const int* in, int64_t n, int* tot) {
+    if (n <= 0) return;
+    const int nb = (int)scan_block_count(n);
+    hipLaunchKernelGGL(k_block_reduce, dim3(nb), dim3(256), 0, s, in, n, tot, nullptr, nullptr);
+    if (nb > SCAN_DIRECT_BLOCKS) hipLaunchKernelGGL(k_scan_totals, dim3(1), dim3(1024), 0, s, tot, nb);
 }
 
 void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* tot) {
