@@ -610,11 +610,11 @@ void launch_run_edges(hipStream_t s, int64_t n, const uint32_t* sorted_keys, int
 
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
                         uint32_t* dval2, int* radix_temp, const uint2* rect, uint2* rect_sorted,
-                        int* rcount, int* rtot, uint32_t** order_out) {
+                        int* rcount, int* rtot, const SlotSum* ss, uint32_t** order_out) {
     // the sort's last pass gathers the rectangles into depth order and
     // counts their super-tiles
     const RectGather rg{rect, rect_sorted, rcount};
-    const bool flip = launch_radix_sort(s, dkey, dval, dkey2, dval2, N, 32, radix_temp, &rg);
+    const bool flip = launch_radix_sort(s, dkey, dval, dkey2, dval2, N, 32, radix_temp, &rg, ss);
     uint32_t* order = flip ? dval2 : dval;
     *order_out = order;
     if (N <= 0) return;

@@ -86,7 +86,7 @@ struct Ctx {
     int64_t stage_cnt[kNumStages] = {};
     int64_t calls = 0;
     std::vector<double> call_ms;   // bracketed milliseconds of each timed call since the last drain
-    hipEvent_t ev_total = nullptr;   // recorded after the intersection total's copy to the host
+    hipEvent_t ev_total = nullptr;   // recorded after the depth sort's first kernel (totals in isect_h)
 
     // per gaussian
     Buf rec, radii, tiles_hit, rect, gacc;
@@ -105,10 +105,12 @@ struct Ctx {
     Buf final_T, final_idx, out_img, dbuf, v_rendered, loss_part;
     // scalars
     Buf meta_d, loss_d, count_d, work_d;
-    // intersection total of the projection: ISECT_SLOTS counters, one per
-    // 128-byte line (workgroup b adds to slot b % ISECT_SLOTS), summed on the host
+    // intersection and reference totals of the projection: ISECT_SLOTS
+    // counter pairs, one per 128-byte line (workgroup b adds to slot b %
+    // ISECT_SLOTS), summed by the depth sort's first kernel
     Buf isect_d;
-    uint64_t* isect_h = nullptr;
+    uint64_t* isect_h = nullptr;     // the two totals, written by the depth sort's first kernel
+    unsigned long long* isect_hd = nullptr;   // isect_h as a device pointer
     bool isect_dirty = false;   // counters written and not yet cleared by a tile scan
     // evaluation: per-workgroup fp64 partials and the three sums
     Buf eval_part, eval_out;
@@ -395,15 +397,18 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     c->last_N = N; c->last_T = T; c->last_W = p.W; c->last_H = p.H;
     c->have_bwd = false;
 
-    // The projection adds up the intersection total, which goes to the host
-    // while the GPU sorts by depth: the host waits on an event recorded after
-    // the copy, not on the stream.
-    // (the counters arrive zeroed: fresh buffers are, and the tile scan of
-    // the previous frame cleared them, unless that frame stopped before it)
-    const size_t slots_bytes = (size_t)ISECT_SLOTS * ISECT_STRIDE * 8;
-    ENSURE(c->isect_d, slots_bytes);
-    if (c->isect_dirty) HIP_TRY(hipMemsetAsync(c->isect_d.p, 0, slots_bytes, c->stream));
+    // The projection adds up the intersection and reference totals, which
+    // the depth sort's first kernel writes to mapped host memory (isect_h)
+    // while the GPU goes on sorting: the host waits on an event recorded
+    // after that kernel, not on the stream.  (isect_h is zeroed first: with
+    // no gaussians neither kernel runs.  The device counters arrive zeroed:
+    // fresh buffers are, and the tile scan of the previous frame cleared
+    // them, unless that frame stopped before it.)
+    ENSURE(c->isect_d, ISECT_BYTES);
+    if (c->isect_dirty) HIP_TRY(hipMemsetAsync(c->isect_d.p, 0, ISECT_BYTES, c->stream));
     c->isect_dirty = true;
+    c->isect_h[0] = 0;
+    c->isect_h[1] = 0;
     stage_mark(c, S_PROJ);
     GaussOut go = gauss_out(c);
     launch_project_fwd(c->stream, p, a->means3d, a->scales, a->quats, a->features_dc,
@@ -411,24 +416,19 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
                        P<uint32_t>(c->dval), training ? P<float>(c->gacc) : nullptr,
                        P<unsigned long long>(c->isect_d));
     stage_mark(c, S_DEPTH);
-    HIP_TRY(hipMemcpyAsync(c->isect_h, c->isect_d.p, slots_bytes, hipMemcpyDeviceToHost, c->stream));
-    HIP_TRY(hipEventRecord(c->ev_total, c->stream));
     uint32_t* order = nullptr;
+    const SlotSum totals{P<unsigned long long>(c->isect_d), c->isect_hd, c->ev_total};
     launch_depth_order(c->stream, N, P<uint32_t>(c->dkey), P<uint32_t>(c->dval),
                        P<uint32_t>(c->dkey2), P<uint32_t>(c->dval2), P<int>(c->dtemp),
                        P<uint2>(c->rect), P<uint2>(c->rect_sorted), P<int>(c->hits),
-                       P<int>(c->stemp), &order);
+                       P<int>(c->stemp), &totals, &order);
     HIP_TRY(hipEventSynchronize(c->ev_total));
     if (c->timing) stage_fold(c, c->cur ^ 1);   // the previous call has completed
     if (c->loss_pending) {                       // so has its loss copy
         c->last_loss = c->loss_h[1] * c->loss_scale;
         c->loss_pending = false;
     }
-    int64_t I64 = 0, R64 = 0;
-    for (int k = 0; k < ISECT_SLOTS; ++k) {
-        I64 += (int64_t)c->isect_h[(size_t)k * ISECT_STRIDE];
-        R64 += (int64_t)c->isect_h[(size_t)k * ISECT_STRIDE + 1];
-    }
+    const int64_t I64 = (int64_t)c->isect_h[0], R64 = (int64_t)c->isect_h[1];
     if (I64 > (int64_t)0x7FFFFFFF - 4096)
         return fail(MSPLAT_ERR_ARG, "%lld tile intersections exceed the 32-bit index range",
                     (long long)I64);
@@ -534,7 +534,8 @@ int msplat_hip_init(int device) {
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->loss_h), 16));
     HIP_TRY(hipHostGetDevicePointer(reinterpret_cast<void**>(&c->loss_hd), c->loss_h, 0));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->count_h), 16));
-    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->isect_h), ISECT_SLOTS * ISECT_STRIDE * 8));
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->isect_h), 16));
+    HIP_TRY(hipHostGetDevicePointer(reinterpret_cast<void**>(&c->isect_hd), c->isect_h, 0));
     for (auto& row : c->ev)
         for (auto& e : row) HIP_TRY(hipEventCreate(&e));
     HIP_TRY(hipEventCreateWithFlags(&c->ev_total, hipEventDisableTiming));

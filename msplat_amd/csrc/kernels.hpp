@@ -87,9 +87,11 @@ struct ChunkBufs {
 // Intersection-total counters of the projection: ISECT_SLOTS u64 counter
 // pairs ISECT_STRIDE u64 apart (one 128-byte line each); the first of a pair
 // counts (gaussian, tile) pairs, the second (gaussian, super-tile)
-// references; the totals are the sums over the slots.
+// references; the totals are the sums over the slots, formed by the first
+// kernel of the depth sort (SlotSum) for the host.
 constexpr int ISECT_SLOTS = 64;
 constexpr int ISECT_STRIDE = 16;
+constexpr size_t ISECT_BYTES = (size_t)ISECT_SLOTS * ISECT_STRIDE * 8;
 void launch_project_fwd(hipStream_t s, const CamParams& p, const float* means,
                         const float* scales, const float* quats, const float* f_dc,
                         const float* f_rest, const float* opac_logits, GaussOut go,
@@ -111,6 +113,15 @@ void launch_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* blo
 void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n, int* block_tot,
                                const uint32_t* gather = nullptr, int* gathered = nullptr);
 int64_t radix_temp_ints(int64_t n);
+// Optional side job of a sort's first kernel, for the depth order: its
+// workgroup 0 sums the projection's ISECT_SLOTS counter pairs and writes the
+// two totals to out (mapped host memory), and `after` (if not null) is
+// recorded on the stream after that kernel.
+struct SlotSum {
+    const unsigned long long* slots;
+    unsigned long long* out;
+    hipEvent_t after;
+};
 // Optional epilogue of a sort's last pass, for the depth order: output
 // position i also gets rs[i] = rect[value] (zero for the culled key
 // 0xFFFFFFFF) and cnt[i] = the super-tile count of that rectangle.
@@ -120,7 +131,8 @@ struct RectGather {
     int* cnt;
 };
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
-                       int64_t n, int bits, int* temp, const RectGather* rg = nullptr);
+                       int64_t n, int bits, int* temp, const RectGather* rg = nullptr,
+                       const SlotSum* ss = nullptr);
 
 // Super-tiles: SUPER x SUPER tiles of the tile grid.  A gaussian's tile
 // rectangle is cut into one reference per super-tile it overlaps; the
@@ -147,7 +159,7 @@ __host__ __device__ inline int super_span(int x0, int y0, int x1, int y1) {
 // emission takes each gaussian's first reference slot.
 void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, uint32_t* dkey2,
                         uint32_t* dval2, int* radix_temp, const uint2* rect, uint2* rect_sorted,
-                        int* rcount, int* rtot, uint32_t** order_out);
+                        int* rcount, int* rtot, const SlotSum* ss, uint32_t** order_out);
 
 // Scratch of launch_tile_lists for R references, S super-tiles, NS =
 // segments_bound(R, S) segments and T tiles.

@@ -145,8 +145,16 @@ __global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
 
 __global__ __launch_bounds__(RT) void k_radix_hist(const uint32_t* __restrict__ keys, int64_t n,
                                                    int shift, uint32_t mask, int nblocks,
-                                                   int* __restrict__ hist, int* __restrict__ dtot) {
+                                                   int* __restrict__ hist, int* __restrict__ dtot,
+                                                   SlotSum ss) {
     __shared__ int h[256];
+    if (ss.out && blockIdx.x == 0 && threadIdx.x < 2) {
+        unsigned long long t = 0;
+        for (int k = 0; k < ISECT_SLOTS; ++k)
+            t += __hip_atomic_load(ss.slots + (size_t)k * ISECT_STRIDE + threadIdx.x, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        ss.out[threadIdx.x] = t;
+    }
     if (threadIdx.x < 256) h[threadIdx.x] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * RB;
@@ -380,9 +388,10 @@ int64_t radix_temp_ints(int64_t n) {
 // The bits are split into ceil(bits / 8) passes of equal width (fewer digit
 // values give longer runs per digit and block).  Returns true when the result
 // ends up in (k1, v1).  With rg the last pass also writes each output
-// position's rectangle and super-tile count (RectGather).
+// position's rectangle and super-tile count (RectGather); with ss the first
+// kernel also does the SlotSum job.
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
-                       int64_t n, int bits, int* temp, const RectGather* rg) {
+                       int64_t n, int bits, int* temp, const RectGather* rg, const SlotSum* ss) {
     if (n <= 0 || bits <= 0) return false;
     const int nb = (int)((n + RB - 1) / RB);
     const int passes = (bits + 7) / 8;
@@ -403,8 +412,10 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
         uint32_t* ko = flip ? k0 : k1;
         uint32_t* vo = flip ? v0 : v1;
         int* dt = dtot + DCOPIES * 256 * pass;
+        const SlotSum side = ss && pass == 0 ? *ss : SlotSum{nullptr, nullptr, nullptr};
         hipLaunchKernelGGL(k_radix_hist, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki, n, shift,
-                           mask, nb, hist, dt);
+                           mask, nb, hist, dt, side);
+        if (side.after) (void)hipEventRecord(side.after, s);
         hipLaunchKernelGGL(k_radix_offsets, dim3(mask + 1), dim3(1024), 0, s, hist, nb,
                            (const int*)dt);
         if (rg && pass == passes - 1)
