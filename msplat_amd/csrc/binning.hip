@@ -637,12 +637,16 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
                            p.N, sbx, order, rtot, rect_sorted, rb.key, rb.val);
         int bits = 0;
         while ((1 << bits) < S) ++bits;
-        if (launch_radix_sort(s, rb.key, rb.val, rb.key2, rb.val2, R, bits, rb.radix_temp)) {
+        // a single-pass sort (at most 256 super-tiles) writes the super-tiles'
+        // reference ranges itself; otherwise they are found in the sorted keys
+        if (launch_radix_sort(s, rb.key, rb.val, rb.key2, rb.val2, R, bits, rb.radix_temp, nullptr,
+                              nullptr, rb.st_r0, rb.st_r1)) {
             rk = rb.key2;
             rv = rb.val2;
         }
-        hipLaunchKernelGGL(k_ref_edges, dim3(blocks_for(R)), dim3(256), 0, s, (int)R, rk,
-                           rb.st_r0, rb.st_r1);
+        if (bits == 0 || bits > 8)   // one super-tile (no sort), or a two-pass sort
+            hipLaunchKernelGGL(k_ref_edges, dim3(blocks_for(R)), dim3(256), 0, s, (int)R, rk,
+                               rb.st_r0, rb.st_r1);
     }
     // with no references every super-tile is empty: no segments (workgroup 0
     // still writes the segment table), zero counts

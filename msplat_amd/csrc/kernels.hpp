@@ -132,7 +132,7 @@ struct RectGather {
 };
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
                        int64_t n, int bits, int* temp, const RectGather* rg = nullptr,
-                       const SlotSum* ss = nullptr);
+                       const SlotSum* ss = nullptr, int* edge0 = nullptr, int* edge1 = nullptr);
 
 // Super-tiles: SUPER x SUPER tiles of the tile grid.  A gaussian's tile
 // rectangle is cut into one reference per super-tile it overlaps; the

@@ -194,8 +194,12 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* sh) {
 // becomes the position of block b's first key with digit d, i.e. the keys
 // of all smaller digits (sum of the dtot copies over d' < d) plus those of
 // digit d in the blocks before b (exclusive scan of the row).
+// With edge0 (a single-pass sort) the digit's output range [start, end)
+// also goes to edge0[d], edge1[d] when the digit occurs.
 __global__ __launch_bounds__(1024) void k_radix_offsets(int* __restrict__ hist, int nblocks,
-                                                        const int* __restrict__ dtot) {
+                                                        const int* __restrict__ dtot,
+                                                        int* __restrict__ edge0,
+                                                        int* __restrict__ edge1) {
     __shared__ int sh[16];
     const int d = blockIdx.x, t = threadIdx.x;
     int lower = 0;
@@ -204,6 +208,7 @@ __global__ __launch_bounds__(1024) void k_radix_offsets(int* __restrict__ hist, 
         for (int c = 0; c < DCOPIES; ++c) lower += dtot[c * 256 + t];
     }
     int carry = block_sum<1024>(lower, sh);
+    const int start = carry;
     int* row = hist + (size_t)d * nblocks;
     for (int c = 0; c < nblocks; c += 1024) {
         const int i = c + t;
@@ -211,6 +216,10 @@ __global__ __launch_bounds__(1024) void k_radix_offsets(int* __restrict__ hist, 
         const int ex = block_exclusive_scan<1024>(v, sh);
         if (i < nblocks) row[i] = carry + ex;
         carry += block_sum<1024>(v, sh);
+    }
+    if (edge0 && t == 0 && carry > start) {
+        edge0[d] = start;
+        edge1[d] = carry;
     }
 }
 
@@ -389,9 +398,12 @@ int64_t radix_temp_ints(int64_t n) {
 // values give longer runs per digit and block).  Returns true when the result
 // ends up in (k1, v1).  With rg the last pass also writes each output
 // position's rectangle and super-tile count (RectGather); with ss the first
-// kernel also does the SlotSum job.
+// kernel also does the SlotSum job; with edge0 / edge1 and at most 8 bits
+// (one pass) each occurring key value k gets its output range
+// [edge0[k], edge1[k]) (entries of absent values are not written).
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
-                       int64_t n, int bits, int* temp, const RectGather* rg, const SlotSum* ss) {
+                       int64_t n, int bits, int* temp, const RectGather* rg, const SlotSum* ss,
+                       int* edge0, int* edge1) {
     if (n <= 0 || bits <= 0) return false;
     const int nb = (int)((n + RB - 1) / RB);
     const int passes = (bits + 7) / 8;
@@ -417,7 +429,8 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
                            mask, nb, hist, dt, side);
         if (side.after) (void)hipEventRecord(side.after, s);
         hipLaunchKernelGGL(k_radix_offsets, dim3(mask + 1), dim3(1024), 0, s, hist, nb,
-                           (const int*)dt);
+                           (const int*)dt, passes == 1 ? edge0 : nullptr,
+                           passes == 1 ? edge1 : nullptr);
         if (rg && pass == passes - 1)
             hipLaunchKernelGGL(k_radix_scatter<true>, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki,
                                (const uint32_t*)vi, ko, vo, n, shift, mask, width, nb,
