@@ -86,7 +86,6 @@ struct Ctx {
     int64_t stage_cnt[kNumStages] = {};
     int64_t calls = 0;
     std::vector<double> call_ms;   // bracketed milliseconds of each timed call since the last drain
-    hipEvent_t ev_total = nullptr;   // recorded after the depth sort's first kernel (totals in isect_h)
 
     // per gaussian
     Buf rec, radii, tiles_hit, rect, gacc;
@@ -109,7 +108,7 @@ struct Ctx {
     // counter pairs, one per 128-byte line (workgroup b adds to slot b %
     // ISECT_SLOTS), summed by the depth sort's first kernel
     Buf isect_d;
-    uint64_t* isect_h = nullptr;     // the two totals, written by the depth sort's first kernel
+    uint64_t* isect_h = nullptr;     // totals_word(I, R), written by the depth sort's first kernel
     unsigned long long* isect_hd = nullptr;   // isect_h as a device pointer
     bool isect_dirty = false;   // counters written and not yet cleared by a tile scan
     // evaluation: per-workgroup fp64 partials and the three sums
@@ -211,7 +210,6 @@ void free_all(Ctx* c) {
     for (auto& row : c->ev)
         for (auto& e : row)
             if (e) (void)hipEventDestroy(e);
-    if (c->ev_total) (void)hipEventDestroy(c->ev_total);
     if (c->own) (void)hipStreamDestroy(c->own);
 }
 
@@ -354,6 +352,37 @@ CamParams cam_params(const MsplatRenderArgs* a) {
 
 // forward_pipeline (.mm:462-750): project -> depth order -> tile lists -> raster (+merge).
 // The image goes to dst_img, or to the context's own buffer when NULL.
+// Waits for the totals word of the current frame (bit 63 set) in coherent
+// host memory.  With no gaussians nothing writes it: the stream is drained
+// instead, so that the caller may rely on the earlier work having completed
+// either way.  A failed or stopped stream ends the wait with its error.
+hipError_t wait_totals(Ctx* c, int N, uint64_t* word) {
+    if (N <= 0) {
+        *word = 0;
+        return hipStreamSynchronize(c->stream);
+    }
+    for (unsigned k = 1;; ++k) {
+        const uint64_t w = __atomic_load_n(&c->isect_h[0], __ATOMIC_ACQUIRE);
+        if (w >> 63) {
+            *word = w;
+            return hipSuccess;
+        }
+        if ((k & 4095) == 0) {
+            const hipError_t e = hipStreamQuery(c->stream);
+            if (e == hipSuccess) {   // drained: the word must be there now
+                const uint64_t v = __atomic_load_n(&c->isect_h[0], __ATOMIC_ACQUIRE);
+                if (v >> 63) {
+                    *word = v;
+                    return hipSuccess;
+                }
+                return hipErrorUnknown;
+            }
+            if (e != hipErrorNotReady) return e;
+        }
+        __builtin_ia32_pause();
+    }
+}
+
 int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = nullptr,
             int32_t* radii_dst = nullptr) {
     const CamParams p = cam_params(a);
@@ -398,17 +427,16 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     c->have_bwd = false;
 
     // The projection adds up the intersection and reference totals, which
-    // the depth sort's first kernel writes to mapped host memory (isect_h)
-    // while the GPU goes on sorting: the host waits on an event recorded
-    // after that kernel, not on the stream.  (isect_h is zeroed first: with
-    // no gaussians neither kernel runs.  The device counters arrive zeroed:
-    // fresh buffers are, and the tile scan of the previous frame cleared
-    // them, unless that frame stopped before it.)
+    // the depth sort's first kernel writes to coherent host memory (isect_h,
+    // one word with a ready bit) while the GPU goes on sorting: the host
+    // polls that word, without an event on the stream.  (isect_h is zeroed
+    // first.  The device counters arrive zeroed: fresh buffers are, and the
+    // tile scan of the previous frame cleared them, unless that frame
+    // stopped before it.)
     ENSURE(c->isect_d, ISECT_BYTES);
     if (c->isect_dirty) HIP_TRY(hipMemsetAsync(c->isect_d.p, 0, ISECT_BYTES, c->stream));
     c->isect_dirty = true;
-    c->isect_h[0] = 0;
-    c->isect_h[1] = 0;
+    __atomic_store_n(&c->isect_h[0], (uint64_t)0, __ATOMIC_RELEASE);
     stage_mark(c, S_PROJ);
     GaussOut go = gauss_out(c);
     launch_project_fwd(c->stream, p, a->means3d, a->scales, a->quats, a->features_dc,
@@ -417,18 +445,21 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
                        P<unsigned long long>(c->isect_d));
     stage_mark(c, S_DEPTH);
     uint32_t* order = nullptr;
-    const SlotSum totals{P<unsigned long long>(c->isect_d), c->isect_hd, c->ev_total};
+    const SlotSum totals{P<unsigned long long>(c->isect_d), c->isect_hd};
     launch_depth_order(c->stream, N, P<uint32_t>(c->dkey), P<uint32_t>(c->dval),
                        P<uint32_t>(c->dkey2), P<uint32_t>(c->dval2), P<int>(c->dtemp),
                        P<uint2>(c->rect), P<uint2>(c->rect_sorted), P<int>(c->hits),
                        P<int>(c->stemp), &totals, &order);
-    HIP_TRY(hipEventSynchronize(c->ev_total));
-    if (c->timing) stage_fold(c, c->cur ^ 1);   // the previous call has completed
-    if (c->loss_pending) {                       // so has its loss copy
+    uint64_t word = 0;
+    HIP_TRY(wait_totals(c, N, &word));
+    // everything queued before the sort's first kernel has completed now,
+    // the previous call's loss kernel included
+    if (c->loss_pending) {
         c->last_loss = c->loss_h[1] * c->loss_scale;
         c->loss_pending = false;
     }
-    const int64_t I64 = (int64_t)c->isect_h[0], R64 = (int64_t)c->isect_h[1];
+    const int64_t I64 = (int64_t)((word >> 31) & 0x7FFFFFFFull);
+    const int64_t R64 = (int64_t)(word & 0x7FFFFFFFull);
     if (I64 > (int64_t)0x7FFFFFFF - 4096)
         return fail(MSPLAT_ERR_ARG, "%lld tile intersections exceed the 32-bit index range",
                     (long long)I64);
@@ -496,6 +527,9 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
         launch_render_tiles(c->stream, p, it, P<int>(c->tile_bins), pk, P<float>(c->final_T),
                             P<int>(c->final_idx), img, work_counters(c));
     }
+    // the previous call's stage times (it has completed: the event above
+    // follows it), read once this call's kernels are queued
+    if (c->timing) stage_fold(c, c->cur ^ 1);
     HIP_TRY(hipGetLastError());
     c->meta_valid = false;
     return MSPLAT_OK;
@@ -534,11 +568,11 @@ int msplat_hip_init(int device) {
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->loss_h), 16));
     HIP_TRY(hipHostGetDevicePointer(reinterpret_cast<void**>(&c->loss_hd), c->loss_h, 0));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->count_h), 16));
-    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->isect_h), 16));
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->isect_h), 16,
+                          hipHostMallocMapped | hipHostMallocCoherent));
     HIP_TRY(hipHostGetDevicePointer(reinterpret_cast<void**>(&c->isect_hd), c->isect_h, 0));
     for (auto& row : c->ev)
         for (auto& e : row) HIP_TRY(hipEventCreate(&e));
-    HIP_TRY(hipEventCreateWithFlags(&c->ev_total, hipEventDisableTiming));
     return MSPLAT_OK;
 }
 

@@ -115,13 +115,19 @@ void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n
 int64_t radix_temp_ints(int64_t n);
 // Optional side job of a sort's first kernel, for the depth order: its
 // workgroup 0 sums the projection's ISECT_SLOTS counter pairs and writes the
-// two totals to out (mapped host memory), and `after` (if not null) is
-// recorded on the stream after that kernel.
+// two totals to *out (coherent host memory) as one 64-bit word,
+// totals_word(I, R), which the host polls.
 struct SlotSum {
     const unsigned long long* slots;
     unsigned long long* out;
-    hipEvent_t after;
 };
+// Bit 63 set (so that a zeroed word means "not yet"), the intersection total
+// in bits 31..61 and the reference total in bits 0..30, each saturated at
+// 2^31 - 1.
+__host__ __device__ inline unsigned long long totals_word(unsigned long long i, unsigned long long r) {
+    const unsigned long long cap = 0x7FFFFFFFull;
+    return (1ull << 63) | ((i < cap ? i : cap) << 31) | (r < cap ? r : cap);
+}
 // Optional epilogue of a sort's last pass, for the depth order: output
 // position i also gets rs[i] = rect[value] (zero for the culled key
 // 0xFFFFFFFF) and cnt[i] = the super-tile count of that rectangle.

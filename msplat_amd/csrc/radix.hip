@@ -148,12 +148,21 @@ __global__ __launch_bounds__(RT) void k_radix_hist(const uint32_t* __restrict__ 
                                                    int* __restrict__ hist, int* __restrict__ dtot,
                                                    SlotSum ss) {
     __shared__ int h[256];
-    if (ss.out && blockIdx.x == 0 && threadIdx.x < 2) {
-        unsigned long long t = 0;
-        for (int k = 0; k < ISECT_SLOTS; ++k)
-            t += __hip_atomic_load(ss.slots + (size_t)k * ISECT_STRIDE + threadIdx.x, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        ss.out[threadIdx.x] = t;
+    if (ss.out && blockIdx.x == 0 && threadIdx.x < 64) {
+        // lane k reads slot k's pair; the wave sums them
+        unsigned long long ti = 0, tr = 0;
+        for (int k = threadIdx.x; k < ISECT_SLOTS; k += 64) {
+            ti += __hip_atomic_load(ss.slots + (size_t)k * ISECT_STRIDE, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+            tr += __hip_atomic_load(ss.slots + (size_t)k * ISECT_STRIDE + 1, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+        }
+        for (int off = 32; off >= 1; off >>= 1) {
+            ti += __shfl_xor(ti, off, 64);
+            tr += __shfl_xor(tr, off, 64);
+        }
+        if (threadIdx.x == 0)
+            __hip_atomic_store(ss.out, totals_word(ti, tr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     if (threadIdx.x < 256) h[threadIdx.x] = 0;
     __syncthreads();
@@ -424,10 +433,9 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
         uint32_t* ko = flip ? k0 : k1;
         uint32_t* vo = flip ? v0 : v1;
         int* dt = dtot + DCOPIES * 256 * pass;
-        const SlotSum side = ss && pass == 0 ? *ss : SlotSum{nullptr, nullptr, nullptr};
+        const SlotSum side = ss && pass == 0 ? *ss : SlotSum{nullptr, nullptr};
         hipLaunchKernelGGL(k_radix_hist, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki, n, shift,
                            mask, nb, hist, dt, side);
-        if (side.after) (void)hipEventRecord(side.after, s);
         hipLaunchKernelGGL(k_radix_offsets, dim3(mask + 1), dim3(1024), 0, s, hist, nb,
                            (const int*)dt, passes == 1 ? edge0 : nullptr,
                            passes == 1 ? edge1 : nullptr);
