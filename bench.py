@@ -584,16 +584,16 @@ def main():
     poses = [np.asarray(c.cam_to_world, np.float32) for c in cams]
     for i in range(5):
         tr.render_pose_device(poses[i % len(poses)], i % len(poses), out)
-    _abi.check(lib.msplat_hip_set_stage_timing_mask(1 << STAGES.index("rast_fwd")))
-    _abi.check(lib.msplat_hip_enable_stage_timing(1))
+    # the FPS window runs with no events and no pair counters (neither is
+    # part of a render); the render forward's kernel time and pairs come
+    # from the bracketed frames after it
+    _abi.check(lib.msplat_hip_enable_stage_timing(0))
     device.sync()
     r0 = time.perf_counter()
     for i in range(args.frames):
         tr.render_pose_device(poses[i % len(poses)], i % len(poses), out)
     device.sync()
     r1 = time.perf_counter()
-    rtimed, _ = stage_times(lib)
-    render_pairs = device.drain_raster_counters()
     fps = args.frames / (r1 - r0)
     log(f"render: {args.frames} frames in {r1 - r0:.3f}s = {fps:.1f} FPS at N={tr.splat_count()}")
     _abi.check(lib.msplat_hip_set_stage_timing_mask(0xFFFFFFFF))
@@ -602,7 +602,8 @@ def main():
         tr.render_pose_device(poses[i % len(poses)], i % len(poses), out)
     device.sync()
     rstages, _ = stage_times(lib)
-    device.drain_raster_counters()
+    render_pairs = device.drain_raster_counters()
+    rtimed = rstages
     _abi.check(lib.msplat_hip_enable_stage_timing(0))
     rparts = _stage_line(rstages)
     for k, v in rparts.items():

@@ -255,9 +255,10 @@ ChunkBufs chunks(Ctx* c) {
 int sh_bases(int degree) { return degree == 0 ? 1 : degree == 1 ? 4 : degree == 2 ? 9 : degree == 3 ? 16 : 25; }
 
 // Raster pair counters (composited forward, gradient-carrying backward),
-// accumulated while stage timing is enabled.
-unsigned long long* work_counters(Ctx* c) {
-    return c->timing ? P<unsigned long long>(c->work_d) : nullptr;
+// accumulated while stage timing is enabled for the rasteriser's stage st;
+// otherwise null, and the kernels then run without counting.
+unsigned long long* work_counters(Ctx* c, int st) {
+    return c->timing && ((c->stage_mask >> st) & 1u) ? P<unsigned long long>(c->work_d) : nullptr;
 }
 
 // Record the start of stage `st` (S_END closes the call).  Only stages in
@@ -519,13 +520,13 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
         // all chunks of a tile
         launch_raster_fwd(c->stream, p, max_items, P<Meta>(c->meta_d), it, P<int>(c->tile_bins),
                           pk, P<float>(c->final_T), P<int>(c->final_idx), img, cb,
-                          work_counters(c), P<int>(c->l_chunked), P<int>(c->tile_done));
+                          work_counters(c, S_RFWD), P<int>(c->l_chunked), P<int>(c->tile_done));
         launch_raster_merge(c->stream, p, P<Meta>(c->meta_d), P<int>(c->l_chunked), it,
                             P<float>(c->final_T), P<int>(c->final_idx), img, cb, true,
                             P<int>(c->tile_done));
     } else {
         launch_render_tiles(c->stream, p, it, P<int>(c->tile_bins), pk, P<float>(c->final_T),
-                            P<int>(c->final_idx), img, work_counters(c));
+                            P<int>(c->final_idx), img, work_counters(c, S_RFWD));
     }
     // the previous call's stage times (it has completed: the event above
     // follows it), read once this call's kernels are queued
@@ -701,7 +702,7 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
     launch_raster_bwd(c->stream, p, c->max_items, P<Meta>(c->meta_d), items(c),
                       P<int>(c->tile_bins), packed(c),
                       P<float>(c->final_T), P<int>(c->final_idx), chunks(c),
-                      P<float>(c->v_rendered), P<float>(c->gacc), work_counters(c));
+                      P<float>(c->v_rendered), P<float>(c->gacc), work_counters(c, S_RBWD));
     AdamHP hp;
     for (int g = 0; g < 6; ++g) { hp.step[g] = a->adam_step_sizes[g]; hp.inv_bc2[g] = 1.0f / a->adam_bc2_sqrts[g]; }
     hp.b1 = a->adam_beta1;

@@ -154,6 +154,7 @@ __device__ __forceinline__ float wave_sum8_lds(const float* v, int lane, float* 
 // each wave walks the entries of its quadrant in order.  live: the lanes
 // whose pixel still composites (wave-uniform mask).  Every thread of the
 // workgroup calls this with the same range (it holds workgroup barriers).
+template <bool COUNT>
 __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float fx, float fy,
                                           int tx0, int ty0, const Entries& pk, float4* s_geo,
                                           float4* s_col, float4* s_aux, float& T, float& C0,
@@ -180,7 +181,7 @@ __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float f
         for (int ch = 0; ch < nb; ch += 64) {
             const int q = ch + lane;
             uint64_t m = wave_ballot(q < nb && ((__float_as_int(s_aux[q].y) >> w) & 1));
-            nwit += __popcll(m);
+            if (COUNT) nwit += __popcll(m);
             // the chunk's byte offset in a VGPR: each entry's offset is then
             // one vector shift-add from the bit index, shared by its LDS reads
             int chb = ch * (int)sizeof(float4);
@@ -213,7 +214,7 @@ __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float f
                     C2 = fmaf(cb, vis, C2);
                     T = nT;
                     last = b + qq;
-                    ++ncl;
+                    if (COUNT) ++ncl;
                 }
                 if (sm) {      // at most once per pixel
                     if (lane_of(sm)) last = b + qq - 1;
@@ -225,8 +226,9 @@ __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float f
     }
 }
 
+template <bool COUNT>
 __device__ __forceinline__ void add_work(unsigned long long* work, unsigned ncl, unsigned nwit) {
-    if (!work) return;
+    if (!COUNT || !work) return;
     unsigned long long* ws = work_slot(work);
     unsigned ncomp = ncl;
     for (int off = 32; off >= 1; off >>= 1) ncomp += __shfl_xor(ncomp, off, 64);
@@ -237,6 +239,7 @@ __device__ __forceinline__ void add_work(unsigned long long* work, unsigned ncl,
 
 // One work item of the training forward: its chunk's state (chunked tile)
 // or the tile's final pixels (tile in one piece).
+template <bool COUNT>
 __device__ __forceinline__ void fwd_item(int item, int W, int H, int tbx, float bg0, float bg1,
                                          float bg2, const Items& it, const int* tile_bins,
                                          const Entries& pk, float* final_T, int* final_idx,
@@ -256,9 +259,9 @@ __device__ __forceinline__ void fwd_item(int item, int W, int H, int tbx, float 
     int last = cs - 1;
     unsigned ncl = 0;       // pairs composited by this lane
     unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
-    fwd_range(cs, ce, wave_ballot(px.inside), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, T, C0, C1,
+    fwd_range<COUNT>(cs, ce, wave_ballot(px.inside), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, T, C0, C1,
               C2, last, ncl, nwit);
-    add_work(work, ncl, nwit);
+    add_work<COUNT>(work, ncl, nwit);
     if (!px.inside) return;
     if (K == 1) {
         const size_t pix = (size_t)px.i * W + px.j;
@@ -278,6 +281,7 @@ __device__ __forceinline__ void fwd_item(int item, int W, int H, int tbx, float 
 }
 
 // Chunks 0 .. kmax - 1 of every tile, one item per workgroup.
+template <bool COUNT>
 __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float bg0, float bg1,
                                                     float bg2, const Meta* __restrict__ meta,
                                                     Items it,
@@ -294,12 +298,13 @@ __global__ __launch_bounds__(256) void k_raster_fwd(int W, int H, int tbx, float
     if ((int)blockIdx.x >= meta->n_items) return;
     const int item = it.order[blockIdx.x];
     if (it.k[item] >= kmax) return;
-    fwd_item(item, W, H, tbx, bg0, bg1, bg2, it, tile_bins, pk, final_T, final_idx, out_img, cb,
+    fwd_item<COUNT>(item, W, H, tbx, bg0, bg1, bg2, it, tile_bins, pk, final_T, final_idx, out_img, cb,
              work, s_geo, s_col, s_aux);
 }
 
 // Chunks kmin and later of the tiles not marked done, the workgroups striding
 // over the items (few items qualify, so a small grid visits them all).
+template <bool COUNT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k_raster_fwd_tail(int W, int H, int tbx,
                                                          const Meta* __restrict__ meta, Items it,
                                                          const int* __restrict__ tile_bins,
@@ -313,7 +318,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
     for (int item = blockIdx.x; item < n; item += gridDim.x) {
         if (it.k[item] < kmin || done[it.tile[item]]) continue;
         // chunked tiles only (k >= kmin > 0): no final pixels are written
-        fwd_item(item, W, H, tbx, 0.f, 0.f, 0.f, it, tile_bins, pk, nullptr, nullptr, nullptr, cb,
+        fwd_item<COUNT>(item, W, H, tbx, 0.f, 0.f, 0.f, it, tile_bins, pk, nullptr, nullptr, nullptr, cb,
                  work, s_geo, s_col, s_aux);
     }
 }
@@ -330,6 +335,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
 // results are those of the chunk items plus the merge, bit for bit.
 // At most 64 VGPRs (8 waves per SIMD; 71 unbounded, 7 waves): 1.5% more
 // render FPS at config 3.
+template <bool COUNT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k_render_tiles(int W, int H, int tbx, float bg0,
                                                       float bg1, float bg2, Items it,
                                                       const int* __restrict__ tile_bins,
@@ -352,7 +358,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
     int li;
     if (K == 1) {
         li = s - 1;
-        fwd_range(s, e, wave_ballot(px.inside), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, Tr, R0,
+        fwd_range<COUNT>(s, e, wave_ballot(px.inside), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, Tr, R0,
                   R1, R2, li, ncl, nwit);
     } else {
         li = -1;
@@ -362,7 +368,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
             const int cs = s + k * CHUNK, ce = min(cs + CHUNK, e);
             float T = 1.f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
             int last = cs - 1;
-            fwd_range(cs, ce, wave_ballot(!done), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, T,
+            fwd_range<COUNT>(cs, ce, wave_ballot(!done), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, T,
                       C0, C1, C2, last, ncl, nwit);
             if (!done) {
                 R0 = fmaf(C0, Tr, R0);
@@ -374,7 +380,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
             }
         }
     }
-    add_work(work, ncl, nwit);
+    add_work<COUNT>(work, ncl, nwit);
     if (!px.inside) return;
     const size_t pix = (size_t)px.i * W + px.j;
     final_T[pix] = Tr;
@@ -784,15 +790,25 @@ void launch_raster_fwd(hipStream_t s, const CamParams& p, int64_t max_items, con
     if (max_items <= 0) return;
     // chunks 0 .. FWD_P - 1 of every tile, then the tiles' later chunks that
     // k_chunk_done does not mark as past an all-zero running transmittance
-    hipLaunchKernelGGL(k_raster_fwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
-                       p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx,
-                       out_img, cb, work, FWD_P);
+    // the counting variants only when pair counters are asked for
+    if (work)
+        hipLaunchKernelGGL(k_raster_fwd<true>, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H,
+                           p.tbx, p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T,
+                           final_idx, out_img, cb, work, FWD_P);
+    else
+        hipLaunchKernelGGL(k_raster_fwd<false>, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H,
+                           p.tbx, p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T,
+                           final_idx, out_img, cb, work, FWD_P);
     const int T = p.tbx * p.tby;
     hipLaunchKernelGGL(k_chunk_done, dim3((unsigned)std::min(T, 256)), dim3(256), 0, s, p.W, p.H,
                        p.tbx, meta, chunked, it, cb, done);
-    hipLaunchKernelGGL(k_raster_fwd_tail, dim3((unsigned)std::min<int64_t>(max_items, 1024)),
-                       dim3(256), 0, s, p.W, p.H, p.tbx, meta, it, tile_bins, pk, cb, work, FWD_P,
-                       (const int*)done);
+    const dim3 tg((unsigned)std::min<int64_t>(max_items, 1024));
+    if (work)
+        hipLaunchKernelGGL(k_raster_fwd_tail<true>, tg, dim3(256), 0, s, p.W, p.H, p.tbx, meta, it,
+                           tile_bins, pk, cb, work, FWD_P, (const int*)done);
+    else
+        hipLaunchKernelGGL(k_raster_fwd_tail<false>, tg, dim3(256), 0, s, p.W, p.H, p.tbx, meta, it,
+                           tile_bins, pk, cb, work, FWD_P, (const int*)done);
 }
 
 void launch_render_tiles(hipStream_t s, const CamParams& p, Items it, const int* tile_bins,
@@ -800,9 +816,14 @@ void launch_render_tiles(hipStream_t s, const CamParams& p, Items it, const int*
                          unsigned long long* work) {
     const int T = p.tbx * p.tby;
     if (T <= 0) return;
-    hipLaunchKernelGGL(k_render_tiles, dim3((unsigned)T), dim3(256), 0, s, p.W, p.H, p.tbx,
-                       p.bg[0], p.bg[1], p.bg[2], it, tile_bins, pk, final_T, final_idx, out_img,
-                       work);
+    if (work)
+        hipLaunchKernelGGL(k_render_tiles<true>, dim3((unsigned)T), dim3(256), 0, s, p.W, p.H, p.tbx,
+                           p.bg[0], p.bg[1], p.bg[2], it, tile_bins, pk, final_T, final_idx, out_img,
+                           work);
+    else
+        hipLaunchKernelGGL(k_render_tiles<false>, dim3((unsigned)T), dim3(256), 0, s, p.W, p.H, p.tbx,
+                           p.bg[0], p.bg[1], p.bg[2], it, tile_bins, pk, final_T, final_idx, out_img,
+                           work);
 }
 
 void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
