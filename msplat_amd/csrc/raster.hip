@@ -178,6 +178,9 @@ __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float f
         s_aux[tid] = make_float4(fmaxf(bl_raw + 0.5f, 0.f), __int_as_float(mask), 0.f, 0.f);
         __syncthreads();
         const int nb = min(256, ce - b);
+        // this batch's last contributor as the entry's LDS byte offset (a
+        // vector register copy per step), turned into the index at the end
+        int lqb = INT_MIN;
         for (int ch = 0; ch < nb; ch += 64) {
             const int q = ch + lane;
             uint64_t m = wave_ballot(q < nb && ((__float_as_int(s_aux[q].y) >> w) & 1));
@@ -187,9 +190,7 @@ __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float f
             int chb = ch * (int)sizeof(float4);
             asm volatile("" : "+v"(chb));
             while (m) {
-                const int bit = pop_low_bit(m);
-                const int qq = ch + bit;
-                const int qb = chb + bit * (int)sizeof(float4);
+                const int qb = chb + pop_low_bit(m) * (int)sizeof(float4);
                 const float4 g = lds_f4(s_geo, qb);
                 const float4 c = lds_f4(s_col, qb);
                 const float cb = lds_f4(s_aux, qb).x;
@@ -213,16 +214,17 @@ __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float f
                     C1 = fmaf(c.w, vis, C1);
                     C2 = fmaf(cb, vis, C2);
                     T = nT;
-                    last = b + qq;
+                    lqb = qb;
                     if (COUNT) ++ncl;
                 }
-                if (sm) {      // at most once per pixel
-                    if (lane_of(sm)) last = b + qq - 1;
+                if (sm) {      // at most once per pixel: the entry before this one
+                    if (lane_of(sm)) lqb = qb - (int)sizeof(float4);
                     live &= ~sm;
                 }
             }
             if (live == 0) break;
         }
+        if (lqb != INT_MIN) last = b + (lqb >> 4);   // sizeof(float4) = 16; -16 gives b - 1
     }
 }
 
