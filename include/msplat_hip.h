@@ -256,9 +256,11 @@ int msplat_hip_drain_call_times(double* ms, int max_calls, int* n_calls);
  * counts[0] (pixel, entry) pairs composited by the forward, counts[1] pairs
  * that carry a gradient in the backward, and counts[2] / counts[3] the
  * entries evaluated per 64-pixel wave in the forward / backward (each one
- * wave-wide step), summed over the timed calls.  drain returns them (zeros
- * when timing is off) and restarts the sums.  Part of the profiler interface
- * above; the reference has no counterpart. */
+ * wave-wide step), summed over the timed calls.  The forward counts only
+ * while its stage (rast_fwd) is in the stage mask and the backward only
+ * while rast_bwd is (other calls run kernels without the counting).  drain
+ * returns them (zeros when timing is off) and restarts the sums.  Part of
+ * the profiler interface above; the reference has no counterpart. */
 int msplat_hip_drain_raster_counters(int64_t counts[4]);
 
 /* Copy a named intermediate of the last render / train step to host memory.
