@@ -566,7 +566,10 @@ int msplat_hip_init(int device) {
     }
     c->stream = c->own;
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->meta_h), sizeof(Meta)));
-    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->loss_h), 16));
+    // coherent: the host reads the previous step's loss without a stream
+    // sync once a later kernel has published the totals word (isect_h)
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->loss_h), 16,
+                          hipHostMallocMapped | hipHostMallocCoherent));
     HIP_TRY(hipHostGetDevicePointer(reinterpret_cast<void**>(&c->loss_hd), c->loss_h, 0));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->count_h), 16));
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->isect_h), 16,

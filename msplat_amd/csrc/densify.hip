@@ -226,7 +226,9 @@ __global__ __launch_bounds__(256) void k_copy_back_rows(Packed18 P, int cnt,
     if (4 * i + 4 <= nf && P.vec[k]) {
         reinterpret_cast<float4*>(d)[i] = reinterpret_cast<const float4*>(s)[i];
     } else {
-        for (int64_t e = 4 * i; e < nf; ++e) d[e] = s[e];
+        // this thread's own four elements only (fewer at the buffer's end)
+        const int64_t e_end = 4 * i + 4 < nf ? 4 * i + 4 : nf;
+        for (int64_t e = 4 * i; e < e_end; ++e) d[e] = s[e];
     }
 }
 

@@ -244,7 +244,10 @@ __global__ __launch_bounds__(LF_T) void k_loss_final(int nparts, const float* __
     }
     if (threadIdx.x == 0) {
         const double w = w_ssim;
-        out[0] = (float)(w * s[2][0] - (w / 3.0) * s[0][0] + ((1.0 - w) / 3.0) * s[1][0]);
+        // out may be coherent host memory that the host reads without a
+        // stream sync: a system-scope store makes the value visible there
+        __hip_atomic_store(out, (float)(w * s[2][0] - (w / 3.0) * s[0][0] + ((1.0 - w) / 3.0) * s[1][0]),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 

@@ -5,13 +5,18 @@
 // channel becomes byte / 255 in fp32.  This file decodes PNG files with
 // zlib (the only image library whose headers this platform ships) into the
 // same float RGB: non-interlaced PNGs of every colour type (grey, RGB,
-// palette, grey + alpha, RGBA) at bit depths 1-16.  Alpha is dropped; 16-bit
-// samples keep their high byte; sub-byte grey levels are scaled to 0..255 as
-// the PNG specification's sample depth scaling prescribes (v * 255 / (2^d - 1)).
+// palette, grey + alpha, RGBA) at bit depths 1-16.  16-bit samples keep their
+// high byte; sub-byte grey levels are scaled to 0..255 as the PNG
+// specification's sample depth scaling prescribes (v * 255 / (2^d - 1)).
+// Transparency: the reference draws the image into a zero-filled context
+// without alpha (kCGImageAlphaNoneSkipLast), i.e. source-over black, so a
+// sample with alpha a (from the alpha channel or a tRNS chunk) becomes
+// round(c * a / 255), and fully transparent pixels are black.
 #include "png_decode.hpp"
 
 #include <zlib.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -62,7 +67,7 @@ DecodedImage decode_png(const std::string& path) {
         throw std::runtime_error(path + ": not a PNG file");
     uint32_t W = 0, H = 0;
     int depth = 0, ctype = -1, interlace = 0;
-    std::vector<uint8_t> palette, idat;
+    std::vector<uint8_t> palette, trns, idat;
     size_t pos = 8;
     bool seen_end = false;
     while (pos + 12 <= file.size()) {
@@ -79,6 +84,8 @@ DecodedImage decode_png(const std::string& path) {
             interlace = data[12];
         } else if (std::memcmp(type, "PLTE", 4) == 0) {
             palette.assign(data, data + len);
+        } else if (std::memcmp(type, "tRNS", 4) == 0) {
+            trns.assign(data, data + len);
         } else if (std::memcmp(type, "IDAT", 4) == 0) {
             idat.insert(idat.end(), data, data + len);
         } else if (std::memcmp(type, "IEND", 4) == 0) {
@@ -108,16 +115,35 @@ DecodedImage decode_png(const std::string& path) {
     const size_t stride = (W * bits_per_px + 7) / 8;   // bytes per scanline (no filter byte)
     const size_t bpp = std::max<size_t>(1, bits_per_px / 8);
     std::vector<uint8_t> raw((stride + 1) * H);
+    // zlib counts bytes in 32-bit fields: inflate in pieces of at most
+    // UINT_MAX bytes of input and output (16-bit RGBA images reach 8 GiB)
     z_stream zs{};
     if (inflateInit(&zs) != Z_OK) throw std::runtime_error("zlib init failed");
+    const size_t kPiece = 0xFFFFFFFFu;
+    size_t in_left = idat.size(), out_left = raw.size();
     zs.next_in = idat.data();
-    zs.avail_in = (uInt)idat.size();
     zs.next_out = raw.data();
-    zs.avail_out = (uInt)raw.size();
-    const int zr = inflate(&zs, Z_FINISH);
-    const size_t produced = raw.size() - zs.avail_out;
+    int zr = Z_OK;
+    while (zr == Z_OK) {
+        if (zs.avail_in == 0 && in_left > 0) {
+            zs.avail_in = (uInt)std::min(in_left, kPiece);
+            in_left -= zs.avail_in;
+        }
+        if (zs.avail_out == 0 && out_left > 0) {
+            zs.avail_out = (uInt)std::min(out_left, kPiece);
+            out_left -= zs.avail_out;
+        }
+        const uInt before_in = zs.avail_in, before_out = zs.avail_out;
+        zr = inflate(&zs, in_left == 0 ? Z_FINISH : Z_NO_FLUSH);
+        if (zr == Z_BUF_ERROR && (zs.avail_in != before_in || zs.avail_out != before_out)) zr = Z_OK;
+        if (zr == Z_OK && zs.avail_out == 0 && out_left == 0) break;   // image data complete
+        if (zr == Z_OK && zs.avail_in == 0 && in_left == 0 && zs.avail_out != 0) {
+            zr = Z_DATA_ERROR;   // stream ended early
+        }
+    }
+    const size_t produced = raw.size() - out_left - zs.avail_out;
     inflateEnd(&zs);
-    if ((zr != Z_STREAM_END && zr != Z_BUF_ERROR) || produced != raw.size())
+    if ((zr != Z_STREAM_END && zr != Z_OK) || produced != raw.size())
         throw std::runtime_error(path + ": corrupt PNG image data");
     // Undo the per-scanline filters in place.
     std::vector<uint8_t> prev(stride, 0);
@@ -140,6 +166,15 @@ DecodedImage decode_png(const std::string& path) {
         }
         std::memcpy(prev.data(), cur, stride);
     }
+    // tRNS (PNG spec 11.3.2.1): palette alphas (entries past the chunk are
+    // opaque), or one grey / RGB sample value, at the image's bit depth, that
+    // marks fully transparent pixels
+    const bool key_grey = ctype == 0 && trns.size() >= 2;
+    const bool key_rgb = ctype == 2 && trns.size() >= 6;
+    const uint32_t kg = key_grey ? ((uint32_t)trns[0] << 8 | trns[1]) : 0;
+    const uint32_t kr = key_rgb ? ((uint32_t)trns[0] << 8 | trns[1]) : 0;
+    const uint32_t kgn = key_rgb ? ((uint32_t)trns[2] << 8 | trns[3]) : 0;
+    const uint32_t kb = key_rgb ? ((uint32_t)trns[4] << 8 | trns[5]) : 0;
     DecodedImage img;
     img.width = (int)W;
     img.height = (int)H;
@@ -149,29 +184,43 @@ DecodedImage decode_png(const std::string& path) {
         const uint8_t* cur = &raw[(size_t)y * (stride + 1) + 1];
         for (uint32_t x = 0; x < W; ++x) {
             uint8_t px[3];
+            int alpha = 255;
             if (depth < 8) {   // grey or palette, packed from the high bits
                 const size_t bit = (size_t)x * depth;
                 const int v = (cur[bit / 8] >> (8 - depth - (int)(bit % 8))) & maxv;
                 if (ctype == 3) {
                     if ((size_t)v * 3 + 2 >= palette.size()) throw std::runtime_error(path + ": palette index out of range");
                     for (int c = 0; c < 3; ++c) px[c] = palette[(size_t)v * 3 + c];
+                    if ((size_t)v < trns.size()) alpha = trns[v];
                 } else {
                     px[0] = px[1] = px[2] = (uint8_t)(v * 255 / maxv);
+                    if (key_grey && (uint32_t)v == kg) alpha = 0;
                 }
             } else {
                 const size_t step = (size_t)channels * (depth / 8);
                 const uint8_t* s = cur + (size_t)x * step;   // high byte first (16-bit)
                 const size_t hb = depth / 8;
+                // a whole sample at the image's depth (for the tRNS key)
+                auto sample = [&](int c) -> uint32_t {
+                    return hb == 2 ? ((uint32_t)s[2 * c] << 8 | s[2 * c + 1]) : s[c];
+                };
                 if (ctype == 3) {
                     const size_t v = s[0];
                     if (v * 3 + 2 >= palette.size()) throw std::runtime_error(path + ": palette index out of range");
                     for (int c = 0; c < 3; ++c) px[c] = palette[v * 3 + c];
+                    if (v < trns.size()) alpha = trns[v];
                 } else if (channels <= 2) {
                     px[0] = px[1] = px[2] = s[0];
+                    if (channels == 2) alpha = s[hb];
+                    else if (key_grey && sample(0) == kg) alpha = 0;
                 } else {
                     for (int c = 0; c < 3; ++c) px[c] = s[c * hb];
+                    if (channels == 4) alpha = s[3 * hb];
+                    else if (key_rgb && sample(0) == kr && sample(1) == kgn && sample(2) == kb) alpha = 0;
                 }
             }
+            if (alpha != 255)   // source-over black, rounded to the nearest level
+                for (int c = 0; c < 3; ++c) px[c] = (uint8_t)((px[c] * alpha + 127) / 255);
             float* o = &img.rgb[((size_t)y * W + x) * 3];
             for (int c = 0; c < 3; ++c) o[c] = px[c] / 255.0f;
         }

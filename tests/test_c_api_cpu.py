@@ -121,22 +121,40 @@ def _read(lib, path):
         ctypes.CDLL(None).free(ctypes.cast(rgb, ctypes.c_void_p))
 
 
-@pytest.mark.parametrize("mode", ["RGB", "RGBA", "L", "LA", "P", "1"])
+@pytest.mark.parametrize("mode", ["RGB", "RGBA", "L", "LA", "P", "1", "P+tRNS", "L+tRNS", "RGB+tRNS"])
 def test_png_decoder_matches_pillow(mode, tmp_path):
+    """Opaque images decode to Pillow's RGB bit for bit.  Transparent ones
+    (alpha channel or tRNS chunk) become the image drawn source-over black,
+    as the reference's CoreGraphics context without alpha draws it
+    (image_io.cpp:33-41): round(c * a / 255) of Pillow's RGBA samples."""
     Image = pytest.importorskip("PIL.Image")
     lib = _lib()
     rng = np.random.default_rng(31)
     h, w = 37, 53   # odd sizes: rows of sub-byte pixels end mid-byte
     rgb = rng.integers(0, 256, (h, w, 3), dtype=np.uint8)
+    base = mode.split("+")[0]
     im = Image.fromarray(rgb, "RGB")
-    im = im.convert(mode) if mode != "P" else im.quantize(colors=61)
+    im = im.convert(base) if base != "P" else im.quantize(colors=61)
+    save_kw = {}
     if mode in ("RGBA", "LA"):
         alpha = Image.fromarray(rng.integers(0, 256, (h, w), dtype=np.uint8), "L")
         im.putalpha(alpha)
+    elif mode == "P+tRNS":
+        save_kw["transparency"] = bytes(rng.integers(0, 256, 40, dtype=np.uint8))   # 21 entries stay opaque
+    elif mode == "L+tRNS":
+        save_kw["transparency"] = int(np.asarray(im)[3, 4])
+    elif mode == "RGB+tRNS":
+        save_kw["transparency"] = tuple(int(v) for v in np.asarray(im)[5, 6])
     path = tmp_path / f"img_{mode}.png"
-    im.save(path, format="PNG")
+    im.save(path, format="PNG", **save_kw)
     with Image.open(path) as f:
-        want = np.asarray(f.convert("RGB"), dtype=np.uint8).astype(np.float32) / np.float32(255.0)
+        if mode in ("RGB", "L", "P", "1"):
+            want8 = np.asarray(f.convert("RGB"), dtype=np.uint8)
+        else:
+            rgba = np.asarray(f.convert("RGBA"), dtype=np.uint32)
+            assert (rgba[..., 3] < 255).any(), "the fixture must hold transparent pixels"
+            want8 = ((rgba[..., :3] * rgba[..., 3:] + 127) // 255).astype(np.uint8)
+    want = want8.astype(np.float32) / np.float32(255.0)
     got, err = _read(lib, path)
     assert got is not None, err
     assert got.shape == want.shape

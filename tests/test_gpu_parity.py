@@ -259,17 +259,38 @@ def test_densify_stage_timing(dev):
 
 
 def test_train_three_steps(dev):
-    """Adam state carried over three steps (bias corrections t = 1, 2, 3)."""
-    _train_compare(dev, small_scene(n=2000, seed_off=83), steps=3, check_grads=False)
+    """Adam state carried over three steps (bias corrections t = 1, 2, 3):
+    each step checked in full from the GPU's state before it (forward bit
+    for bit, gradients and updates within their bounds)."""
+    _train_compare(dev, small_scene(n=2000, seed_off=83), steps=3)
 
 
-def test_densify_parity(dev):
-    """Identical statistics and random samples -> identical densify result (counts, order, values)."""
+def _misalign(t):
+    """A copy of device tensor t whose data starts 4 bytes past a 16-byte
+    boundary (one float into a larger allocation)."""
+    import torch
+    flat = torch.zeros(t.numel() + 1, dtype=t.dtype, device=t.device)
+    out = flat[1:].view(t.shape)
+    out.copy_(t)
+    assert out.data_ptr() % 16 == 4
+    return out
+
+
+@pytest.mark.parametrize("misaligned", [False, True], ids=["aligned", "misaligned"])
+def test_densify_parity(dev, misaligned):
+    """Identical statistics and random samples -> identical densify result
+    (counts, order, values).  The misaligned case puts every parameter and
+    moment buffer 4 bytes off a 16-byte boundary, which takes the scalar
+    copy-back path of the compaction instead of float4 stores."""
     torch = pytest.importorskip("torch")
     sc = small_scene(n=5000, seed_off=84)
     n = sc.n
     cap = 3 * n
     g = dev.DeviceGaussians.from_arrays(sc.params(), 3, capacity=cap)
+    if misaligned:
+        g.bufs = [_misalign(b) for b in g.bufs]
+        g.m = [_misalign(b) for b in g.m]
+        g.v = [_misalign(b) for b in g.v]
     st = synthetic.Stream(synthetic.BASE_SEED + 85)
     vis = np.floor(st.uniform(n) * 4).astype(np.float32)
     gnorm = (st.uniform(n) * 4e-3 * vis).astype(np.float32)
