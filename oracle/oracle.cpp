@@ -131,43 +131,92 @@ inline int f2i(float v) { return (int)std::fmin(std::fmax(v, -1073741824.f), 107
 inline float sigmoid(float o) { return 1.f / (1.f + oexp(-o)); }   // .metal:2133
 inline float clampf(float v, float lo, float hi) { return std::fmin(std::fmax(v, lo), hi); }
 
-struct F3 { float x, y, z; };
+// Running error analysis (Wilkinson; Higham, "Accuracy and Stability of
+// Numerical Algorithms", 2nd ed., section 3.3).  An RE carries a value v and
+// a first-order bound e on the absolute error of a float computation of v,
+// in units of u = 2^-24.  Every operation adds its own rounding (|result|)
+// to the errors its operands carry, scaled by the partial derivatives:
+//   e(a +- b) = e(a) + e(b) + |a +- b|
+//   e(a * b)  = e(a) |b| + |a| e(b) + |a b|
+//   e(a / b)  = (e(a) + |a / b| e(b)) / |b| + |a / b|
+//   e(sqrt a) = e(a) / (2 sqrt a) + sqrt a
+// The backward helpers below are templates over the scalar type: S = float
+// is the oracle itself (the same float operations as before), S = RE
+// evaluates the same expression graph for its error bound.
+constexpr double kU = 1.0 / 16777216.0;   // u = 2^-24, the fp32 unit roundoff
 
+struct RE {
+    double v = 0.0, e = 0.0;
+    RE() = default;
+    RE(float x) : v(x), e(0.0) {}          // exact operand
+    RE(double x, double err) : v(x), e(err) {}
+};
+inline RE operator+(RE a, RE b) { const double v = a.v + b.v; return RE(v, a.e + b.e + std::fabs(v)); }
+inline RE operator-(RE a, RE b) { const double v = a.v - b.v; return RE(v, a.e + b.e + std::fabs(v)); }
+inline RE operator-(RE a) { return RE(-a.v, a.e); }
+inline RE operator*(RE a, RE b) {
+    const double v = a.v * b.v;
+    return RE(v, a.e * std::fabs(b.v) + std::fabs(a.v) * b.e + std::fabs(v));
+}
+inline RE operator/(RE a, RE b) {
+    const double v = a.v / b.v;
+    return RE(v, (a.e + std::fabs(v) * b.e) / std::fabs(b.v) + std::fabs(v));
+}
+inline RE& operator+=(RE& a, RE b) { a = a + b; return a; }
+inline float msqrt(float x) { return std::sqrt(x); }
+inline RE msqrt(RE a) {
+    const double v = std::sqrt(a.v);
+    return RE(v, (v > 0.0 ? a.e / (2.0 * v) : 0.0) + v);
+}
+inline float mfmin(float a, float b) { return std::fmin(a, b); }
+inline float mfmax(float a, float b) { return std::fmax(a, b); }
+inline RE mfmin(RE a, RE b) { return RE(std::fmin(a.v, b.v), std::fmax(a.e, b.e)); }
+inline RE mfmax(RE a, RE b) { return RE(std::fmax(a.v, b.v), std::fmax(a.e, b.e)); }
+
+template <class S> struct V3 { S x, y, z; };
 // Column-major 3x3 (m[col][row]) like Metal's float3x3.
-struct M3 { float m[3][3]; };
+template <class S> struct Mat3 { S m[3][3]; };
+using F3 = V3<float>;
+using M3 = Mat3<float>;
 
-inline F3 mat_vec(const M3& A, F3 v) {   // A * v = A[0]*v.x + A[1]*v.y + A[2]*v.z
-    F3 r;
+template <class S>
+inline V3<S> mat_vec(const Mat3<S>& A, V3<S> v) {   // A * v = A[0]*v.x + A[1]*v.y + A[2]*v.z
+    V3<S> r;
     r.x = A.m[0][0] * v.x + A.m[1][0] * v.y + A.m[2][0] * v.z;
     r.y = A.m[0][1] * v.x + A.m[1][1] * v.y + A.m[2][1] * v.z;
     r.z = A.m[0][2] * v.x + A.m[1][2] * v.y + A.m[2][2] * v.z;
     return r;
 }
-inline M3 mat_mul(const M3& A, const M3& B) {
-    M3 C;
+template <class S>
+inline Mat3<S> mat_mul(const Mat3<S>& A, const Mat3<S>& B) {
+    Mat3<S> C;
     for (int j = 0; j < 3; ++j) {
-        F3 col = mat_vec(A, F3{B.m[j][0], B.m[j][1], B.m[j][2]});
+        V3<S> col = mat_vec(A, V3<S>{B.m[j][0], B.m[j][1], B.m[j][2]});
         C.m[j][0] = col.x; C.m[j][1] = col.y; C.m[j][2] = col.z;
     }
     return C;
 }
-inline M3 transpose(const M3& A) {
-    M3 T;
+template <class S>
+inline Mat3<S> transpose(const Mat3<S>& A) {
+    Mat3<S> T;
     for (int i = 0; i < 3; ++i) for (int j = 0; j < 3; ++j) T.m[i][j] = A.m[j][i];
     return T;
 }
-inline M3 mat_add(const M3& A, const M3& B) {
-    M3 C;
+template <class S>
+inline Mat3<S> mat_add(const Mat3<S>& A, const Mat3<S>& B) {
+    Mat3<S> C;
     for (int i = 0; i < 3; ++i) for (int j = 0; j < 3; ++j) C.m[i][j] = A.m[i][j] + B.m[i][j];
     return C;
 }
-inline float dot3(F3 a, F3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+template <class S>
+inline S dot3(V3<S> a, V3<S> b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
 
 // .metal:111-131.  quat stored (w,x,y,z); 1/sqrt stands in for rsqrt.
-inline M3 quat_to_rotmat(const float* q) {
-    const float s = 1.f / std::sqrt(q[3] * q[3] + q[0] * q[0] + q[1] * q[1] + q[2] * q[2]);
-    const float w = q[0] * s, x = q[1] * s, y = q[2] * s, z = q[3] * s;
-    M3 R;
+template <class S>
+inline Mat3<S> quat_to_rotmat(const S* q) {
+    const S s = S(1.f) / msqrt(q[3] * q[3] + q[0] * q[0] + q[1] * q[1] + q[2] * q[2]);
+    const S w = q[0] * s, x = q[1] * s, y = q[2] * s, z = q[3] * s;
+    Mat3<S> R;
     R.m[0][0] = 1.f - 2.f * (y * y + z * z);
     R.m[0][1] = 2.f * (x * y + w * z);
     R.m[0][2] = 2.f * (x * z - w * y);
@@ -181,10 +230,11 @@ inline M3 quat_to_rotmat(const float* q) {
 }
 
 // .metal:175-188: cov = (R S)(R S)^T, upper triangle.  M[j] = R[j] * s_j.
-inline void scale_rot_to_cov3d(const float* s3, float glob, const float* q, float* cov) {
-    const M3 R = quat_to_rotmat(q);
-    const float sv[3] = {glob * s3[0], glob * s3[1], glob * s3[2]};
-    M3 M;
+template <class S>
+inline void scale_rot_to_cov3d(const S* s3, float glob, const S* q, S* cov) {
+    const Mat3<S> R = quat_to_rotmat(q);
+    const S sv[3] = {glob * s3[0], glob * s3[1], glob * s3[2]};
+    Mat3<S> M;
     for (int j = 0; j < 3; ++j) for (int i = 0; i < 3; ++i) M.m[j][i] = R.m[j][i] * sv[j];
     auto t = [&](int i, int j) {   // tmp[j][i] = sum_k M[k][i] * M[k][j]
         return M.m[0][i] * M.m[0][j] + M.m[1][i] * M.m[1][j] + M.m[2][i] * M.m[2][j];
@@ -194,10 +244,11 @@ inline void scale_rot_to_cov3d(const float* s3, float glob, const float* q, floa
 }
 
 // .metal:90-108.
-inline F3 transform_4x3(const float* m, F3 p) {
-    return F3{m[0] * p.x + m[1] * p.y + m[2] * p.z + m[3],
-              m[4] * p.x + m[5] * p.y + m[6] * p.z + m[7],
-              m[8] * p.x + m[9] * p.y + m[10] * p.z + m[11]};
+template <class S>
+inline V3<S> transform_4x3(const float* m, V3<S> p) {
+    return V3<S>{m[0] * p.x + m[1] * p.y + m[2] * p.z + m[3],
+                 m[4] * p.x + m[5] * p.y + m[6] * p.z + m[7],
+                 m[8] * p.x + m[9] * p.y + m[10] * p.z + m[11]};
 }
 
 // .metal:241-281.
@@ -258,10 +309,11 @@ inline void tile_bbox(const float* xy, const float* ext, int tbx, int tby, int* 
 
 // SH basis values for bands 1..degree (.metal:602-652), written in the order
 // of the rest coefficients.  Returns the number of rest bases filled.
-inline int sh_rest_basis(int degree, F3 d, float* out) {
+template <class S>
+inline int sh_rest_basis(int degree, V3<S> d, S* out) {
     if (degree < 1) return 0;
-    const float x = d.x, y = d.y, z = d.z;
-    const float xx = x * x, xy = x * y, xz = x * z, yy = y * y, yz = y * z, zz = z * z;
+    const S x = d.x, y = d.y, z = d.z;
+    const S xx = x * x, xy = x * y, xz = x * z, yy = y * y, yz = y * z, zz = z * z;
     out[0] = -SH_C1 * y; out[1] = SH_C1 * z; out[2] = -SH_C1 * x;
     if (degree < 2) return 3;
     out[3] = SH_C2[0] * xy;
@@ -339,82 +391,86 @@ inline int tiles_y(const OrcCamera* c) { return (c->height + BLOCK - 1) / BLOCK;
 // ---------------- backward helpers ----------------
 
 // .metal:1216-1234: only the x/y rows through a fixed 1/w (the w row is dropped).
-inline F3 project_pix_vjp(const float* m, F3 p, int W, int H, const float* v_xy) {
-    const float hw = m[12] * p.x + m[13] * p.y + m[14] * p.z + m[15];
-    const float rw = 1.f / (hw + 1e-6f);
-    const float vnx = 0.5f * (float)W * v_xy[0], vny = 0.5f * (float)H * v_xy[1];
-    const float vpx = vnx * rw, vpy = vny * rw, vpz = 0.f;
-    return F3{m[0] * vpx + m[4] * vpy + m[8] * vpz,
-              m[1] * vpx + m[5] * vpy + m[9] * vpz,
-              m[2] * vpx + m[6] * vpy + m[10] * vpz};
+template <class S>
+inline V3<S> project_pix_vjp(const float* m, V3<S> p, int W, int H, const S* v_xy) {
+    const S hw = m[12] * p.x + m[13] * p.y + m[14] * p.z + m[15];
+    const S rw = S(1.f) / (hw + 1e-6f);
+    const S vnx = 0.5f * (float)W * v_xy[0], vny = 0.5f * (float)H * v_xy[1];
+    const S vpx = vnx * rw, vpy = vny * rw, vpz = 0.f;
+    return V3<S>{m[0] * vpx + m[4] * vpy + m[8] * vpz,
+                 m[1] * vpx + m[5] * vpy + m[9] * vpz,
+                 m[2] * vpx + m[6] * vpy + m[10] * vpz};
 }
 
 // .metal:1253-1264: v_Sigma = -X G X (2x2 symmetric), off-diagonal summed.
-inline void cov2d_to_conic_vjp(const float* conic, const float* v_conic, float* v_cov2d) {
-    const float X[2][2] = {{conic[0], conic[1]}, {conic[1], conic[2]}};   // [col][row]
-    const float G[2][2] = {{v_conic[0], v_conic[1]}, {v_conic[1], v_conic[2]}};
-    float nX[2][2];
+template <class S>
+inline void cov2d_to_conic_vjp(const S* conic, const S* v_conic, S* v_cov2d) {
+    const S X[2][2] = {{conic[0], conic[1]}, {conic[1], conic[2]}};   // [col][row]
+    const S G[2][2] = {{v_conic[0], v_conic[1]}, {v_conic[1], v_conic[2]}};
+    S nX[2][2];
     for (int i = 0; i < 2; ++i) for (int j = 0; j < 2; ++j) nX[i][j] = -1.f * X[i][j];
-    auto mul = [](const float A[2][2], const float B[2][2], float C[2][2]) {
+    auto mul = [](const S A[2][2], const S B[2][2], S C[2][2]) {
         for (int j = 0; j < 2; ++j)
             for (int i = 0; i < 2; ++i) C[j][i] = A[0][i] * B[j][0] + A[1][i] * B[j][1];
     };
-    float T1[2][2], S[2][2];
+    S T1[2][2], Sm[2][2];
     mul(nX, G, T1);
-    mul(T1, X, S);
-    v_cov2d[0] = S[0][0];
-    v_cov2d[1] = S[1][0] + S[0][1];
-    v_cov2d[2] = S[1][1];
+    mul(T1, X, Sm);
+    v_cov2d[0] = Sm[0][0];
+    v_cov2d[1] = Sm[1][0] + Sm[0][1];
+    v_cov2d[2] = Sm[1][1];
 }
 
 // .metal:1339-1407.
-inline void project_cov3d_ewa_vjp(const float* cov3d, const float* vm, float fx, float fy,
-                                  float tan_fovx, float tan_fovy, const float* v_cov2d,
-                                  F3& v_mean, float* v_cov3d, F3 pv) {
+template <class S>
+inline void project_cov3d_ewa_vjp(const S* cov3d, const float* vm, float fx, float fy,
+                                  float tan_fovx, float tan_fovy, const S* v_cov2d,
+                                  V3<S>& v_mean, S* v_cov3d, V3<S> pv) {
     const float lim_x = 1.3f * tan_fovx, lim_y = 1.3f * tan_fovy;
-    pv.x = pv.z * std::fmin(lim_x, std::fmax(-lim_x, pv.x / pv.z));
-    pv.y = pv.z * std::fmin(lim_y, std::fmax(-lim_y, pv.y / pv.z));
-    const float rz = 1.f / pv.z, rz2 = rz * rz;
-    M3 W;   // columns (vm0,vm4,vm8), (vm1,vm5,vm9), (vm2,vm6,vm10)
+    pv.x = pv.z * mfmin(S(lim_x), mfmax(S(-lim_x), pv.x / pv.z));
+    pv.y = pv.z * mfmin(S(lim_y), mfmax(S(-lim_y), pv.y / pv.z));
+    const S rz = S(1.f) / pv.z, rz2 = rz * rz;
+    Mat3<S> W;   // columns (vm0,vm4,vm8), (vm1,vm5,vm9), (vm2,vm6,vm10)
     W.m[0][0] = vm[0]; W.m[0][1] = vm[4]; W.m[0][2] = vm[8];
     W.m[1][0] = vm[1]; W.m[1][1] = vm[5]; W.m[1][2] = vm[9];
     W.m[2][0] = vm[2]; W.m[2][1] = vm[6]; W.m[2][2] = vm[10];
-    M3 J;
+    Mat3<S> J;
     J.m[0][0] = fx * rz; J.m[0][1] = 0.f; J.m[0][2] = 0.f;
     J.m[1][0] = 0.f; J.m[1][1] = fy * rz; J.m[1][2] = 0.f;
     J.m[2][0] = -fx * pv.x * rz2; J.m[2][1] = -fy * pv.y * rz2; J.m[2][2] = 0.f;
-    M3 V;
+    Mat3<S> V;
     V.m[0][0] = cov3d[0]; V.m[0][1] = cov3d[1]; V.m[0][2] = cov3d[2];
     V.m[1][0] = cov3d[1]; V.m[1][1] = cov3d[3]; V.m[1][2] = cov3d[4];
     V.m[2][0] = cov3d[2]; V.m[2][1] = cov3d[4]; V.m[2][2] = cov3d[5];
-    M3 vc;
+    Mat3<S> vc;
     vc.m[0][0] = v_cov2d[0]; vc.m[0][1] = 0.5f * v_cov2d[1]; vc.m[0][2] = 0.f;
     vc.m[1][0] = 0.5f * v_cov2d[1]; vc.m[1][1] = v_cov2d[2]; vc.m[1][2] = 0.f;
     vc.m[2][0] = 0.f; vc.m[2][1] = 0.f; vc.m[2][2] = 0.f;
-    const M3 T = mat_mul(J, W);
-    const M3 Tt = transpose(T), Vt = transpose(V);
-    const M3 vV = mat_mul(mat_mul(Tt, vc), T);
-    const M3 vT = mat_add(mat_mul(mat_mul(vc, T), Vt), mat_mul(mat_mul(transpose(vc), T), V));
+    const Mat3<S> T = mat_mul(J, W);
+    const Mat3<S> Tt = transpose(T), Vt = transpose(V);
+    const Mat3<S> vV = mat_mul(mat_mul(Tt, vc), T);
+    const Mat3<S> vT = mat_add(mat_mul(mat_mul(vc, T), Vt), mat_mul(mat_mul(transpose(vc), T), V));
     v_cov3d[0] = vV.m[0][0];
     v_cov3d[1] = vV.m[0][1] + vV.m[1][0];
     v_cov3d[2] = vV.m[0][2] + vV.m[2][0];
     v_cov3d[3] = vV.m[1][1];
     v_cov3d[4] = vV.m[1][2] + vV.m[2][1];
     v_cov3d[5] = vV.m[2][2];
-    const M3 vJ = mat_mul(vT, transpose(W));
-    const float fx_rz2 = fx * rz2, fy_rz2 = fy * rz2, rz3 = rz2 * rz;
-    const F3 vt{-fx_rz2 * vJ.m[2][0], -fy_rz2 * vJ.m[2][1],
-                -fx_rz2 * vJ.m[0][0] + 2.f * fx * pv.x * rz3 * vJ.m[2][0] -
-                    fy_rz2 * vJ.m[1][1] + 2.f * fy * pv.y * rz3 * vJ.m[2][1]};
-    v_mean.x += dot3(vt, F3{W.m[0][0], W.m[0][1], W.m[0][2]});
-    v_mean.y += dot3(vt, F3{W.m[1][0], W.m[1][1], W.m[1][2]});
-    v_mean.z += dot3(vt, F3{W.m[2][0], W.m[2][1], W.m[2][2]});
+    const Mat3<S> vJ = mat_mul(vT, transpose(W));
+    const S fx_rz2 = fx * rz2, fy_rz2 = fy * rz2, rz3 = rz2 * rz;
+    const V3<S> vt{-fx_rz2 * vJ.m[2][0], -fy_rz2 * vJ.m[2][1],
+                   -fx_rz2 * vJ.m[0][0] + 2.f * fx * pv.x * rz3 * vJ.m[2][0] -
+                       fy_rz2 * vJ.m[1][1] + 2.f * fy * pv.y * rz3 * vJ.m[2][1]};
+    v_mean.x += dot3(vt, V3<S>{W.m[0][0], W.m[0][1], W.m[0][2]});
+    v_mean.y += dot3(vt, V3<S>{W.m[1][0], W.m[1][1], W.m[1][2]});
+    v_mean.z += dot3(vt, V3<S>{W.m[2][0], W.m[2][1], W.m[2][2]});
 }
 
 // .metal:1409-1452 (derivative w.r.t. the normalised components).
-inline void quat_to_rotmat_vjp(const float* q, const M3& vR, float* out) {
-    const float s = 1.f / std::sqrt(q[3] * q[3] + q[0] * q[0] + q[1] * q[1] + q[2] * q[2]);
-    const float w = q[0] * s, x = q[1] * s, y = q[2] * s, z = q[3] * s;
+template <class S>
+inline void quat_to_rotmat_vjp(const S* q, const Mat3<S>& vR, S* out) {
+    const S s = S(1.f) / msqrt(q[3] * q[3] + q[0] * q[0] + q[1] * q[1] + q[2] * q[2]);
+    const S w = q[0] * s, x = q[1] * s, y = q[2] * s, z = q[3] * s;
     const auto& R = vR.m;
     out[0] = 2.f * (x * (R[1][2] - R[2][1]) + y * (R[2][0] - R[0][2]) + z * (R[0][1] - R[1][0]));
     out[1] = 2.f * (-2.f * x * (R[1][1] + R[2][2]) + y * (R[0][1] + R[1][0]) +
@@ -426,21 +482,22 @@ inline void quat_to_rotmat_vjp(const float* q, const M3& vR, float* out) {
 }
 
 // .metal:1498-1531.
-inline void scale_rot_to_cov3d_vjp(const float* s3, float glob, const float* q,
-                                   const float* v_cov3d, float* v_scale, float* v_quat) {
-    M3 vV;
+template <class S>
+inline void scale_rot_to_cov3d_vjp(const S* s3, float glob, const S* q,
+                                   const S* v_cov3d, S* v_scale, S* v_quat) {
+    Mat3<S> vV;
     vV.m[0][0] = v_cov3d[0]; vV.m[0][1] = 0.5f * v_cov3d[1]; vV.m[0][2] = 0.5f * v_cov3d[2];
     vV.m[1][0] = 0.5f * v_cov3d[1]; vV.m[1][1] = v_cov3d[3]; vV.m[1][2] = 0.5f * v_cov3d[4];
     vV.m[2][0] = 0.5f * v_cov3d[2]; vV.m[2][1] = 0.5f * v_cov3d[4]; vV.m[2][2] = v_cov3d[5];
-    const M3 R = quat_to_rotmat(q);
-    M3 S{};
-    S.m[0][0] = glob * s3[0]; S.m[1][1] = glob * s3[1]; S.m[2][2] = glob * s3[2];
-    const M3 M = mat_mul(R, S);
-    M3 vM = mat_mul(vV, M);
+    const Mat3<S> R = quat_to_rotmat(q);
+    Mat3<S> Sc{};
+    Sc.m[0][0] = glob * s3[0]; Sc.m[1][1] = glob * s3[1]; Sc.m[2][2] = glob * s3[2];
+    const Mat3<S> M = mat_mul(R, Sc);
+    Mat3<S> vM = mat_mul(vV, M);
     for (int i = 0; i < 3; ++i) for (int j = 0; j < 3; ++j) vM.m[i][j] = 2.f * vM.m[i][j];
     for (int i = 0; i < 3; ++i)
-        v_scale[i] = dot3(F3{R.m[i][0], R.m[i][1], R.m[i][2]}, F3{vM.m[i][0], vM.m[i][1], vM.m[i][2]});
-    const M3 vR = mat_mul(vM, S);
+        v_scale[i] = dot3(V3<S>{R.m[i][0], R.m[i][1], R.m[i][2]}, V3<S>{vM.m[i][0], vM.m[i][1], vM.m[i][2]});
+    const Mat3<S> vR = mat_mul(vM, Sc);
     quat_to_rotmat_vjp(q, vR, v_quat);
 }
 
@@ -494,13 +551,50 @@ inline float raster_pixel_fwd(const Entry* ent, int s, int e, float px, float py
     return T;
 }
 
+// Optional error-bound accumulators of the raster backward, per entry:
+// mag[i*9+q] = sum over the entry's pairs of the magnitude of gradient term q
+// (the term with every signed quantity replaced by the sum of the absolute
+// values it is formed from), err[i*9+q] = the same weighted by the term's
+// two-sided relative error bound in units of u (below), quad[i] = bit set of
+// the tile's 8x8 quadrants with at least one pair carrying a gradient.
+struct BwdBounds { float* mag; float* err; uint8_t* quad; };
+
 // Backward over entries [s, bin_final] for one pixel, back to front
 // (.metal:1015-1096 / 2963-3028).  Accumulates per-entry gradients into acc[i*9..].
+//
+// Error bounds (bb != NULL).  The GPU kernel evaluates the same pairs with
+// the same alpha (bit-identical forward) but its own arithmetic: the
+// transmittance is recovered with a hardware reciprocal (1 ulp) instead of a
+// division, the colour behind is carried as E = sum_k v_out_k B_k + sum_k
+// v_out_k T_final bg_k instead of per channel, and v_xy / v_conic come from
+// moments of v_sigma (sum v dx, sum v dy, ...) formed with the conic once per
+// gaussian.  At the d-th pair with a gradient of a pixel's walk (d = 1 at the
+// walk's first), first-order bounds on the relative difference of the two
+// evaluations, in units of u = 2^-24:
+//   T:     7 d   (1 - alpha rounded once, reciprocal 2 + division 1, product
+//                 1 + 1, accumulated over the walk from the exact T_final)
+//   fac = alpha T:             7 d + 2
+//   E, or v_out . B:           8 d + 6 relative to E_mag = sum_k |v_out_k|
+//                              (B_k + |T_final bg_k|), B_k >= 0
+//   v_alpha:                   8 d + 15 relative to
+//                              mva = T sum_k r_k |v_out_k| + ra E_mag
+//   v_sigma = -alpha v_alpha:  8 d + 17
+//   the nine terms:            <= 8 d + 24 relative to their magnitudes
+//                              (v_sigma mag alpha mva times |a dx| + |b dy|,
+//                              dx^2 / 2 ..., fac |v_out_k|, |1 - o|)
+// so err accumulates (8 d + 24) x magnitude; the per-gaussian summation of
+// the terms adds (n_w + 10) x the gaussian's total magnitude (done by the
+// caller): a tree of at most 10 levels inside a wave plus n_w float atomics,
+// one per 8x8 quadrant and entry with a gradient.
 inline void raster_pixel_bwd(const Entry* ent, int s, int bin_final, float px, float py,
                              float T, const float* buf0, float T_final, const float* bg,
-                             const float* v_out, double* acc, int acc_base, Counts* cnt) {
+                             const float* v_out, double* acc, int acc_base, Counts* cnt,
+                             const BwdBounds* bb = nullptr, int quad = 0) {
     float buffer[3] = {buf0[0], buf0[1], buf0[2]};
     const float Tfb[3] = {T_final * bg[0], T_final * bg[1], T_final * bg[2]};
+    const double tb_mag = std::fabs((double)Tfb[0] * v_out[0]) + std::fabs((double)Tfb[1] * v_out[1]) +
+                          std::fabs((double)Tfb[2] * v_out[2]);
+    int d = 0;
     for (int i = bin_final; i >= s; --i) {
         const Entry& en = ent[i];
         ++cnt->e;
@@ -530,6 +624,37 @@ inline void raster_pixel_bwd(const Entry* ent, int s, int bin_final, float px, f
             buffer[c] = std::fma(rgb, fac, buffer[c]);
         }
         const float v_sigma = -alpha * v_alpha;
+        if (bb) {
+            ++d;
+            // buffer[] already holds this pair's colour: the magnitude uses the
+            // colour behind it, as v_alpha does
+            double rv = 0.0, eb = tb_mag;
+            for (int c = 0; c < 3; ++c) {
+                const double rgb = std::fmax(rawc[c] + 0.5f, 0.f);
+                rv += rgb * std::fabs(v_out[c]);
+                eb += std::fabs(v_out[c]) * std::fmax(0.0, (double)buffer[c] - rgb * fac);
+            }
+            const double mva = (double)T * rv + (double)ra * eb;
+            const double vsm = (double)alpha * mva;
+            const double adx = std::fabs(dx), ady = std::fabs(dy);
+            double tm[9];
+            tm[0] = vsm * (std::fabs(en.a) * adx + std::fabs(en.b) * ady);
+            tm[1] = vsm * (std::fabs(en.b) * adx + std::fabs(en.c) * ady);
+            tm[2] = 0.5 * vsm * adx * adx;
+            tm[3] = 0.5 * vsm * adx * ady;
+            tm[4] = 0.5 * vsm * ady * ady;
+            for (int c = 0; c < 3; ++c)
+                tm[5 + c] = rawc[c] + 0.5f >= 0.f ? (double)fac * std::fabs(v_out[c]) : 0.0;
+            tm[8] = vsm * std::fabs(1.0 - (double)opac);
+            const double w = 8.0 * d + 24.0;
+            float* bm = bb->mag + (size_t)(i - acc_base) * 9;
+            float* be = bb->err + (size_t)(i - acc_base) * 9;
+            for (int q = 0; q < 9; ++q) {
+                bm[q] += (float)tm[q];
+                be[q] += (float)(w * tm[q]);
+            }
+            bb->quad[i - acc_base] |= (uint8_t)(1u << quad);
+        }
         double* a = acc + (size_t)(i - acc_base) * 9;
         // v_xy (2), v_conic (3), v_rgb (3), v_opacity (1)
         a[0] += v_sigma * std::fma(en.a, dx, en.b * dy);
@@ -711,11 +836,20 @@ int32_t orc_tile_chunks(int32_t n, int32_t num_tiles) {
     return 1;
 }
 
-void orc_rasterize(const OrcCamera* cam, int32_t N, const float* xys, const float* conics,
-                   const float* colors, const float* opacity_logits, const int32_t* tile_bins,
-                   const int32_t* gaussian_ids, float* final_Ts, int32_t* final_index,
-                   float* out_img, const float* v_out, float* v_xy, float* v_conic,
-                   float* v_rgb, float* v_opacity) {
+}  // extern "C"
+
+namespace {
+
+// orc_rasterize, plus (mag9 / err9 != NULL, backward only) the per-gaussian
+// magnitudes and error bounds of the nine raster gradients (BwdBounds):
+// mag9[g*9+q] = sum of the term magnitudes, err9[g*9+q] = the two-sided bound
+// on |GPU - oracle| in units of u = 2^-24, both in the order v_xy (2),
+// v_conic (3), v_rgb (3), v_opacity (1).
+void rasterize_impl(const OrcCamera* cam, int32_t N, const float* xys, const float* conics,
+                    const float* colors, const float* opacity_logits, const int32_t* tile_bins,
+                    const int32_t* gaussian_ids, float* final_Ts, int32_t* final_index,
+                    float* out_img, const float* v_out, float* v_xy, float* v_conic,
+                    float* v_rgb, float* v_opacity, double* mag9, double* err9) {
     const int W = cam->width, H = cam->height;
     const int tbx = tiles_x(cam), tby = tiles_y(cam), T = tbx * tby;
     const int64_t I = tile_bins[2 * (T - 1) + 1];
@@ -735,6 +869,17 @@ void orc_rasterize(const OrcCamera* cam, int32_t N, const float* xys, const floa
     }
     std::vector<double> acc;
     if (v_out) acc.assign((size_t)I * 9, 0.0);
+    std::vector<float> bmag, berr;
+    std::vector<uint8_t> bquad;
+    BwdBounds bbs{nullptr, nullptr, nullptr};
+    const BwdBounds* bb = nullptr;
+    if (v_out && mag9 && err9) {
+        bmag.assign((size_t)I * 9, 0.f);
+        berr.assign((size_t)I * 9, 0.f);
+        bquad.assign((size_t)I, 0);
+        bbs = BwdBounds{bmag.data(), berr.data(), bquad.data()};
+        bb = &bbs;
+    }
     int64_t fe = 0, fr = 0, fs = 0, be = 0, br = 0, bs = 0;
 
 #pragma omp parallel for schedule(dynamic, 4) reduction(+ : fe, fr, fs, be, br, bs)
@@ -782,10 +927,11 @@ void orc_rasterize(const OrcCamera* cam, int32_t N, const float* xys, const floa
 
                 if (!v_out) continue;
                 const float* vo = v_out + 3 * pix;
+                const int quad = ((ly >> 3) << 1) | (lx >> 3);   // the 8x8 quadrant (one GPU wave)
                 if (K == 1) {
                     const float zero[3] = {0.f, 0.f, 0.f};
                     raster_pixel_bwd(ent.data(), s, last, px, py, Tfin, zero, Tfin, bg, vo,
-                                     acc.data(), 0, &cbk);
+                                     acc.data(), 0, &cbk, bb, quad);
                 } else {
                     // compute_chunk_prefix_suffix_kernel (.metal:2820-2839)
                     float p = 1.f;
@@ -801,7 +947,8 @@ void orc_rasterize(const OrcCamera* cam, int32_t N, const float* xys, const floa
                         const int bf = cidx[k];
                         if (cs >= ce || bf < cs) continue;
                         raster_pixel_bwd(ent.data(), cs, std::min(bf, ce - 1), px, py,
-                                         pT[k] * cT[k], &aC[3 * k], Tfin, bg, vo, acc.data(), 0, &cbk);
+                                         pT[k] * cT[k], &aC[3 * k], Tfin, bg, vo, acc.data(), 0, &cbk,
+                                         bb, quad);
                     }
                 }
             }
@@ -825,6 +972,33 @@ void orc_rasterize(const OrcCamera* cam, int32_t N, const float* xys, const floa
         v_rgb[3 * g] = (float)a[5]; v_rgb[3 * g + 1] = (float)a[6]; v_rgb[3 * g + 2] = (float)a[7];
         v_opacity[g] = (float)a[8];
     }
+    if (!bb) return;
+    std::fill(mag9, mag9 + (size_t)N * 9, 0.0);
+    std::fill(err9, err9 + (size_t)N * 9, 0.0);
+    std::vector<int32_t> nw((size_t)N, 0);
+    for (int64_t i = 0; i < I; ++i) {
+        const int g = ent[i].id;
+        nw[g] += __builtin_popcount(bquad[i]);
+        for (int q = 0; q < 9; ++q) {
+            mag9[(size_t)g * 9 + q] += bmag[(size_t)i * 9 + q];
+            err9[(size_t)g * 9 + q] += berr[(size_t)i * 9 + q];
+        }
+    }
+    for (int32_t g = 0; g < N; ++g)
+        for (int q = 0; q < 9; ++q) err9[(size_t)g * 9 + q] += (nw[g] + 10.0) * mag9[(size_t)g * 9 + q];
+}
+
+}  // namespace
+
+extern "C" {
+
+void orc_rasterize(const OrcCamera* cam, int32_t N, const float* xys, const float* conics,
+                   const float* colors, const float* opacity_logits, const int32_t* tile_bins,
+                   const int32_t* gaussian_ids, float* final_Ts, int32_t* final_index,
+                   float* out_img, const float* v_out, float* v_xy, float* v_conic,
+                   float* v_rgb, float* v_opacity) {
+    rasterize_impl(cam, N, xys, conics, colors, opacity_logits, tile_bins, gaussian_ids, final_Ts,
+                   final_index, out_img, v_out, v_xy, v_conic, v_rgb, v_opacity, nullptr, nullptr);
 }
 
 double orc_ssim_loss(int32_t H, int32_t W, const float* img, const float* gt, float w_ssim,
@@ -950,13 +1124,108 @@ double orc_ssim_loss(int32_t H, int32_t W, const float* img, const float* gt, fl
     return total;
 }
 
+}  // extern "C"
+
+namespace {
+
+// One gaussian of the projection backward (.metal:1813-1910): mean, the
+// exponentiated scales es, quaternion, conic and the raster gradients in;
+// v_mean3d, v_scale (w.r.t. the log scale) and v_quat out.
+template <class S>
+inline void project_backward_one(const OrcCamera* cam, const S* mean, const S* es, const S* q,
+                                 const S* conic, const S* v_xy, const S* v_conic, S* v_mean3d,
+                                 S* v_scale, S* v_quat) {
+    const int W = cam->width, H = cam->height;
+    const float fx = cam->fx, fy = cam->fy;
+    const float tan_fovx = 0.5f * (float)W / fx, tan_fovy = 0.5f * (float)H / fy;
+    const V3<S> pw{mean[0], mean[1], mean[2]};
+    V3<S> vm = project_pix_vjp(cam->projmat, pw, W, H, v_xy);
+    const float v_z = 0.f;   // v_depth is zero-filled and never written (.mm:1168)
+    vm.x = vm.x + cam->viewmat[8] * v_z;
+    vm.y = vm.y + cam->viewmat[9] * v_z;
+    vm.z = vm.z + cam->viewmat[10] * v_z;
+    S v_cov2d[3];
+    cov2d_to_conic_vjp(conic, v_conic, v_cov2d);
+    S cov3d[6];
+    scale_rot_to_cov3d(es, cam->glob_scale, q, cov3d);
+    const V3<S> pv = transform_4x3(cam->viewmat, pw);
+    S v_cov3d[6];
+    project_cov3d_ewa_vjp(cov3d, cam->viewmat, fx, fy, tan_fovx, tan_fovy, v_cov2d, vm, v_cov3d, pv);
+    S vs[3], vq[4];
+    scale_rot_to_cov3d_vjp(es, cam->glob_scale, q, v_cov3d, vs, vq);
+    v_mean3d[0] = vm.x; v_mean3d[1] = vm.y; v_mean3d[2] = vm.z;
+    for (int k = 0; k < 3; ++k) v_scale[k] = vs[k] * es[k];
+    for (int k = 0; k < 4; ++k) v_quat[k] = vq[k];
+}
+
+// Error bounds of the projection backward of gaussian g, by running error
+// analysis of project_backward_one (RE).  The inputs (mean, scale, quat,
+// conic) are exact: the projection forward is bit-identical on both sides.
+// The raster gradients v_xy / v_conic come with magnitudes a_* (sums of
+// |contribution|) and two-sided error bounds e_* (in units of u).  Outputs,
+// per component of v_mean3d (3), v_scale (3), v_quat (4):
+//   a_out = propagation of a_in + the rounding of every operation once
+//           (first-order error of one float evaluation whose inputs err by a_in);
+//   e_out = propagation of e_in + 4 x the operations' own rounding: the
+//           oracle rounds each operation once (u), the GPU kernel up to 3 u
+//           (hardware reciprocal and square root of about 1 ulp = 2 u, and
+//           x * rcp(z) in place of x / z: 2 u + u).
+inline void project_backward_bounds(const OrcCamera* cam, const float* mean, const float* es_f,
+                                    const float* q_f, const float* conic_f, const float* vxy,
+                                    const float* vconic, const double* a_xy, const double* a_conic,
+                                    const double* e_xy, const double* e_conic, double* a_out,
+                                    double* e_out) {
+    RE m[3], es[3], q[4], cn[3];
+    for (int k = 0; k < 3; ++k) { m[k] = RE(mean[k]); es[k] = RE(es_f[k]); cn[k] = RE(conic_f[k]); }
+    for (int k = 0; k < 4; ++k) q[k] = RE(q_f[k]);
+    auto run = [&](const double* exy, const double* ecn, double* out) {
+        RE vx[2] = {RE((double)vxy[0], exy ? exy[0] : 0.0), RE((double)vxy[1], exy ? exy[1] : 0.0)};
+        RE vc[3];
+        for (int k = 0; k < 3; ++k) vc[k] = RE((double)vconic[k], ecn ? ecn[k] : 0.0);
+        RE om[3], os[3], oq[4];
+        project_backward_one(cam, m, es, q, cn, vx, vc, om, os, oq);
+        for (int k = 0; k < 3; ++k) { out[k] = om[k].e; out[3 + k] = os[k].e; }
+        for (int k = 0; k < 4; ++k) out[6 + k] = oq[k].e;
+    };
+    double ops[10], prop_a[10], prop_e[10];
+    run(nullptr, nullptr, ops);
+    run(a_xy, a_conic, prop_a);
+    run(e_xy, e_conic, prop_e);
+    for (int k = 0; k < 10; ++k) {
+        a_out[k] = prop_a[k];
+        e_out[k] = (prop_e[k] - ops[k]) + 4.0 * ops[k];
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+void orc_project_backward_err(const OrcCamera* cam, int32_t N, const float* means,
+                              const float* scales, const float* quats, const int32_t* radii,
+                              const float* conics, const float* v_xy, const float* v_conic,
+                              const float* err_xy, const float* err_conic, float* err_out) {
+#pragma omp parallel for schedule(static)
+    for (int32_t g = 0; g < N; ++g) {
+        float* o = err_out + (size_t)g * 10;
+        if (radii[g] <= 0) {
+            for (int k = 0; k < 10; ++k) o[k] = 0.f;
+            continue;
+        }
+        const float es[3] = {oexp(scales[3 * g]), oexp(scales[3 * g + 1]), oexp(scales[3 * g + 2])};
+        double ex[2] = {0.0, 0.0}, ec[3] = {0.0, 0.0, 0.0}, pa[10], pe[10];
+        for (int k = 0; k < 2; ++k) ex[k] = err_xy ? err_xy[2 * (size_t)g + k] / kU : 0.0;
+        for (int k = 0; k < 3; ++k) ec[k] = err_conic ? err_conic[3 * (size_t)g + k] / kU : 0.0;
+        project_backward_bounds(cam, means + 3 * g, es, quats + 4 * g, conics + 3 * g, v_xy + 2 * g,
+                                v_conic + 3 * g, ex, ec, ex, ec, pa, pe);
+        for (int k = 0; k < 10; ++k) o[k] = (float)(pe[k] * kU);
+    }
+}
+
 void orc_project_backward(const OrcCamera* cam, int32_t N, const float* means,
                           const float* scales, const float* quats, const int32_t* radii,
                           const float* conics, const float* v_xy, const float* v_conic,
                           float* v_mean3d, float* v_scale, float* v_quat) {
-    const int W = cam->width, H = cam->height;
-    const float fx = cam->fx, fy = cam->fy;
-    const float tan_fovx = 0.5f * (float)W / fx, tan_fovy = 0.5f * (float)H / fy;
 #pragma omp parallel for schedule(static)
     for (int32_t g = 0; g < N; ++g) {
         if (radii[g] <= 0) {
@@ -964,25 +1233,9 @@ void orc_project_backward(const OrcCamera* cam, int32_t N, const float* means,
             for (int k = 0; k < 4; ++k) v_quat[4 * g + k] = 0.f;
             continue;
         }
-        const F3 pw{means[3 * g], means[3 * g + 1], means[3 * g + 2]};
-        F3 vm = project_pix_vjp(cam->projmat, pw, W, H, v_xy + 2 * g);
-        const float v_z = 0.f;   // v_depth is zero-filled and never written (.mm:1168)
-        vm.x = vm.x + cam->viewmat[8] * v_z;
-        vm.y = vm.y + cam->viewmat[9] * v_z;
-        vm.z = vm.z + cam->viewmat[10] * v_z;
-        float v_cov2d[3];
-        cov2d_to_conic_vjp(conics + 3 * g, v_conic + 3 * g, v_cov2d);
         const float es[3] = {oexp(scales[3 * g]), oexp(scales[3 * g + 1]), oexp(scales[3 * g + 2])};
-        float cov3d[6];
-        scale_rot_to_cov3d(es, cam->glob_scale, quats + 4 * g, cov3d);
-        const F3 pv = transform_4x3(cam->viewmat, pw);
-        float v_cov3d[6];
-        project_cov3d_ewa_vjp(cov3d, cam->viewmat, fx, fy, tan_fovx, tan_fovy, v_cov2d, vm, v_cov3d, pv);
-        float vs[3], vq[4];
-        scale_rot_to_cov3d_vjp(es, cam->glob_scale, quats + 4 * g, v_cov3d, vs, vq);
-        v_mean3d[3 * g] = vm.x; v_mean3d[3 * g + 1] = vm.y; v_mean3d[3 * g + 2] = vm.z;
-        for (int k = 0; k < 3; ++k) v_scale[3 * g + k] = vs[k] * es[k];
-        for (int k = 0; k < 4; ++k) v_quat[4 * g + k] = vq[k];
+        project_backward_one(cam, means + 3 * g, es, quats + 4 * g, conics + 3 * g, v_xy + 2 * g,
+                             v_conic + 3 * g, v_mean3d + 3 * g, v_scale + 3 * g, v_quat + 4 * g);
     }
 }
 
@@ -1023,6 +1276,86 @@ void orc_grad_stats(int32_t N, const int32_t* radii, const float* v_xy, float* v
     }
 }
 
+}  // extern "C"
+
+namespace {
+
+// Gradients fed to Adam and their bounds (OrcTrainOut.grad / grad_mag /
+// grad_err), from the raster gradients' magnitudes and bounds (units of u):
+// means / scales / quats through the running error analysis of the
+// projection backward, opacity as the raster's, f_dc = SH_C0 v_rgb and
+// f_rest = basis_b(dir) v_rgb (the basis evaluated in RE from the exact view
+// direction; each product adds its own rounding, counted 3 x in the
+// two-sided bound).  The raster outputs: mag_raster = magnitudes, err_raster
+// = absolute bounds.  pb holds means [N,3], scales [N,3], quats [N,4] as the
+// step read them.
+void train_step_bounds(const OrcCamera* cam, int32_t N, int32_t rest_bases, const float* pb,
+                       const int32_t* radii, const float* conics, const float* v_xy,
+                       const float* v_conic, const float* v_rgb, const float* v_op,
+                       const float* v_mean, const float* v_scale, const float* v_quat,
+                       const double* mag9, const double* err9, const OrcTrainOut* out) {
+    const float* means = pb;
+    const float* scales = pb + (size_t)N * 3;
+    const float* quats = pb + (size_t)N * 6;
+    const int rp = rest_bases * 3;
+    const int dtu = std::min(cam->degrees_to_use, 3);
+    const int64_t numel[6] = {3LL * N, 3LL * N, 4LL * N, 3LL * N, (int64_t)rp * N, (int64_t)N};
+    for (int gi = 0; gi < 6; ++gi) {
+        if (out->grad[gi]) std::fill(out->grad[gi], out->grad[gi] + numel[gi], 0.f);
+        if (out->grad_mag[gi]) std::fill(out->grad_mag[gi], out->grad_mag[gi] + numel[gi], 0.f);
+        if (out->grad_err[gi]) std::fill(out->grad_err[gi], out->grad_err[gi] + numel[gi], 0.f);
+    }
+    auto put = [&](int gi, size_t i, float g, double mag, double err_u) {
+        if (out->grad[gi]) out->grad[gi][i] = g;
+        if (out->grad_mag[gi]) out->grad_mag[gi][i] = (float)mag;
+        if (out->grad_err[gi]) out->grad_err[gi][i] = (float)(err_u * kU);
+    };
+#pragma omp parallel for schedule(static)
+    for (int32_t g = 0; g < N; ++g) {
+        const double* a = mag9 + (size_t)g * 9;
+        const double* e = err9 + (size_t)g * 9;
+        if (out->mag_raster)
+            for (int q = 0; q < 9; ++q) out->mag_raster[(size_t)g * 9 + q] = (float)a[q];
+        if (out->err_raster)
+            for (int q = 0; q < 9; ++q) out->err_raster[(size_t)g * 9 + q] = (float)(e[q] * kU);
+        // opacity: the raster's own (dense: every gaussian)
+        put(5, g, v_op[g], a[8], e[8]);
+        if (radii[g] <= 0) {   // zero gradients, exactly, on both sides
+            continue;
+        }
+        const float es[3] = {oexp(scales[3 * g]), oexp(scales[3 * g + 1]), oexp(scales[3 * g + 2])};
+        double pa[10], pe[10];
+        project_backward_bounds(cam, means + 3 * g, es, quats + 4 * g, conics + 3 * g, v_xy + 2 * g,
+                                v_conic + 3 * g, a, a + 2, e, e + 2, pa, pe);
+        for (int k = 0; k < 3; ++k) put(0, 3 * (size_t)g + k, v_mean[3 * g + k], pa[k], pe[k]);
+        for (int k = 0; k < 3; ++k) put(1, 3 * (size_t)g + k, v_scale[3 * g + k], pa[3 + k], pe[3 + k]);
+        for (int k = 0; k < 4; ++k) put(2, 4 * (size_t)g + k, v_quat[4 * g + k], pa[6 + k], pe[6 + k]);
+        for (int c = 0; c < 3; ++c) {
+            const float gr = SH_C0 * v_rgb[3 * g + c];
+            const double ag = std::fabs((double)gr);
+            put(3, 3 * (size_t)g + c, gr, SH_C0 * a[5 + c] + ag, SH_C0 * e[5 + c] + 3.0 * ag);
+        }
+        if (dtu < 1) continue;
+        const F3 dir = view_dir(means + 3 * g, cam->cam_pos);
+        float basis[24];
+        RE rb[24];
+        const int nb = std::min(sh_rest_basis(dtu, dir, basis), rest_bases);
+        sh_rest_basis(dtu, V3<RE>{RE(dir.x), RE(dir.y), RE(dir.z)}, rb);
+        for (int b = 0; b < nb; ++b)
+            for (int c = 0; c < 3; ++c) {
+                const float gr = basis[b] * v_rgb[3 * g + c];
+                const double ag = std::fabs((double)gr), vr = std::fabs((double)v_rgb[3 * g + c]);
+                const double bm = std::fabs(rb[b].v);
+                put(4, (size_t)rp * g + b * 3 + c, gr, bm * a[5 + c] + rb[b].e * vr + ag,
+                    bm * e[5 + c] + 3.0 * rb[b].e * vr + 3.0 * ag);
+            }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
 float orc_train_step(const OrcCamera* cam, int32_t N, int32_t rest_bases,
                      float* const params[6], float* const m[6], float* const v[6],
                      const OrcAdam* ad, const float* gt, float ssim_weight, float* vis,
@@ -1030,6 +1363,14 @@ float orc_train_step(const OrcCamera* cam, int32_t N, int32_t rest_bases,
     const int W = cam->width, H = cam->height, T = tiles_x(cam) * tiles_y(cam);
     const size_t P = (size_t)H * W;
     const int rp = rest_bases * 3;
+    // the bounds of the projection backward need the parameters it read
+    std::vector<float> params_before;
+    if (out && (out->mag_raster || out->err_raster || out->grad[0])) {
+        params_before.resize((size_t)N * 10);
+        std::memcpy(params_before.data(), params[0], (size_t)N * 12);
+        std::memcpy(params_before.data() + (size_t)N * 3, params[1], (size_t)N * 12);
+        std::memcpy(params_before.data() + (size_t)N * 6, params[2], (size_t)N * 16);
+    }
     StageClock clk;
     std::vector<float> xys(2 * (size_t)N, 0.f), depths(N, 0.f), conics(3 * (size_t)N, 0.f),
         colors(3 * (size_t)N, 0.f), aabb(2 * (size_t)N, 0.f);
@@ -1057,9 +1398,16 @@ float orc_train_step(const OrcCamera* cam, int32_t N, int32_t rest_bases,
                                           v_rendered.data(), nullptr, nullptr);
     clk.lap(4);   // loss_fwd_bwd
     std::vector<float> v_xy(2 * (size_t)N), v_conic(3 * (size_t)N), v_rgb(3 * (size_t)N), v_op(N);
-    orc_rasterize(cam, N, xys.data(), conics.data(), colors.data(), params[5], tile_bins.data(),
-                  ids.data(), Ts.data(), fidx.data(), img.data(), v_rendered.data(), v_xy.data(),
-                  v_conic.data(), v_rgb.data(), v_op.data());
+    const bool bounds = out && (out->mag_raster || out->err_raster || out->grad[0]);
+    std::vector<double> mag9, err9;
+    if (bounds) {
+        mag9.assign((size_t)N * 9, 0.0);
+        err9.assign((size_t)N * 9, 0.0);
+    }
+    rasterize_impl(cam, N, xys.data(), conics.data(), colors.data(), params[5], tile_bins.data(),
+                   ids.data(), Ts.data(), fidx.data(), img.data(), v_rendered.data(), v_xy.data(),
+                   v_conic.data(), v_rgb.data(), v_op.data(), bounds ? mag9.data() : nullptr,
+                   bounds ? err9.data() : nullptr);
     clk.lap(5);   // rast_bwd (the backward call recomputes each pixel's forward)
     std::vector<float> v_mean(3 * (size_t)N), v_scale(3 * (size_t)N), v_quat(4 * (size_t)N);
     orc_project_backward(cam, N, params[0], params[1], params[2], radii.data(), conics.data(),
@@ -1096,6 +1444,10 @@ float orc_train_step(const OrcCamera* cam, int32_t N, int32_t rest_bases,
     orc_grad_stats(N, radii.data(), v_xy.data(), vis, gnorm, max2d,
                    1.0f / (float)std::max(H, W));
     clk.lap(7);   // grad_stats
+    if (bounds)
+        train_step_bounds(cam, N, rest_bases, params_before.data(), radii.data(), conics.data(),
+                          v_xy.data(), v_conic.data(), v_rgb.data(), v_op.data(), v_mean.data(),
+                          v_scale.data(), v_quat.data(), mag9.data(), err9.data(), out);
     if (out) {
         if (out->out_img) std::memcpy(out->out_img, img.data(), P * 3 * sizeof(float));
         if (out->radii) std::memcpy(out->radii, radii.data(), (size_t)N * 4);

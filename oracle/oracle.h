@@ -125,6 +125,18 @@ void orc_project_backward(const OrcCamera* cam, int32_t N,
                           const float* v_xy, const float* v_conic,
                           float* v_mean3d, float* v_scale, float* v_quat);
 
+/* Bound on |GPU - oracle| of each gaussian's projection backward outputs
+ * err_out[N,10] = (v_mean3d 3, v_scale 3, v_quat 4), absolute, by running
+ * error analysis of the oracle's formulas evaluated on these inputs: the
+ * inputs' own bounds err_xy[N,2] / err_conic[N,3] (NULL = exact inputs)
+ * propagated, plus 4 x each operation's rounding (the GPU kernel's hardware
+ * reciprocal / square root round to about 1 ulp).  Zeros for radii <= 0. */
+void orc_project_backward_err(const OrcCamera* cam, int32_t N,
+                              const float* means, const float* scales, const float* quats,
+                              const int32_t* radii, const float* conics,
+                              const float* v_xy, const float* v_conic,
+                              const float* err_xy, const float* err_conic, float* err_out);
+
 /* SH colour backward (sh_coeffs_to_color_vjp semantics, .metal:656-743 / 1924-1985):
  * for radii > 0 writes v_dc[N,3], v_rest[N,K-1,3] (zeros for unused bands). */
 void orc_sh_backward(const OrcCamera* cam, int32_t N, const float* means,
@@ -150,6 +162,16 @@ typedef struct OrcTrainOut {
     float* v_xy; float* v_conic; float* v_rgb; float* v_opacity;
     float* v_mean3d; float* v_scale; float* v_quat;
     float* v_rendered;
+    /* Error bounds of the gradients (all optional).  mag_raster / err_raster
+     * [N,9] for v_xy (2), v_conic (3), v_rgb (3), v_opacity (1): the sum of
+     * the magnitudes of the terms each gradient is summed from, and a
+     * first-order bound on |GPU - oracle| from the two evaluations'
+     * arithmetic (running error analysis; absolute).  grad / grad_mag /
+     * grad_err [6]: the gradient each Adam group is updated with (means,
+     * scales, quats, f_dc, f_rest, opacities; zero where Adam leaves the
+     * element as it is), its magnitude and its bound, shaped like the group. */
+    float* mag_raster; float* err_raster;
+    float* grad[6]; float* grad_mag[6]; float* grad_err[6];
 } OrcTrainOut;
 
 float orc_train_step(const OrcCamera* cam, int32_t N, int32_t rest_bases,

@@ -6,7 +6,9 @@ the CPU oracle, whose functions are pinned by tests/test_oracle_pins.py.
 Each fixture holds one small seeded scene, its camera and target, and the
 oracle's outputs of every stage: projection, tile bins and sorted ids, the
 forward image / final T / final index, the SSIM loss and its image gradient,
-the raster and projection gradients, and the parameters after one Adam step.
+the raster and projection gradients with the oracle's bounds on a GPU's
+rounding difference, the gradient of each Adam group, and the parameters
+and moments after one Adam step.
 
 Run from the repository root:  python tests/golden/make_golden.py
 """
@@ -45,7 +47,7 @@ def make(name, n, width, height, seed, spread, degree):
     v = [np.zeros_like(a) for a in params]
     vis, gnorm, max2d = (np.zeros(sc.n, np.float32) for _ in range(3))
     want = ("out_img", "radii", "v_xy", "v_conic", "v_rgb", "v_opacity", "v_mean3d", "v_scale", "v_quat",
-            "v_rendered")
+            "v_rendered", "err_raster", "grad", "grad_err")
     loss, o = orc.train_step(cam, params, m, v, orc.adam_hparams(LRS, 1), gt, 0.2, vis, gnorm, max2d, want=want)
     out = dict(
         # inputs
@@ -62,6 +64,10 @@ def make(name, n, width, height, seed, spread, degree):
         loss=np.float32(loss), v_rendered=o["v_rendered"], v_xy=o["v_xy"], v_conic=o["v_conic"],
         v_rgb=o["v_rgb"], v_opacity=o["v_opacity"], v_mean3d=o["v_mean3d"], v_scale=o["v_scale"],
         v_quat=o["v_quat"], vis_counts=vis, xys_grad_norm=gnorm, max_2d_size=max2d,
+        # the oracle's bounds on a GPU's difference (running error analysis)
+        err_raster=o["err_raster"],
+        **{f"grad{i}": o["grad"][i] for i in range(6)},
+        **{f"grad_err{i}": o["grad_err"][i] for i in range(6)},
         **{f"param{i}_after": params[i] for i in range(6)},
         **{f"exp_avg{i}_after": m[i] for i in range(6)},
         **{f"exp_avg_sq{i}_after": v[i] for i in range(6)},

@@ -37,7 +37,8 @@ class OrcAdam(ctypes.Structure):
 class OrcTrainOut(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in
                 ("out_img", "radii", "v_xy", "v_conic", "v_rgb", "v_opacity", "v_mean3d", "v_scale", "v_quat",
-                 "v_rendered")]
+                 "v_rendered", "mag_raster", "err_raster")] + [
+        ("grad", ctypes.c_void_p * 6), ("grad_mag", ctypes.c_void_p * 6), ("grad_err", ctypes.c_void_p * 6)]
 
 
 class OrcDensifyArgs(ctypes.Structure):
@@ -147,6 +148,38 @@ def rasterize(cam: OrcCamera, proj: dict, opac_logits, tile_bins, ids, v_out=Non
     return out
 
 
+def project_backward(cam: OrcCamera, means, scales, quats, radii, conics, v_xy, v_conic, err_xy=None,
+                     err_conic=None):
+    """Projection backward of the given raster gradients: (v_mean3d, v_scale,
+    v_quat, err[N,10]) where err bounds |GPU - oracle| of the three outputs
+    (v_mean3d 3, v_scale 3, v_quat 4) given inputs that err by err_xy /
+    err_conic (None: exact inputs, the bound is the arithmetic's own)."""
+    n = means.shape[0]
+    means, scales, quats, conics, v_xy, v_conic = map(f32, (means, scales, quats, conics, v_xy, v_conic))
+    radii = np.ascontiguousarray(radii, np.int32)
+    vm, vs, vq = np.zeros((n, 3), np.float32), np.zeros((n, 3), np.float32), np.zeros((n, 4), np.float32)
+    err = np.zeros((n, 10), np.float32)
+    L = lib()
+    L.orc_project_backward(ctypes.byref(cam), n, P(means), P(scales), P(quats), P(radii), P(conics), P(v_xy),
+                           P(v_conic), P(vm), P(vs), P(vq))
+    L.orc_project_backward_err(ctypes.byref(cam), n, P(means), P(scales), P(quats), P(radii), P(conics), P(v_xy),
+                               P(v_conic), P(f32(err_xy)) if err_xy is not None else None,
+                               P(f32(err_conic)) if err_conic is not None else None, P(err))
+    return vm, vs, vq, err
+
+
+def sh_backward(cam: OrcCamera, means, radii, v_rgb, rest_bases: int):
+    """(v_dc [N,3], v_rest [N,rest_bases,3]) of the given colour gradients."""
+    n = means.shape[0]
+    nb = max(rest_bases, 0)
+    full = (((cam.degree + 1) ** 2) - 1)
+    v_dc = np.zeros((n, 3), np.float32)
+    v_rest = np.zeros((n, full, 3), np.float32)
+    lib().orc_sh_backward(ctypes.byref(cam), n, P(f32(means)), P(np.ascontiguousarray(radii, np.int32)),
+                          P(f32(v_rgb)), P(v_dc), P(v_rest))
+    return v_dc, np.ascontiguousarray(v_rest[:, :nb])
+
+
 def raster_counts():
     """Pair counts of the last orc_rasterize call (fwd tested/in range/composited, bwd tested/in range/grad)."""
     out = (c_int64 * 6)()
@@ -243,7 +276,11 @@ def adam_hparams(lrs, step: int, beta1=0.9, beta2=0.999, eps=1e-8) -> OrcAdam:
 
 
 def train_step(cam: OrcCamera, params, m, v, adam: OrcAdam, gt, ssim_weight, vis, gnorm, max2d, want=()):
-    """One oracle train step; params/m/v are lists of 6 float32 arrays updated in place."""
+    """One oracle train step; params/m/v are lists of 6 float32 arrays updated in place.
+
+    want names the outputs to return: the fields of OrcTrainOut
+    (out_img, radii, v_xy ... v_rendered, mag_raster, err_raster: arrays) and
+    grad / grad_mag / grad_err (lists of six arrays shaped like params)."""
     n = params[0].shape[0]
     H, W = cam.height, cam.width
     rest_bases = params[4].shape[1] if params[4].ndim == 3 else 0
@@ -251,9 +288,16 @@ def train_step(cam: OrcCamera, params, m, v, adam: OrcAdam, gt, ssim_weight, vis
     shapes = dict(out_img=((H, W, 3), np.float32), radii=((n,), np.int32), v_xy=((n, 2), np.float32),
                   v_conic=((n, 3), np.float32), v_rgb=((n, 3), np.float32), v_opacity=((n,), np.float32),
                   v_mean3d=((n, 3), np.float32), v_scale=((n, 3), np.float32), v_quat=((n, 4), np.float32),
-                  v_rendered=((H, W, 3), np.float32))
+                  v_rendered=((H, W, 3), np.float32), mag_raster=((n, 9), np.float32),
+                  err_raster=((n, 9), np.float32))
     to = OrcTrainOut()
     for k in want:
+        if k in ("grad", "grad_mag", "grad_err"):
+            outs[k] = [np.zeros(a.shape, np.float32) for a in params]
+            arr = getattr(to, k)
+            for i in range(6):
+                arr[i] = P(outs[k][i]).value
+            continue
         shp, dt = shapes[k]
         outs[k] = np.zeros(shp, dt)
         setattr(to, k, P(outs[k]).value)

@@ -1,10 +1,11 @@
 """Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
 
-CPU: the oracle still reproduces every stored stage output (forward stages
-bit for bit, gradients and Adam state to fp32 rounding), so a change of the
-checker shows up here.  GPU: the HIP path reproduces the stored outputs
-directly (forward bit for bit, gradients and updated parameters within the
-parity tolerance), without running the oracle.
+CPU: the oracle still reproduces every stored output bit for bit (stages,
+gradients, bounds, Adam state), so a change of the checker shows up here.
+GPU: the HIP path reproduces the stored outputs directly, without running
+the oracle: forward bit for bit, gradients within rel 1e-3 plus the stored
+rounding bounds, Adam moments with those bounds carried through and the
+update where the gradient's bound is the relative one.
 """
 from __future__ import annotations
 
@@ -15,7 +16,7 @@ import numpy as np
 import pytest
 
 import orc
-from helpers import assert_bits_equal, grad_close
+from helpers import U, assert_bits_equal, bound_check
 from msplat_amd import camera
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -64,13 +65,20 @@ def test_oracle_reproduces_golden(path):
     n = params[0].shape[0]
     vc, gn, mx = (np.zeros(n, np.float32) for _ in range(3))
     loss, o = orc.train_step(cam, params, m, v, orc.adam_hparams(list(f["lrs"]), 1), f["gt"], 0.2, vc, gn, mx,
-                             want=("v_rendered", "v_xy", "v_conic", "v_rgb", "v_opacity"))
+                             want=("v_rendered", "v_xy", "v_conic", "v_rgb", "v_opacity", "v_mean3d", "v_scale",
+                                   "v_quat", "err_raster", "grad", "grad_err"))
     assert np.float32(loss) == f["loss"]
-    assert_bits_equal(o["v_rendered"], f["v_rendered"], "v_rendered")
-    for k in ("v_xy", "v_conic", "v_rgb", "v_opacity"):
-        grad_close(o[k], f[k], rtol=1e-6, floor=1e-7, what=k)
+    for k in ("v_rendered", "v_xy", "v_conic", "v_rgb", "v_opacity", "v_mean3d", "v_scale", "v_quat",
+              "err_raster"):
+        assert_bits_equal(o[k], f[k], k)
     for i in range(6):
-        grad_close(params[i], f[f"param{i}_after"], rtol=1e-6, floor=1e-7, what=f"param{i}")
+        assert_bits_equal(o["grad"][i], f[f"grad{i}"], f"grad{i}")
+        assert_bits_equal(o["grad_err"][i], f[f"grad_err{i}"], f"grad_err{i}")
+        assert_bits_equal(params[i], f[f"param{i}_after"], f"param{i}")
+        assert_bits_equal(m[i], f[f"exp_avg{i}_after"], f"exp_avg{i}")
+        assert_bits_equal(v[i], f[f"exp_avg_sq{i}_after"], f"exp_avg_sq{i}")
+    for k in ("vis_counts", "max_2d_size", "xys_grad_norm"):
+        assert_bits_equal({"vis_counts": vc, "max_2d_size": mx, "xys_grad_norm": gn}[k], f[k], k)
 
 
 @pytest.mark.gpu
@@ -97,11 +105,26 @@ def test_gpu_matches_golden(path):
     loss = device.train_step(g, su, deg, bg, device.to_dev(f["gt"]), 0.2, list(f["lrs"]), 1, grads_out=grads)
     assert abs(loss - float(f["loss"])) <= 1e-5 * abs(float(f["loss"]))
     assert_bits_equal(device.intermediate("v_rendered").reshape(H, W, 3), f["v_rendered"], "v_rendered")
-    for k, d in (("v_xy", 2), ("v_conic", 3), ("v_rgb", 3), ("v_opacity", 1)):
-        got = device.intermediate(k)
-        grad_close(got.reshape(n, d) if d > 1 else got, f[k], what=k)
-    for k in ("v_mean3d", "v_scale", "v_quat"):
-        grad_close(grads[k].cpu().numpy(), f[k], what=k)
-    gp = g.numpy()
+    er = f["err_raster"]
+    for k, q0, d in (("v_xy", 0, 2), ("v_conic", 2, 3), ("v_rgb", 5, 3), ("v_opacity", 8, 1)):
+        got = device.intermediate(k).reshape(n, d)
+        bound_check(got, f[k].reshape(n, d), er[:, q0:q0 + d], what=k)
+    for i, k in enumerate(("v_mean3d", "v_scale", "v_quat")):
+        bound_check(grads[k].cpu().numpy(), f[f"grad{i}"], f[f"grad_err{i}"], what=k)
+    # Adam from zero moments: m = (1 - b1) g, and the update where the
+    # gradient's bound is its relative term (then the update, about
+    # -lr sign(g) at step 1, is fixed to its rounding)
+    om1 = float(np.float32(1) - np.float32(0.9))
+    params0 = _params(f)
     for i in range(6):
-        grad_close(gp[i], f[f"param{i}_after"], rtol=1e-3, floor=1e-6, what=f"param{i}")
+        go, ge = f[f"grad{i}"].astype(np.float64), f[f"grad_err{i}"].astype(np.float64)
+        bound_check(g.m[i][:n].cpu().numpy(), f[f"exp_avg{i}_after"], om1 * ge + 6 * U * om1 * np.abs(go) + 1e-45,
+                    what=f"exp_avg{i}")
+        rd = (ge <= 1e-3 * np.abs(go)) & (go != 0)
+        p0 = np.asarray(params0[i], np.float64)
+        du = g.bufs[i][:n].cpu().numpy().astype(np.float64) - p0
+        du_o = f[f"param{i}_after"].astype(np.float64) - p0
+        ulp = np.spacing(np.abs(f[f"param{i}_after"]).astype(np.float32)).astype(np.float64)
+        bound_check(du[rd], du_o[rd], 4 * ulp[rd] + 1e-3 * np.abs(du_o[rd]), rel=1e-5, what=f"update{i}")
+        assert_bits_equal(g.bufs[i][:n].cpu().numpy()[go == 0] if i in (3, 4) else np.zeros(0),
+                          f[f"param{i}_after"][go == 0] if i in (3, 4) else np.zeros(0), f"untouched {i}")
