@@ -435,6 +435,10 @@ def main():
     ap.add_argument("--n", type=int, default=1_500_000)
     ap.add_argument("--cpu-steps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the config-4 train window and the config-5 render window that the "
+                         "default run times after the headline and reports as extra keys")
+    ap.add_argument("--c4-steps", type=int, default=50, help="timed config-4 train steps of the default run")
     ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5),
                     help="3 (default): the headline train + render workload; 4: heavy-tile train "
                          "steps at 2594x1680; 5: 6M-gaussian render at 4946x3286 (extra lines, "
@@ -677,6 +681,26 @@ def main():
         log(f"cpu baseline: {rate:.4f} it/s on {cores} threads ({cpu['cpu_model']}, "
             f"OMP_PROC_BIND={cpu['binding']})")
 
+    # The other benchmark workloads on the same clock: a config-4 train
+    # window (heavy tiles) and a config-5 render window (6M gaussians),
+    # each on its own scene after the headline's state is released.
+    extra = {}
+    if not args.no_extra:
+        del tr, params, targets, out, cpu_state
+        import gc
+        gc.collect()
+        torch.cuda.empty_cache()
+        c4 = bench_config4(argparse.Namespace(steps=args.c4_steps, warmup=10, stage_steps=20))
+        torch.cuda.empty_cache()
+        c5 = bench_config5(argparse.Namespace())
+        torch.cuda.empty_cache()
+        extra = {"config4_it_s": c4["value"], "config4_ms_per_step": c4["ms_per_step"],
+                 "config4_steps": c4["steps"], "config4_workload": c4["config"],
+                 "config4_stage_ms": c4["stage_ms"], "config4_raster_per_step": c4["raster_per_step"],
+                 "config5_fps": c5["value"], "config5_ms_per_frame": c5["ms_per_step"],
+                 "config5_frames": c5["steps"], "config5_workload": c5["config"],
+                 "config5_stage_ms": c5["stage_ms"], "config5_hbm_stages": c5["hbm_stages"]}
+
     res = {
         "metric": METRIC, "value": its, "unit": "it/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
@@ -697,6 +721,7 @@ def main():
         "visible_gaussians": n_vis,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        **extra,
     }
     print(json.dumps(res), flush=True)
 
