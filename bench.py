@@ -685,6 +685,7 @@ def main():
     # window (heavy tiles) and a config-5 render window (6M gaussians),
     # each on its own scene after the headline's state is released.
     extra = {}
+    n_end = tr.splat_count()
     if not args.no_extra:
         del tr, params, targets, out, cpu_state
         import gc
@@ -708,7 +709,7 @@ def main():
         "config": {"workload": "config3: 1.5M SH3 gaussians, 1297x840, 32 cameras cycled, densify every 100 "
                                "steps; timed after the opacity reset and the first densification",
                    "preroll_steps": args.preroll, "timed_steps": [first_step, first_step + args.steps - 1],
-                   "gaussians_start": n_start, "gaussians_end": tr.splat_count(), "render_frames": args.frames},
+                   "gaussians_start": n_start, "gaussians_end": n_end, "render_frames": args.frames},
         "window_wall_it_s": args.steps / window_s,
         "step_ms_without_densify": step_ms_no_densify,
         "densify_ms": densify_ms, "densifies_measured": dens_n, "densifies_in_window": win_dens_n,

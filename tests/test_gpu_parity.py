@@ -265,6 +265,35 @@ def test_train_three_steps(dev):
     _train_compare(dev, small_scene(n=2000, seed_off=83), steps=3)
 
 
+def test_unsynchronised_loss_reads(dev):
+    """msplat_hip_last_loss without a wait returns the loss of the latest
+    step known to have completed: after a train step whose loss was not
+    requested, the previous step's (the step's own totals wait has passed
+    it).  With zero learning rates the parameters stay as they are, so each
+    step's loss depends only on its target; six targets give six losses, read
+    once with a stream sync per step and once without any sync."""
+    import ctypes
+    sc = small_scene(n=3000, seed_off=80)
+    su = camera.prepare_cam(sc.cameras[0])
+    g = dev.DeviceGaussians.from_arrays(sc.params(), 3)
+    tg = [dev.to_dev(target_for(sc, (su.height, su.width), seed_off=500 + k)) for k in range(6)]
+    lr0 = [0.0] * 6
+    synced = [dev.train_step(g, su, 3, BG, tg[k], 0.2, lr0, k + 1) for k in range(6)]
+    assert len(set(synced)) == 6, synced
+    lib = dev.init()
+    got = []
+    for k in range(6):
+        dev.train_step(g, su, 3, BG, tg[k], 0.2, lr0, 7 + k, want_loss=False)
+        v = ctypes.c_float(0.0)
+        dev._abi.check(lib.msplat_hip_last_loss(ctypes.byref(v), 0))
+        got.append(v.value)
+    # the first read sees the last synced step's loss, then each the step before
+    assert got == [synced[5]] + synced[:5], (got, synced)
+    v = ctypes.c_float(0.0)
+    dev._abi.check(lib.msplat_hip_last_loss(ctypes.byref(v), 1))
+    assert v.value == synced[5]
+
+
 def _misalign(t):
     """A copy of device tensor t whose data starts 4 bytes past a 16-byte
     boundary (one float into a larger allocation)."""
