@@ -141,7 +141,7 @@ __global__ __launch_bounds__(SHA_T) void k_sh_rest_adam(int64_t n, int rest_per,
                                                         float* __restrict__ f_rest,
                                                         float* __restrict__ m,
                                                         float* __restrict__ v, AdamHP hp) {
-    __shared__ float s_basis[SHA_MAXG][16];
+    __shared__ float s_basis[SHA_MAXG][17];   // odd row stride: the per-gaussian writes hit distinct banks
     __shared__ float s_vrgb[SHA_MAXG][3];
     __shared__ int s_vis[SHA_MAXG];
     const int64_t eb = (int64_t)blockIdx.x * SHA_E;

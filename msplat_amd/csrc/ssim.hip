@@ -34,20 +34,36 @@ constexpr int WIN = 11;
 // pixels per workgroup of FT threads.  The horizontal sums are needed at
 // (FY + 10) x (FX + 10) positions and the derivative fields at FY x (FX + 10),
 // so a wide tile spends less of its work on the halo than a 16 x 16 one;
-// staging one channel at a time keeps the LDS at 40 KB for three
+// staging one channel at a time keeps the LDS at 48 KB for three
 // workgroups (six waves per SIMD) per CU.
 constexpr int FX = 32, FY = 16, FT = FX * FY;
 constexpr int FHX = FX + 2 * HALF;   // 42: columns with horizontal sums / fields
 constexpr int FHY = FY + 2 * HALF;   // 26: rows with horizontal sums
 constexpr int FIN = FHX + 2 * HALF;  // 52: input columns
+// LDS layouts, chosen so that every read of the three passes is free of bank
+// conflicts (64 banks of 4 bytes; a wave's 8-byte reads are served 32 lanes
+// at a time, its 16-byte reads 16 lanes at a time):
+//  * input: (gt, render) of a position as one float2, rows FIN_S float2
+//    apart.  The horizontal pass gives lane l the position p + l of a
+//    row-major walk over FHY x FHX, so 32 lanes cover at most two row pieces,
+//    [a, 42) of one row and [0, a - 10) of the next; FIN_S = 74 = 10 (mod 32)
+//    puts the second piece on exactly the 8-byte bank pairs the first leaves.
+//  * horizontal sums: (mu_x, mu_y, E[x^2], E[y^2]) as a float4 and E[xy] as a
+//    float, row-major over FHY x FHX (the passes' lanes read consecutive
+//    positions).
+//  * derivative fields (f1, f2, f3) as one float4 per position: the
+//    horizontal backward's 16-lane quarters read 16 consecutive positions of
+//    one row.
+constexpr int FIN_S = 74;
 
 __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __restrict__ img,
                                                    const float* __restrict__ gt,
                                                    float* __restrict__ dbuf,
                                                    float* __restrict__ loss_part) {
-    __shared__ float s_in[2][FHY][FIN];     // gt / render of one channel, rows y0-5.., cols x0-10..
-    __shared__ float s_hp[FHY][FHX][5];
-    __shared__ float s_f1[FY][FHX], s_f2[FY][FHX], s_f3[FY][FHX];
+    __shared__ float2 s_in[FHY * FIN_S];     // (gt, render) of one channel, rows y0-5.., cols x0-10..
+    __shared__ float4 s_h4[FHY * FHX];       // mu_x, mu_y, E[x^2], E[y^2]
+    __shared__ float s_h1[FHY * FHX];        // E[xy]
+    __shared__ float4 s_f[FY * FHX];         // f1, f2, f3, (unused)
     __shared__ float s_red[3][FT / 64];
     const int tr = threadIdx.x, lx = tr % FX, ly = tr / FX;
     const int bx = blockIdx.x * FX - HALF, by = blockIdx.y * FY - HALF;
@@ -78,8 +94,7 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
             const int i = tr + k * FT;
             if (i < FHY * FIN) {
                 const int sy = i / FIN, sx = i - sy * FIN;
-                s_in[0][sy][sx] = rg[k][c];
-                s_in[1][sy][sx] = rr[k][c];
+                s_in[sy * FIN_S + sx] = make_float2(rg[k][c], rr[k][c]);
             }
         }
         __syncthreads();
@@ -89,10 +104,12 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
             const int sy = i / FHX, sx = i - sy * FHX, gy = by + sy, gx = bx + sx;
             float mx = 0.f, my = 0.f, sxx = 0.f, syy = 0.f, cxy = 0.f;
             if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
+                const float2* row = s_in + sy * FIN_S + sx;
 #pragma unroll
                 for (int d = 0; d < WIN; ++d) {
                     const float w = GAUSS_1D[d];
-                    const float gv = s_in[0][sy][sx + d], rv = s_in[1][sy][sx + d];
+                    const float2 v = row[d];
+                    const float gv = v.x, rv = v.y;
                     mx += w * gv;
                     my += w * rv;
                     sxx += w * gv * gv;
@@ -100,11 +117,8 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
                     cxy += w * gv * rv;
                 }
             }
-            s_hp[sy][sx][0] = mx;
-            s_hp[sy][sx][1] = my;
-            s_hp[sy][sx][2] = sxx;
-            s_hp[sy][sx][3] = syy;
-            s_hp[sy][sx][4] = cxy;
+            s_h4[i] = make_float4(mx, my, sxx, syy);
+            s_h1[i] = cxy;
         }
         __syncthreads();
         for (int i = tr; i < FY * FHX; i += FT) {
@@ -113,12 +127,13 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
 #pragma unroll
             for (int k = 0; k < WIN; ++k) {
                 const float w = GAUSS_1D[k];
-                const float* h = s_hp[dy + k][dx];
-                mx += w * h[0];
-                my += w * h[1];
-                sx += w * h[2];
-                sy += w * h[3];
-                cxy += w * h[4];
+                const float4 h = s_h4[i + k * FHX];
+                const float h4 = s_h1[i + k * FHX];
+                mx += w * h.x;
+                my += w * h.y;
+                sx += w * h.z;
+                sy += w * h.w;
+                cxy += w * h4;
             }
             const float sxs = sx - mx * mx, sys = sy - my * my, sxy = cxy - mx * my;
             const float A = 2.0f * mx * my + SSIM_C1, B = 2.0f * sxy + SSIM_C2;
@@ -126,14 +141,13 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
             const float iCD = 1.0f / (Cd * D);
             const float dmu = 2.0f * B * (mx * Cd - A * my) / (Cd * Cd * D);
             const float dsyq = -A * B * iCD / D, dsxy = 2.0f * A * iCD;
-            s_f1[dy][dx] = dmu - 2.0f * my * dsyq - mx * dsxy;
-            s_f2[dy][dx] = 2.0f * dsyq;
-            s_f3[dy][dx] = dsxy;
+            s_f[i] = make_float4(dmu - 2.0f * my * dsyq - mx * dsxy, 2.0f * dsyq, dsxy, 0.f);
             if (dx >= HALF && dx < HALF + FX) {
                 const int gpx = bx + dx, gpy = by + dy + HALF;
                 if (gpx >= 0 && gpx < W && gpy >= 0 && gpy < H) {
                     ssim_sum += (A * B) / (Cd * D);
-                    l1_sum += fabsf(s_in[0][dy + HALF][dx + HALF] - s_in[1][dy + HALF][dx + HALF]);
+                    const float2 v = s_in[(dy + HALF) * FIN_S + dx + HALF];
+                    l1_sum += fabsf(v.x - v.y);
                     if (c == 0) cnt += 1.f;
                 }
             }
@@ -142,12 +156,14 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
         const int px = blockIdx.x * FX + lx, py = blockIdx.y * FY + ly;
         if (px < W && py < H) {
             float h1 = 0.f, h2 = 0.f, h3 = 0.f;
+            const float4* fr = s_f + ly * FHX + lx;
 #pragma unroll
             for (int d = 0; d < WIN; ++d) {
                 const float w = GAUSS_1D[WIN - 1 - d];
-                h1 += w * s_f1[ly][lx + d];
-                h2 += w * s_f2[ly][lx + d];
-                h3 += w * s_f3[ly][lx + d];
+                const float4 f = fr[d];
+                h1 += w * f.x;
+                h2 += w * f.y;
+                h3 += w * f.z;
             }
             float* o = dbuf + ((size_t)py * W + px) * 9 + c * 3;
             o[0] = h1;
@@ -174,26 +190,28 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
 // Vertical backward tile: VX columns x VY rows of output pixels, 256
 // threads, each thread VY / 16 rows.  The derivative fields of the tile's
 // columns are read row by row as contiguous floats (VX pixels x 9 values),
-// so the loads are coalesced; VY + 10 rows are read for VY outputs.
+// so the loads are coalesced; VY + 10 rows are read for VY outputs.  They
+// are kept in LDS in the same order ([row][column][9]): the staging writes
+// are consecutive, and a wave's reads of one field (4 rows x 16 columns,
+// 64 consecutive positions) are 9 floats apart, an odd stride that puts the
+// 64 lanes on 64 different banks.
 constexpr int VX = 16, VY = 32, VR = VY + 2 * HALF;
-constexpr int VPLANE = VR * VX + 1;   // one (channel, field) plane; odd stride spreads the banks
 
 __global__ __launch_bounds__(256) void k_ssim_v_bwd(int W, int H, const float* __restrict__ img,
                                                     const float* __restrict__ gt,
                                                     const float* __restrict__ dbuf, float w_ssim,
                                                     float inv_n, float* __restrict__ v_rendered) {
-    __shared__ float s_h[9 * VPLANE];   // plane c * 3 + field, rows by.., columns bx..
+    __shared__ float s_h[VR * VX * 9];   // rows by.., columns bx.., 9 fields (channel c: 3c..3c+2)
     const int tr = threadIdx.x, lx = tr & 15, ly = tr >> 4;
     const int bx = blockIdx.x * VX, by = blockIdx.y * VY - HALF;
     const int nf = min(VX, W - bx) * 9;   // in-image floats of a row
     constexpr int ROWF = VX * 9;
     for (int i = tr; i < VR * ROWF; i += 256) {
         const int sy = i / ROWF, f = i - sy * ROWF;
-        const int sx = f / 9, j = f - sx * 9;
         const int gy = by + sy;
         float v = 0.f;
         if (f < nf && gy >= 0 && gy < H) v = dbuf[((size_t)gy * W + bx) * 9 + f];
-        s_h[j * VPLANE + sy * VX + sx] = v;
+        s_h[i] = v;
     }
     __syncthreads();
     const int px = bx + lx;
@@ -203,14 +221,14 @@ __global__ __launch_bounds__(256) void k_ssim_v_bwd(int W, int H, const float* _
         const int oy = ly + 16 * rr, py = blockIdx.y * VY + oy;
         if (py >= H) break;
         for (int c = 0; c < 3; ++c) {
-            const float* h1 = s_h + (c * 3) * VPLANE + oy * VX + lx;
+            const float* h1 = s_h + (oy * VX + lx) * 9 + c * 3;
             float f1 = 0.f, f2 = 0.f, f3 = 0.f;
 #pragma unroll
             for (int d = 0; d < WIN; ++d) {
                 const float w = GAUSS_1D[WIN - 1 - d];
-                f1 += w * h1[d * VX];
-                f2 += w * h1[VPLANE + d * VX];
-                f3 += w * h1[2 * VPLANE + d * VX];
+                f1 += w * h1[d * VX * 9];
+                f2 += w * h1[d * VX * 9 + 1];
+                f3 += w * h1[d * VX * 9 + 2];
             }
             const size_t q = ((size_t)py * W + px) * 3 + c;
             const float r = img[q], g = gt[q];
