@@ -13,10 +13,10 @@
  *  - the device context is created on the first call that needs it (GPU 0),
  *    as the reference creates its Metal context lazily; msplat_cleanup
  *    releases it;
- *  - the dataset's images are decoded by the library's PNG decoder, or by a
- *    decoder the application registers with msplat_set_image_decoder
- *    (msplat_trainer.h) for other formats (the reference decodes through
- *    CoreGraphics, which has no counterpart here);
+ *  - the dataset's images are decoded by the library's PNG and JPEG
+ *    decoders, or by a decoder the application registers with
+ *    msplat_set_image_decoder (msplat_trainer.h) for other formats (the
+ *    reference decodes through CoreGraphics, which has no counterpart here);
  *  - failures that the reference reports by exception or by an empty result
  *    give the same empty result here (NULL handle, zero-sized buffer,
  *    negative count) and leave a message in msplat_trainer_last_error().

@@ -181,19 +181,21 @@ int32_t msplat_trainer_group(MsplatTrainer t, int32_t g, int32_t which, float** 
 /* Image decoding for msplat_dataset_create: a function that decodes the
  * file at path into a malloc'ed float32 RGB HWC buffer in [0, 1] (*rgb, which
  * the library free()s) of *width x *height pixels and returns 0, or returns
- * nonzero if it cannot.  PNG files are decoded by the library itself; other
- * formats (e.g. the JPEG files of most COLMAP datasets) need a registered
- * decoder.  NULL removes it. */
+ * nonzero if it cannot.  PNG and JPEG files are decoded by the library
+ * itself; other formats need a registered decoder, which, when set, decodes
+ * every file.  NULL removes it. */
 typedef int (*MsplatImageDecoder)(const char* path, float** rgb, int* width, int* height);
 void msplat_set_image_decoder(MsplatImageDecoder decoder);
 
 /* An image file decoded as msplat_dataset_create decodes it (the registered
- * decoder, else the built-in PNG decoder: colour types grey, RGB, palette,
- * grey + alpha and RGBA at 1-16 bits, not interlaced; alpha dropped, 16-bit
- * samples by their high byte, each channel byte / 255 as imreadRGB,
- * image_io.cpp:12-50): a malloc'ed float32 RGB HWC buffer in *rgb that the
- * caller free()s.  Host only.  0 or a negative code (message in
- * msplat_trainer_last_error). */
+ * decoder, else the built-in decoders, each channel byte / 255 as imreadRGB,
+ * image_io.cpp:12-50: PNG of colour types grey, RGB, palette, grey + alpha
+ * and RGBA at 1-16 bits, not interlaced, 16-bit samples by their high byte,
+ * transparency (alpha or tRNS) drawn over black; JPEG baseline, extended
+ * sequential or progressive with Huffman coding, grey or three components,
+ * any sampling factors, the samples libjpeg's default decoding gives): a
+ * malloc'ed float32 RGB HWC buffer in *rgb that the caller free()s.  Host
+ * only.  0 or a negative code (message in msplat_trainer_last_error). */
 int32_t msplat_image_read(const char* path, float** rgb, int32_t* width, int32_t* height);
 
 #ifdef __cplusplus

@@ -17,6 +17,7 @@
 
 #include "dataset.hpp"
 #include "model.hpp"
+#include "jpeg_decode.hpp"
 #include "png_decode.hpp"
 
 namespace msplat {
@@ -291,7 +292,8 @@ void ensure_device() {
     throw std::runtime_error(std::string("device initialisation failed: ") + msplat_hip_last_error());
 }
 
-// imreadRGB (image_io.cpp:12-50): a registered decoder, else the PNG decoder.
+// imreadRGB (image_io.cpp:12-50): a registered decoder, else the library's
+// PNG or JPEG decoder by the file's signature.
 msplat::DecodedImage read_image(const std::string& path) {
     if (g_decoder) {
         float* rgb = nullptr;
@@ -307,10 +309,10 @@ msplat::DecodedImage read_image(const std::string& path) {
         std::free(rgb);
         return img;
     }
-    if (!msplat::is_png_file(path))
-        throw std::runtime_error(path + ": not a PNG file; register a decoder for this format "
-                                        "with msplat_set_image_decoder");
-    return msplat::decode_png(path);
+    if (msplat::is_png_file(path)) return msplat::decode_png(path);
+    if (msplat::is_jpeg_file(path)) return msplat::decode_jpeg(path);
+    throw std::runtime_error(path + ": neither PNG nor JPEG; register a decoder for this format "
+                                    "with msplat_set_image_decoder");
 }
 
 // Camera::loadImage (input_data.cpp:17-52) on the GPU: intrinsics rescaled

@@ -1,10 +1,12 @@
 """Camera images: decode / encode and the load-time preparation of a target
 image (Camera::loadImage, input_data.cpp:17-52).
 
-* imread_rgb (imreadRGB, image_io.cpp:12-50): any format Pillow decodes, as
-  float32 RGB in [0, 1], each byte / 255 (the reference decodes with
-  CoreGraphics; PNG and other lossless files decode to the same bytes, JPEG
-  decoders may differ in the last bit of a sample).
+* imread_rgb (imreadRGB, image_io.cpp:12-50): float32 RGB in [0, 1], each
+  byte / 255, transparent pixels drawn over black as the reference's
+  CoreGraphics context without alpha draws them.  PNG and JPEG are decoded
+  by the library itself (msplat_image_read: the same samples as libjpeg's
+  default decoding for JPEG; the reference's closed decoder may differ in
+  the last bit of a JPEG sample); other formats by Pillow.
 * imwrite_rgb (imwriteRGB, image_io.cpp:54-89): PNG, each channel
   clamp(v * 255, 0, 255) + 0.5 truncated to a byte.
 * load_camera_image: the decoded image on the GPU, the camera's intrinsics
@@ -29,9 +31,22 @@ F32 = np.float32
 
 
 def imread_rgb(path: str) -> np.ndarray:
+    with open(path, "rb") as f:
+        sig = f.read(8)
+    if sig.startswith(b"\x89PNG\r\n\x1a\n") or sig.startswith(b"\xff\xd8\xff"):
+        lib = _abi.load()
+        rgb = ctypes.POINTER(ctypes.c_float)()
+        w, h = ctypes.c_int32(0), ctypes.c_int32(0)
+        if lib.msplat_image_read(path.encode(), ctypes.byref(rgb), ctypes.byref(w), ctypes.byref(h)) != 0:
+            raise RuntimeError(lib.msplat_trainer_last_error().decode())
+        try:
+            return np.ctypeslib.as_array(rgb, shape=(h.value, w.value, 3)).copy()
+        finally:
+            ctypes.CDLL(None).free(ctypes.cast(rgb, ctypes.c_void_p))
     from PIL import Image
     with Image.open(path) as im:
-        rgb = np.asarray(im.convert("RGB"), dtype=np.uint8)
+        rgba = np.asarray(im.convert("RGBA"), dtype=np.uint32)
+    rgb = (rgba[..., :3] * rgba[..., 3:] + 127) // 255   # over black
     return rgb.astype(np.float32) / np.float32(255.0)
 
 

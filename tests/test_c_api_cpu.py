@@ -178,10 +178,79 @@ def test_png_decoder_16_bit_grey_and_errors(tmp_path):
     data = open(path, "rb").read()
     (tmp_path / "cut.png").write_bytes(data[: len(data) // 2])
     (tmp_path / "text.png").write_bytes(b"not an image at all")
-    for p, msg in ((tmp_path / "cut.png", "PNG"), (tmp_path / "text.png", "not a PNG"),
+    for p, msg in ((tmp_path / "cut.png", "PNG"), (tmp_path / "text.png", "neither PNG nor JPEG"),
                    (tmp_path / "none.png", "")):
         got, err = _read(lib, p)
         assert got is None and msg in err, (p, err)
+
+
+def _jpeg_fixture(h=61, w=83, seed=5):
+    """A smooth gradient image with noise (odd sizes: partial MCUs)."""
+    rng = np.random.default_rng(seed)
+    yy, xx = np.mgrid[0:h, 0:w]
+    base = np.stack([(xx * 3 + yy) % 256, (yy * 4) % 256, (xx * yy) % 256], -1).astype(np.float32)
+    return np.clip(base + rng.normal(0, 20, base.shape), 0, 255).astype(np.uint8)
+
+
+JPEG_CASES = {
+    "444_q90": dict(quality=90, subsampling=0),
+    "422_q75": dict(quality=75, subsampling=1),
+    "420_q75": dict(quality=75, subsampling=2),
+    "411_q75": dict(quality=75, subsampling="4:1:1"),
+    "420_q50_optimized": dict(quality=50, subsampling=2, optimize=True),
+    "420_q100": dict(quality=100, subsampling=2),
+    "420_progressive": dict(quality=95, subsampling=2, progressive=True),
+    "420_progressive_optimized": dict(quality=80, subsampling=2, progressive=True, optimize=True),
+    "444_progressive": dict(quality=85, subsampling=0, progressive=True),
+    "420_restarts": dict(quality=85, subsampling=2, restart_marker_blocks=3),
+    "422_progressive_restarts": dict(quality=85, subsampling=1, progressive=True, restart_marker_rows=1),
+    "grey": dict(quality=80, mode="L"),
+    "grey_progressive": dict(quality=80, mode="L", progressive=True),
+}
+
+
+@pytest.mark.parametrize("case", sorted(JPEG_CASES))
+def test_jpeg_decoder_matches_pillow(case, tmp_path):
+    """The library's JPEG decoder against Pillow's (libjpeg-turbo, default
+    settings) on baseline / progressive, 4:4:4 / 4:2:2 / 4:2:0 / 4:1:1 /
+    grey, optimised Huffman tables and restart intervals: equal samples."""
+    Image = pytest.importorskip("PIL.Image")
+    lib = _lib()
+    kw = dict(JPEG_CASES[case])
+    mode = kw.pop("mode", "RGB")
+    img = _jpeg_fixture()
+    im = Image.fromarray(img if mode == "RGB" else img[..., 0], mode)
+    path = tmp_path / f"{case}.jpg"
+    im.save(path, "JPEG", **kw)
+    data = open(path, "rb").read()
+    if "restart" in case:
+        assert b"\xff\xd0" in data and b"\xff\xdd" in data, "the file must use restart markers"
+    if "progressive" in case:
+        assert b"\xff\xc2" in data
+    with Image.open(path) as f:
+        want = np.asarray(f.convert("RGB"), dtype=np.uint8).astype(np.float32) / np.float32(255.0)
+    got, err = _read(lib, path)
+    assert got is not None, err
+    assert got.shape == want.shape
+    assert (got.view(np.uint32) == want.view(np.uint32)).all(), \
+        f"{int((got != want).sum())} samples differ, max {float(np.abs(got - want).max()) * 255:.1f} levels"
+
+
+def test_jpeg_decoder_errors(tmp_path):
+    """Truncated data, CMYK and non-image files fail with a message."""
+    Image = pytest.importorskip("PIL.Image")
+    lib = _lib()
+    p = tmp_path / "a.jpg"
+    Image.fromarray(_jpeg_fixture(), "RGB").save(p, "JPEG", quality=90)
+    data = open(p, "rb").read()
+    (tmp_path / "cut.jpg").write_bytes(data[: len(data) // 3])
+    Image.new("CMYK", (20, 16), (10, 20, 30, 40)).save(tmp_path / "cmyk.jpg", "JPEG")
+    (tmp_path / "soi_only.jpg").write_bytes(b"\xff\xd8\xff\xd9")
+    (tmp_path / "text.jpg").write_bytes(b"not an image at all")
+    for name, msg in (("cut.jpg", ""), ("cmyk.jpg", "4 components"), ("soi_only.jpg", "JPEG"),
+                      ("text.jpg", "neither PNG nor JPEG")):
+        got, err = _read(lib, tmp_path / name)
+        assert got is None and msg in err, (name, err)
 
 
 def test_c_api_calls_that_fail_before_device_work(tmp_path):

@@ -150,14 +150,35 @@ def test_c_api_trains_like_the_python_trainer(lib, tmp_path):
         lib.msplat_dataset_destroy(ds)
 
 
-def test_c_api_registered_decoder_for_jpeg(lib, tmp_path):
-    """JPEG images need a registered decoder; with one (Pillow through a
-    ctypes callback) the dataset loads and trains."""
+def test_c_api_jpeg_dataset_native_and_registered_decoder(lib, tmp_path):
+    """A COLMAP scene with JPEG images loads and trains with no decoder
+    registered (the library's own JPEG decoder, as the reference decodes its
+    JPEG datasets itself).  A decoder the application registers (Pillow
+    through a ctypes callback) takes precedence; both decode the same
+    samples, so the first train step's loss is the same bit for bit."""
     from PIL import Image
     from msplat_amd import _abi
     _dataset(tmp_path, fmt="JPEG", n_points=500)
-    assert not lib.msplat_dataset_create(str(tmp_path).encode(), 1.0, False, 8)
-    assert b"msplat_set_image_decoder" in lib.msplat_trainer_last_error()
+
+    def first_loss():
+        ds = lib.msplat_dataset_create(str(tmp_path).encode(), 2.0, False, 8)
+        assert ds, lib.msplat_trainer_last_error()
+        try:
+            assert lib.msplat_dataset_num_test(ds) == 0
+            t = lib.msplat_trainer_create(ds, _config(iterations=2))
+            assert t, lib.msplat_trainer_last_error()
+            try:
+                s = lib.msplat_trainer_step(t)
+                assert s.iteration == 1 and s.splatCount == 500
+                img = _take(lib.msplat_trainer_render(t, 0, False))
+                assert np.isfinite(img).all()
+                return lib.msplat_trainer_last_loss(t, 1), lib.msplat_dataset_num_train(ds)
+            finally:
+                lib.msplat_trainer_destroy(t)
+        finally:
+            lib.msplat_dataset_destroy(ds)
+
+    native, n_train = first_loss()
     libc = ctypes.CDLL(None)
     libc.malloc.restype = ctypes.c_void_p
     libc.malloc.argtypes = [ctypes.c_size_t]
@@ -176,16 +197,8 @@ def test_c_api_registered_decoder_for_jpeg(lib, tmp_path):
     cb = _abi.ImageDecoder(decode)
     lib.msplat_set_image_decoder(cb)
     try:
-        ds = lib.msplat_dataset_create(str(tmp_path).encode(), 2.0, False, 8)
-        assert ds, lib.msplat_trainer_last_error()
-        assert len(calls) == lib.msplat_dataset_num_train(ds) and lib.msplat_dataset_num_test(ds) == 0
-        t = lib.msplat_trainer_create(ds, _config(iterations=2))
-        assert t, lib.msplat_trainer_last_error()
-        s = lib.msplat_trainer_step(t)
-        assert s.iteration == 1 and s.splatCount == 500
-        img = _take(lib.msplat_trainer_render(t, 0, False))
-        assert np.isfinite(img).all()
-        lib.msplat_trainer_destroy(t)
-        lib.msplat_dataset_destroy(ds)
+        registered, _ = first_loss()
+        assert len(calls) == n_train
+        assert np.isfinite(native) and native == registered, (native, registered)
     finally:
         lib.msplat_set_image_decoder(_abi.ImageDecoder(0))
