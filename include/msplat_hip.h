@@ -120,6 +120,15 @@ int msplat_hip_memset(void* ptr, int value, size_t bytes);
 int msplat_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int msplat_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int msplat_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* Coherent host memory mapped into the device's address space at the same
+ * address: the host writes and reads it through the pointer with no copy or
+ * stream wait, kernels read it directly (the reference's MTensor storage is
+ * such shared memory, metal_tensor.hpp:48-50, MTLResourceStorageModeShared).
+ * The host layer backs tensors of at most 256 bytes (camera matrices,
+ * background colour) with it.  Accesses race with kernels still running
+ * that use it, as on the reference's shared buffers. */
+int msplat_hip_alloc_mapped(void** ptr, size_t bytes);
+int msplat_hip_free_mapped(void* ptr);
 
 /* msplat_commit (bindings.h:22): flush; a no-op on HIP (work is issued eagerly).
  * msplat_gpu_sync (bindings.h:25): wait for all work on the stream. */

@@ -184,6 +184,8 @@ SIGNATURES = [
     ("msplat_hip_memcpy_h2d", c_int, [c_void_p, c_void_p, c_size_t]),
     ("msplat_hip_memcpy_d2h", c_int, [c_void_p, c_void_p, c_size_t]),
     ("msplat_hip_memcpy_d2d", c_int, [c_void_p, c_void_p, c_size_t]),
+    ("msplat_hip_alloc_mapped", c_int, [POINTER(c_void_p), c_size_t]),
+    ("msplat_hip_free_mapped", c_int, [c_void_p]),
     ("msplat_hip_commit", c_int, []),
     ("msplat_hip_sync", c_int, []),
     ("msplat_hip_render", c_int, [POINTER(RenderArgs), c_void_p]),

@@ -606,6 +606,30 @@ int msplat_hip_alloc(void** ptr, size_t bytes) {
     return MSPLAT_OK;
 }
 
+int msplat_hip_alloc_mapped(void** ptr, size_t bytes) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (!ptr) return fail(MSPLAT_ERR_ARG, "null ptr");
+    void* h = nullptr;
+    if (hipHostMalloc(&h, bytes ? bytes : 4, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+        return fail(MSPLAT_ERR_NOMEM, "hipHostMalloc(%zu)", bytes);
+    void* d = nullptr;
+    if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess || d != h) {
+        (void)hipHostFree(h);
+        return fail(MSPLAT_ERR_HIP, "mapped host memory is not at the same device address");
+    }
+    *ptr = h;
+    return MSPLAT_OK;
+}
+
+int msplat_hip_free_mapped(void* ptr) {
+    if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
+    if (ptr) {
+        HIP_TRY(hipStreamSynchronize(g_ctx->stream));
+        HIP_TRY(hipHostFree(ptr));
+    }
+    return MSPLAT_OK;
+}
+
 int msplat_hip_free(void* ptr) {
     if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
     if (ptr) {
@@ -637,7 +661,7 @@ int msplat_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
 
 int msplat_hip_memcpy_d2d(void* dst, const void* src, size_t bytes) {
     if (!g_ctx) return fail(MSPLAT_ERR_NOINIT, "not initialised");
-    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_ctx->stream));
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, g_ctx->stream));
     return MSPLAT_OK;
 }
 

@@ -164,11 +164,17 @@ std::tuple<MTensor, float> msplat_train_step(
 }
 
 namespace {
-// A camera matrix or colour held in a device tensor, read back to the host.
+// A camera matrix or colour held in a tensor, as host values.  gpu_empty /
+// gpu_zeros back such small tensors with mapped host memory, which the
+// caller writes on the host as the reference's Model writes its shared
+// buffers (model.cpp:113-115, prepareCam): it is read here directly, with no
+// copy and no wait for the stream.  A larger, device-resident tensor is
+// copied back (which waits for the stream).
 template <int K>
 void host_floats(const MTensor& t, float (&dst)[K], const char* what) {
     if (!t.defined() || t.numel() < K) throw std::runtime_error(std::string(what) + ": too few elements");
-    t.copy_to_host(dst, sizeof(dst));
+    if (t.mapped()) std::memcpy(dst, t.data<float>(), sizeof(dst));
+    else t.copy_to_host(dst, sizeof(dst));
 }
 }  // namespace
 

@@ -8,6 +8,7 @@
 #pragma once
 
 #include <cstdint>
+#include <cstring>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -58,13 +59,41 @@ public:
         return v;
     }
 
-    void zero() { if (numel()) check(msplat_hip_memset(ptr_, 0, nbytes()), "memset"); }
+    // Small tensors (at most kMappedBytes) live in coherent host memory
+    // mapped into the device's address space, like the reference's
+    // shared-storage buffers: data() is then valid on the host too, and the
+    // host reads and writes it directly.
+    static constexpr size_t kMappedBytes = 256;
+    bool mapped() const { return mapped_; }
 
+    // Copies and fills keep the stream order for every tensor (a mapped one
+    // waits for the stream first).
+    void zero() {
+        if (!numel()) return;
+        if (mapped_) {
+            check(msplat_hip_sync(), "sync");
+            std::memset(ptr_, 0, nbytes());
+        } else {
+            check(msplat_hip_memset(ptr_, 0, nbytes()), "memset");
+        }
+    }
     void copy_from_host(const void* src, size_t bytes) {
-        if (bytes) check(msplat_hip_memcpy_h2d(ptr_, src, bytes), "memcpy h2d");
+        if (!bytes) return;
+        if (mapped_) {
+            check(msplat_hip_sync(), "sync");
+            std::memcpy(ptr_, src, bytes);
+        } else {
+            check(msplat_hip_memcpy_h2d(ptr_, src, bytes), "memcpy h2d");
+        }
     }
     void copy_to_host(void* dst, size_t bytes) const {
-        if (bytes) check(msplat_hip_memcpy_d2h(dst, ptr_, bytes), "memcpy d2h");
+        if (!bytes) return;
+        if (mapped_) {
+            check(msplat_hip_sync(), "sync");
+            std::memcpy(dst, ptr_, bytes);
+        } else {
+            check(msplat_hip_memcpy_d2h(dst, ptr_, bytes), "memcpy d2h");
+        }
     }
     void copy_from_device(const void* src, size_t bytes) {
         if (bytes) check(msplat_hip_memcpy_d2d(ptr_, src, bytes), "memcpy d2d");
@@ -76,8 +105,14 @@ public:
         t.dtype_ = dt;
         size_t bytes = (size_t)t.numel() * dtype_size(dt);
         void* p = nullptr;
-        check(msplat_hip_alloc(&p, bytes ? bytes : 16), "alloc");
-        t.mem_ = std::shared_ptr<void>(p, [](void* q) { msplat_hip_free(q); });
+        if (bytes <= kMappedBytes) {
+            check(msplat_hip_alloc_mapped(&p, bytes ? bytes : 16), "alloc mapped");
+            t.mem_ = std::shared_ptr<void>(p, [](void* q) { msplat_hip_free_mapped(q); });
+            t.mapped_ = true;
+        } else {
+            check(msplat_hip_alloc(&p, bytes), "alloc");
+            t.mem_ = std::shared_ptr<void>(p, [](void* q) { msplat_hip_free(q); });
+        }
         t.ptr_ = p;
         return t;
     }
@@ -90,6 +125,7 @@ public:
 private:
     std::shared_ptr<void> mem_;
     void* ptr_ = nullptr;
+    bool mapped_ = false;
     std::vector<int64_t> shape_;
     DType dtype_ = DType::Float32;
 };
