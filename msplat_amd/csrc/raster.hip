@@ -110,6 +110,20 @@ __device__ __forceinline__ int quad_mask(float x, float y, float a, float b, flo
     return m;
 }
 
+// The reference's range early-out, skip when sigma < 0 || sigma >= 5.55
+// (.metal:551, 1029, 2718, 2976), folded into the alpha test: sigma's bits
+// are clamped with one unsigned min to those of 5.55f (0x40B1999A), so sigma
+// in [+0, 5.55) keeps its value and everything else (negative, -0, >= 5.55,
+// +inf, NaN) becomes 5.55, where alpha = min(0.999, o exp(-5.55)) <=
+// 0.0038875 < 1/255 for every opacity in [0, 1] and the alpha test rejects
+// the pair.  One vector min replaces two compares and two scalar ands per
+// entry step; the decision differs from the reference's only for sigma = -0
+// or NaN (a degenerate conic), which are rejected here, and for a NaN
+// opacity (alpha 0.999 wherever the entry is walked).
+__device__ __forceinline__ float sigma_clamp(float s) {
+    return __uint_as_float(min(__float_as_uint(s), 0x40B1999Au));
+}
+
 // Entry record at byte offset qb of an LDS array of float4.
 __device__ __forceinline__ float4 lds_f4(const float4* base, int qb) {
     return *static_cast<const float4*>(
@@ -196,10 +210,9 @@ __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float f
                 const float cb = lds_f4(s_aux, qb).x;
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-                const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma));
-                // hit: live && !(sigma < 0 || sigma >= 5.55) && !(alpha < 1/255)
-                const uint64_t hm = live & mask_uge(sigma, 0.f) & mask_ult(sigma, 5.55f) &
-                                    mask_uge(alpha, 1.f / 255.f);
+                const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma_clamp(sigma)));
+                // hit: live && !(alpha < 1/255) (sigma out of range: alpha < 1/255)
+                const uint64_t hm = live & mask_uge(alpha, 1.f / 255.f);
                 const float nT = T * (1.f - alpha);
                 const uint64_t sm = hm & mask_le(nT, 1e-4f);     // stops here
                 const uint64_t cm = hm & ~sm;                    // composites
@@ -656,10 +669,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
                 const float4 x = lds_f4(s_aux, qb);
                 const float dx = g.x - fx, dy = g.y - fy;
                 const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-                const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma));
-                // valid: qq >= qlo && !(sigma < 0 || sigma >= 5.55) && !(alpha < 1/255)
-                const uint64_t vmask = mask_ge_i(qb, qlob) & mask_uge(sigma, 0.f) &
-                                       mask_ult(sigma, 5.55f) & mask_uge(alpha, 1.f / 255.f);
+                const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma_clamp(sigma)));
+                // valid: qq >= qlo && !(alpha < 1/255) (sigma out of range: alpha < 1/255)
+                const uint64_t vmask = mask_ge_i(qb, qlob) & mask_uge(alpha, 1.f / 255.f);
                 if (vmask == 0) continue;
                 // Branch-free per lane: lanes without a gradient run the same
                 // steps with alpha = 0, which leaves their state as it is
@@ -742,9 +754,8 @@ __global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
             const float4 c = r[1];
             const float dx = g.x - fx, dy = g.y - fy;
             const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-            if (sigma < 0.f || sigma >= 5.55f) continue;
-            ++n[1];
-            const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma));
+            if (!(sigma < 0.f || sigma >= 5.55f)) ++n[1];
+            const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma_clamp(sigma)));
             if (alpha < 1.f / 255.f) continue;
             const float nT = T * (1.f - alpha);
             if (nT <= 1e-4f) break;
@@ -760,9 +771,8 @@ __global__ __launch_bounds__(256) void k_raster_work(int W, int H, int tbx,
             const float4 c = r[1];
             const float dx = g.x - fx, dy = g.y - fy;
             const float sigma = fmaf(0.5f, fmaf(g.z, dx * dx, c.x * dy * dy), g.w * dx * dy);
-            if (sigma < 0.f || sigma >= 5.55f) continue;
-            ++n[4];
-            const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma));
+            if (!(sigma < 0.f || sigma >= 5.55f)) ++n[4];
+            const float alpha = fminf(0.999f, c.y * exp_neg_raster(sigma_clamp(sigma)));
             if (alpha < 1.f / 255.f || !(alpha < 0.999f)) continue;
             ++n[5];
         }

@@ -124,6 +124,27 @@ inline float oexp_raster(float x) {
     return std::ldexp(p, (int)std::fmin(std::fmax(k, -256.f), 256.f));
 }
 
+// The rasteriser's range early-out (.metal:551, 1029, 2718, 2976: skip when
+// sigma < 0 || sigma >= 5.55), as the HIP kernels evaluate it: sigma's bits
+// clamped with one unsigned min to those of 5.55f, so that sigma in
+// [+0, 5.55) keeps its value and everything else (negative, -0, >= 5.55,
+// +inf, NaN) becomes 5.55, where alpha = min(0.999, o exp(-5.55)) <=
+// 0.0038875 < 1/255 for every opacity o in [0, 1] and the alpha test rejects
+// the pair.  Returns whether the pair goes on to the alpha test, and the
+// sigma it uses there.  This equals the reference's test for every sigma
+// but -0 and NaN (rejected here), which only a degenerate conic produces,
+// and for every opacity but NaN (whose alpha is 0.999 either way).
+inline bool sigma_in(float sigma, float opac, float* s_used) {
+    uint32_t b;
+    std::memcpy(&b, &sigma, 4);
+    if (b < 0x40B1999Au) {   // 0x40B1999A = 5.55f
+        *s_used = sigma;
+        return true;
+    }
+    *s_used = 5.55f;
+    return opac != opac;     // a NaN opacity makes alpha 0.999 even here
+}
+
 // float -> int with the operand clamped to [-2^30, 2^30] first, so every
 // input (inf and NaN included) has one defined result on every target.
 inline int f2i(float v) { return (int)std::fmin(std::fmax(v, -1073741824.f), 1073741824.f); }
@@ -533,9 +554,10 @@ inline float raster_pixel_fwd(const Entry* ent, int s, int e, float px, float py
         ++cnt->e;
         const float dx = en.x - px, dy = en.y - py;
         const float sigma = std::fma(0.5f, std::fma(en.a, dx * dx, en.c * dy * dy), en.b * dx * dy);
-        if (sigma < 0.f || sigma >= 5.55f) continue;
-        ++cnt->r;
-        const float alpha = std::fmin(0.999f, en.o * oexp_raster(-sigma));
+        if (!(sigma < 0.f || sigma >= 5.55f)) ++cnt->r;
+        float su;
+        if (!sigma_in(sigma, en.o, &su)) continue;
+        const float alpha = std::fmin(0.999f, en.o * oexp_raster(-su));
         if (alpha < 1.f / 255.f) continue;
         const float next_T = T * (1.f - alpha);
         if (next_T <= 1e-4f) { lc = i - 1; break; }
@@ -601,9 +623,10 @@ inline void raster_pixel_bwd(const Entry* ent, int s, int bin_final, float px, f
         const float opac = en.o;
         const float dx = en.x - px, dy = en.y - py;
         const float sigma = std::fma(0.5f, std::fma(en.a, dx * dx, en.c * dy * dy), en.b * dx * dy);
-        if (sigma < 0.f || sigma >= 5.55f) continue;
-        ++cnt->r;
-        const float vis = oexp_raster(-sigma);
+        if (!(sigma < 0.f || sigma >= 5.55f)) ++cnt->r;
+        float su;
+        if (!sigma_in(sigma, opac, &su)) continue;
+        const float vis = oexp_raster(-su);
         const float alpha = std::fmin(0.999f, opac * vis);
         if (alpha < 1.f / 255.f) continue;
         if (!(alpha < 0.999f)) continue;

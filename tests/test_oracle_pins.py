@@ -83,6 +83,32 @@ def test_exp_raster_against_libm():
     assert np.all(np.diff(ys.astype(np.float64)) >= 0)
 
 
+def test_sigma_clamp_rejects_through_alpha():
+    """The raster kernels fold the range early-out (skip sigma < 0 or >= 5.55)
+    into the alpha test by clamping sigma's bits to those of 5.55f with an
+    unsigned min.  That rejects exactly the out-of-range pairs because
+    min(0.999, o exp(-5.55)) < 1/255 for every opacity in [0, 1] (float32
+    arithmetic, the largest opacity below 1 and 1 itself), while every sigma
+    in [+0, 5.55) keeps its bits; -0, negatives, >= 5.55, inf and NaN clamp."""
+    e = np.float32(orc.lib().orc_expf_raster(-5.55))
+    thr = np.float32(1.0) / np.float32(255.0)
+    for o in (np.float32(1.0), np.nextafter(np.float32(1.0), np.float32(0.0)), np.float32(0.5)):
+        assert np.minimum(np.float32(0.999), o * e) < thr
+    cap = np.uint32(0x40B1999A)
+    assert np.array([5.55], F32).view(np.uint32)[0] == cap
+    s = np.array([0.0, 1e-30, 1.0, 5.5499997, 5.55, 6.0, np.inf, np.nan, -0.0, -1e-30, -1.0, -np.inf],
+                 F32)
+    clamped = np.minimum(s.view(np.uint32), cap).view(F32)
+    ref_in = ~((s < 0) | (s >= F32(5.55)))            # the reference's test (NaN passes it)
+    kept = s.view(np.uint32) < cap                    # below the cap: sigma keeps its bits
+    assert np.array_equal(clamped[kept].view(np.uint32), s[kept].view(np.uint32))
+    # identical for every sigma but -0 and NaN, which the clamp rejects
+    special = (np.signbit(s) & (s == 0)) | np.isnan(s)
+    assert np.array_equal(kept[~special], ref_in[~special])
+    assert not kept[special].any()
+    assert np.all(clamped[~kept] == F32(5.55))
+
+
 # ---------------------------------------------------------------- SH ---------
 
 SH_CLOSED = [
