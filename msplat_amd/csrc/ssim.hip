@@ -16,7 +16,11 @@
 //                (rows outside the image contribute nothing) and the
 //                combination with the L1 sign term.
 // Every sum is accumulated in the same order as the reference's separate
-// kernels, so the fusion changes no bit of the result.
+// kernels, so the fusion changes no bit of the result.  Each window term is
+// added with one fused multiply-add (w gv gv as the product w gv, then an
+// fma with gv): the reference writes a product and a sum, which its
+// fast-math Metal build may contract the same way; the CPU oracle evaluates
+// exactly these operations.
 // The loss is reduced per workgroup into (sum SSIM, sum L1, pixel count) and
 // folded by one final workgroup in a fixed order; it equals the sum over
 // pixels of w*(1 - mean_c SSIM) + (1-w)*mean_c |gt - r|.
@@ -110,11 +114,12 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
                     const float w = GAUSS_1D[d];
                     const float2 v = row[d];
                     const float gv = v.x, rv = v.y;
-                    mx += w * gv;
-                    my += w * rv;
-                    sxx += w * gv * gv;
-                    syy += w * rv * rv;
-                    cxy += w * gv * rv;
+                    const float wg = w * gv, wr = w * rv;
+                    mx = fmaf(w, gv, mx);
+                    my = fmaf(w, rv, my);
+                    sxx = fmaf(wg, gv, sxx);
+                    syy = fmaf(wr, rv, syy);
+                    cxy = fmaf(wg, rv, cxy);
                 }
             }
             s_h4[i] = make_float4(mx, my, sxx, syy);
@@ -129,11 +134,11 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
                 const float w = GAUSS_1D[k];
                 const float4 h = s_h4[i + k * FHX];
                 const float h4 = s_h1[i + k * FHX];
-                mx += w * h.x;
-                my += w * h.y;
-                sx += w * h.z;
-                sy += w * h.w;
-                cxy += w * h4;
+                mx = fmaf(w, h.x, mx);
+                my = fmaf(w, h.y, my);
+                sx = fmaf(w, h.z, sx);
+                sy = fmaf(w, h.w, sy);
+                cxy = fmaf(w, h4, cxy);
             }
             const float sxs = sx - mx * mx, sys = sy - my * my, sxy = cxy - mx * my;
             const float A = 2.0f * mx * my + SSIM_C1, B = 2.0f * sxy + SSIM_C2;
@@ -161,9 +166,9 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
             for (int d = 0; d < WIN; ++d) {
                 const float w = GAUSS_1D[WIN - 1 - d];
                 const float4 f = fr[d];
-                h1 += w * f.x;
-                h2 += w * f.y;
-                h3 += w * f.z;
+                h1 = fmaf(w, f.x, h1);
+                h2 = fmaf(w, f.y, h2);
+                h3 = fmaf(w, f.z, h3);
             }
             float* o = dbuf + ((size_t)py * W + px) * 9 + c * 3;
             o[0] = h1;
@@ -226,9 +231,9 @@ __global__ __launch_bounds__(256) void k_ssim_v_bwd(int W, int H, const float* _
 #pragma unroll
             for (int d = 0; d < WIN; ++d) {
                 const float w = GAUSS_1D[WIN - 1 - d];
-                f1 += w * h1[d * VX * 9];
-                f2 += w * h1[d * VX * 9 + 1];
-                f3 += w * h1[d * VX * 9 + 2];
+                f1 = fmaf(w, h1[d * VX * 9], f1);
+                f2 = fmaf(w, h1[d * VX * 9 + 1], f2);
+                f3 = fmaf(w, h1[d * VX * 9 + 2], f3);
             }
             const size_t q = ((size_t)py * W + px) * 3 + c;
             const float r = img[q], g = gt[q];

@@ -1041,9 +1041,14 @@ double orc_ssim_loss(int32_t H, int32_t W, const float* img, const float* gt, fl
                         gv = gt[((size_t)y * W + xx) * 3 + c];
                         rv = img[((size_t)y * W + xx) * 3 + c];
                     }
+                    // one fma per window term, (w gv) gv as a product then an
+                    // fma: the reference's w * gv * gv with the sum contracted
+                    // as its fast-math Metal build may do (and the kernels do)
                     const float w = GAUSS_1D[d];
-                    mx += w * gv; my += w * rv; sx += w * gv * gv; sy += w * rv * rv;
-                    cxy += w * gv * rv;
+                    const float wg = w * gv, wr = w * rv;
+                    mx = std::fma(w, gv, mx); my = std::fma(w, rv, my);
+                    sx = std::fma(wg, gv, sx); sy = std::fma(wr, rv, sy);
+                    cxy = std::fma(wg, rv, cxy);
                 }
                 float* o = &hb[((size_t)y * W + x) * 15 + c * 5];
                 o[0] = mx; o[1] = my; o[2] = sx; o[3] = sy; o[4] = cxy;
@@ -1071,7 +1076,9 @@ double orc_ssim_loss(int32_t H, int32_t W, const float* img, const float* gt, fl
                     if (x >= 0 && x < W && yy >= 0 && yy < H)
                         for (int f = 0; f < 5; ++f) h[f] = hb[((size_t)yy * W + x) * 15 + c * 5 + f];
                     const float w = GAUSS_1D[k];
-                    mx += w * h[0]; my += w * h[1]; sx += w * h[2]; sy += w * h[3]; cxy += w * h[4];
+                    mx = std::fma(w, h[0], mx); my = std::fma(w, h[1], my);
+                    sx = std::fma(w, h[2], sx); sy = std::fma(w, h[3], sy);
+                    cxy = std::fma(w, h[4], cxy);
                 }
                 const float sxs = sx - mx * mx, sys = sy - my * my, sxy = cxy - mx * my;
                 const float A = 2.0f * mx * my + SSIM_C1, B = 2.0f * sxy + SSIM_C2;
@@ -1103,7 +1110,7 @@ double orc_ssim_loss(int32_t H, int32_t W, const float* img, const float* gt, fl
                 for (int d = 0; d < 11; ++d) {
                     const float w = GAUSS_1D[10 - d];
                     const float* f = &F[((size_t)y * WE + (x + d)) * 9 + c * 3];
-                    h1 += w * f[0]; h2 += w * f[1]; h3 += w * f[2];
+                    h1 = std::fma(w, f[0], h1); h2 = std::fma(w, f[1], h2); h3 = std::fma(w, f[2], h3);
                 }
                 float* o = &D[((size_t)y * W + x) * 9 + c * 3];
                 o[0] = h1; o[1] = h2; o[2] = h3;
@@ -1133,7 +1140,7 @@ double orc_ssim_loss(int32_t H, int32_t W, const float* img, const float* gt, fl
                             a = o[0]; b = o[1]; cc = o[2];
                         }
                         const float w = GAUSS_1D[10 - d];
-                        f1 += w * a; f2 += w * b; f3 += w * cc;
+                        f1 = std::fma(w, a, f1); f2 = std::fma(w, b, f2); f3 = std::fma(w, cc, f3);
                     }
                     const size_t q = ((size_t)y * W + x) * 3 + c;
                     const float r = img[q], g = gt[q];
