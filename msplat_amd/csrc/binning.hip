@@ -614,7 +614,10 @@ void launch_depth_order(hipStream_t s, int N, uint32_t* dkey, uint32_t* dval, ui
     // the sort's last pass gathers the rectangles into depth order and
     // counts their super-tiles
     const RectGather rg{rect, rect_sorted, rcount};
-    const bool flip = launch_radix_sort(s, dkey, dval, dkey2, dval2, N, 32, radix_temp, &rg, ss);
+    // culled gaussians (key 0xFFFFFFFF) go behind the visible ones in the
+    // first pass and the later passes sort only the visible ones
+    const bool flip = launch_radix_sort(s, dkey, dval, dkey2, dval2, N, 32, radix_temp, &rg, ss,
+                                        nullptr, nullptr, true);
     uint32_t* order = flip ? dval2 : dval;
     *order_out = order;
     if (N <= 0) return;
@@ -637,14 +640,15 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
                            p.N, sbx, order, rtot, rect_sorted, rb.key, rb.val);
         int bits = 0;
         while ((1 << bits) < S) ++bits;
-        // a single-pass sort (at most 256 super-tiles) writes the super-tiles'
-        // reference ranges itself; otherwise they are found in the sorted keys
+        // a single-pass sort (at most 512 super-tiles, 9 bits) writes the
+        // super-tiles' reference ranges itself; otherwise they are found in
+        // the sorted keys
         if (launch_radix_sort(s, rb.key, rb.val, rb.key2, rb.val2, R, bits, rb.radix_temp, nullptr,
                               nullptr, rb.st_r0, rb.st_r1)) {
             rk = rb.key2;
             rv = rb.val2;
         }
-        if (bits == 0 || bits > 8)   // one super-tile (no sort), or a two-pass sort
+        if (bits == 0 || bits > 9)   // one super-tile (no sort), or a two-pass sort
             hipLaunchKernelGGL(k_ref_edges, dim3(blocks_for(R)), dim3(256), 0, s, (int)R, rk,
                                rb.st_r0, rb.st_r1);
     }

@@ -129,8 +129,9 @@ __host__ __device__ inline unsigned long long totals_word(unsigned long long i, 
     return (1ull << 63) | ((i < cap ? i : cap) << 31) | (r < cap ? r : cap);
 }
 // Optional epilogue of a sort's last pass, for the depth order: output
-// position i also gets rs[i] = rect[value] (zero for the culled key
-// 0xFFFFFFFF) and cnt[i] = the super-tile count of that rectangle.
+// position i also gets rs[i] = rect[value] and cnt[i] = the super-tile count
+// of that rectangle (both zero for the culled key 0xFFFFFFFF, and at the
+// positions of a culling sort's culled tail).
 struct RectGather {
     const uint2* rect;
     uint2* rs;
@@ -138,7 +139,8 @@ struct RectGather {
 };
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
                        int64_t n, int bits, int* temp, const RectGather* rg = nullptr,
-                       const SlotSum* ss = nullptr, int* edge0 = nullptr, int* edge1 = nullptr);
+                       const SlotSum* ss = nullptr, int* edge0 = nullptr, int* edge1 = nullptr,
+                       bool cull = false);
 
 // Super-tiles: SUPER x SUPER tiles of the tile grid.  A gaussian's tile
 // rectangle is cut into one reference per super-tile it overlaps; the

@@ -3,8 +3,9 @@
 // their super-tile references by super-tile, and by the nearest-neighbour
 // search to order points by cell.
 //
-// Sort: digits of up to 8 bits, reduce-then-scan per pass over 2048-key
-// blocks (512 threads x 4 keys):
+// Sort: digits of up to 8 bits (9 for a sort of at most 9 bits, done in one
+// pass), reduce-then-scan per pass over 2048-key blocks (512 threads x 4
+// keys):
 //   1. per-block digit histograms in LDS -> hist[digit][block], and the
 //      digit totals over all blocks (one global atomic per block and digit)
 //   2. one workgroup per digit scans its row of hist and adds the keys of
@@ -16,6 +17,13 @@
 //      runs (coalesced stores).
 // Stability makes the result independent of how work is scheduled: equal keys
 // keep their input order.
+// The depth order sorts with "cull" set: in the first pass the key
+// 0xFFFFFFFF (a culled gaussian) is a digit of its own after all others, so
+// the culled keys end up behind the visible ones in input order, and the
+// later passes sort only the visible keys (their count, written by the first
+// pass, is read on the device).  The visible keys get the order a full sort
+// of all keys gives them; the culled tail is left where the first pass put
+// it, and the last pass writes empty rectangles for it.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -30,7 +38,19 @@ constexpr int RB = RT * RK;        // keys per block
 constexpr int WK = RK * 64;        // keys per wave (RK rounds of 64)
 constexpr int SB = SCAN_BLOCK;     // elements per scan block
 constexpr int MAX_PASSES = 4;      // 32-bit keys in 8-bit digits
+constexpr int DMAX = 512;          // digit slots of the widest pass (9 bits, or 8 + the culled digit)
 constexpr int DCOPIES = 16;        // copies of the digit totals (block b adds to copy b % 16)
+
+// Digit of key k in a pass: bits [shift, shift + width) (mask), or mask + 1
+// for the culled key 0xFFFFFFFF when cull is set.
+__device__ __forceinline__ int digit_of(uint32_t k, int shift, uint32_t mask, bool cull) {
+    return (cull && k == 0xFFFFFFFFu) ? (int)mask + 1 : (int)((k >> shift) & mask);
+}
+
+// Keys a pass covers: n, or the count the culling first pass wrote.
+__device__ __forceinline__ int64_t pass_n(int64_t n, const int* n_dev) {
+    return n_dev ? (int64_t)*n_dev : n;
+}
 
 // Sum of v over the NT threads of a block (sh: NT / 64 ints).
 template <int NT>
@@ -143,11 +163,18 @@ __global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
     }
 }
 
+// Per-block digit counts.  D: digit slots (256, or 512 for a 9-bit or
+// culling pass).  With agg (the top byte of depth keys, where a wave's keys
+// mostly share one or two digits) a wave first adds up to four groups of
+// lanes with equal digits with one atomic each, so that the LDS atomics of
+// one address are not serialised 64 deep; the lanes left add one each.
+template <int D>
 __global__ __launch_bounds__(RT) void k_radix_hist(const uint32_t* __restrict__ keys, int64_t n,
-                                                   int shift, uint32_t mask, int nblocks,
+                                                   const int* __restrict__ n_dev, int shift,
+                                                   uint32_t mask, int cull, int agg, int nblocks,
                                                    int* __restrict__ hist, int* __restrict__ dtot,
                                                    SlotSum ss) {
-    __shared__ int h[256];
+    __shared__ int h[D];
     if (ss.out && blockIdx.x == 0 && threadIdx.x < 64) {
         // lane k reads slot k's pair; the wave sums them
         unsigned long long ti = 0, tr = 0;
@@ -164,20 +191,39 @@ __global__ __launch_bounds__(RT) void k_radix_hist(const uint32_t* __restrict__ 
         if (threadIdx.x == 0)
             __hip_atomic_store(ss.out, totals_word(ti, tr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
-    if (threadIdx.x < 256) h[threadIdx.x] = 0;
-    __syncthreads();
+    const int64_t ne = pass_n(n, n_dev);
     const int64_t base = (int64_t)blockIdx.x * RB;
+    if (base >= ne) return;   // beyond the keys (the offsets scan only the blocks that hold some)
+    if (threadIdx.x < D) h[threadIdx.x] = 0;
+    __syncthreads();
+    const bool cl = cull != 0;
 #pragma unroll
     for (int k = 0; k < RK; ++k) {
         const int64_t i = base + k * RT + threadIdx.x;
-        if (i < n) atomicAdd(&h[(keys[i] >> shift) & mask], 1);
+        const bool ok = i < ne;
+        const int d = ok ? digit_of(keys[i], shift, mask, cl) : 0;
+        bool left = ok;
+        if (agg) {
+            for (int r = 0; r < 4; ++r) {
+                const uint64_t act = wave_ballot(left);
+                if (act == 0) break;
+                // the lowest lane still left picks the digit of this round
+                const int first = (int)__builtin_ctzll(act);
+                const int dl = __builtin_amdgcn_readlane(d, first);
+                const uint64_t same = wave_ballot(left && d == dl);
+                if ((int)(threadIdx.x & 63) == first) atomicAdd(&h[dl], __popcll(same));
+                if (left && d == dl) left = false;
+            }
+        }
+        if (left) atomicAdd(&h[d], 1);
     }
     __syncthreads();
-    if (threadIdx.x <= mask) {
+    const int nd = (int)mask + 1 + (cl ? 1 : 0);
+    if ((int)threadIdx.x < nd) {
         const int c = h[threadIdx.x];
         hist[(size_t)threadIdx.x * nblocks + blockIdx.x] = c;
         // the digit's total over all blocks, spread over DCOPIES addresses
-        if (c) atomicAdd(&dtot[(blockIdx.x % DCOPIES) * 256 + threadIdx.x], c);
+        if (c) atomicAdd(&dtot[(blockIdx.x % DCOPIES) * D + threadIdx.x], c);
     }
 }
 
@@ -202,28 +248,36 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* sh) {
 // Scatter offsets of one digit (one workgroup per digit d): hist[d][b]
 // becomes the position of block b's first key with digit d, i.e. the keys
 // of all smaller digits (sum of the dtot copies over d' < d) plus those of
-// digit d in the blocks before b (exclusive scan of the row).
+// digit d in the blocks before b (exclusive scan of the row over the blocks
+// that hold keys of this pass).
 // With edge0 (a single-pass sort) the digit's output range [start, end)
-// also goes to edge0[d], edge1[d] when the digit occurs.
+// also goes to edge0[d], edge1[d] when the digit occurs.  With nvis the
+// workgroup of digit cull_digit (the culled key's) writes its start, the
+// number of visible keys, there.
+template <int D>
 __global__ __launch_bounds__(1024) void k_radix_offsets(int* __restrict__ hist, int nblocks,
+                                                        int64_t n, const int* __restrict__ n_dev,
                                                         const int* __restrict__ dtot,
                                                         int* __restrict__ edge0,
-                                                        int* __restrict__ edge1) {
+                                                        int* __restrict__ edge1,
+                                                        int* __restrict__ nvis, int cull_digit) {
     __shared__ int sh[16];
     const int d = blockIdx.x, t = threadIdx.x;
     int lower = 0;
     if (t < d) {
 #pragma unroll
-        for (int c = 0; c < DCOPIES; ++c) lower += dtot[c * 256 + t];
+        for (int c = 0; c < DCOPIES; ++c) lower += dtot[c * D + t];
     }
     int carry = block_sum<1024>(lower, sh);
     const int start = carry;
+    if (nvis && d == cull_digit && t == 0) *nvis = start;
+    const int nbe = (int)((pass_n(n, n_dev) + RB - 1) / RB);
     int* row = hist + (size_t)d * nblocks;
-    for (int c = 0; c < nblocks; c += 1024) {
+    for (int c = 0; c < nbe; c += 1024) {
         const int i = c + t;
-        const int v = i < nblocks ? row[i] : 0;
+        const int v = i < nbe ? row[i] : 0;
         const int ex = block_exclusive_scan<1024>(v, sh);
-        if (i < nblocks) row[i] = carry + ex;
+        if (i < nbe) row[i] = carry + ex;
         carry += block_sum<1024>(v, sh);
     }
     if (edge0 && t == 0 && carry > start) {
@@ -232,36 +286,52 @@ __global__ __launch_bounds__(1024) void k_radix_offsets(int* __restrict__ hist, 
     }
 }
 
-// One LSD pass over the digit (key >> shift) & mask (nbits bits, <= 8).
-// Keys are ranked stably inside the block (each wave ranks its RB/4
+// One LSD pass over the digit of each key (digit_of: dbits bits, at most D
+// values).  Keys are ranked stably inside the block (each wave ranks its RB/4
 // consecutive keys in 64-key rounds by ballot-matching the digit bits and
 // keeps per-digit running counts), reordered by digit in LDS, and written out
 // in digit runs so that neighbouring lanes store neighbouring addresses.
-template <bool RG>
+// With RG (the depth order's last pass) the rectangles of the values go to
+// the same positions with their super-tile counts, and the positions past
+// the pass's keys (the culled tail) get empty ones.
+template <bool RG, int D>
 __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict__ kin,
                                                       const uint32_t* __restrict__ vin,
                                                       uint32_t* __restrict__ kout,
                                                       uint32_t* __restrict__ vout, int64_t n,
-                                                      int shift, uint32_t mask, int nbits,
+                                                      const int* __restrict__ n_dev, int shift,
+                                                      uint32_t mask, int cull, int dbits,
                                                       int nblocks, const int* __restrict__ offs,
                                                       int* __restrict__ dtot, RectGather rg) {
     // The pass's digit totals were last read by the offsets kernel: block 0
     // clears them for the next sort that uses this scratch.
     if (blockIdx.x == 0)
-        for (int i = threadIdx.x; i < DCOPIES * 256; i += RT) dtot[i] = 0;
+        for (int i = threadIdx.x; i < DCOPIES * D; i += RT) dtot[i] = 0;
+    const int64_t ne = pass_n(n, n_dev);
+    const int64_t bbase = (int64_t)blockIdx.x * RB;
+    if (RG) {
+        // output positions [ne, n) of this block's range: the culled tail
+        for (int64_t p = max(bbase, ne) + threadIdx.x; p < min(bbase + RB, n); p += RT) {
+            rg.rs[p] = make_uint2(0u, 0u);
+            rg.cnt[p] = 0;
+        }
+    }
+    if (bbase >= ne) return;
     __shared__ uint32_t s_key[RB];
     __shared__ uint32_t s_val[RB];
-    __shared__ int wcnt[RW][256];
-    __shared__ int dstart[256];
-    __shared__ int gofs[256];
+    __shared__ int wcnt[RW][D];
+    __shared__ int dstart[D];
+    __shared__ int gofs[D];
     __shared__ int scan_sh[RW];
+    const bool cl = cull != 0;
+    const int nd = (int)mask + 1 + (cl ? 1 : 0);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     // this block's scatter offset of digit tid, loaded now so that its latency
     // overlaps the key loads and the ranking
-    const int my_gofs = (tid < 256 && (uint32_t)tid <= mask) ? offs[(size_t)tid * nblocks + blockIdx.x] : 0;
-    for (int i = tid; i < RW * 256; i += RT) (&wcnt[0][0])[i] = 0;
+    const int my_gofs = tid < nd ? offs[(size_t)tid * nblocks + blockIdx.x] : 0;
+    for (int i = tid; i < RW * D; i += RT) (&wcnt[0][0])[i] = 0;
     __syncthreads();
-    const int64_t wbase = (int64_t)blockIdx.x * RB + (int64_t)w * WK;
+    const int64_t wbase = bbase + (int64_t)w * WK;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     uint32_t key[RK], val[RK];
     int dig[RK], rank[RK];
@@ -269,15 +339,15 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
 #pragma unroll
     for (int j = 0; j < RK; ++j) {
         const int64_t i = wbase + j * 64 + lane;
-        const bool ok = i < n;
+        const bool ok = i < ne;
         key[j] = ok ? kin[i] : 0u;
         val[j] = ok ? vin[i] : 0u;
         if (RG) rc[j] = ok && key[j] != 0xFFFFFFFFu ? rg.rect[val[j]] : make_uint2(0u, 0u);
-        const int d = ok ? (int)((key[j] >> shift) & mask) : 256;
+        const int d = ok ? digit_of(key[j], shift, mask, cl) : D;
         dig[j] = d;
         uint64_t peers = wave_ballot(ok);
         if (!ok) peers = ~peers;
-        for (int b = 0; b < nbits; ++b) {
+        for (int b = 0; b < dbits; ++b) {
             const uint64_t bb = wave_ballot((d >> b) & 1);
             peers &= ((d >> b) & 1) ? bb : ~bb;
         }
@@ -289,10 +359,10 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
         if (ok && before == 0) wcnt[w][dd] = base_cnt + __popcll(peers);
     }
     __syncthreads();
-    // per digit (threads 0..255): offsets of the waves in wave order, the
+    // per digit (threads 0..D-1): offsets of the waves in wave order, the
     // block's count and its start
     int cnt = 0;
-    if (tid < 256) {
+    if (tid < D) {
         const int d = tid;
 #pragma unroll
         for (int ww = 0; ww < RW; ++ww) {
@@ -303,21 +373,21 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
         gofs[d] = my_gofs;
     }
     const int start = block_exclusive_scan<RT>(cnt, scan_sh);
-    if (tid < 256) dstart[tid] = start;
+    if (tid < D) dstart[tid] = start;
     __syncthreads();
     int lpos[RK];      // each key's place in the block's digit order
 #pragma unroll
     for (int j = 0; j < RK; ++j) {
         const int d = dig[j];
         lpos[j] = -1;
-        if (d > 255) continue;
+        if (d >= D) continue;
         const int p = dstart[d] + wcnt[w][d] + rank[j];
         lpos[j] = p;
         s_key[p] = key[j];
         s_val[p] = val[j];
     }
     __syncthreads();
-    const int nvalid = (int)min((int64_t)RB, n - (int64_t)blockIdx.x * RB);
+    const int nvalid = (int)min((int64_t)RB, ne - bbase);
     int64_t opos[RK];  // output position of block element tid + u RT
 #pragma unroll
     for (int u = 0; u < RK; ++u) {
@@ -325,7 +395,7 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
         opos[u] = -1;
         if (p >= nvalid) continue;
         const uint32_t k = s_key[p];
-        const int d = (int)((k >> shift) & mask);
+        const int d = digit_of(k, shift, mask, cl);
         const int64_t pos = (int64_t)gofs[d] + (p - dstart[d]);
         kout[pos] = k;
         vout[pos] = s_val[p];
@@ -399,28 +469,58 @@ void launch_exclusive_scan_i32(hipStream_t s, const int* in, int* out, int64_t n
 
 int64_t radix_temp_ints(int64_t n) {
     const int64_t nb = (n + RB - 1) / RB;
-    return DCOPIES * 256 * MAX_PASSES + 256 * nb + 8;
+    return DCOPIES * DMAX * MAX_PASSES + (int64_t)DMAX * nb + 16;
 }
 
+namespace {
+
+// The three kernels of one pass with D digit slots.
+template <int D>
+void launch_pass(hipStream_t s, const uint32_t* ki, const uint32_t* vi, uint32_t* ko, uint32_t* vo,
+                 int64_t n, const int* n_dev, int shift, uint32_t mask, bool cull, int dbits, bool agg,
+                 int nb, int* hist, int* dt, const SlotSum& side, int* edge0, int* edge1, int* nvis,
+                 const RectGather* rg) {
+    const int nd = (int)mask + 1 + (cull ? 1 : 0);
+    hipLaunchKernelGGL(k_radix_hist<D>, dim3(nb), dim3(RT), 0, s, ki, n, n_dev, shift, mask,
+                       cull ? 1 : 0, agg ? 1 : 0, nb, hist, dt, side);
+    hipLaunchKernelGGL(k_radix_offsets<D>, dim3(nd), dim3(1024), 0, s, hist, nb, n, n_dev,
+                       (const int*)dt, edge0, edge1, cull ? nvis : nullptr, nd - 1);
+    if (rg)
+        hipLaunchKernelGGL((k_radix_scatter<true, D>), dim3(nb), dim3(RT), 0, s, ki, vi, ko, vo, n, n_dev,
+                           shift, mask, cull ? 1 : 0, dbits, nb, (const int*)hist, dt, *rg);
+    else
+        hipLaunchKernelGGL((k_radix_scatter<false, D>), dim3(nb), dim3(RT), 0, s, ki, vi, ko, vo, n,
+                           n_dev, shift, mask, cull ? 1 : 0, dbits, nb, (const int*)hist, dt,
+                           RectGather{});
+}
+
+}  // namespace
+
 // Sorts (k0, v0) by the bits [0, bits) of the keys; ping-pongs with (k1, v1).
-// The bits are split into ceil(bits / 8) passes of equal width (fewer digit
-// values give longer runs per digit and block).  Returns true when the result
-// ends up in (k1, v1).  With rg the last pass also writes each output
-// position's rectangle and super-tile count (RectGather); with ss the first
-// kernel also does the SlotSum job; with edge0 / edge1 and at most 8 bits
-// (one pass) each occurring key value k gets its output range
-// [edge0[k], edge1[k]) (entries of absent values are not written).
+// A sort of at most 9 bits takes one pass; otherwise the bits are split into
+// ceil(bits / 8) passes of equal width (fewer digit values give longer runs
+// per digit and block).  Returns true when the result ends up in (k1, v1).
+// With rg the last pass also writes each output position's rectangle and
+// super-tile count (RectGather); with ss the first kernel also does the
+// SlotSum job; with edge0 / edge1 and one pass each occurring key value k
+// gets its output range [edge0[k], edge1[k]) (entries of absent values are
+// not written).  With cull (32-bit depth keys) the keys 0xFFFFFFFF are put
+// behind the others by the first pass and the later passes sort only the
+// others; positions [visible, n) of the result then hold no sorted keys,
+// and rg marks them empty.
 bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1,
                        int64_t n, int bits, int* temp, const RectGather* rg, const SlotSum* ss,
-                       int* edge0, int* edge1) {
+                       int* edge0, int* edge1, bool cull) {
     if (n <= 0 || bits <= 0) return false;
     const int nb = (int)((n + RB - 1) / RB);
-    const int passes = (bits + 7) / 8;
+    const int passes = bits <= 9 ? 1 : (bits + 7) / 8;
     // Scratch layout: the digit totals first, at a fixed place whatever n is
-    // (DCOPIES x 256 per pass; each pass's scatter clears its totals for the
-    // next sort on this scratch), then the per-block histograms.
+    // (DCOPIES x DMAX per pass; each pass's scatter clears its totals for the
+    // next sort on this scratch), then the per-block histograms, then the
+    // visible count of a culling sort.
     int* dtot = temp;
-    int* hist = temp + DCOPIES * 256 * MAX_PASSES;
+    int* hist = temp + DCOPIES * DMAX * MAX_PASSES;
+    int* nvis = hist + (size_t)DMAX * nb;
     // the digit totals arrive zeroed: fresh scratch is, and each pass's
     // scatter clears its own
     bool flip = false;
@@ -428,25 +528,28 @@ bool launch_radix_sort(hipStream_t s, uint32_t* k0, uint32_t* v0, uint32_t* k1, 
     for (int pass = 0; pass < passes; ++pass) {
         const int width = (bits - shift + (passes - pass) - 1) / (passes - pass);
         const uint32_t mask = (1u << width) - 1u;
+        const bool pcull = cull && pass == 0;
+        const int nd = (int)mask + 1 + (pcull ? 1 : 0);
+        int dbits = 0;
+        while ((1 << dbits) < nd) ++dbits;
         uint32_t* ki = flip ? k1 : k0;
         uint32_t* vi = flip ? v1 : v0;
         uint32_t* ko = flip ? k0 : k1;
         uint32_t* vo = flip ? v0 : v1;
-        int* dt = dtot + DCOPIES * 256 * pass;
+        int* dt = dtot + DCOPIES * DMAX * pass;
         const SlotSum side = ss && pass == 0 ? *ss : SlotSum{nullptr, nullptr};
-        hipLaunchKernelGGL(k_radix_hist, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki, n, shift,
-                           mask, nb, hist, dt, side);
-        hipLaunchKernelGGL(k_radix_offsets, dim3(mask + 1), dim3(1024), 0, s, hist, nb,
-                           (const int*)dt, passes == 1 ? edge0 : nullptr,
-                           passes == 1 ? edge1 : nullptr);
-        if (rg && pass == passes - 1)
-            hipLaunchKernelGGL(k_radix_scatter<true>, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki,
-                               (const uint32_t*)vi, ko, vo, n, shift, mask, width, nb,
-                               (const int*)hist, dt, *rg);
+        const int* n_dev = cull && pass > 0 ? nvis : nullptr;
+        // the top byte of depth keys: a wave's keys mostly share a digit
+        const bool agg = cull && shift == 24;
+        const RectGather* prg = rg && pass == passes - 1 ? rg : nullptr;
+        int* e0 = passes == 1 ? edge0 : nullptr;
+        int* e1 = passes == 1 ? edge1 : nullptr;
+        if (nd > 256)
+            launch_pass<DMAX>(s, ki, vi, ko, vo, n, n_dev, shift, mask, pcull, dbits, agg, nb, hist, dt,
+                              side, e0, e1, nvis, prg);
         else
-            hipLaunchKernelGGL(k_radix_scatter<false>, dim3(nb), dim3(RT), 0, s, (const uint32_t*)ki,
-                               (const uint32_t*)vi, ko, vo, n, shift, mask, width, nb,
-                               (const int*)hist, dt, RectGather{});
+            launch_pass<256>(s, ki, vi, ko, vo, n, n_dev, shift, mask, pcull, dbits, agg, nb, hist, dt,
+                             side, e0, e1, nvis, prg);
         flip = !flip;
         shift += width;
     }
