@@ -452,25 +452,27 @@ def main():
     ap.add_argument("--pmc-summary", default="",
                     help="only print a markdown table of the counters of this rocprofv3 --pmc csv output "
                          "directory for --pmc-kernels (last --steps dispatches of each) and exit")
-    ap.add_argument("--pmc-kernels", default="k_raster_fwd,k_raster_bwd,k_radix_hist,k_radix_scatter<false>,"
-                                             "k_radix_scatter<true>,k_seg_write,"
-                                             "k_ssim_fused,k_ssim_v_bwd,k_project_fwd,k_sh_rest_adam,"
-                                             "k_proj_bwd_adam")
+    ap.add_argument("--pmc-kernels", default="k_raster_fwd;k_raster_bwd;k_radix_hist<256>;k_radix_hist<512>;"
+                                             "k_radix_scatter<false, 256>;k_radix_scatter<false, 512>;"
+                                             "k_radix_scatter<true, 256>;k_seg_write;"
+                                             "k_ssim_fused;k_ssim_v_bwd;k_project_fwd;k_sh_rest_adam;"
+                                             "k_proj_bwd_adam",
+                    help="semicolon-separated kernels for --pmc-summary (template arguments hold commas)")
     ap.add_argument("--traffic-summary", nargs=4, default=None,
                     metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="only print the HBM traffic JSON of the raster backward from four "
                          "rocprofv3 --pmc csv directories (the copy runs use --copy-mib) and exit")
     ap.add_argument("--traffic-kernels", default="k_raster_bwd",
-                    help="comma-separated kernels for --traffic-summary (one: a flat JSON object)")
+                    help="semicolon-separated kernels for --traffic-summary (one: a flat JSON object)")
     args = ap.parse_args()
     if args.traffic_summary:
-        kernels = args.traffic_kernels.split(",")
+        kernels = args.traffic_kernels.split(";")
         res = {k: traffic_summary(args.traffic_summary, args.copy_mib or 1024, args.steps,
                                   args.rocprof_command, k) for k in kernels}
         print(json.dumps(res[kernels[0]] if len(kernels) == 1 else res, indent=1))
         return
     if args.pmc_summary:
-        print(pmc_summary(args.pmc_summary, args.pmc_kernels.split(","), args.steps, args.rocprof_command), end="")
+        print(pmc_summary(args.pmc_summary, args.pmc_kernels.split(";"), args.steps, args.rocprof_command), end="")
         return
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary, args.preroll + args.warmup, args.steps,

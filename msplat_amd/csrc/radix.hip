@@ -164,10 +164,11 @@ __global__ __launch_bounds__(256) void k_block_scan(const int* __restrict__ in,
 }
 
 // Per-block digit counts.  D: digit slots (256, or 512 for a 9-bit or
-// culling pass).  With agg (the top byte of depth keys, where a wave's keys
-// mostly share one or two digits) a wave first adds up to four groups of
-// lanes with equal digits with one atomic each, so that the LDS atomics of
-// one address are not serialised 64 deep; the lanes left add one each.
+// culling pass).  LDS atomics on one address from many lanes of a wave are
+// serialised, so lanes that share a digit are counted with one atomic where
+// that is common: the culled keys' digit of a culling pass, and with agg (the
+// top byte of depth keys, where a wave's keys mostly share one or two
+// digits) up to four groups of equal digits; the lanes left add one each.
 template <int D>
 __global__ __launch_bounds__(RT) void k_radix_hist(const uint32_t* __restrict__ keys, int64_t n,
                                                    const int* __restrict__ n_dev, int shift,
@@ -203,6 +204,15 @@ __global__ __launch_bounds__(RT) void k_radix_hist(const uint32_t* __restrict__ 
         const bool ok = i < ne;
         const int d = ok ? digit_of(keys[i], shift, mask, cl) : 0;
         bool left = ok;
+        if (cl) {
+            // the culled keys' digit (about a third of the keys): one atomic
+            // for all of the wave's lanes that hold it
+            const bool cu = ok && d == (int)mask + 1;
+            const uint64_t cm = wave_ballot(cu);
+            if (cm && (int)(threadIdx.x & 63) == (int)__builtin_ctzll(cm))
+                atomicAdd(&h[mask + 1], __popcll(cm));
+            if (cu) left = false;
+        }
         if (agg) {
             for (int r = 0; r < 4; ++r) {
                 const uint64_t act = wave_ballot(left);
