@@ -101,7 +101,7 @@ struct Ctx {
     // per item
     Buf it_tile, it_k, it_order, tile_order, it_cls, c_T, c_C, c_idx, c_pT, c_aC;
     // per pixel
-    Buf final_T, final_idx, out_img, dbuf, v_rendered, loss_part;
+    Buf final_T, final_idx, out_img, v_rendered, loss_part;
     // scalars
     Buf meta_d, loss_d, count_d, work_d;
     // intersection and reference totals of the projection: ISECT_SLOTS
@@ -197,7 +197,7 @@ void free_all(Ctx* c) {
                    &c->tval,
                    &c->it_tile, &c->it_k, &c->it_order, &c->tile_order, &c->it_cls, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
-                   &c->dbuf, &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
+                   &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
                    &c->count_d, &c->work_d, &c->isect_d, &c->eval_part, &c->eval_out, &c->knn_k, &c->knn_v, &c->knn_k2, &c->knn_v2,
                    &c->knn_tmp, &c->knn_s, &c->knn_e, &c->d_split, &c->d_dup, &c->d_sp, &c->d_dp, &c->d_keep, &c->d_kp,
                    &c->d_tot, &c->d_scratch, &c->d_rnd, &c->d_src};
@@ -716,14 +716,13 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
     const CamParams p = cam_params(&a->r);
     const size_t Px = (size_t)p.W * p.H;
     const dim3 sgrid((p.W + 15) / 16, (p.H + 15) / 16);
-    ENSURE(c->dbuf, Px * 36);
     ENSURE(c->v_rendered, Px * 12);
     ENSURE(c->loss_part, (size_t)sgrid.x * sgrid.y * 12);
     ENSURE(c->loss_d, 16);
     stage_mark(c, S_LOSS);
     // the loss sum goes straight to pinned host memory (loss_h[1])
     launch_ssim(c->stream, p.H, p.W, P<float>(c->out_img), a->gt, a->ssim_weight, a->loss_inv_n,
-                P<float>(c->dbuf), P<float>(c->v_rendered), P<float>(c->loss_part),
+                P<float>(c->v_rendered), P<float>(c->loss_part),
                 c->loss_hd + 1);
     stage_mark(c, S_RBWD);
     launch_raster_bwd(c->stream, p, c->max_items, P<Meta>(c->meta_d), items(c),

@@ -233,7 +233,7 @@ void launch_raster_work(hipStream_t s, const CamParams& p, int64_t max_items, co
                         ChunkBufs cb, unsigned long long* out);
 
 void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
-                 float inv_n, float* dbuf, float* v_rendered, float* loss_part, float* loss_out);
+                 float inv_n, float* v_rendered, float* loss_part, float* loss_out);
 
 struct AdamHP {
     float step[6];

@@ -1,24 +1,26 @@
-// ssim.hip — separable 11-tap SSIM + L1 loss, forward and backward, on
-// LDS-staged tiles with halos.
+// ssim.hip — separable 11-tap SSIM + L1 loss, forward and backward, in one
+// LDS-staged tile kernel.
 //
-// Two passes with the reference's training semantics:
-//   h-fwd + v-fwd + h-bwd   ssim_h_fwd_kernel (.metal:3053-3115) and
-//                ssim_fused_v_fwd_h_bwd_kernel (.metal:3226-3313) in one
-//                workgroup per 16x16 tile: the horizontal zero-padded sums of
-//                x=gt, y=render (mu_x, mu_y, E[x^2], E[y^2], E[xy]) for the
-//                tile rows +-5 and columns +-5 are computed into LDS from the
-//                input (no intermediate buffer), then the vertical sums ->
-//                SSIM and its derivative fields f1, f2, f3 at every centre of
-//                the tile rows, including the 5-column halo outside the image
-//                (whose zero statistics give f = (0, -2/C2, 2/C2)), then the
-//                mirrored horizontal pass
+// The reference's training semantics, in five separable passes per channel:
+//   h-fwd        ssim_h_fwd_kernel (.metal:3053-3115): horizontal
+//                zero-padded sums of x = gt, y = render (mu_x, mu_y, E[x^2],
+//                E[y^2], E[xy]) at the in-image positions
+//   v-fwd + h-bwd  ssim_fused_v_fwd_h_bwd_kernel (.metal:3226-3313): the
+//                vertical sums -> SSIM and its derivative fields f1, f2, f3
+//                at every centre of the in-image rows, including the 5-column
+//                halo outside the image (whose zero statistics give
+//                f = (0, -2/C2, 2/C2)), then the mirrored horizontal pass
 //   v-bwd        ssim_v_bwd_kernel (.metal:3396-3464): mirrored vertical pass
 //                (rows outside the image contribute nothing) and the
 //                combination with the L1 sign term.
+// One workgroup computes all five for a TX x TY block of output pixels,
+// recomputing the halo each pass needs (rows +-10, columns +-10 of input)
+// instead of passing the horizontal-backward fields through memory: the
+// only HBM traffic is the two images with their halo and the gradient image.
 // Every sum is accumulated in the same order as the reference's separate
-// kernels, so the fusion changes no bit of the result.  Each window term is
-// added with one fused multiply-add (w gv gv as the product w gv, then an
-// fma with gv): the reference writes a product and a sum, which its
+// kernels, so the fusion changes no bit of the gradient image.  Each window
+// term is added with one fused multiply-add (w gv gv as the product w gv,
+// then an fma with gv): the reference writes a product and a sum, which its
 // fast-math Metal build may contract the same way; the CPU oracle evaluates
 // exactly these operations.
 // The loss is reduced per workgroup into (sum SSIM, sum L1, pixel count) and
@@ -34,55 +36,74 @@ namespace {
 constexpr int HALF = 5;
 constexpr int WIN = 11;
 
-// Fused forward / derivative / horizontal-backward tile: FX x FY output
-// pixels per workgroup of FT threads.  The horizontal sums are needed at
-// (FY + 10) x (FX + 10) positions and the derivative fields at FY x (FX + 10),
-// so a wide tile spends less of its work on the halo than a 16 x 16 one;
-// staging one channel at a time keeps the LDS at 48 KB for three
-// workgroups (six waves per SIMD) per CU.
-constexpr int FX = 32, FY = 16, FT = FX * FY;
-constexpr int FHX = FX + 2 * HALF;   // 42: columns with horizontal sums / fields
-constexpr int FHY = FY + 2 * HALF;   // 26: rows with horizontal sums
-constexpr int FIN = FHX + 2 * HALF;  // 52: input columns
-// LDS layouts, chosen so that every read of the three passes is free of bank
-// conflicts (64 banks of 4 bytes; a wave's 8-byte reads are served 32 lanes
-// at a time, its 16-byte reads 16 lanes at a time):
-//  * input: (gt, render) of a position as one float2, rows FIN_S float2
-//    apart.  The horizontal pass gives lane l the position p + l of a
-//    row-major walk over FHY x FHX, so 32 lanes cover at most two row pieces,
-//    [a, 42) of one row and [0, a - 10) of the next; FIN_S = 74 = 10 (mod 32)
-//    puts the second piece on exactly the 8-byte bank pairs the first leaves.
+// Tile of TX x TY output pixels, NT threads, and the regions of its passes
+// (rows / columns relative to the tile's first output pixel (x0, y0)):
+//   input (gt, render)    rows -10 .. TY+9,  columns -10 .. TX+9   IN_H x IN_W
+//   horizontal sums       rows -10 .. TY+9,  columns -5 .. TX+4    HS_H x HS_W
+//   fields f1, f2, f3     rows -5 .. TY+4,   columns -5 .. TX+4    FD_H x FD_W
+//   horizontal backward   rows -5 .. TY+4,   columns 0 .. TX-1     FD_H x TX
+//   vertical backward     rows 0 .. TY-1,    columns 0 .. TX-1     the outputs
+// For 32 x 32 outputs the horizontal sums are evaluated 2.13 times per
+// output, the fields 1.72 times and the horizontal backward 1.31 times.
+constexpr int TX = 32, TY = 32, NT = 512;
+constexpr int IN_W = TX + 4 * HALF;   // 52
+constexpr int IN_H = TY + 4 * HALF;   // 52
+constexpr int HS_W = TX + 2 * HALF;   // 42
+constexpr int HS_H = IN_H;            // 52
+constexpr int FD_W = HS_W;            // 42
+constexpr int FD_H = TY + 2 * HALF;   // 42
+// LDS layouts, chosen so that the passes' reads are free of bank conflicts
+// (64 banks of 4 bytes; a wave's 8-byte reads are served 32 lanes at a time,
+// its 16-byte reads 16 lanes at a time):
+//  * input: (gt, render) of a position as one float2, rows IN_S float2 apart.
+//    The horizontal pass gives lane l the position p + l of a row-major walk
+//    over HS_H x HS_W, so 32 lanes cover at most two row pieces, [a, 42) of
+//    one row and [0, a - 10) of the next; IN_S = 74 = 10 (mod 32) puts the
+//    second piece on exactly the 8-byte bank pairs the first leaves.
 //  * horizontal sums: (mu_x, mu_y, E[x^2], E[y^2]) as a float4 and E[xy] as a
-//    float, row-major over FHY x FHX (the passes' lanes read consecutive
-//    positions).
-//  * derivative fields (f1, f2, f3) as one float4 per position: the
-//    horizontal backward's 16-lane quarters read 16 consecutive positions of
-//    one row.
-constexpr int FIN_S = 74;
+//    float, row-major over HS_H x HS_W (the vertical pass's lanes read
+//    consecutive positions).
+//  * fields (f1, f2, f3) as one float4 per position, row-major over
+//    FD_H x FD_W: the horizontal backward's 16-lane quarters read 16
+//    consecutive positions of one row.
+//  * horizontal backward (h1, h2, h3) as one float4 per position, row-major
+//    over FD_H x TX: the vertical backward's lanes read consecutive columns.
+// The input and the fields share one LDS area, the horizontal sums and the
+// horizontal backward another (each pass reads one and writes the other):
+// 74.5 KB, two workgroups (four waves per SIMD) per CU.
+constexpr int IN_S = 74;
+constexpr int LDS_A = IN_H * IN_S * 8;                  // input; the fields (FD_H x FD_W x 16) fit
+constexpr int LDS_B = HS_H * HS_W * (16 + 4);           // horizontal sums; the backward (FD_H x TX x 16) fits
+static_assert(FD_H * FD_W * 16 <= LDS_A, "fields overflow the input's area");
+static_assert(FD_H * TX * 16 <= LDS_B, "horizontal backward overflows the sums' area");
+constexpr int NPOS = (IN_H * IN_W + NT - 1) / NT;      // input positions per thread
+constexpr int NOUT = TX * TY / NT;                      // output pixels per thread
 
-__global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __restrict__ img,
-                                                   const float* __restrict__ gt,
-                                                   float* __restrict__ dbuf,
-                                                   float* __restrict__ loss_part) {
-    __shared__ float2 s_in[FHY * FIN_S];     // (gt, render) of one channel, rows y0-5.., cols x0-10..
-    __shared__ float4 s_h4[FHY * FHX];       // mu_x, mu_y, E[x^2], E[y^2]
-    __shared__ float s_h1[FHY * FHX];        // E[xy]
-    __shared__ float4 s_f[FY * FHX];         // f1, f2, f3, (unused)
-    __shared__ float s_red[3][FT / 64];
-    const int tr = threadIdx.x, lx = tr % FX, ly = tr / FX;
-    const int bx = blockIdx.x * FX - HALF, by = blockIdx.y * FY - HALF;
+__global__ __launch_bounds__(NT) void k_ssim_tile(int W, int H, const float* __restrict__ img,
+                                                  const float* __restrict__ gt, float w_ssim,
+                                                  float inv_n, float* __restrict__ v_rendered,
+                                                  float* __restrict__ loss_part) {
+    __shared__ __align__(16) char lds_a[LDS_A];
+    __shared__ __align__(16) char lds_b[LDS_B];
+    __shared__ float s_red[3][NT / 64];
+    float2* s_in = reinterpret_cast<float2*>(lds_a);
+    float4* s_f = reinterpret_cast<float4*>(lds_a);
+    float4* s_h4 = reinterpret_cast<float4*>(lds_b);
+    float* s_h1 = reinterpret_cast<float*>(lds_b + HS_H * HS_W * 16);
+    float4* s_hb = reinterpret_cast<float4*>(lds_b);
+    const int t = threadIdx.x;
+    const int x0 = blockIdx.x * TX, y0 = blockIdx.y * TY;
     float ssim_sum = 0.f, l1_sum = 0.f, cnt = 0.f;
-    // The three channels of this thread's input pixels (rows by .. by+25,
-    // columns bx-5 .. bx+46, zero outside the image) are loaded once, into
-    // registers; each channel pass copies its component into LDS.
-    constexpr int NPOS = (FHY * FIN + FT - 1) / FT;
+    // The three channels of this thread's input positions (zero outside the
+    // image) are loaded once, into registers; each channel pass copies its
+    // component into LDS.
     float rg[NPOS][3], rr[NPOS][3];
 #pragma unroll
     for (int k = 0; k < NPOS; ++k) {
-        const int i = tr + k * FT;
-        const int sy = i / FIN, sx = i - sy * FIN;
-        const int gy = by + sy, gx = bx - HALF + sx;
-        const bool in = i < FHY * FIN && gx >= 0 && gx < W && gy >= 0 && gy < H;
+        const int i = t + k * NT;
+        const int iy = i / IN_W, ix = i - iy * IN_W;
+        const int gy = y0 - 2 * HALF + iy, gx = x0 - 2 * HALF + ix;
+        const bool in = i < IN_H * IN_W && gx >= 0 && gx < W && gy >= 0 && gy < H;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             const size_t q = ((size_t)gy * W + gx) * 3 + c;
@@ -90,25 +111,46 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
             rr[k][c] = in ? img[q] : 0.f;
         }
     }
+    // this thread's output pixels: column t % TX, rows t / TX + (NT / TX) j
+    const int ox = t % TX, oy0 = t / TX;
+    float og[NOUT][3], orr[NOUT][3], vr[NOUT][3];
+    bool oin[NOUT];
+#pragma unroll
+    for (int j = 0; j < NOUT; ++j) {
+        const int gx = x0 + ox, gy = y0 + oy0 + (NT / TX) * j;
+        oin[j] = gx < W && gy < H;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const size_t q = ((size_t)gy * W + gx) * 3 + c;
+            og[j][c] = oin[j] ? gt[q] : 0.f;
+            orr[j][c] = oin[j] ? img[q] : 0.f;
+            vr[j][c] = 0.f;
+        }
+        if (oin[j]) cnt += 1.f;
+    }
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
+        // the previous channel's vertical backward has read the horizontal
+        // backward before this channel's sums overwrite it, and its fields
+        // are consumed
         if (c > 0) __syncthreads();
 #pragma unroll
         for (int k = 0; k < NPOS; ++k) {
-            const int i = tr + k * FT;
-            if (i < FHY * FIN) {
-                const int sy = i / FIN, sx = i - sy * FIN;
-                s_in[sy * FIN_S + sx] = make_float2(rg[k][c], rr[k][c]);
+            const int i = t + k * NT;
+            if (i < IN_H * IN_W) {
+                const int iy = i / IN_W, ix = i - iy * IN_W;
+                s_in[iy * IN_S + ix] = make_float2(rg[k][c], rr[k][c]);
             }
         }
         __syncthreads();
-        // horizontal zero-padded sums (ssim_h_fwd, .metal:3053-3115) at the
-        // in-image positions of rows by.., columns bx..; zero elsewhere
-        for (int i = tr; i < FHY * FHX; i += FT) {
-            const int sy = i / FHX, sx = i - sy * FHX, gy = by + sy, gx = bx + sx;
+        // horizontal zero-padded sums (ssim_h_fwd, .metal:3094-3114) at the
+        // in-image positions; zero elsewhere
+        for (int i = t; i < HS_H * HS_W; i += NT) {
+            const int hy = i / HS_W, hx = i - hy * HS_W;
+            const int gy = y0 - 2 * HALF + hy, gx = x0 - HALF + hx;
             float mx = 0.f, my = 0.f, sxx = 0.f, syy = 0.f, cxy = 0.f;
             if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
-                const float2* row = s_in + sy * FIN_S + sx;
+                const float2* row = s_in + hy * IN_S + hx;
 #pragma unroll
                 for (int d = 0; d < WIN; ++d) {
                     const float w = GAUSS_1D[d];
@@ -126,14 +168,19 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
             s_h1[i] = cxy;
         }
         __syncthreads();
-        for (int i = tr; i < FY * FHX; i += FT) {
-            const int dy = i / FHX, dx = i - dy * FHX;
+        // vertical sums, SSIM and the derivative fields (.metal:3243-3300)
+        // at the centres of the in-image rows (the fields of other rows are
+        // never read: their horizontal backward is zero)
+        for (int i = t; i < FD_H * FD_W; i += NT) {
+            const int fy = i / FD_W, fx = i - fy * FD_W;
+            const int gy = y0 - HALF + fy, gx = x0 - HALF + fx;
+            if (gy < 0 || gy >= H) continue;
             float mx = 0.f, my = 0.f, sx = 0.f, sy = 0.f, cxy = 0.f;
 #pragma unroll
             for (int k = 0; k < WIN; ++k) {
                 const float w = GAUSS_1D[k];
-                const float4 h = s_h4[i + k * FHX];
-                const float h4 = s_h1[i + k * FHX];
+                const float4 h = s_h4[(fy + k) * HS_W + fx];
+                const float h4 = s_h1[(fy + k) * HS_W + fx];
                 mx = fmaf(w, h.x, mx);
                 my = fmaf(w, h.y, my);
                 sx = fmaf(w, h.z, sx);
@@ -147,100 +194,74 @@ __global__ __launch_bounds__(FT) void k_ssim_fused(int W, int H, const float* __
             const float dmu = 2.0f * B * (mx * Cd - A * my) / (Cd * Cd * D);
             const float dsyq = -A * B * iCD / D, dsxy = 2.0f * A * iCD;
             s_f[i] = make_float4(dmu - 2.0f * my * dsyq - mx * dsxy, 2.0f * dsyq, dsxy, 0.f);
-            if (dx >= HALF && dx < HALF + FX) {
-                const int gpx = bx + dx, gpy = by + dy + HALF;
-                if (gpx >= 0 && gpx < W && gpy >= 0 && gpy < H) {
-                    ssim_sum += (A * B) / (Cd * D);
-                    const float2 v = s_in[(dy + HALF) * FIN_S + dx + HALF];
-                    l1_sum += fabsf(v.x - v.y);
-                    if (c == 0) cnt += 1.f;
-                }
-            }
+            // the tile's own in-image outputs add their SSIM to the loss
+            if (fy >= HALF && fy < HALF + TY && fx >= HALF && fx < HALF + TX && gx >= 0 && gx < W)
+                ssim_sum += (A * B) / (Cd * D);
         }
         __syncthreads();
-        const int px = blockIdx.x * FX + lx, py = blockIdx.y * FY + ly;
-        if (px < W && py < H) {
+        // mirrored horizontal backward at the in-image rows of the tile's
+        // columns +- 5 rows (zero at rows outside the image)
+        for (int i = t; i < FD_H * TX; i += NT) {
+            const int by = i / TX, bx = i - by * TX;
+            const int gy = y0 - HALF + by;
             float h1 = 0.f, h2 = 0.f, h3 = 0.f;
-            const float4* fr = s_f + ly * FHX + lx;
+            if (gy >= 0 && gy < H) {
+                const float4* fr = s_f + by * FD_W + bx;
+#pragma unroll
+                for (int d = 0; d < WIN; ++d) {
+                    const float w = GAUSS_1D[WIN - 1 - d];
+                    const float4 f = fr[d];
+                    h1 = fmaf(w, f.x, h1);
+                    h2 = fmaf(w, f.y, h2);
+                    h3 = fmaf(w, f.z, h3);
+                }
+            }
+            s_hb[i] = make_float4(h1, h2, h3, 0.f);
+        }
+        __syncthreads();
+        // mirrored vertical backward (.metal:3443-3463) and the L1 term
+#pragma unroll
+        for (int j = 0; j < NOUT; ++j) {
+            if (!oin[j]) continue;
+            const int oy = oy0 + (NT / TX) * j;
+            float f1 = 0.f, f2 = 0.f, f3 = 0.f;
+            const float4* hr = s_hb + oy * TX + ox;
 #pragma unroll
             for (int d = 0; d < WIN; ++d) {
                 const float w = GAUSS_1D[WIN - 1 - d];
-                const float4 f = fr[d];
-                h1 = fmaf(w, f.x, h1);
-                h2 = fmaf(w, f.y, h2);
-                h3 = fmaf(w, f.z, h3);
+                const float4 h = hr[d * TX];
+                f1 = fmaf(w, h.x, f1);
+                f2 = fmaf(w, h.y, f2);
+                f3 = fmaf(w, h.z, f3);
             }
-            float* o = dbuf + ((size_t)py * W + px) * 9 + c * 3;
-            o[0] = h1;
-            o[1] = h2;
-            o[2] = h3;
+            const float r = orr[j][c], g = og[j][c];
+            const float v_ssim = f1 + r * f2 + g * f3;
+            const float v_l1 = (g > r) ? -1.0f : ((g < r) ? 1.0f : 0.0f);
+            vr[j][c] = inv_n * (-w_ssim * v_ssim + (1.0f - w_ssim) * v_l1);
+            l1_sum += fabsf(g - r);
         }
+    }
+#pragma unroll
+    for (int j = 0; j < NOUT; ++j) {
+        if (!oin[j]) continue;
+        const size_t q = ((size_t)(y0 + oy0 + (NT / TX) * j) * W + x0 + ox) * 3;
+        v_rendered[q + 0] = vr[j][0];
+        v_rendered[q + 1] = vr[j][1];
+        v_rendered[q + 2] = vr[j][2];
     }
     // Workgroup partials of (sum SSIM, sum L1, pixels).
     const float a = wave_sum(ssim_sum), b = wave_sum(l1_sum), n = wave_sum(cnt);
-    if ((tr & 63) == 0) {
-        s_red[0][tr >> 6] = a;
-        s_red[1][tr >> 6] = b;
-        s_red[2][tr >> 6] = n;
+    if ((t & 63) == 0) {
+        s_red[0][t >> 6] = a;
+        s_red[1][t >> 6] = b;
+        s_red[2][t >> 6] = n;
     }
     __syncthreads();
-    if (tr < 3) {
+    if (t < 3) {
         float v = 0.f;
 #pragma unroll
-        for (int k = 0; k < FT / 64; ++k) v += s_red[tr][k];
-        loss_part[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 3 + tr] = v;
-    }
-}
-
-// Vertical backward tile: VX columns x VY rows of output pixels, 256
-// threads, each thread VY / 16 rows.  The derivative fields of the tile's
-// columns are read row by row as contiguous floats (VX pixels x 9 values),
-// so the loads are coalesced; VY + 10 rows are read for VY outputs.  They
-// are kept in LDS in the same order ([row][column][9]): the staging writes
-// are consecutive, and a wave's reads of one field (4 rows x 16 columns,
-// 64 consecutive positions) are 9 floats apart, an odd stride that puts the
-// 64 lanes on 64 different banks.
-constexpr int VX = 16, VY = 32, VR = VY + 2 * HALF;
-
-__global__ __launch_bounds__(256) void k_ssim_v_bwd(int W, int H, const float* __restrict__ img,
-                                                    const float* __restrict__ gt,
-                                                    const float* __restrict__ dbuf, float w_ssim,
-                                                    float inv_n, float* __restrict__ v_rendered) {
-    __shared__ float s_h[VR * VX * 9];   // rows by.., columns bx.., 9 fields (channel c: 3c..3c+2)
-    const int tr = threadIdx.x, lx = tr & 15, ly = tr >> 4;
-    const int bx = blockIdx.x * VX, by = blockIdx.y * VY - HALF;
-    const int nf = min(VX, W - bx) * 9;   // in-image floats of a row
-    constexpr int ROWF = VX * 9;
-    for (int i = tr; i < VR * ROWF; i += 256) {
-        const int sy = i / ROWF, f = i - sy * ROWF;
-        const int gy = by + sy;
-        float v = 0.f;
-        if (f < nf && gy >= 0 && gy < H) v = dbuf[((size_t)gy * W + bx) * 9 + f];
-        s_h[i] = v;
-    }
-    __syncthreads();
-    const int px = bx + lx;
-    if (px >= W) return;
-#pragma unroll
-    for (int rr = 0; rr < VY / 16; ++rr) {
-        const int oy = ly + 16 * rr, py = blockIdx.y * VY + oy;
-        if (py >= H) break;
-        for (int c = 0; c < 3; ++c) {
-            const float* h1 = s_h + (oy * VX + lx) * 9 + c * 3;
-            float f1 = 0.f, f2 = 0.f, f3 = 0.f;
-#pragma unroll
-            for (int d = 0; d < WIN; ++d) {
-                const float w = GAUSS_1D[WIN - 1 - d];
-                f1 = fmaf(w, h1[d * VX * 9], f1);
-                f2 = fmaf(w, h1[d * VX * 9 + 1], f2);
-                f3 = fmaf(w, h1[d * VX * 9 + 2], f3);
-            }
-            const size_t q = ((size_t)py * W + px) * 3 + c;
-            const float r = img[q], g = gt[q];
-            const float v_ssim = f1 + r * f2 + g * f3;
-            const float v_l1 = (g > r) ? -1.0f : ((g < r) ? 1.0f : 0.0f);
-            v_rendered[q] = inv_n * (-w_ssim * v_ssim + (1.0f - w_ssim) * v_l1);
-        }
+        for (int k = 0; k < NT / 64; ++k) v += s_red[t][k];
+        loss_part[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 3 + t] = v;
     }
 }
 
@@ -277,14 +298,12 @@ __global__ __launch_bounds__(LF_T) void k_loss_final(int nparts, const float* __
 }  // namespace
 
 void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
-                 float inv_n, float* dbuf, float* v_rendered, float* loss_part, float* loss_out) {
-    const dim3 fgrid((W + FX - 1) / FX, (H + FY - 1) / FY);
-    hipLaunchKernelGGL(k_ssim_fused, fgrid, dim3(FT), 0, s, W, H, img, gt, dbuf, loss_part);
-    const dim3 grid((W + VX - 1) / VX, (H + VY - 1) / VY);
-    hipLaunchKernelGGL(k_ssim_v_bwd, grid, dim3(256), 0, s, W, H, img, gt, dbuf, w, inv_n,
-                       v_rendered);
-    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(LF_T), 0, s, (int)(fgrid.x * fgrid.y),
-                       loss_part, w, loss_out);
+                 float inv_n, float* v_rendered, float* loss_part, float* loss_out) {
+    const dim3 grid((W + TX - 1) / TX, (H + TY - 1) / TY);
+    hipLaunchKernelGGL(k_ssim_tile, grid, dim3(NT), 0, s, W, H, img, gt, w, inv_n, v_rendered,
+                       loss_part);
+    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(LF_T), 0, s, (int)(grid.x * grid.y), loss_part, w,
+                       loss_out);
 }
 
 }  // namespace msp
