@@ -454,7 +454,7 @@ def main():
                          "directory for --pmc-kernels (last --steps dispatches of each) and exit")
     ap.add_argument("--pmc-kernels", default="k_raster_fwd;k_raster_bwd;k_radix_hist<256>;k_radix_hist<512>;"
                                              "k_radix_scatter<false, 256>;k_radix_scatter<false, 512>;"
-                                             "k_radix_scatter<true, 256>;k_seg_write;"
+                                             "k_radix_scatter<true, 256>;k_lists_and_items;"
                                              "k_ssim_tile;k_project_fwd;k_sh_rest_adam;"
                                              "k_proj_bwd_adam",
                     help="semicolon-separated kernels for --pmc-summary (template arguments hold commas)")

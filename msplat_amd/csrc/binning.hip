@@ -313,16 +313,17 @@ __device__ __forceinline__ void write_row_refs(bool ok, uint32_t k, uint32_t g, 
 // tile's next free slot starts at the tile's start + its pairs in earlier
 // segments; the 16 of the row are wave-uniform (scalar registers).  Entries
 // keep reference (depth) order per tile.
-__global__ __launch_bounds__(1024) void k_seg_write(int S, const int* __restrict__ sstart,
-                                                    const int4* __restrict__ seg,
-                                                    const uint32_t* __restrict__ rkey,
-                                                    const uint32_t* __restrict__ rval,
-                                                    const int* __restrict__ hist,
-                                                    const int* __restrict__ tile_bins, int tbx,
-                                                    int tby, int sbx, uint32_t* __restrict__ ids) {
+// Segment j's part, by a workgroup of 1024 threads (16 waves).
+__device__ __forceinline__ void seg_write(int j, int S, const int* __restrict__ sstart,
+                                          const int4* __restrict__ seg,
+                                          const uint32_t* __restrict__ rkey,
+                                          const uint32_t* __restrict__ rval,
+                                          const int* __restrict__ hist,
+                                          const int* __restrict__ tile_bins, int tbx, int tby,
+                                          int sbx, uint32_t* __restrict__ ids) {
     __shared__ uint32_t s_k[SEG_REFS], s_g[SEG_REFS];
     __shared__ uint16_t s_q[SUPER][128];   // per row: ring of covering reference indices
-    const int j = blockIdx.x, lane = threadIdx.x & 63, ly = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, ly = threadIdx.x >> 6;
     const int nseg = sstart[S];
     const int4 sg = seg[j];
     if (j >= nseg) return;
@@ -405,7 +406,8 @@ __global__ __launch_bounds__(256) void k_run_edges(int64_t I, const uint32_t* __
 // k_tile_offsets: each block adds the totals of the blocks before it, scans
 // its own tiles and writes tile_bins, the chunk counts and first items and
 // the list of chunked tiles; the last block writes the summary.  Then
-// k_build_items writes the work items (tile, chunk), one thread per item.
+// build_items (in k_lists_and_items) writes the work items (tile, chunk), one
+// thread per item.
 constexpr int TS_T = 256, TS_PER = 4, TS_BLOCK = TS_T * TS_PER;
 
 template <bool MAX>
@@ -562,10 +564,11 @@ __device__ __forceinline__ int class_slot(bool ok, int c, const int* base, int* 
 // tile has at least one item, so the first items ascend), found by binary
 // search, and its chunk i - tile_item0[t].  Each item, and each tile (thread
 // i < T), also takes its slot in the launch orders, heaviest class first.
-__global__ __launch_bounds__(256) void k_build_items(int T, const Meta* __restrict__ meta,
-                                                     const int* __restrict__ tile_bins, Items it) {
+// Items vb * blockDim.x .. of the workgroup's share (any block size).
+__device__ __forceinline__ void build_items(int vb, int T, const Meta* __restrict__ meta,
+                                            const int* __restrict__ tile_bins, Items it) {
     __shared__ int s_base[2][32];
-    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int i = vb * (int)blockDim.x + (int)threadIdx.x;
     if (threadIdx.x < 64) {
         // first slot of each class: the elements of all higher classes
         const int k = threadIdx.x >> 5, c = threadIdx.x & 31;
@@ -598,6 +601,27 @@ __global__ __launch_bounds__(256) void k_build_items(int T, const Meta* __restri
         const int slot = class_slot(tile_ok, ct, s_base[1], it.cls + 96);
         if (tile_ok) it.tile_order[slot] = i;
     }
+}
+
+// The tile lists' last two jobs in one launch, both reading the tile
+// ranges of the tile scan and nothing of each other: workgroups 0 .. nsb - 1
+// write segment j's ids (seg_write), the rest build the work items and the
+// launch orders (build_items), so the item build runs beside the id writes
+// instead of after a launch of its own.
+__global__ __launch_bounds__(1024) void k_lists_and_items(int nsb, int S, const int* __restrict__ sstart,
+                                                          const int4* __restrict__ seg,
+                                                          const uint32_t* __restrict__ rkey,
+                                                          const uint32_t* __restrict__ rval,
+                                                          const int* __restrict__ hist,
+                                                          const int* __restrict__ tile_bins, int tbx,
+                                                          int tby, int sbx, uint32_t* __restrict__ ids,
+                                                          int T, const Meta* __restrict__ meta,
+                                                          Items it) {
+    if ((int)blockIdx.x >= nsb) {
+        build_items((int)blockIdx.x - nsb, T, meta, tile_bins, it);
+        return;
+    }
+    seg_write((int)blockIdx.x, S, sstart, seg, rkey, rval, hist, tile_bins, tbx, tby, sbx, ids);
 }
 
 }  // namespace
@@ -665,12 +689,12 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
                        meta, it.cls);
     hipLaunchKernelGGL(k_tile_offsets, dim3(nb), dim3(TS_T), 0, s, T, nb, (const int*)rb.tcount,
                        (const int*)tscan, isect, tile_bins, it, tl, meta);
-    hipLaunchKernelGGL(k_build_items, dim3(blocks_for(std::max<int64_t>(items_bound(T, I), T))),
-                       dim3(256), 0, s, T, (const Meta*)meta, (const int*)tile_bins, it);
-    if (R > 0)
-        hipLaunchKernelGGL(k_seg_write, dim3((unsigned)NS), dim3(1024), 0, s, S,
-                           (const int*)rb.sstart, (const int4*)rb.seg, rk, rv,
-                           (const int*)rb.hist, (const int*)tile_bins, p.tbx, p.tby, sbx, ids);
+    // segment ids (with any references) and work items in one launch
+    const int nsb = R > 0 ? (int)NS : 0;
+    const int nib = (int)((std::max<int64_t>(items_bound(T, I), T) + 1023) / 1024);
+    hipLaunchKernelGGL(k_lists_and_items, dim3((unsigned)(nsb + nib)), dim3(1024), 0, s, nsb, S,
+                       (const int*)rb.sstart, (const int4*)rb.seg, rk, rv, (const int*)rb.hist,
+                       (const int*)tile_bins, p.tbx, p.tby, sbx, ids, T, (const Meta*)meta, it);
 }
 
 }  // namespace msp
