@@ -721,14 +721,15 @@ int msplat_hip_train_step(const MsplatTrainArgs* a, int32_t* radii_out, float* l
     ENSURE(c->loss_d, 16);
     stage_mark(c, S_LOSS);
     // the loss sum goes straight to pinned host memory (loss_h[1])
-    launch_ssim(c->stream, p.H, p.W, P<float>(c->out_img), a->gt, a->ssim_weight, a->loss_inv_n,
-                P<float>(c->v_rendered), P<float>(c->loss_part),
-                c->loss_hd + 1);
+    const int nparts = launch_ssim(c->stream, p.H, p.W, P<float>(c->out_img), a->gt, a->ssim_weight,
+                                   a->loss_inv_n, P<float>(c->v_rendered), P<float>(c->loss_part));
+    // the raster backward's workgroup 0 folds the partials into loss_h[1]
+    const LossFold lf{P<float>(c->loss_part), nparts, a->ssim_weight, c->loss_hd + 1};
     stage_mark(c, S_RBWD);
     launch_raster_bwd(c->stream, p, c->max_items, P<Meta>(c->meta_d), items(c),
                       P<int>(c->tile_bins), packed(c),
                       P<float>(c->final_T), P<int>(c->final_idx), chunks(c),
-                      P<float>(c->v_rendered), P<float>(c->gacc), work_counters(c, S_RBWD));
+                      P<float>(c->v_rendered), P<float>(c->gacc), work_counters(c, S_RBWD), lf);
     AdamHP hp;
     for (int g = 0; g < 6; ++g) { hp.step[g] = a->adam_step_sizes[g]; hp.inv_bc2[g] = 1.0f / a->adam_bc2_sqrts[g]; }
     hp.b1 = a->adam_beta1;

@@ -223,17 +223,61 @@ void launch_render_tiles(hipStream_t s, const CamParams& p, Items it, const int*
 void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, const int* chunked,
                          Items it, float* final_T, int* final_idx, float* out_img, ChunkBufs cb,
                          bool with_suffix, const int* done);
+// Fold of the SSIM tiles' loss partials into the loss sum, done by one
+// workgroup of a later kernel (the raster backward's first): in float64, in a
+// fixed order (thread t adds parts t, t + blockDim.x, ... in order, then a
+// tree over the threads), stored to out (which may be coherent host memory
+// that the host reads without a stream sync: a system-scope store makes the
+// value visible there).  s: 3 x blockDim.x doubles of LDS; blockDim.x a power
+// of two.  Every thread of the workgroup calls it.
+struct LossFold {
+    const float* part;
+    int nparts;
+    float w;
+    float* out;
+};
+__device__ inline void loss_fold(const LossFold& lf, double* s) {
+    const int t = threadIdx.x, nt = blockDim.x;
+    double a = 0.0, b = 0.0, n = 0.0;
+    for (int i = t; i < lf.nparts; i += nt) {
+        a += lf.part[3 * i];
+        b += lf.part[3 * i + 1];
+        n += lf.part[3 * i + 2];
+    }
+    s[t] = a;
+    s[nt + t] = b;
+    s[2 * nt + t] = n;
+    __syncthreads();
+    for (int off = nt / 2; off > 0; off >>= 1) {
+        if (t < off)
+            for (int k = 0; k < 3; ++k) s[k * nt + t] += s[k * nt + t + off];
+        __syncthreads();
+    }
+    if (t == 0) {
+        const double w = lf.w;
+        __hip_atomic_store(lf.out, (float)(w * s[2 * nt] - (w / 3.0) * s[0] + ((1.0 - w) / 3.0) * s[nt]),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    __syncthreads();
+}
+// Workgroup 0 of the launch folds the loss when lf.part is set (loss_fold);
+// the items take workgroups 1 ...
 void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Entries pk, const float* final_T,
                        const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc,
-                       unsigned long long* work);
+                       unsigned long long* work, const LossFold& lf);
 // Adds the six pair counts of the most recent forward/backward into out[6].
 void launch_raster_work(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                         Items it, const int* tile_bins, Entries pk, const int* final_idx,
                         ChunkBufs cb, unsigned long long* out);
 
-void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
-                 float inv_n, float* v_rendered, float* loss_part, float* loss_out);
+// The loss: SSIM + L1 forward and backward per 32x32 tile; writes the loss
+// gradient image and one partial (sum SSIM, sum L1, pixels) per tile, and
+// returns the number of partials.
+int launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
+                float inv_n, float* v_rendered, float* loss_part);
+
+
 
 struct AdamHP {
     float step[6];

@@ -564,7 +564,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
                                                     const int* __restrict__ final_idx,
                                                     ChunkBufs cb, const float* __restrict__ v_out,
                                                     float* __restrict__ gacc,
-                                                    unsigned long long* __restrict__ work) {
+                                                    unsigned long long* __restrict__ work,
+                                                    LossFold lf) {
     __shared__ float4 s_geo[256];    // x, y, conic a, b
     __shared__ float4 s_col[256];    // conic c, opacity, clamped r, g
     __shared__ float4 s_aux[256];    // clamped b, opacity - 1, accumulator byte offset, mask
@@ -572,9 +573,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
     // largest final index before the entry loop uses the area
     __shared__ float4 s_red4[4 * 8 * RED_ROW / 4];
     int& s_max = *reinterpret_cast<int*>(s_red4);
+    // Workgroup 0 folds the loss partials of the SSIM tiles (in the reduction
+    // area) and takes no item: dispatched first, it runs beside the heaviest
+    // items instead of at the end of the launch.
+    static_assert(sizeof(s_red4) >= 3 * 256 * sizeof(double), "loss fold area");
+    if (blockIdx.x == 0) {
+        if (lf.part) loss_fold(lf, reinterpret_cast<double*>(s_red4));
+        return;
+    }
     // items in launch order (heaviest size class first)
-    if ((int)blockIdx.x >= meta->n_items) return;
-    const int item = it.order[blockIdx.x];
+    const int bi = (int)blockIdx.x - 1;
+    if (bi >= meta->n_items) return;
+    const int item = it.order[bi];
     int t, K, cs, ce;
     item_range(it, tile_bins, item, t, K, cs, ce);
     const Px px = pixel_of(t, tbx, W, H);
@@ -850,11 +860,12 @@ void launch_raster_merge(hipStream_t s, const CamParams& p, const Meta* meta, co
 void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, const Meta* meta,
                        Items it, const int* tile_bins, Entries pk, const float* final_T,
                        const int* final_idx, ChunkBufs cb, const float* v_out, float* gacc,
-                       unsigned long long* work) {
-    if (max_items <= 0) return;
-    hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)max_items), dim3(256), 0, s, p.W, p.H, p.tbx,
+                       unsigned long long* work, const LossFold& lf) {
+    // workgroup 0 folds the loss, the others take the items
+    const int64_t g = std::max<int64_t>(max_items, 0) + 1;
+    hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)g), dim3(256), 0, s, p.W, p.H, p.tbx,
                        p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx, cb,
-                       v_out, gacc, work);
+                       v_out, gacc, work, lf);
 }
 
 }  // namespace msp

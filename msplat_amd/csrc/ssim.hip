@@ -24,8 +24,9 @@
 // fast-math Metal build may contract the same way; the CPU oracle evaluates
 // exactly these operations.
 // The loss is reduced per workgroup into (sum SSIM, sum L1, pixel count) and
-// folded by one final workgroup in a fixed order; it equals the sum over
-// pixels of w*(1 - mean_c SSIM) + (1-w)*mean_c |gt - r|.
+// folded in a fixed order by one workgroup of the next kernel (loss_fold in
+// kernels.hpp); it equals the sum over pixels of
+// w*(1 - mean_c SSIM) + (1-w)*mean_c |gt - r|.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -265,45 +266,14 @@ __global__ __launch_bounds__(NT) void k_ssim_tile(int W, int H, const float* __r
     }
 }
 
-// Final fold of the workgroup partials in a fixed order (float64): thread t
-// adds parts t, t + 1024, ... in order, then a tree over the 1024 threads.
-constexpr int LF_T = 1024;
-__global__ __launch_bounds__(LF_T) void k_loss_final(int nparts, const float* __restrict__ part,
-                                                     float w_ssim, float* __restrict__ out) {
-    __shared__ double s[3][LF_T];
-    double a = 0.0, b = 0.0, n = 0.0;
-    for (int i = threadIdx.x; i < nparts; i += LF_T) {
-        a += part[3 * i];
-        b += part[3 * i + 1];
-        n += part[3 * i + 2];
-    }
-    s[0][threadIdx.x] = a;
-    s[1][threadIdx.x] = b;
-    s[2][threadIdx.x] = n;
-    __syncthreads();
-    for (int off = LF_T / 2; off > 0; off >>= 1) {
-        if ((int)threadIdx.x < off)
-            for (int k = 0; k < 3; ++k) s[k][threadIdx.x] += s[k][threadIdx.x + off];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-        const double w = w_ssim;
-        // out may be coherent host memory that the host reads without a
-        // stream sync: a system-scope store makes the value visible there
-        __hip_atomic_store(out, (float)(w * s[2][0] - (w / 3.0) * s[0][0] + ((1.0 - w) / 3.0) * s[1][0]),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-}
-
 }  // namespace
 
-void launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
-                 float inv_n, float* v_rendered, float* loss_part, float* loss_out) {
+int launch_ssim(hipStream_t s, int H, int W, const float* img, const float* gt, float w,
+                float inv_n, float* v_rendered, float* loss_part) {
     const dim3 grid((W + TX - 1) / TX, (H + TY - 1) / TY);
     hipLaunchKernelGGL(k_ssim_tile, grid, dim3(NT), 0, s, W, H, img, gt, w, inv_n, v_rendered,
                        loss_part);
-    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(LF_T), 0, s, (int)(grid.x * grid.y), loss_part, w,
-                       loss_out);
+    return (int)(grid.x * grid.y);
 }
 
 }  // namespace msp
