@@ -151,6 +151,11 @@ __device__ __forceinline__ void ref_rect(uint32_t k, int& x0, int& y0, int& x1, 
     y1 = y0 + (int)((k >> 28) & 15u) + 1;
 }
 
+// Tile scan blocks: TS_BLOCK tiles of the row-major tile order per
+// workgroup of TS_T threads (k_tile_offsets); their sums (count, chunk
+// items, largest count) are added up by k_seg_offsets.
+constexpr int TS_T = 256, TS_PER = 4, TS_BLOCK = TS_T * TS_PER;
+
 // Segments and their pair counts, one workgroup per segment (grid: the
 // segments_bound of the call).  Each workgroup first works out the segment
 // table itself from the super-tiles' reference ranges [st_r0, st_r1):
@@ -169,11 +174,21 @@ __global__ __launch_bounds__(256) void k_seg_count(int S, const int* __restrict_
                                                    int* __restrict__ sstart,
                                                    int4* __restrict__ seg,
                                                    const uint32_t* __restrict__ rkey,
-                                                   int* __restrict__ hist) {
+                                                   int* __restrict__ hist, int* __restrict__ tot,
+                                                   int ntb, int* __restrict__ cls,
+                                                   Meta* __restrict__ meta) {
     __shared__ int diff[DW * DW];
     __shared__ int sh[4];
     __shared__ int4 s_rec;
     const int j = blockIdx.x, tid = threadIdx.x;
+    if (j == 0) {
+        // this frame's tile scan sums (k_seg_offsets adds to them), size-class
+        // counters (k_tile_offsets adds, the item build reads) and chunked-tile
+        // count start at zero; the previous frame read them before this launch
+        for (int i = tid; i < 3 * ntb; i += 256) tot[i] = 0;
+        if (tid < 128) cls[tid] = 0;
+        if (tid == 0) meta->n_chunked_tiles = 0;
+    }
     const int per = (S + 255) / 256;
     const int b = min(tid * per, S), e = min(b + per, S);
     int sum = 0;
@@ -241,7 +256,8 @@ __global__ __launch_bounds__(SO_T) void k_seg_offsets(int tbx, int tby, int sbx,
                                                       int* __restrict__ hist,
                                                       int* __restrict__ tcount,
                                                       int* __restrict__ st_r0,
-                                                      int* __restrict__ st_r1) {
+                                                      int* __restrict__ st_r1,
+                                                      int* __restrict__ tot) {
     __shared__ int part[SO_G][SO_D];
     const int s = blockIdx.x, tile = blockIdx.y * SO_D + threadIdx.x % SO_D;
     if (blockIdx.y == 0 && threadIdx.x == 0) {
@@ -277,9 +293,35 @@ __global__ __launch_bounds__(SO_T) void k_seg_offsets(int tbx, int tby, int sbx,
             run += c[u];
         }
     }
-    if (g == 0) {
+    if (g == 0) {   // wave 0: the quarter's 64 tiles
         const int tx = (s % sbx) * SUPER + (tile % SUPER), ty = (s / sbx) * SUPER + tile / SUPER;
-        if (tx < tbx && ty < tby) tcount[ty * tbx + tx] = total;
+        const bool in = tx < tbx && ty < tby;
+        const int t = ty * tbx + tx;
+        if (in) tcount[t] = total;
+        // The tile scan's block sums: count, chunk items and largest count of
+        // each block of TS_BLOCK row-major tiles.  The quarter's 64 tiles fall
+        // in a few blocks; each block's lanes add with one atomic per sum.
+        const int blk = in ? t / TS_BLOCK : -1;
+        const int kch = in ? tile_chunks(total, tbx * tby) : 0;
+        const int lane = threadIdx.x & 63;
+        uint64_t left = wave_ballot(in);
+        while (left) {
+            const int first = (int)__builtin_ctzll(left);
+            const int bl = __builtin_amdgcn_readlane(blk, first);
+            const bool mine = in && blk == bl;
+            int sn = mine ? total : 0, sk = mine ? kch : 0, mx = mine ? total : 0;
+            for (int off = 32; off >= 1; off >>= 1) {
+                sn += __shfl_xor(sn, off, 64);
+                sk += __shfl_xor(sk, off, 64);
+                mx = max(mx, __shfl_xor(mx, off, 64));
+            }
+            if (lane == first) {
+                atomicAdd(&tot[3 * bl], sn);
+                atomicAdd(&tot[3 * bl + 1], sk);
+                atomicMax(&tot[3 * bl + 2], mx);
+            }
+            left &= ~wave_ballot(mine);
+        }
     }
 }
 
@@ -401,14 +443,13 @@ __global__ __launch_bounds__(256) void k_run_edges(int64_t I, const uint32_t* __
     }
 }
 
-// Tile scan over TS_BLOCK tiles per workgroup in two kernels.  k_tile_counts:
+// Tile scan over TS_BLOCK tiles per workgroup: k_seg_offsets has added up
 // each block's tile count total, chunk-item total and largest count.
 // k_tile_offsets: each block adds the totals of the blocks before it, scans
 // its own tiles and writes tile_bins, the chunk counts and first items and
 // the list of chunked tiles; the last block writes the summary.  Then
 // build_items (in k_lists_and_items) writes the work items (tile, chunk), one
 // thread per item.
-constexpr int TS_T = 256, TS_PER = 4, TS_BLOCK = TS_T * TS_PER;
 
 template <bool MAX>
 __device__ __forceinline__ int block_combine(int v, int* sh) {
@@ -431,37 +472,6 @@ __device__ __forceinline__ int block_combine(int v, int* sh) {
 __device__ __forceinline__ int size_class(int n, int K) {
     const int w = K == 1 ? n : min(n, CHUNK);
     return w > 0 ? 31 - __clz(w) : 0;
-}
-
-__global__ __launch_bounds__(TS_T) void k_tile_counts(int T, const int* __restrict__ tcount,
-                                                      int* __restrict__ tot,
-                                                      Meta* __restrict__ meta,
-                                                      int* __restrict__ cls) {
-    __shared__ int sh[TS_T / 64];
-    const int b = blockIdx.x;
-    // the class counters, read by this frame's item build, cleared before
-    // the tile offsets add to them
-    if (b == 0 && threadIdx.x < 128) cls[threadIdx.x] = 0;
-    int sn = 0, sk = 0, mx = 0;
-#pragma unroll
-    for (int k = 0; k < TS_PER; ++k) {
-        const int t = b * TS_BLOCK + k * TS_T + (int)threadIdx.x;
-        if (t < T) {
-            const int n = tcount[t];
-            sn += n;
-            sk += tile_chunks(n, T);
-            mx = max(mx, n);
-        }
-    }
-    sn = block_combine<false>(sn, sh);
-    sk = block_combine<false>(sk, sh);
-    mx = block_combine<true>(mx, sh);
-    if (threadIdx.x == 0) {
-        tot[3 * b] = sn;
-        tot[3 * b + 1] = sk;
-        tot[3 * b + 2] = mx;
-        if (b == 0) meta->n_chunked_tiles = 0;
-    }
 }
 
 __global__ __launch_bounds__(TS_T) void k_tile_offsets(int T, int nb,
@@ -679,14 +689,13 @@ void launch_tile_lists(hipStream_t s, const CamParams& p, int64_t I, int64_t R,
     // with no references every super-tile is empty: no segments (workgroup 0
     // still writes the segment table), zero counts
     const int64_t NS = segments_bound(R, S);
+    const int nb = (T + TS_BLOCK - 1) / TS_BLOCK;
     hipLaunchKernelGGL(k_seg_count, dim3((unsigned)NS), dim3(256), 0, s, S,
-                       (const int*)rb.st_r0, (const int*)rb.st_r1, rb.sstart, rb.seg, rk, rb.hist);
+                       (const int*)rb.st_r0, (const int*)rb.st_r1, rb.sstart, rb.seg, rk, rb.hist,
+                       tscan, nb, it.cls, meta);
     hipLaunchKernelGGL(k_seg_offsets, dim3(S, SUPER * SUPER / SO_D), dim3(SO_T), 0, s, p.tbx,
                        p.tby, sbx,
-                       (const int*)rb.sstart, rb.hist, rb.tcount, rb.st_r0, rb.st_r1);
-    const int nb = (T + TS_BLOCK - 1) / TS_BLOCK;
-    hipLaunchKernelGGL(k_tile_counts, dim3(nb), dim3(TS_T), 0, s, T, (const int*)rb.tcount, tscan,
-                       meta, it.cls);
+                       (const int*)rb.sstart, rb.hist, rb.tcount, rb.st_r0, rb.st_r1, tscan);
     hipLaunchKernelGGL(k_tile_offsets, dim3(nb), dim3(TS_T), 0, s, T, nb, (const int*)rb.tcount,
                        (const int*)tscan, isect, tile_bins, it, tl, meta);
     // segment ids (with any references) and work items in one launch
