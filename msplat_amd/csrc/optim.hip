@@ -94,7 +94,10 @@ __device__ __forceinline__ void adam_elem(float& p, float& m, float& v, float g,
 // per gaussian it touches (view direction from the projection record) into
 // LDS.  Elements of culled gaussians and of bands above degrees_to_use keep
 // their values (the reference updates visible gaussians' used bands only,
-// .metal:1846-1848, 1931-1985).
+// .metal:1846-1848, 1931-1985).  Blocks take their element ranges last to
+// first: the rows written last are then the first gaussians', which the next
+// step's projection reads first, while they are still in the last-level
+// cache.
 constexpr int SHA_T = 256;
 constexpr int SHA_E = 4 * SHA_T;
 constexpr int SHA_MAXG = SHA_E / 9 + 2;   // rest_per >= 9
@@ -144,7 +147,7 @@ __global__ __launch_bounds__(SHA_T) void k_sh_rest_adam(int64_t n, int rest_per,
     __shared__ float s_basis[SHA_MAXG][17];   // odd row stride: the per-gaussian writes hit distinct banks
     __shared__ float s_vrgb[SHA_MAXG][3];
     __shared__ int s_vis[SHA_MAXG];
-    const int64_t eb = (int64_t)blockIdx.x * SHA_E;
+    const int64_t eb = (int64_t)(gridDim.x - 1 - blockIdx.x) * SHA_E;
     const int gA = (int)(eb / rest_per);
     const int gB = (int)((min(eb + SHA_E, n) - 1) / rest_per);
     for (int t = threadIdx.x; t <= gB - gA; t += SHA_T) {

@@ -135,13 +135,13 @@ def render_args(g: DeviceGaussians, setup, degrees_to_use: int, background, clip
     return a
 
 
-def render(g: DeviceGaussians, setup, degrees_to_use: int, background, out=None):
+def render(g: DeviceGaussians, setup, degrees_to_use: int, background, out=None, clip=0.01):
     """msplat_render: returns a (H, W, 3) float32 device tensor."""
     T = torch()
     lib = init()
     if out is None:
         out = T.empty((setup.height, setup.width, 3), dtype=T.float32, device="cuda")
-    a = render_args(g, setup, degrees_to_use, background)
+    a = render_args(g, setup, degrees_to_use, background, clip=clip)
     _abi.check(lib.msplat_hip_render(ctypes.byref(a), ptr(out)))
     return out
 

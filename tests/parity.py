@@ -33,7 +33,7 @@ def say(msg):
     print(f"[parity {time.strftime('%H:%M:%S')}] {msg}", flush=True)
 
 
-def render_and_compare(dev, params, degree, cam_obj, dtu=None, bg=BG, label=""):
+def render_and_compare(dev, params, degree, cam_obj, dtu=None, bg=BG, label="", clip=0.01):
     """Render through the C ABI and compare every forward stage with the oracle.
     params: six host float32 arrays.  Returns (meta, tile counts)."""
     dtu = degree if dtu is None else dtu
@@ -42,9 +42,9 @@ def render_and_compare(dev, params, degree, cam_obj, dtu=None, bg=BG, label=""):
     n = int(means.shape[0])
     say(f"render {label}: {n} gaussians, {su.width}x{su.height}, SH {degree}/{dtu}")
     g = dev.DeviceGaussians.from_arrays(params, degree)
-    img = dev.render(g, su, dtu, bg).cpu().numpy()
+    img = dev.render(g, su, dtu, bg, clip=clip).cpu().numpy()
     say(f"render {label}: GPU done, oracle projection")
-    cam = orc.camera(su, degree, dtu, bg)
+    cam = orc.camera(su, degree, dtu, bg, clip=clip)
     p = orc.project(cam, means, scales, quats, f_dc, f_rest)
     assert_bits_equal(dev.intermediate("radii", np.int32), p["radii"], "radii")
     assert_bits_equal(dev.intermediate("num_tiles_hit", np.int32), p["num_tiles_hit"], "num_tiles_hit")

@@ -118,6 +118,47 @@ def test_train_step_deep_chunks_past_zero_transmittance(dev):
     assert set(np.nonzero(done == 0)[0]) == {0, 3, 12, 15}, done
 
 
+def _far_scene(seed_off):
+    """A small scene whose first 400 gaussians sit at depths 700..3200 (five
+    to twelve binades above the rest, 18 above the 0.01 clip), each about a
+    pixel across; gaussians 400..439 repeat the positions of 0..39 (equal
+    depths, ordered by id)."""
+    sc = small_scene(n=3000, seed_off=seed_off)
+    c2w = np.asarray(sc.cameras[0].cam_to_world, np.float64)
+    pos, right, up, fwd = c2w[:3, 3], c2w[:3, 0], c2w[:3, 1], -c2w[:3, 2]
+    st = synthetic.Stream(synthetic.BASE_SEED + seed_off + 1)
+    k = 400
+    far = st.uniform(k) * 2500.0 + 700.0
+    lat = (st.uniform(2 * k).reshape(k, 2) - 0.5) * 0.8       # inside the 70 degree view
+    pts = pos + far[:, None] * (fwd + lat[:, :1] * right + lat[:, 1:] * up)
+    sc.means[:k] = pts.astype(np.float32)
+    sc.scales[:k] = np.log(0.01 * far)[:, None].astype(np.float32) + np.zeros((1, 3), np.float32)
+    sc.means[k:k + 40] = sc.means[:40]
+    return sc
+
+
+def test_render_far_depths_and_ties(dev):
+    """Depths over 18 binades with ties: the depth order (all 32 key bits)
+    and every forward stage bit-exact."""
+    sc = _far_scene(74)
+    _render_and_compare(dev, sc)
+    far_vis = dev.intermediate("radii", np.int32)[:400] > 0
+    assert far_vis.sum() > 100, far_vis.sum()
+
+
+def test_render_zero_clip(dev):
+    """clip_thresh 0: every gaussian in front of the camera is kept, however
+    near; equal depths ordered by id."""
+    sc = small_scene(n=3000, seed_off=76)
+    sc.means[100:140] = sc.means[:40]
+    parity.render_and_compare(dev, sc.params(), sc.sh_degree, sc.cameras[0], clip=0.0, label="clip 0")
+
+
+def test_train_step_far_depths_and_ties(dev):
+    """A train step over the far scene (depths over 18 binades, ties)."""
+    _train_compare(dev, _far_scene(78))
+
+
 def test_train_step_monolithic(dev):
     _train_compare(dev, small_scene(n=12000, width=336, height=208, seed_off=82))
 
