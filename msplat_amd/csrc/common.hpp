@@ -221,6 +221,20 @@ __device__ __forceinline__ int wave_max_i(int v) {
     return v;
 }
 
+// Loads and stores marked non-temporal (nt): for data touched once here and
+// not again before the next step, so that it does not take the place of
+// lines that a later kernel reads.
+typedef float ntf4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float ld_nt(const float* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ float4 ld_nt4(const float* p) {
+    const ntf4 v = __builtin_nontemporal_load(reinterpret_cast<const ntf4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_nt(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void st_nt4(float* p, float4 v) {
+    __builtin_nontemporal_store(ntf4{v.x, v.y, v.z, v.w}, reinterpret_cast<ntf4*>(p));
+}
+
 __device__ __forceinline__ unsigned lane_id() { return __lane_id(); }
 
 }  // namespace msp

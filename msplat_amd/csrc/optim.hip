@@ -97,7 +97,10 @@ __device__ __forceinline__ void adam_elem(float& p, float& m, float& v, float g,
 // .metal:1846-1848, 1931-1985).  Blocks take their element ranges last to
 // first: the rows written last are then the first gaussians', which the next
 // step's projection reads first, while they are still in the last-level
-// cache.
+// cache.  The moments, and the record fields and accumulators read here (the
+// step's last use of them), are loaded and the moments stored non-temporally,
+// so that the caches keep the features_rest rows for that projection
+// (non-temporal loads with ordinary stores of the same lines were slower).
 constexpr int SHA_T = 256;
 constexpr int SHA_E = 4 * SHA_T;
 constexpr int SHA_MAXG = SHA_E / 9 + 2;   // rest_per >= 9
@@ -124,14 +127,18 @@ __device__ __forceinline__ void sh_basis15(float x, float y, float z, float* o) 
 // v_rgb of gaussian g from its accumulators, each channel kept only where
 // the raw colour + 0.5 >= 0 (rasterize_backward_kernel masks it there,
 // .metal:1083-1086; the mask is the gaussian's, so the raster backward sums
-// every channel and the mask is applied here once).
+// every channel and the mask is applied here once).  NT: non-temporal loads
+// (the step's last reads of the record and the accumulators).
+template <bool NT>
 __device__ __forceinline__ void masked_vrgb(const float* ga, const float4* rec, size_t g,
                                             float out[3]) {
     // loaded unconditionally (a conditional load would be a branch and a
     // separate memory round trip per channel)
-    const float4 r1 = rec[4 * g + 1];
-    const float rb = rec[4 * g + 2].x;
-    const float v0 = ga[5], v1 = ga[6], v2 = ga[7];
+    const float* r = reinterpret_cast<const float*>(rec + 4 * g);
+    const float4 r1 = NT ? ld_nt4(r + 4) : rec[4 * g + 1];
+    const float rb = NT ? ld_nt(r + 8) : r[8];
+    const float v0 = NT ? ld_nt(ga + 5) : ga[5], v1 = NT ? ld_nt(ga + 6) : ga[6],
+                v2 = NT ? ld_nt(ga + 7) : ga[7];
     out[0] = r1.z + 0.5f >= 0.f ? v0 : 0.f;
     out[1] = r1.w + 0.5f >= 0.f ? v1 : 0.f;
     out[2] = rb + 0.5f >= 0.f ? v2 : 0.f;
@@ -155,13 +162,13 @@ __global__ __launch_bounds__(SHA_T) void k_sh_rest_adam(int64_t n, int rest_per,
         const bool vis = radii[g] > 0;
         s_vis[t] = vis;
         if (vis) {
-            const float4 d = rec[4 * (size_t)g + 3];
+            const float4 d = ld_nt4(reinterpret_cast<const float*>(rec + 4 * (size_t)g + 3));
             float bs[15];
             sh_basis15(d.x, d.y, d.z, bs);
 #pragma unroll
             for (int b = 0; b < 15; ++b) s_basis[t][b] = bs[b];
             float vr[3];
-            masked_vrgb(gacc + (size_t)g * 9, rec, (size_t)g, vr);
+            masked_vrgb<true>(gacc + (size_t)g * 9, rec, (size_t)g, vr);
 #pragma unroll
             for (int c = 0; c < 3; ++c) s_vrgb[t][c] = vr[c];
         }
@@ -178,13 +185,17 @@ __global__ __launch_bounds__(SHA_T) void k_sh_rest_adam(int64_t n, int rest_per,
     const bool full = cnt == 4;
     if (full) {
         const float4 a = *reinterpret_cast<const float4*>(f_rest + e0);
-        const float4 b = *reinterpret_cast<const float4*>(m + e0);
-        const float4 c = *reinterpret_cast<const float4*>(v + e0);
+        const float4 b = ld_nt4(m + e0);
+        const float4 c = ld_nt4(v + e0);
         pv[0] = a.x; pv[1] = a.y; pv[2] = a.z; pv[3] = a.w;
         mv[0] = b.x; mv[1] = b.y; mv[2] = b.z; mv[3] = b.w;
         vv[0] = c.x; vv[1] = c.y; vv[2] = c.z; vv[3] = c.w;
     } else {
-        for (int k = 0; k < cnt; ++k) { pv[k] = f_rest[e0 + k]; mv[k] = m[e0 + k]; vv[k] = v[e0 + k]; }
+        for (int k = 0; k < cnt; ++k) {
+            pv[k] = f_rest[e0 + k];
+            mv[k] = ld_nt(m + e0 + k);
+            vv[k] = ld_nt(v + e0 + k);
+        }
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -199,10 +210,14 @@ __global__ __launch_bounds__(SHA_T) void k_sh_rest_adam(int64_t n, int rest_per,
     }
     if (full) {
         *reinterpret_cast<float4*>(f_rest + e0) = make_float4(pv[0], pv[1], pv[2], pv[3]);
-        *reinterpret_cast<float4*>(m + e0) = make_float4(mv[0], mv[1], mv[2], mv[3]);
-        *reinterpret_cast<float4*>(v + e0) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+        st_nt4(m + e0, make_float4(mv[0], mv[1], mv[2], mv[3]));
+        st_nt4(v + e0, make_float4(vv[0], vv[1], vv[2], vv[3]));
     } else {
-        for (int k = 0; k < cnt; ++k) { f_rest[e0 + k] = pv[k]; m[e0 + k] = mv[k]; v[e0 + k] = vv[k]; }
+        for (int k = 0; k < cnt; ++k) {
+            f_rest[e0 + k] = pv[k];
+            st_nt(m + e0 + k, mv[k]);
+            st_nt(v + e0 + k, vv[k]);
+        }
     }
 }
 
@@ -227,30 +242,32 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
     const int g = blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= p.N) return;
     // The dense parameters and moments are loaded up front, so that these
-    // loads and the gradient inputs share one memory round trip.
+    // loads and the gradient inputs share one memory round trip.  The moments
+    // are loaded and stored non-temporally (nothing else reads them in the
+    // step); the parameters are not, as the next projection reads them.
     // sp / sm / sv [k]: 0-2 means, 3-5 scales, 6-9 quats, 10 opacity (the
     // visible-only f_dc update loads its own).
     float sp[11], sm[11], sv[11];
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         sp[k] = P.params[0][3 * (size_t)g + k];
-        sm[k] = P.m[0][3 * (size_t)g + k];
-        sv[k] = P.v[0][3 * (size_t)g + k];
+        sm[k] = ld_nt(P.m[0] + 3 * (size_t)g + k);
+        sv[k] = ld_nt(P.v[0] + 3 * (size_t)g + k);
         sp[3 + k] = P.params[1][3 * (size_t)g + k];
-        sm[3 + k] = P.m[1][3 * (size_t)g + k];
-        sv[3 + k] = P.v[1][3 * (size_t)g + k];
+        sm[3 + k] = ld_nt(P.m[1] + 3 * (size_t)g + k);
+        sv[3 + k] = ld_nt(P.v[1] + 3 * (size_t)g + k);
     }
     {
         const float4 a = reinterpret_cast<const float4*>(P.params[2])[g];
-        const float4 b = reinterpret_cast<const float4*>(P.m[2])[g];
-        const float4 c = reinterpret_cast<const float4*>(P.v[2])[g];
+        const float4 b = ld_nt4(P.m[2] + 4 * (size_t)g);
+        const float4 c = ld_nt4(P.v[2] + 4 * (size_t)g);
         sp[6] = a.x; sp[7] = a.y; sp[8] = a.z; sp[9] = a.w;
         sm[6] = b.x; sm[7] = b.y; sm[8] = b.z; sm[9] = b.w;
         sv[6] = c.x; sv[7] = c.y; sv[8] = c.z; sv[9] = c.w;
     }
     sp[10] = P.params[5][g];
-    sm[10] = P.m[5][g];
-    sv[10] = P.v[5][g];
+    sm[10] = ld_nt(P.m[5] + g);
+    sv[10] = ld_nt(P.v[5] + g);
     const int rad = go.radii[g];
     const float* ga = gacc + (size_t)g * 9;
     F3 vm{0.f, 0.f, 0.f};
@@ -265,12 +282,12 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             dp[c] = P.params[3][3 * (size_t)g + c];
-            dm[c] = P.m[3][3 * (size_t)g + c];
-            dv[c] = P.v[3][3 * (size_t)g + c];
+            dm[c] = ld_nt(P.m[3] + 3 * (size_t)g + c);
+            dv[c] = ld_nt(P.v[3] + 3 * (size_t)g + c);
         }
         const float st_vis = vis[g], st_gnorm = gnorm[g], st_max2d = max2d[g];
         float vrgb[3];
-        masked_vrgb(ga, go.rec, (size_t)g, vrgb);
+        masked_vrgb<false>(ga, go.rec, (size_t)g, vrgb);
         // The raster backward sums the moments of v_sigma over the pixels
         // (m0 = sum v dx, m1 = sum v dy, m2..m4 = sum v (dx^2, dx dy, dy^2));
         // with this gaussian's conic (a, b, c) they give v_xy = (a m0 + b m1,
@@ -424,8 +441,8 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             P.params[3][3 * (size_t)g + c] = dp[c];
-            P.m[3][3 * (size_t)g + c] = dm[c];
-            P.v[3][3 * (size_t)g + c] = dv[c];
+            st_nt(P.m[3] + 3 * (size_t)g + c, dm[c]);
+            st_nt(P.v[3] + 3 * (size_t)g + c, dv[c]);
         }
         vis[g] = st_vis + 1.0f;
         gnorm[g] = st_gnorm + sqrtf(vxy0 * vxy0 + vxy1 * vxy1);
@@ -450,15 +467,15 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         const size_t i = 3 * (size_t)g + k;
-        P.params[0][i] = sp[k]; P.m[0][i] = sm[k]; P.v[0][i] = sv[k];
-        P.params[1][i] = sp[3 + k]; P.m[1][i] = sm[3 + k]; P.v[1][i] = sv[3 + k];
+        P.params[0][i] = sp[k]; st_nt(P.m[0] + i, sm[k]); st_nt(P.v[0] + i, sv[k]);
+        P.params[1][i] = sp[3 + k]; st_nt(P.m[1] + i, sm[3 + k]); st_nt(P.v[1] + i, sv[3 + k]);
     }
     reinterpret_cast<float4*>(P.params[2])[g] = make_float4(sp[6], sp[7], sp[8], sp[9]);
-    reinterpret_cast<float4*>(P.m[2])[g] = make_float4(sm[6], sm[7], sm[8], sm[9]);
-    reinterpret_cast<float4*>(P.v[2])[g] = make_float4(sv[6], sv[7], sv[8], sv[9]);
+    st_nt4(P.m[2] + 4 * (size_t)g, make_float4(sm[6], sm[7], sm[8], sm[9]));
+    st_nt4(P.v[2] + 4 * (size_t)g, make_float4(sv[6], sv[7], sv[8], sv[9]));
     P.params[5][g] = sp[10];
-    P.m[5][g] = sm[10];
-    P.v[5][g] = sv[10];
+    st_nt(P.m[5] + g, sm[10]);
+    st_nt(P.v[5] + g, sv[10]);
 }
 
 }  // namespace

@@ -112,18 +112,22 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
     const int g = g0 + threadIdx.x;
     const bool live = g < p.N;
     // Per-gaussian inputs first, so that their loads overlap the staging below.
+    // The parameters (these and the features_rest rows staged below) are
+    // read once per step here, and next by the Adam step after the raster
+    // kernels: their loads are non-temporal, so that they do not displace the
+    // records this kernel writes, which the raster kernels gather next.
     V3 pw{0.f, 0.f, 0.f};
     float sc[3] = {0.f, 0.f, 0.f}, dc[3] = {0.f, 0.f, 0.f}, ol = 0.f;
     float4 q = make_float4(1.f, 0.f, 0.f, 0.f);
     if (live) {
-        pw = V3{means[3 * g], means[3 * g + 1], means[3 * g + 2]};
+        pw = V3{ld_nt(means + 3 * g), ld_nt(means + 3 * g + 1), ld_nt(means + 3 * g + 2)};
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
-            sc[k] = scales[3 * (size_t)g + k];
-            dc[k] = f_dc[3 * (size_t)g + k];
+            sc[k] = ld_nt(scales + 3 * (size_t)g + k);
+            dc[k] = ld_nt(f_dc + 3 * (size_t)g + k);
         }
-        q = reinterpret_cast<const float4*>(quats)[g];
-        ol = opac_logits[g];
+        q = ld_nt4(quats + 4 * (size_t)g);
+        ol = ld_nt(opac_logits + g);
     }
     // Zero this workgroup's raster gradient accumulators (PROJ_T * 9
     // contiguous floats) with 16-byte stores; render-only calls pass none.
@@ -168,7 +172,8 @@ __global__ __launch_bounds__(PROJ_T) void k_project_fwd(
                 const int i = min((int)threadIdx.x + k * PROJ_T, nv - 1);
                 const int r0 = (int)(((float)(4 * i) + 0.5f) * inv_rest);
                 const int r1 = min((int)(((float)(4 * i) + 3.5f) * inv_rest), PROJ_T - 1);
-                stage[k] = src4[(s_vis[r0] | s_vis[r1]) ? i : nv - 1];
+                const int src = (s_vis[r0] | s_vis[r1]) ? i : nv - 1;
+                stage[k] = ld_nt4(reinterpret_cast<const float*>(src4 + src));
             }
 #pragma unroll
             for (int k = 0; k < PROJ_STAGE; ++k) {
