@@ -17,6 +17,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -356,19 +357,25 @@ CamParams cam_params(const MsplatRenderArgs* a) {
 // Waits for the totals word of the current frame (bit 63 set) in coherent
 // host memory.  With no gaussians nothing writes it: the stream is drained
 // instead, so that the caller may rely on the earlier work having completed
-// either way.  A failed or stopped stream ends the wait with its error.
+// either way.  A failed or stopped stream ends the wait with its error: the
+// stream is queried once the wait has lasted 20 ms, then every 20 ms (a
+// stream query queues a packet that holds the GPU for about 5 us between
+// two kernels, so a frame's ordinary wait of a millisecond or two makes none).
 hipError_t wait_totals(Ctx* c, int N, uint64_t* word) {
     if (N <= 0) {
         *word = 0;
         return hipStreamSynchronize(c->stream);
     }
+    using clock = std::chrono::steady_clock;
+    auto next_query = clock::now() + std::chrono::milliseconds(20);
     for (unsigned k = 1;; ++k) {
         const uint64_t w = __atomic_load_n(&c->isect_h[0], __ATOMIC_ACQUIRE);
         if (w >> 63) {
             *word = w;
             return hipSuccess;
         }
-        if ((k & 4095) == 0) {
+        if ((k & 255) == 0 && clock::now() >= next_query) {
+            next_query = clock::now() + std::chrono::milliseconds(20);
             const hipError_t e = hipStreamQuery(c->stream);
             if (e == hipSuccess) {   // drained: the word must be there now
                 const uint64_t v = __atomic_load_n(&c->isect_h[0], __ATOMIC_ACQUIRE);
