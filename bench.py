@@ -56,6 +56,9 @@ FP32_PEAK = 157.3e12
 # tested and rejected add nothing, so the figure is a lower bound.
 FWD_PAIR_FLOPS = 11 + 3 + 9
 BWD_PAIR_FLOPS = 11 + 3 + 64
+# Timed train steps whose raster backward is bracketed with HIP events (and
+# counted): every third, a stride coprime with the 32 config-3 cameras.
+BWD_SAMPLE = 3
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "raster_bwd_config3_traffic.json")
 # Stage names in the order of the library's stage-timing bits: the
 # reference profiler's train stages (msplat_metal.mm:30-34), ".part" where a
@@ -535,17 +538,21 @@ def main():
     for _ in range(args.warmup):
         tr.step()
     device.sync()
-    # The timed steps bracket only the raster backward (the roofline kernel)
-    # and densification calls with HIP events: every event leaves the GPU idle
-    # for a few microseconds.
-    _abi.check(lib.msplat_hip_set_stage_timing_mask((1 << STAGES.index("rast_bwd")) |
-                                                    (1 << STAGES.index("densify"))))
+    # The timed steps bracket densification calls and the raster backward (the
+    # roofline kernel) of every BWD_SAMPLE-th step with HIP events: each event
+    # leaves the GPU idle for about 4.5 us.  The stride is coprime with the 32
+    # cameras, so the sampled launches visit every camera; the raster pair
+    # counters run on exactly the sampled launches.
+    mask_dens = 1 << STAGES.index("densify")
+    mask_bwd = mask_dens | (1 << STAGES.index("rast_bwd"))
+    _abi.check(lib.msplat_hip_set_stage_timing_mask(mask_dens))
     _abi.check(lib.msplat_hip_enable_stage_timing(1))
     n_start = tr.splat_count()
     first_step = args.preroll + args.warmup + 1
     device.sync()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        lib.msplat_hip_set_stage_timing_mask(mask_bwd if i % BWD_SAMPLE == 0 else mask_dens)
         tr.step()
     device.sync()
     t1 = time.perf_counter()
@@ -630,7 +637,8 @@ def main():
     roofline = {"bound": "mfma", "achieved": achieved / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
                 "frac": achieved / FP32_PEAK, "traffic": traffic,
                 "kernel": "k_raster_bwd", "roof": "fp32 vector ALU (the kernel has no matrix-shaped work)",
-                "launches": bwd_n, "launch_ms": bwd_ms, "flops_per_launch": bwd_flops,
+                "launches": bwd_n, "launch_sample": f"1 in {BWD_SAMPLE} timed steps",
+                "launch_ms": bwd_ms, "flops_per_launch": bwd_flops,
                 "grad_pairs_per_launch": train_pairs[1] / max(bwd_n, 1),
                 "lane_use": train_pairs[1] / max(64 * train_pairs[3], 1)}
     log(f"roofline k_raster_bwd: {bwd_flops / 1e9:.2f} GFLOP/launch ({train_pairs[1] / max(bwd_n, 1) / 1e6:.1f}M "
