@@ -227,10 +227,54 @@ struct BwdPtrs {
     float* v[6];
 };
 
+// The six arrays of three-float rows (means, log-scales and their moments)
+// pass through LDS: the workgroup's 256 rows of an array are 768 contiguous
+// floats, loaded and stored as 16-byte vectors (vec3: every array 16-byte
+// aligned) instead of three 4-byte accesses per thread, whose non-temporal
+// forms fetch the same lines once per access.
+constexpr int PBA_T = 256;
+constexpr int PBA_S = 6;   // staged arrays: means p, m, v, scales p, m, v
+
+// Loads (STORE false) or stores the workgroup's nf floats of the staged
+// arrays between memory and s3; the moments non-temporally.
+template <bool STORE>
+__device__ __forceinline__ void stage_rows3(float* const arr[PBA_S], size_t f0, int nf, bool vec3,
+                                            float (*s3)[3 * PBA_T]) {
+    const int t = threadIdx.x;
+    const int nv = vec3 ? nf >> 2 : 0;
+    for (int i = t; i < nv; i += PBA_T) {
+#pragma unroll
+        for (int a = 0; a < PBA_S; ++a) {
+            float* m = arr[a] + f0 + 4 * (size_t)i;
+            float4* s = reinterpret_cast<float4*>(&s3[a][4 * i]);
+            const bool moment = a % 3 != 0;
+            if (STORE) {
+                if (moment) st_nt4(m, *s);
+                else *reinterpret_cast<float4*>(m) = *s;
+            } else {
+                *s = moment ? ld_nt4(m) : *reinterpret_cast<const float4*>(m);
+            }
+        }
+    }
+    for (int i = 4 * nv + t; i < nf; i += PBA_T) {
+#pragma unroll
+        for (int a = 0; a < PBA_S; ++a) {
+            float* m = arr[a] + f0 + i;
+            const bool moment = a % 3 != 0;
+            if (STORE) {
+                if (moment) st_nt(m, s3[a][i]);
+                else *m = s3[a][i];
+            } else {
+                s3[a][i] = moment ? ld_nt(m) : *m;
+            }
+        }
+    }
+}
+
 // At least three waves per SIMD (at most 168 VGPRs): with every load of a
 // thread issued in two batches (dense parameters and gradient inputs, then
 // the visible-only f_dc and statistics), that keeps enough bytes in flight.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ __launch_bounds__(PBA_T) __attribute__((amdgpu_waves_per_eu(3)))
 void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
                                                        GaussOut go, const float* __restrict__ gacc,
                                                        float* __restrict__ vis,
@@ -238,9 +282,15 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
                                                        float* __restrict__ max2d, float inv_max_dim,
                                                        float* __restrict__ v_mean_out,
                                                        float* __restrict__ v_scale_out,
-                                                       float* __restrict__ v_quat_out) {
-    const int g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= p.N) return;
+                                                       float* __restrict__ v_quat_out, int vec3) {
+    __shared__ float s3[PBA_S][3 * PBA_T];
+    const int g0 = blockIdx.x * PBA_T, t = threadIdx.x;
+    // threads past the last gaussian work on a copy of it and store nothing
+    const bool live = g0 + t < p.N;
+    const int g = live ? g0 + t : p.N - 1;
+    const int nf = 3 * min(PBA_T, p.N - g0);
+    float* const arr3[PBA_S] = {P.params[0], P.m[0], P.v[0], P.params[1], P.m[1], P.v[1]};
+    stage_rows3<false>(arr3, 3 * (size_t)g0, nf, vec3 != 0, s3);
     // The dense parameters and moments are loaded up front, so that these
     // loads and the gradient inputs share one memory round trip.  The moments
     // are loaded and stored non-temporally (nothing else reads them in the
@@ -248,14 +298,15 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
     // sp / sm / sv [k]: 0-2 means, 3-5 scales, 6-9 quats, 10 opacity (the
     // visible-only f_dc update loads its own).
     float sp[11], sm[11], sv[11];
+    __syncthreads();
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-        sp[k] = P.params[0][3 * (size_t)g + k];
-        sm[k] = ld_nt(P.m[0] + 3 * (size_t)g + k);
-        sv[k] = ld_nt(P.v[0] + 3 * (size_t)g + k);
-        sp[3 + k] = P.params[1][3 * (size_t)g + k];
-        sm[3 + k] = ld_nt(P.m[1] + 3 * (size_t)g + k);
-        sv[3 + k] = ld_nt(P.v[1] + 3 * (size_t)g + k);
+        sp[k] = s3[0][3 * t + k];
+        sm[k] = s3[1][3 * t + k];
+        sv[k] = s3[2][3 * t + k];
+        sp[3 + k] = s3[3][3 * t + k];
+        sm[3 + k] = s3[4][3 * t + k];
+        sv[3 + k] = s3[5][3 * t + k];
     }
     {
         const float4 a = reinterpret_cast<const float4*>(P.params[2])[g];
@@ -268,7 +319,7 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
     sp[10] = P.params[5][g];
     sm[10] = ld_nt(P.m[5] + g);
     sv[10] = ld_nt(P.v[5] + g);
-    const int rad = go.radii[g];
+    const int rad = live ? go.radii[g] : 0;
     const float* ga = gacc + (size_t)g * 9;
     F3 vm{0.f, 0.f, 0.f};
     float vs[3] = {0.f, 0.f, 0.f}, vq[4] = {0.f, 0.f, 0.f, 0.f};
@@ -448,13 +499,13 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
         gnorm[g] = st_gnorm + sqrtf(vxy0 * vxy0 + vxy1 * vxy1);
         max2d[g] = fmaxf(st_max2d, (float)rad * inv_max_dim);
     }
-    if (v_mean_out) {
+    if (v_mean_out && live) {
         v_mean_out[3 * g] = vm.x; v_mean_out[3 * g + 1] = vm.y; v_mean_out[3 * g + 2] = vm.z;
     }
-    if (v_scale_out) {
+    if (v_scale_out && live) {
         v_scale_out[3 * g] = vs[0]; v_scale_out[3 * g + 1] = vs[1]; v_scale_out[3 * g + 2] = vs[2];
     }
-    if (v_quat_out) {
+    if (v_quat_out && live) {
         v_quat_out[4 * g] = vq[0]; v_quat_out[4 * g + 1] = vq[1];
         v_quat_out[4 * g + 2] = vq[2]; v_quat_out[4 * g + 3] = vq[3];
     }
@@ -466,16 +517,23 @@ void k_proj_bwd_adam(CamParams p, BwdPtrs P, AdamHP hp,
         adam_elem(sp[k], sm[k], sv[k], gr[k], hp.step[grp[k]], hp.b1, hp.b2, hp.inv_bc2[grp[k]], hp.eps);
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-        const size_t i = 3 * (size_t)g + k;
-        P.params[0][i] = sp[k]; st_nt(P.m[0] + i, sm[k]); st_nt(P.v[0] + i, sv[k]);
-        P.params[1][i] = sp[3 + k]; st_nt(P.m[1] + i, sm[3 + k]); st_nt(P.v[1] + i, sv[3 + k]);
+        s3[0][3 * t + k] = sp[k];
+        s3[1][3 * t + k] = sm[k];
+        s3[2][3 * t + k] = sv[k];
+        s3[3][3 * t + k] = sp[3 + k];
+        s3[4][3 * t + k] = sm[3 + k];
+        s3[5][3 * t + k] = sv[3 + k];
     }
-    reinterpret_cast<float4*>(P.params[2])[g] = make_float4(sp[6], sp[7], sp[8], sp[9]);
-    st_nt4(P.m[2] + 4 * (size_t)g, make_float4(sm[6], sm[7], sm[8], sm[9]));
-    st_nt4(P.v[2] + 4 * (size_t)g, make_float4(sv[6], sv[7], sv[8], sv[9]));
-    P.params[5][g] = sp[10];
-    st_nt(P.m[5] + g, sm[10]);
-    st_nt(P.v[5] + g, sv[10]);
+    if (live) {
+        reinterpret_cast<float4*>(P.params[2])[g] = make_float4(sp[6], sp[7], sp[8], sp[9]);
+        st_nt4(P.m[2] + 4 * (size_t)g, make_float4(sm[6], sm[7], sm[8], sm[9]));
+        st_nt4(P.v[2] + 4 * (size_t)g, make_float4(sv[6], sv[7], sv[8], sv[9]));
+        P.params[5][g] = sp[10];
+        st_nt(P.m[5] + g, sm[10]);
+        st_nt(P.v[5] + g, sv[10]);
+    }
+    __syncthreads();
+    stage_rows3<true>(arr3, 3 * (size_t)g0, nf, vec3 != 0, s3);
 }
 
 }  // namespace
@@ -499,8 +557,13 @@ void launch_proj_bwd_adam(hipStream_t s, const CamParams& p, float* const params
     if (p.N <= 0) return;
     BwdPtrs P;
     for (int i = 0; i < 6; ++i) { P.params[i] = params[i]; P.m[i] = m[i]; P.v[i] = v[i]; }
-    hipLaunchKernelGGL(k_proj_bwd_adam, dim3((p.N + 255) / 256), dim3(256), 0, s, p, P, hp, go,
-                       gacc, vis, gnorm, max2d, inv_max_dim, v_mean_out, v_scale_out, v_quat_out);
+    bool vec3 = true;
+    for (int i = 0; i < 2; ++i)
+        for (const float* q : {params[i], m[i], v[i]})
+            vec3 = vec3 && reinterpret_cast<uintptr_t>(q) % 16 == 0;
+    hipLaunchKernelGGL(k_proj_bwd_adam, dim3((p.N + PBA_T - 1) / PBA_T), dim3(PBA_T), 0, s, p, P,
+                       hp, go, gacc, vis, gnorm, max2d, inv_max_dim, v_mean_out, v_scale_out,
+                       v_quat_out, vec3 ? 1 : 0);
 }
 
 
