@@ -364,6 +364,9 @@ __device__ __forceinline__ void seg_write(int j, int S, const int* __restrict__ 
                                           const int* __restrict__ tile_bins, int tbx, int tby,
                                           int sbx, uint32_t* __restrict__ ids) {
     __shared__ uint32_t s_k[SEG_REFS], s_g[SEG_REFS];
+    // bit y: the reference covers local tile row y; zero past the segment's
+    // last reference up to a multiple of 64
+    __shared__ uint16_t s_m[SEG_REFS];
     __shared__ uint16_t s_q[SUPER][128];   // per row: ring of covering reference indices
     const int lane = threadIdx.x & 63, ly = threadIdx.x >> 6;
     const int nseg = sstart[S];
@@ -371,9 +374,17 @@ __device__ __forceinline__ void seg_write(int j, int S, const int* __restrict__ 
     if (j >= nseg) return;
     const int s = sg.x;
     const int n = sg.z - sg.y;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        s_k[i] = rkey[sg.y + i];
-        s_g[i] = rval[sg.y + i];
+    const int n64 = (n + 63) & ~63;
+    for (int i = threadIdx.x; i < n64; i += 1024) {
+        uint32_t k = 0u, m = 0u;
+        if (i < n) {
+            k = rkey[sg.y + i];
+            s_k[i] = k;
+            s_g[i] = rval[sg.y + i];
+            const uint32_t y0 = (k >> 20) & 15u, y1 = y0 + ((k >> 28) & 15u) + 1u;
+            m = ((1u << y1) - 1u) & ~((1u << y0) - 1u);
+        }
+        s_m[i] = (uint16_t)m;
     }
     const int ty = (s / sbx) * SUPER + ly;
     int myb = 0;
@@ -389,9 +400,7 @@ __device__ __forceinline__ void seg_write(int j, int S, const int* __restrict__ 
     int head = 0, tail = 0;   // wave-uniform ring positions (tail - head <= 127)
     for (int r0 = 0; r0 < n; r0 += 64) {
         const int r = r0 + lane;
-        const uint32_t k = r < n ? s_k[r] : 0u;
-        const int y0 = (int)((k >> 20) & 15u), y1 = y0 + (int)((k >> 28) & 15u) + 1;
-        const bool cov = r < n && y0 <= ly && ly < y1;
+        const bool cov = (s_m[r] >> ly) & 1u;
         const uint64_t b = wave_ballot(cov);
         const int below = (int)__builtin_amdgcn_mbcnt_hi(
             (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
