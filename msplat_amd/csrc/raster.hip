@@ -556,6 +556,9 @@ __global__ __launch_bounds__(256) void k_raster_merge(int W, int H, int tbx, flo
     }
 }
 
+// COUNT: count the wave's evaluated entries and gradient pairs into work
+// (a launch without counters runs the variant that does not count).
+template <bool COUNT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k_raster_bwd(int W, int H, int tbx, float bg0, float bg1,
                                                     float bg2, const Meta* __restrict__ meta,
                                                     Items it,
@@ -667,7 +670,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
             const int q = ch + lane;
             uint64_t m = wave_ballot(q >= q0 && q < nb &&
                                      ((__float_as_int(s_aux[q].w) >> w) & 1));
-            nwit += __popcll(m);
+            if (COUNT) nwit += __popcll(m);
             // the chunk's byte offset in a VGPR: each entry's offset is then
             // one vector shift-add from the bit index, shared by its LDS reads
             int chb = ch * (int)sizeof(float4);
@@ -689,7 +692,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
                 // unchanged) and makes every term they contribute zero.
                 const uint64_t gmask = vmask & mask_lt(alpha, 0.999f);
                 const float ag = lane_of(gmask) ? alpha : 0.f;
-                ngrad += (unsigned)__popcll(gmask);
+                if (COUNT) ngrad += (unsigned)__popcll(gmask);
                 const float r0 = c.z, r1 = c.w, r2 = x.x;   // max(raw + 0.5, 0)
                 // hardware reciprocal (1 ulp, exact at 1): the backward is
                 // compared with a tolerance
@@ -729,7 +732,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
             }
         }
     }
-    if (work) {
+    if (COUNT && work) {
         unsigned long long* ws = work_slot(work);
         if (lane == 0 && ngrad) atomicAdd(ws + 1, (unsigned long long)ngrad);
         if (lane == 0 && nwit) atomicAdd(ws + 3, (unsigned long long)nwit);
@@ -863,9 +866,14 @@ void launch_raster_bwd(hipStream_t s, const CamParams& p, int64_t max_items, con
                        unsigned long long* work, const LossFold& lf) {
     // workgroup 0 folds the loss, the others take the items
     const int64_t g = std::max<int64_t>(max_items, 0) + 1;
-    hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)g), dim3(256), 0, s, p.W, p.H, p.tbx,
-                       p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T, final_idx, cb,
-                       v_out, gacc, work, lf);
+    if (work)
+        hipLaunchKernelGGL(k_raster_bwd<true>, dim3((unsigned)g), dim3(256), 0, s, p.W, p.H,
+                           p.tbx, p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T,
+                           final_idx, cb, v_out, gacc, work, lf);
+    else
+        hipLaunchKernelGGL(k_raster_bwd<false>, dim3((unsigned)g), dim3(256), 0, s, p.W, p.H,
+                           p.tbx, p.bg[0], p.bg[1], p.bg[2], meta, it, tile_bins, pk, final_T,
+                           final_idx, cb, v_out, gacc, work, lf);
 }
 
 }  // namespace msp
