@@ -46,7 +46,7 @@ constexpr int WIN = 11;
 //   vertical backward     rows 0 .. TY-1,    columns 0 .. TX-1     the outputs
 // For 32 x 32 outputs the horizontal sums are evaluated 2.13 times per
 // output, the fields 1.72 times and the horizontal backward 1.31 times.
-constexpr int TX = 32, TY = 32, NT = 512;
+constexpr int TX = 32, TY = 32, NT = 1024;
 constexpr int IN_W = TX + 4 * HALF;   // 52
 constexpr int IN_H = TY + 4 * HALF;   // 52
 constexpr int HS_W = TX + 2 * HALF;   // 42
@@ -71,7 +71,9 @@ constexpr int FD_H = TY + 2 * HALF;   // 42
 //    over FD_H x TX: the vertical backward's lanes read consecutive columns.
 // The input and the fields share one LDS area, the horizontal sums and the
 // horizontal backward another (each pass reads one and writes the other):
-// 74.5 KB, two workgroups (four waves per SIMD) per CU.
+// 74.5 KB, two workgroups per CU; 1024 threads each (at most 64 VGPRs) make
+// that eight waves per SIMD, which hide the passes' LDS latency and barriers
+// better than 512 threads (four waves per SIMD) did.
 constexpr int IN_S = 74;
 constexpr int LDS_A = IN_H * IN_S * 8;                  // input; the fields (FD_H x FD_W x 16) fit
 constexpr int LDS_B = HS_H * HS_W * (16 + 4);           // horizontal sums; the backward (FD_H x TX x 16) fits
@@ -80,7 +82,7 @@ static_assert(FD_H * TX * 16 <= LDS_B, "horizontal backward overflows the sums' 
 constexpr int NPOS = (IN_H * IN_W + NT - 1) / NT;      // input positions per thread
 constexpr int NOUT = TX * TY / NT;                      // output pixels per thread
 
-__global__ __launch_bounds__(NT) void k_ssim_tile(int W, int H, const float* __restrict__ img,
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_ssim_tile(int W, int H, const float* __restrict__ img,
                                                   const float* __restrict__ gt, float w_ssim,
                                                   float inv_n, float* __restrict__ v_rendered,
                                                   float* __restrict__ loss_part) {
