@@ -137,23 +137,29 @@ __device__ __forceinline__ float4 lds_f4(const float4* base, int qb) {
 constexpr int RED_ROW = 64;
 
 // Sum over the 64 lanes of a wave of eight values per lane, through the
-// wave's own LDS area red[8][RED_ROW]: each lane writes its eight values to
-// row k, lane l then adds the eight partials 8 (l & 7) .. 8 (l & 7) + 7 of
-// row l >> 3 and the eight lanes of each group combine by DPP (xor 1, xor 2,
-// mirror within 8).  Lane 8k ends with the total of value k.  Only this wave
-// touches red, and a wave's LDS accesses are performed in order, so no
-// barrier is needed; the wave barriers keep the compiler from moving the
-// accesses across each other.  All lanes must be active.
-__device__ __forceinline__ float wave_sum8_lds(const float* v, int lane, float* red) {
+// wave's own LDS area red[8][RED_ROW], in three parts: red8_write puts each
+// lane's eight values in rows 0..7; red8_issue loads, for lane l, the eight
+// partials 8 (l & 7) .. 8 (l & 7) + 7 of row l >> 3; red8_finish adds them
+// and combines the eight lanes of each group by DPP (xor 1, xor 2, mirror
+// within 8), so that lane 8k ends with the total of value k.  The raster
+// backward reads a step's partials back one evaluated step after it wrote
+// them, so that the LDS round trip overlaps that step's arithmetic.  Only
+// this wave touches red, and a wave's LDS accesses are performed in order:
+// a read issued before the next write sees the earlier partials, with no
+// barrier; wave barriers keep the compiler from moving the accesses across
+// each other.  All lanes must be active.
+__device__ __forceinline__ void red8_write(const float* v, int lane, float* red) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) red[k * RED_ROW + lane] = v[k];
-    __builtin_amdgcn_wave_barrier();
+}
+__device__ __forceinline__ void red8_issue(int lane, const float* red, float4& a, float4& b) {
     const int g = lane >> 3, h = (g & 1) << 2;
     const float* rb = red + g * RED_ROW + (lane & 7) * 8;
-    const float4 a = *reinterpret_cast<const float4*>(rb + h);
-    const float4 b = *reinterpret_cast<const float4*>(rb + (h ^ 4));
+    a = *reinterpret_cast<const float4*>(rb + h);
+    b = *reinterpret_cast<const float4*>(rb + (h ^ 4));
+}
+__device__ __forceinline__ float red8_finish(float4 a, float4 b) {
     float u = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
-    __builtin_amdgcn_wave_barrier();
     u += dpp<0xB1>(u);     // quad_perm [1,0,3,2]
     u += dpp<0x4E>(u);     // quad_perm [2,3,0,1]
     u += dpp<0x141>(u);    // row_half_mirror: lane ^ 7 within each 8 lanes
@@ -605,6 +611,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
     const bool own = (lane & 7) == 0 || lane == 63;
     const uint32_t kofs = lane == 63 ? 32u : (uint32_t)(lane >> 3) * 4u;
     float* red = reinterpret_cast<float*>(s_red4) + w * 8 * RED_ROW;
+    // The gradient sums of an evaluated step are completed during the next
+    // one: pend says a step's eight partials are in red, pofs is that
+    // gaussian's accumulator byte offset and puo its per-lane opacity term.
+    bool pend = false;
+    uint32_t pofs = 0u;
+    float puo = 0.f;
     unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
     if (px.inside) {
         const size_t pix = (size_t)px.i * W + px.j;
@@ -686,6 +698,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
                 // valid: qq >= qlo && !(alpha < 1/255) (sigma out of range: alpha < 1/255)
                 const uint64_t vmask = mask_ge_i(qb, qlob) & mask_uge(alpha, 1.f / 255.f);
                 if (vmask == 0) continue;
+                // the previous evaluated step's partials (written a step ago):
+                // read now (unused when there is none), summed below, after
+                // this step's arithmetic
+                float4 pa, pb;
+                __builtin_amdgcn_wave_barrier();
+                red8_issue(lane, red, pa, pb);
                 // Branch-free per lane: lanes without a gradient run the same
                 // steps with alpha = 0, which leaves their state as it is
                 // (1 / (1 - 0) = 1 exactly, so Tn = T; fac = 0, so E is
@@ -721,16 +739,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
                 v[5] = fac * vo0;
                 v[6] = fac * vo1;
                 v[7] = fac * vo2;
-                // opacity (logit) term -v_sigma (1 - o): its total goes to
-                // lane 63 of u (lanes 60..62 are no owners)
-                const float u = wave_sum_into_lane63(vsg * x.y, wave_sum8_lds(v, lane, red));
-                // v_rgb of a channel whose raw colour + 0.5 < 0 is dropped by
-                // its consumers (the mask is per gaussian, not per pixel)
-                float* ap = reinterpret_cast<float*>(reinterpret_cast<char*>(gacc) +
-                                                     ((uint32_t)__float_as_int(x.z) + kofs));
-                if (own) atomicAdd(ap, u);
+                // The previous step's sums follow this step's arithmetic
+                // (the empty asm keeps them there, so that the loads' latency
+                // is spent on it); the opacity (logit) term -v_sigma (1 - o)
+                // goes to lane 63 of them (lanes 60..62 are no owners).  v_rgb
+                // of a channel whose raw colour + 0.5 < 0 is dropped by its
+                // consumers (the mask is per gaussian, not per pixel).
+                asm volatile("" : "+v"(pa.x), "+v"(pa.y), "+v"(pa.z), "+v"(pa.w), "+v"(pb.x),
+                             "+v"(pb.y), "+v"(pb.z), "+v"(pb.w) : "v"(v[7]), "v"(v[4]));
+                if (pend) {
+                    const float s = wave_sum_into_lane63(puo, red8_finish(pa, pb));
+                    float* ap = reinterpret_cast<float*>(reinterpret_cast<char*>(gacc) + (pofs + kofs));
+                    if (own) atomicAdd(ap, s);
+                }
+                __builtin_amdgcn_wave_barrier();
+                red8_write(v, lane, red);
+                __builtin_amdgcn_wave_barrier();
+                pend = true;
+                pofs = (uint32_t)__builtin_amdgcn_readfirstlane(__float_as_int(x.z));
+                puo = vsg * x.y;
             }
         }
+    }
+    if (pend) {   // the last evaluated step's sums
+        __builtin_amdgcn_wave_barrier();
+        float4 pa, pb;
+        red8_issue(lane, red, pa, pb);
+        const float s = wave_sum_into_lane63(puo, red8_finish(pa, pb));
+        float* ap = reinterpret_cast<float*>(reinterpret_cast<char*>(gacc) + (pofs + kofs));
+        if (own) atomicAdd(ap, s);
     }
     if (COUNT && work) {
         unsigned long long* ws = work_slot(work);
