@@ -45,7 +45,11 @@ constexpr int WIN = 11;
 //   horizontal backward   rows -5 .. TY+4,   columns 0 .. TX-1     FD_H x TX
 //   vertical backward     rows 0 .. TY-1,    columns 0 .. TX-1     the outputs
 // For 32 x 32 outputs the horizontal sums are evaluated 2.13 times per
-// output, the fields 1.72 times and the horizontal backward 1.31 times.
+// output, the fields 1.72 times and the horizontal backward 1.31 times.  The
+// two sum passes take two neighbouring positions per item (along the row for
+// the horizontal sums, down the column for the vertical ones): the twelve
+// inputs of the pair are read once instead of eleven per position, and the
+// vertical pass's 21 x 42 items take one round of the 1024 threads.
 constexpr int TX = 32, TY = 32, NT = 1024;
 constexpr int IN_W = TX + 4 * HALF;   // 52
 constexpr int IN_H = TY + 4 * HALF;   // 52
@@ -57,10 +61,12 @@ constexpr int FD_H = TY + 2 * HALF;   // 42
 // (64 banks of 4 bytes; a wave's 8-byte reads are served 32 lanes at a time,
 // its 16-byte reads 16 lanes at a time):
 //  * input: (gt, render) of a position as one float2, rows IN_S float2 apart.
-//    The horizontal pass gives lane l the position p + l of a row-major walk
-//    over HS_H x HS_W, so 32 lanes cover at most two row pieces, [a, 42) of
-//    one row and [0, a - 10) of the next; IN_S = 74 = 10 (mod 32) puts the
-//    second piece on exactly the 8-byte bank pairs the first leaves.
+//    The horizontal pass gives lane l the position pair p + l of a row-major
+//    walk over the HS_H x HS_W / 2 pairs and reads its inputs 16 bytes (two
+//    positions) at a time, so 16 lanes cover at most two row pieces, pairs
+//    [a, 21) of one row and [0, a - 5) of the next; IN_S = 74 = 10 (mod 32)
+//    puts the second piece on exactly the 16-byte bank groups the first
+//    leaves.
 //  * horizontal sums: (mu_x, mu_y, E[x^2], E[y^2]) as a float4 and E[xy] as a
 //    float, row-major over HS_H x HS_W (the vertical pass's lanes read
 //    consecutive positions).
@@ -79,6 +85,7 @@ constexpr int LDS_A = IN_H * IN_S * 8;                  // input; the fields (FD
 constexpr int LDS_B = HS_H * HS_W * (16 + 4);           // horizontal sums; the backward (FD_H x TX x 16) fits
 static_assert(FD_H * FD_W * 16 <= LDS_A, "fields overflow the input's area");
 static_assert(FD_H * TX * 16 <= LDS_B, "horizontal backward overflows the sums' area");
+static_assert(HS_W % 2 == 0 && FD_H % 2 == 0 && IN_S % 2 == 0, "two positions per item, 16-byte aligned");
 constexpr int NPOS = (IN_H * IN_W + NT - 1) / NT;      // input positions per thread
 constexpr int NOUT = TX * TY / NT;                      // output pixels per thread
 
@@ -147,59 +154,107 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
         }
         __syncthreads();
         // horizontal zero-padded sums (ssim_h_fwd, .metal:3094-3114) at the
-        // in-image positions; zero elsewhere
-        for (int i = t; i < HS_H * HS_W; i += NT) {
-            const int hy = i / HS_W, hx = i - hy * HS_W;
+        // in-image positions; zero elsewhere.  An item takes two neighbouring
+        // positions: their twelve inputs are six 16-byte reads (each position
+        // adds its eleven terms in the reference's order).
+        for (int i = t; i < HS_H * (HS_W / 2); i += NT) {
+            const int hy = i / (HS_W / 2), hx = 2 * (i - hy * (HS_W / 2));
             const int gy = y0 - 2 * HALF + hy, gx = x0 - HALF + hx;
-            float mx = 0.f, my = 0.f, sxx = 0.f, syy = 0.f, cxy = 0.f;
-            if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
-                const float2* row = s_in + hy * IN_S + hx;
+            const bool rin = gy >= 0 && gy < H;
+            const bool in0 = rin && gx >= 0 && gx < W, in1 = rin && gx + 1 >= 0 && gx + 1 < W;
+            // inputs hx + k, k = 0..11, read two at a time: input k is term k
+            // of the first position's sums and term k - 1 of the second's
+            float acc[2][5] = {};
+            const float4* row = reinterpret_cast<const float4*>(s_in + hy * IN_S + hx);
 #pragma unroll
-                for (int d = 0; d < WIN; ++d) {
-                    const float w = GAUSS_1D[d];
-                    const float2 v = row[d];
-                    const float gv = v.x, rv = v.y;
-                    const float wg = w * gv, wr = w * rv;
-                    mx = fmaf(w, gv, mx);
-                    my = fmaf(w, rv, my);
-                    sxx = fmaf(wg, gv, sxx);
-                    syy = fmaf(wr, rv, syy);
-                    cxy = fmaf(wg, rv, cxy);
+            for (int q = 0; q < (WIN + 1) / 2; ++q) {
+                const float4 f = row[q];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int k = 2 * q + e;
+                    const float gv = e ? f.z : f.x, rv = e ? f.w : f.y;
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int d = k - u;
+                        if (d < 0 || d >= WIN) continue;
+                        const float w = GAUSS_1D[d];
+                        const float wg = w * gv, wr = w * rv;
+                        acc[u][0] = fmaf(w, gv, acc[u][0]);
+                        acc[u][1] = fmaf(w, rv, acc[u][1]);
+                        acc[u][2] = fmaf(wg, gv, acc[u][2]);
+                        acc[u][3] = fmaf(wr, rv, acc[u][3]);
+                        acc[u][4] = fmaf(wg, rv, acc[u][4]);
+                    }
                 }
             }
-            s_h4[i] = make_float4(mx, my, sxx, syy);
-            s_h1[i] = cxy;
+            float a[2][5];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const bool in = u == 0 ? in0 : in1;
+#pragma unroll
+                for (int r = 0; r < 5; ++r) a[u][r] = in ? acc[u][r] : 0.f;
+            }
+            const int o = hy * HS_W + hx;
+            s_h4[o] = make_float4(a[0][0], a[0][1], a[0][2], a[0][3]);
+            s_h4[o + 1] = make_float4(a[1][0], a[1][1], a[1][2], a[1][3]);
+            *reinterpret_cast<float2*>(s_h1 + o) = make_float2(a[0][4], a[1][4]);
         }
         __syncthreads();
         // vertical sums, SSIM and the derivative fields (.metal:3243-3300)
         // at the centres of the in-image rows (the fields of other rows are
-        // never read: their horizontal backward is zero)
-        for (int i = t; i < FD_H * FD_W; i += NT) {
-            const int fy = i / FD_W, fx = i - fy * FD_W;
-            const int gy = y0 - HALF + fy, gx = x0 - HALF + fx;
-            if (gy < 0 || gy >= H) continue;
-            float mx = 0.f, my = 0.f, sx = 0.f, sy = 0.f, cxy = 0.f;
+        // never read: their horizontal backward is zero).  An item takes two
+        // rows of one column: twelve rows of sums serve both.
+        for (int i = t; i < (FD_H / 2) * FD_W; i += NT) {
+            const int fy0 = 2 * (i / FD_W), fx = i - (i / FD_W) * FD_W;
+            const int gx = x0 - HALF + fx;
+            // rows fy0 + k, k = 0..11: row k is term k of the first row's
+            // sums and term k - 1 of the second's, each added in order
+            float acc[2][5] = {};
 #pragma unroll
-            for (int k = 0; k < WIN; ++k) {
-                const float w = GAUSS_1D[k];
-                const float4 h = s_h4[(fy + k) * HS_W + fx];
-                const float h4 = s_h1[(fy + k) * HS_W + fx];
-                mx = fmaf(w, h.x, mx);
-                my = fmaf(w, h.y, my);
-                sx = fmaf(w, h.z, sx);
-                sy = fmaf(w, h.w, sy);
-                cxy = fmaf(w, h4, cxy);
+            for (int k = 0; k < WIN + 1; ++k) {
+                const float4 q = s_h4[(fy0 + k) * HS_W + fx];
+                const float q4 = s_h1[(fy0 + k) * HS_W + fx];
+                if (k < WIN) {
+                    const float w = GAUSS_1D[k];
+                    acc[0][0] = fmaf(w, q.x, acc[0][0]);
+                    acc[0][1] = fmaf(w, q.y, acc[0][1]);
+                    acc[0][2] = fmaf(w, q.z, acc[0][2]);
+                    acc[0][3] = fmaf(w, q.w, acc[0][3]);
+                    acc[0][4] = fmaf(w, q4, acc[0][4]);
+                }
+                if (k > 0) {
+                    const float w = GAUSS_1D[k - 1];
+                    acc[1][0] = fmaf(w, q.x, acc[1][0]);
+                    acc[1][1] = fmaf(w, q.y, acc[1][1]);
+                    acc[1][2] = fmaf(w, q.z, acc[1][2]);
+                    acc[1][3] = fmaf(w, q.w, acc[1][3]);
+                    acc[1][4] = fmaf(w, q4, acc[1][4]);
+                }
+                // the sums are formed row by row (without this the compiler
+                // sinks them into the per-row validity test and keeps all
+                // twelve rows in registers, which spills)
+                asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]),
+                             "+v"(acc[0][4]), "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(acc[1][2]),
+                             "+v"(acc[1][3]), "+v"(acc[1][4]));
             }
-            const float sxs = sx - mx * mx, sys = sy - my * my, sxy = cxy - mx * my;
-            const float A = 2.0f * mx * my + SSIM_C1, B = 2.0f * sxy + SSIM_C2;
-            const float Cd = mx * mx + my * my + SSIM_C1, D = sxs + sys + SSIM_C2;
-            const float iCD = 1.0f / (Cd * D);
-            const float dmu = 2.0f * B * (mx * Cd - A * my) / (Cd * Cd * D);
-            const float dsyq = -A * B * iCD / D, dsxy = 2.0f * A * iCD;
-            s_f[i] = make_float4(dmu - 2.0f * my * dsyq - mx * dsxy, 2.0f * dsyq, dsxy, 0.f);
-            // the tile's own in-image outputs add their SSIM to the loss
-            if (fy >= HALF && fy < HALF + TY && fx >= HALF && fx < HALF + TX && gx >= 0 && gx < W)
-                ssim_sum += (A * B) / (Cd * D);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int fy = fy0 + u;
+                const int gy = y0 - HALF + fy;
+                if (gy < 0 || gy >= H) continue;
+                const float mx = acc[u][0], my = acc[u][1], sx = acc[u][2], sy = acc[u][3],
+                            cxy = acc[u][4];
+                const float sxs = sx - mx * mx, sys = sy - my * my, sxy = cxy - mx * my;
+                const float A = 2.0f * mx * my + SSIM_C1, B = 2.0f * sxy + SSIM_C2;
+                const float Cd = mx * mx + my * my + SSIM_C1, D = sxs + sys + SSIM_C2;
+                const float iCD = 1.0f / (Cd * D);
+                const float dmu = 2.0f * B * (mx * Cd - A * my) / (Cd * Cd * D);
+                const float dsyq = -A * B * iCD / D, dsxy = 2.0f * A * iCD;
+                s_f[fy * FD_W + fx] = make_float4(dmu - 2.0f * my * dsyq - mx * dsxy, 2.0f * dsyq, dsxy, 0.f);
+                // the tile's own in-image outputs add their SSIM to the loss
+                if (fy >= HALF && fy < HALF + TY && fx >= HALF && fx < HALF + TX && gx >= 0 && gx < W)
+                    ssim_sum += (A * B) / (Cd * D);
+            }
         }
         __syncthreads();
         // mirrored horizontal backward at the in-image rows of the tile's
