@@ -57,8 +57,8 @@ constexpr int HS_W = TX + 2 * HALF;   // 42
 constexpr int HS_H = IN_H;            // 52
 constexpr int FD_W = HS_W;            // 42
 constexpr int FD_H = TY + 2 * HALF;   // 42
-// LDS layouts, chosen so that the passes' reads are free of bank conflicts
-// (64 banks of 4 bytes; a wave's 8-byte reads are served 32 lanes at a time,
+// LDS layouts, chosen so that most of the passes' accesses are free of bank
+// conflicts (64 banks of 4 bytes; a wave's 8-byte reads are served 32 lanes at a time,
 // its 16-byte reads 16 lanes at a time):
 //  * input: (gt, render) of a position as one float2, rows IN_S float2 apart.
 //    The horizontal pass gives lane l the position pair p + l of a row-major
@@ -69,7 +69,10 @@ constexpr int FD_H = TY + 2 * HALF;   // 42
 //    leaves.
 //  * horizontal sums: (mu_x, mu_y, E[x^2], E[y^2]) as a float4 and E[xy] as a
 //    float, row-major over HS_H x HS_W (the vertical pass's lanes read
-//    consecutive positions).
+//    consecutive positions).  Lanes share bank groups where the vertical
+//    pass's items wrap to the row pair below and in the horizontal pass's
+//    two float4 stores per lane; layouts without those conflicts were
+//    measured no faster.
 //  * fields (f1, f2, f3) as one float4 per position, row-major over
 //    FD_H x FD_W: the horizontal backward's 16-lane quarters read 16
 //    consecutive positions of one row.
