@@ -190,6 +190,15 @@ def test_train_step_partial_edge_tiles(dev):
     _train_compare(dev, small_scene(n=5000, width=167, height=93, seed_off=91))
 
 
+@pytest.mark.parametrize("width,height", [(7, 5), (13, 9), (43, 11), (33, 47)])
+def test_train_step_tiny_odd_images(dev, width, height):
+    """Train steps at images smaller than or just past one SSIM tile (32 x 32)
+    and its window: odd widths, so that the horizontal sums' position pairs
+    end half inside the image, heights that cut the vertical pass's row pairs,
+    and a single raster tile; the loss gradient image must stay bit-exact."""
+    _train_compare(dev, small_scene(n=300, width=width, height=height, seed_off=95 + width))
+
+
 def test_train_step_partial_edge_tiles_chunked(dev):
     """Partial edge tiles in chunk mode (fewer than 400 tiles) with
     multi-chunk tiles: prefix / suffix backward at the image border."""
