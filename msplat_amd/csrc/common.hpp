@@ -235,6 +235,15 @@ __device__ __forceinline__ void st_nt4(float* p, float4 v) {
     __builtin_nontemporal_store(ntf4{v.x, v.y, v.z, v.w}, reinterpret_cast<ntf4*>(p));
 }
 
+// Work index of workgroup b < n such that the workgroups of one XCD take
+// consecutive indices: the hardware places workgroups on its 8 XCDs round
+// robin (XCD b % 8), so XCD x's workgroups x, x + 8, ... get a contiguous
+// run of indices.  A bijection of [0, n).
+__device__ __forceinline__ int xcd_order(int b, int n) {
+    const int x = b & 7, q = n >> 3, rem = n & 7;
+    return x * q + min(x, rem) + (b >> 3);
+}
+
 __device__ __forceinline__ unsigned lane_id() { return __lane_id(); }
 
 }  // namespace msp

@@ -193,8 +193,11 @@ __global__ __launch_bounds__(RT) void k_radix_hist(const uint32_t* __restrict__ 
             __hip_atomic_store(ss.out, totals_word(ti, tr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     const int64_t ne = pass_n(n, n_dev);
-    const int64_t base = (int64_t)blockIdx.x * RB;
-    if (base >= ne) return;   // beyond the keys (the offsets scan only the blocks that hold some)
+    const int nbe = (int)((ne + RB - 1) / RB);
+    if ((int)blockIdx.x >= nbe) return;   // beyond the keys (the offsets scan only the blocks that hold some)
+    // this block's key range: the ranges of one XCD's blocks are consecutive
+    const int rb = xcd_order((int)blockIdx.x, nbe);
+    const int64_t base = (int64_t)rb * RB;
     if (threadIdx.x < D) h[threadIdx.x] = 0;
     __syncthreads();
     const bool cl = cull != 0;
@@ -231,7 +234,7 @@ __global__ __launch_bounds__(RT) void k_radix_hist(const uint32_t* __restrict__ 
     const int nd = (int)mask + 1 + (cl ? 1 : 0);
     if ((int)threadIdx.x < nd) {
         const int c = h[threadIdx.x];
-        hist[(size_t)threadIdx.x * nblocks + blockIdx.x] = c;
+        hist[(size_t)threadIdx.x * nblocks + rb] = c;
         // the digit's total over all blocks, spread over DCOPIES addresses
         if (c) atomicAdd(&dtot[(blockIdx.x % DCOPIES) * D + threadIdx.x], c);
     }
@@ -326,7 +329,13 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
             rg.cnt[p] = 0;
         }
     }
-    if (bbase >= ne) return;
+    const int nbe = (int)((ne + RB - 1) / RB);
+    if ((int)blockIdx.x >= nbe) return;
+    // this block's key range (as in the histogram kernel): the blocks of one
+    // XCD write the neighbouring pieces of each digit's output run, which
+    // then meet in that XCD's L2 instead of being written back in parts
+    const int rb = xcd_order((int)blockIdx.x, nbe);
+    const int64_t kbase = (int64_t)rb * RB;
     __shared__ uint32_t s_key[RB];
     __shared__ uint32_t s_val[RB];
     __shared__ int wcnt[RW][D];
@@ -338,10 +347,10 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     // this block's scatter offset of digit tid, loaded now so that its latency
     // overlaps the key loads and the ranking
-    const int my_gofs = tid < nd ? offs[(size_t)tid * nblocks + blockIdx.x] : 0;
+    const int my_gofs = tid < nd ? offs[(size_t)tid * nblocks + rb] : 0;
     for (int i = tid; i < RW * D; i += RT) (&wcnt[0][0])[i] = 0;
     __syncthreads();
-    const int64_t wbase = bbase + (int64_t)w * WK;
+    const int64_t wbase = kbase + (int64_t)w * WK;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     uint32_t key[RK], val[RK];
     int dig[RK], rank[RK];
@@ -397,7 +406,7 @@ __global__ __launch_bounds__(RT) void k_radix_scatter(const uint32_t* __restrict
         s_val[p] = val[j];
     }
     __syncthreads();
-    const int nvalid = (int)min((int64_t)RB, ne - bbase);
+    const int nvalid = (int)min((int64_t)RB, ne - kbase);
     int64_t opos[RK];  // output position of block element tid + u RT
 #pragma unroll
     for (int u = 0; u < RK; ++u) {
