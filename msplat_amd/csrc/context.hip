@@ -98,7 +98,7 @@ struct Ctx {
     Buf rkey, rval, rkey2, rval2, rtemp;
     Buf seg, phist;
     // per intersection: the tile-sorted gaussian ids
-    Buf tval;
+    Buf tval, qmask;
     // per item
     Buf it_tile, it_k, it_order, tile_order, it_cls, c_T, c_C, c_idx, c_pT, c_aC;
     // per pixel
@@ -195,7 +195,7 @@ void free_all(Ctx* c) {
                    &c->dtemp, &c->stemp, &c->tcount, &c->tscan, &c->tile_done, &c->tile_bins, &c->tile_K,
                    &c->tile_item0, &c->l_chunked, &c->st_r0, &c->st_r1, &c->sstart,
                    &c->rkey, &c->rval, &c->rkey2, &c->rval2, &c->rtemp, &c->seg, &c->phist,
-                   &c->tval,
+                   &c->tval, &c->qmask,
                    &c->it_tile, &c->it_k, &c->it_order, &c->tile_order, &c->it_cls, &c->c_T, &c->c_C,
                    &c->c_idx, &c->c_pT, &c->c_aC, &c->final_T, &c->final_idx, &c->out_img,
                    &c->v_rendered, &c->loss_part, &c->meta_d, &c->loss_d,
@@ -240,6 +240,7 @@ Entries packed(Ctx* c) {
     Entries pk;
     pk.ids = c->sorted_ids;
     pk.rec = P<float4>(c->rec);
+    pk.qmask = P<uint8_t>(c->qmask);
     return pk;
 }
 
@@ -475,6 +476,7 @@ int forward(Ctx* c, const MsplatRenderArgs* a, bool training, float* dst_img = n
     const size_t R = (size_t)std::max<int64_t>(R64, 1);
     const size_t NS = (size_t)segments_bound(R64, nst);
     ENSURE(c->tval, I * 4);
+    ENSURE(c->qmask, I);
     ENSURE(c->rkey, R * 4);
     ENSURE(c->rval, R * 4);
     ENSURE(c->rkey2, R * 4);

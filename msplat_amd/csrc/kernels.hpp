@@ -43,6 +43,11 @@ struct GaussOut {
 struct Entries {
     const uint32_t* ids;
     const float4* rec;
+    // One byte per entry: the 4-bit quadrant mask that the training
+    // forward computes for every entry it stages, read back by the backward
+    // (which walks only entries up to the last contributor, all of them
+    // staged by the forward) instead of computing it again.
+    uint8_t* qmask;
 };
 
 // Work items of the rasteriser: item i covers chunk item_k[i] of tile item_tile[i].

@@ -174,7 +174,9 @@ __device__ __forceinline__ float red8_finish(float4 a, float4 b) {
 // each wave walks the entries of its quadrant in order.  live: the lanes
 // whose pixel still composites (wave-uniform mask).  Every thread of the
 // workgroup calls this with the same range (it holds workgroup barriers).
-template <bool COUNT>
+// MASKS (the training forward): each staged entry's quadrant mask is also
+// stored for the backward.
+template <bool COUNT, bool MASKS = false>
 __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float fx, float fy,
                                           int tx0, int ty0, const Entries& pk, float4* s_geo,
                                           float4* s_col, float4* s_aux, float& T, float& C0,
@@ -192,6 +194,7 @@ __device__ __forceinline__ void fwd_range(int cs, int ce, uint64_t live, float f
             const float4 c = r[1];
             bl_raw = r[2].x;
             mask = quad_mask(g.x, g.y, g.z, g.w, c.x, c.y, tx0, ty0);
+            if (MASKS) pk.qmask[idx] = (uint8_t)mask;
             s_geo[tid] = g;
             s_col[tid] = make_float4(c.x, c.y, fmaxf(c.z + 0.5f, 0.f), fmaxf(c.w + 0.5f, 0.f));
         }
@@ -280,8 +283,8 @@ __device__ __forceinline__ void fwd_item(int item, int W, int H, int tbx, float 
     int last = cs - 1;
     unsigned ncl = 0;       // pairs composited by this lane
     unsigned nwit = 0;      // entries this wave evaluated (wave-uniform)
-    fwd_range<COUNT>(cs, ce, wave_ballot(px.inside), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, T, C0, C1,
-              C2, last, ncl, nwit);
+    fwd_range<COUNT, true>(cs, ce, wave_ballot(px.inside), fx, fy, tx0, ty0, pk, s_geo, s_col, s_aux, T,
+                           C0, C1, C2, last, ncl, nwit);
     add_work<COUNT>(work, ncl, nwit);
     if (!px.inside) return;
     if (K == 1) {
@@ -599,7 +602,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
     const Px px = pixel_of(t, tbx, W, H);
     const float fx = (float)px.j, fy = (float)px.i;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int tx0 = (t % tbx) * BLOCK, ty0 = (t / tbx) * BLOCK;
 
     float T = 1.f, Tfin = 1.f, B0 = 0.f, B1 = 0.f, B2 = 0.f, vo0 = 0.f, vo1 = 0.f, vo2 = 0.f;
     // bf = cs - 1 for pixels outside the image: no entry passes e_idx <= bf
@@ -654,13 +656,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
         __syncthreads();
         const int idx = top - tid;
         int mask = 0;
-        if (idx >= cs) {
+        // the entry's quadrant mask from the forward; an entry that reaches
+        // no quadrant is not gathered
+        mask = idx >= cs ? (int)pk.qmask[idx] : 0;
+        if (mask) {
             const int gid = (int)pk.ids[idx];
             const float4* r = pk.rec + 4 * (size_t)gid;
             const float4 g = r[0];
             float4 c = r[1];
             const float braw = r[2].x;
-            mask = quad_mask(g.x, g.y, g.z, g.w, c.x, c.y, tx0, ty0);
             s_geo[tid] = g;
             s_col[tid] = make_float4(c.x, c.y, fmaxf(c.z + 0.5f, 0.f), fmaxf(c.w + 0.5f, 0.f));
             // z: byte offset of the gaussian's accumulators (N * 36 < 2^31)
