@@ -655,10 +655,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
     for (int top = hi; top >= cs; top -= 256) {
         __syncthreads();
         const int idx = top - tid;
-        int mask = 0;
         // the entry's quadrant mask from the forward; an entry that reaches
         // no quadrant is not gathered
-        mask = idx >= cs ? (int)pk.qmask[idx] : 0;
+        const int mask = idx >= cs ? (int)pk.qmask[idx] : 0;
         if (mask) {
             const int gid = (int)pk.ids[idx];
             const float4* r = pk.rec + 4 * (size_t)gid;
